@@ -1,0 +1,145 @@
+/*
+ * phantom_moe.h -- C ABI of the MI355X (gfx950) sparse-MoE layer library
+ * (libphantom_moe.so).
+ *
+ * All pointers are device pointers unless stated otherwise; every entry point
+ * is asynchronous on the caller's stream, performs no device allocation and
+ * no host synchronisation, and returns 0 on success or a negative
+ * PHANTOM_MOE_E* status (the message is available from
+ * phantom_moe_last_error()).  Nothing here exits or aborts the process.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   - the router module PhantomTopKRouter.forward
+ *       tests/test_moe_routing.py:43-72
+ *   - the Q4_0 block format and its dequantisation
+ *       python/phantom/loader/gguf_loader.py:72, :362-381, :588-596
+ *   - the sparse SwiGLU FFN operator C ABI
+ *       kernels/sparse_moe/sparse_matmul.cu:240-255 (sparse_mlp_forward)
+ *   - the active-set compaction
+ *       kernels/sparse_moe/gate_predict.cu:153-177, :200-213
+ *   - the expert combine, which the reference delegates to transformers'
+ *     MoE blocks (python/phantom/phantom_cli.py:1393-1430)
+ *
+ * Data formats
+ *   x            [T, H] bf16 (x_dtype 0) or fp32 (x_dtype 1), row major.
+ *   router_w     [E, H] fp32 (nn.Linear weight layout: out x in).
+ *   router_bias  [E] fp32 or NULL; added to the logit before selection.
+ *   Q4_0         GGUF Q4_0 rows: each row of K weights is K/32 blocks of
+ *                18 bytes (fp16 scale d, then 16 bytes; byte j holds
+ *                element j in its low nibble and element j+16 in its high
+ *                nibble; value = (nibble - 8) * d).
+ *   repacked     the device layout produced by phantom_q4_0_repack: rows are
+ *                grouped 16 at a time and K is padded to a multiple of 128;
+ *                "nib" holds the nibble bytes (rows * Kpad / 2 bytes) in the
+ *                order the gfx950 MFMA operand loads consume them, "scale"
+ *                holds the fp16 scales (rows * Kpad / 32 values).
+ *                Stacked experts are stored back to back.
+ */
+#ifndef PHANTOM_MOE_H
+#define PHANTOM_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#define PHANTOM_MOE_API __attribute__((visibility("default")))
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PHANTOM_MOE_OK 0
+#define PHANTOM_MOE_EINVAL (-1)   /* bad shape, dtype, mode or null pointer */
+#define PHANTOM_MOE_EWORKSPACE (-2) /* workspace missing or too small */
+#define PHANTOM_MOE_ELAUNCH (-3)  /* a HIP launch or runtime call failed */
+#define PHANTOM_MOE_EUNSUPPORTED (-4) /* valid but outside this build's limits */
+
+#define PHANTOM_MOE_X_BF16 0
+#define PHANTOM_MOE_X_F32 1
+
+#define PHANTOM_MOE_SCORE_SOFTMAX 0 /* softmax over the k selected logits */
+#define PHANTOM_MOE_SCORE_SIGMOID 1 /* sigmoid(l_j) / sum_i sigmoid(l_i) over the k */
+
+/* Message describing the most recent failure on the calling thread. */
+PHANTOM_MOE_API const char* phantom_moe_last_error(void);
+
+/* Library version string. */
+PHANTOM_MOE_API const char* phantom_moe_version(void);
+
+/* ---------------------------------------------------------------- */
+/* Q4_0 repack                                                       */
+/* ---------------------------------------------------------------- */
+
+/* Bytes of the repacked nibble and scale buffers for a [rows, K] Q4_0
+ * matrix (rows % 16 == 0, K % 32 == 0); -1 on invalid shape. */
+PHANTOM_MOE_API int64_t phantom_q4_0_nib_bytes(int64_t rows, int64_t K);
+PHANTOM_MOE_API int64_t phantom_q4_0_scale_bytes(int64_t rows, int64_t K);
+
+/* GGUF Q4_0 bytes [rows, K/32, 18] -> repacked (nib, scale).  Lossless.
+ * Replaces the load-time dequantisation of gguf_loader.py:362-381 /
+ * :588-596: weights stay 4-bit in HBM and are expanded in registers. */
+PHANTOM_MOE_API int phantom_q4_0_repack(const uint8_t* q4_0, int64_t rows, int64_t K, uint8_t* nib, uint16_t* scale,
+                        hipStream_t stream);
+
+/* Inverse of phantom_q4_0_repack: reproduces the original bytes exactly. */
+PHANTOM_MOE_API int phantom_q4_0_unrepack(const uint8_t* nib, const uint16_t* scale, int64_t rows, int64_t K,
+                          uint8_t* q4_0, hipStream_t stream);
+
+/* Q4_0 bytes -> fp32 values [rows, K] (the arithmetic of
+ * gguf_loader.py:369-378, kept in fp32 instead of the bf16 cast at :380). */
+PHANTOM_MOE_API int phantom_q4_0_dequant_f32(const uint8_t* q4_0, int64_t rows, int64_t K, float* out,
+                             hipStream_t stream);
+
+/* ---------------------------------------------------------------- */
+/* Router, permute, layer                                            */
+/* ---------------------------------------------------------------- */
+
+/* Workspace bytes needed by phantom_moe_route / _permute / _forward for
+ * these sizes.  The workspace must be zero-filled once before its first use;
+ * the library leaves its internal counters at zero after every call.  One
+ * workspace must not be used by calls that may run concurrently. */
+PHANTOM_MOE_API size_t phantom_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int E, int top_k, int has_shared);
+
+/* Router: logits = x W^T (+ bias) under the fixed-order fp64 contract,
+ * top-k descending with ties to the lower expert index, weights by
+ * score_mode.  Replaces PhantomTopKRouter.forward
+ * (tests/test_moe_routing.py:56-72).
+ * Outputs topk_idx [T, top_k] int32 and topk_w [T, top_k] fp32. */
+PHANTOM_MOE_API int phantom_moe_route(const void* x, int x_dtype, const float* router_w, const float* router_bias,
+                      int64_t T, int64_t H, int E, int top_k, int score_mode, int32_t* topk_idx,
+                      float* topk_w, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Stable counting sort of the T*top_k (token, slot) pairs by expert.
+ * expert_offsets [E+1]: exclusive prefix sum of per-expert counts;
+ * sorted_slots [T*top_k]: slot ids s = t*top_k + j in (expert, s) order;
+ * slot_pos [T*top_k]: inverse permutation.  The device-side analogue of the
+ * compaction in kernels/sparse_moe/gate_predict.cu:153-177, made parallel and
+ * deterministic. */
+PHANTOM_MOE_API int phantom_moe_permute(const int32_t* topk_idx, int64_t T, int top_k, int E, int32_t* expert_offsets,
+                        int32_t* sorted_slots, int32_t* slot_pos, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+
+/* The whole MoE layer:
+ *   y[t] = sum_j w[t,j] * W_down_e (silu(W_gate_e x_t) * (W_up_e x_t)) + shared(x_t)
+ * with e = topk_idx[t,j].  x must be bf16.  Expert weights are repacked Q4_0:
+ * gate/up are E stacked [I, H] matrices, down E stacked [H, I] matrices.
+ * The sh_* pointers describe one always-on shared expert of the same shapes
+ * (weight 1.0), or are all NULL.  Outputs: y [T, H] fp32, topk_idx, topk_w.
+ * The FFN operator semantics follow kernels/sparse_moe/sparse_matmul.cu:120-215
+ * (SwiGLU, fp32 math) with 4-bit weights. */
+PHANTOM_MOE_API int phantom_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int E, int top_k,
+                        int score_mode, const float* router_w, const float* router_bias,
+                        const uint8_t* gate_nib, const uint16_t* gate_scale, const uint8_t* up_nib,
+                        const uint16_t* up_scale, const uint8_t* down_nib, const uint16_t* down_scale,
+                        const uint8_t* sh_gate_nib, const uint16_t* sh_gate_scale,
+                        const uint8_t* sh_up_nib, const uint16_t* sh_up_scale,
+                        const uint8_t* sh_down_nib, const uint16_t* sh_down_scale, float* y,
+                        int32_t* topk_idx, float* topk_w, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PHANTOM_MOE_H */

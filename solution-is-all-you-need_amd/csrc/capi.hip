@@ -1,0 +1,277 @@
+// capi.hip -- extern "C" entry points of libphantom_moe.so (declared in
+// include/phantom_moe.h).  Validates every argument on the host, carves the
+// caller's workspace, and launches the kernels asynchronously on the caller's
+// stream.  Never allocates, synchronises, exits or aborts: the reference's
+// CUDA_CHECK exits the process on error (kernels/common/cuda_utils.h:31-52)
+// and its host API blocks on a timer event (cuda_utils.h:253-257); here every
+// failure is a return code plus a thread-local message.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "moe_common.h"
+#include "moe_launch.h"
+#include "phantom_moe.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return PHANTOM_MOE_OK;
+}
+
+int launch_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(PHANTOM_MOE_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+int check_route_shapes(const void* x, int x_dtype, const float* router_w, int64_t T, int64_t H,
+                       int E, int top_k, int score_mode) {
+  if (!x || !router_w) return fail(PHANTOM_MOE_EINVAL, "x and router_w must be non-null");
+  if (x_dtype != PHANTOM_MOE_X_BF16 && x_dtype != PHANTOM_MOE_X_F32)
+    return fail(PHANTOM_MOE_EINVAL, "x_dtype must be 0 (bf16) or 1 (fp32), got %d", x_dtype);
+  if (T < 1) return fail(PHANTOM_MOE_EINVAL, "T must be >= 1, got %lld", (long long)T);
+  if (T > (int64_t)1 << 24) return fail(PHANTOM_MOE_EUNSUPPORTED, "T above 2^24 is not supported");
+  if (H < 32 || H % 32) return fail(PHANTOM_MOE_EINVAL, "H must be a positive multiple of 32, got %lld", (long long)H);
+  if (E < 1 || E > pmoe::kMaxExperts)
+    return fail(E < 1 ? PHANTOM_MOE_EINVAL : PHANTOM_MOE_EUNSUPPORTED, "E must be in [1, %d], got %d",
+                pmoe::kMaxExperts, E);
+  if (top_k < 1 || top_k > E) return fail(PHANTOM_MOE_EINVAL, "top_k must be in [1, E=%d], got %d", E, top_k);
+  if (top_k > pmoe::kMaxTopK)
+    return fail(PHANTOM_MOE_EUNSUPPORTED, "top_k above %d is not supported", pmoe::kMaxTopK);
+  if (score_mode != PHANTOM_MOE_SCORE_SOFTMAX && score_mode != PHANTOM_MOE_SCORE_SIGMOID)
+    return fail(PHANTOM_MOE_EINVAL, "score_mode must be 0 (softmax) or 1 (sigmoid), got %d", score_mode);
+  if (T * (int64_t)top_k > ((int64_t)1 << 30))
+    return fail(PHANTOM_MOE_EUNSUPPORTED, "T*top_k too large");
+  return 0;
+}
+
+}  // namespace
+
+namespace pmoe {
+
+size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared, void* base,
+                      Workspace* ws) {
+  const int64_t Kpad = round_up(H, kQuad);
+  const int64_t TT = router_token_tile(T);
+  const int64_t n_ttiles = ceil_div(T, TT);
+  const int64_t nslots = T * k;
+  const int64_t rows = nslots + (has_shared ? T : 0);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off = align256(off + bytes);
+    return o;
+  };
+  const size_t o_cnt = take(sizeof(int32_t) * (size_t)(n_ttiles + 1));
+  const size_t o_log = take(sizeof(double) * (size_t)(T * E));
+  const size_t o_xq = take(sizeof(uint16_t) * (size_t)(T * Kpad));
+  const size_t o_xs = take(sizeof(float) * (size_t)(T * (Kpad / kGroup)));
+  const size_t o_off = take(sizeof(int32_t) * (size_t)(E + 2));
+  const size_t o_act = take(sizeof(int32_t) * (size_t)(E + 1));
+  const size_t o_nact = take(sizeof(int32_t));
+  const size_t o_ss = take(sizeof(int32_t) * (size_t)nslots);
+  const size_t o_sp = take(sizeof(int32_t) * (size_t)nslots);
+  const int64_t KpadI = I > 0 ? round_up(I, kQuad) : 0;
+  const size_t o_hq = take(sizeof(uint16_t) * (size_t)(rows * KpadI * 2));
+  const size_t o_hs = take(sizeof(float) * (size_t)(rows * (KpadI / kGroup) * 2));
+  const size_t o_out = take(sizeof(float) * (size_t)(rows * (I > 0 ? H : 0)));
+  if (ws && base) {
+    char* b = static_cast<char*>(base);
+    ws->counters = reinterpret_cast<int32_t*>(b + o_cnt);
+    ws->logits = reinterpret_cast<double*>(b + o_log);
+    ws->xq = reinterpret_cast<uint16_t*>(b + o_xq);
+    ws->xs = reinterpret_cast<float*>(b + o_xs);
+    ws->offsets = reinterpret_cast<int32_t*>(b + o_off);
+    ws->active = reinterpret_cast<int32_t*>(b + o_act);
+    ws->n_active = reinterpret_cast<int32_t*>(b + o_nact);
+    ws->sorted_slots = reinterpret_cast<int32_t*>(b + o_ss);
+    ws->slot_pos = reinterpret_cast<int32_t*>(b + o_sp);
+    ws->hq = reinterpret_cast<uint16_t*>(b + o_hq);
+    ws->hs = reinterpret_cast<float*>(b + o_hs);
+    ws->outbuf = reinterpret_cast<float*>(b + o_out);
+  }
+  return off;
+}
+
+}  // namespace pmoe
+
+extern "C" {
+
+const char* phantom_moe_last_error(void) { return g_err; }
+
+const char* phantom_moe_version(void) { return "phantom_moe 0.1.0 gfx950"; }
+
+int64_t phantom_q4_0_nib_bytes(int64_t rows, int64_t K) {
+  if (rows < 0 || K < 0 || rows % 16 || K % 32) return -1;
+  return rows * pmoe::round_up(K, pmoe::kQuad) / 2;
+}
+
+int64_t phantom_q4_0_scale_bytes(int64_t rows, int64_t K) {
+  if (rows < 0 || K < 0 || rows % 16 || K % 32) return -1;
+  return rows * pmoe::round_up(K, pmoe::kQuad) / 32 * 2;
+}
+
+int phantom_q4_0_repack(const uint8_t* q4_0, int64_t rows, int64_t K, uint8_t* nib, uint16_t* scale,
+                        hipStream_t stream) {
+  if (rows < 0 || K < 0 || rows % 16 || K % 32)
+    return fail(PHANTOM_MOE_EINVAL, "repack needs rows %% 16 == 0 and K %% 32 == 0 (rows=%lld K=%lld)",
+                (long long)rows, (long long)K);
+  if (rows == 0 || K == 0) return ok();
+  if (!q4_0 || !nib || !scale) return fail(PHANTOM_MOE_EINVAL, "repack: null pointer");
+  if (reinterpret_cast<uintptr_t>(nib) % 16 || reinterpret_cast<uintptr_t>(scale) % 8)
+    return fail(PHANTOM_MOE_EINVAL, "repack: nib must be 16-byte and scale 8-byte aligned");
+  return launch_status(pmoe::launch_q4_repack(q4_0, rows, K, nib, scale, stream), "q4_repack");
+}
+
+int phantom_q4_0_unrepack(const uint8_t* nib, const uint16_t* scale, int64_t rows, int64_t K,
+                          uint8_t* q4_0, hipStream_t stream) {
+  if (rows < 0 || K < 0 || rows % 16 || K % 32)
+    return fail(PHANTOM_MOE_EINVAL, "unrepack needs rows %% 16 == 0 and K %% 32 == 0");
+  if (rows == 0 || K == 0) return ok();
+  if (!q4_0 || !nib || !scale) return fail(PHANTOM_MOE_EINVAL, "unrepack: null pointer");
+  return launch_status(pmoe::launch_q4_unrepack(nib, scale, rows, K, q4_0, stream), "q4_unrepack");
+}
+
+int phantom_q4_0_dequant_f32(const uint8_t* q4_0, int64_t rows, int64_t K, float* out,
+                             hipStream_t stream) {
+  if (rows < 0 || K < 0 || K % 32) return fail(PHANTOM_MOE_EINVAL, "dequant needs K %% 32 == 0");
+  if (rows == 0 || K == 0) return ok();
+  if (!q4_0 || !out) return fail(PHANTOM_MOE_EINVAL, "dequant: null pointer");
+  return launch_status(pmoe::launch_q4_dequant_f32(q4_0, rows * (K / 32), out, stream), "q4_dequant");
+}
+
+size_t phantom_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int E, int top_k, int has_shared) {
+  if (T < 1 || H < 1 || E < 1 || top_k < 1 || I < 0) return 0;
+  return pmoe::plan_workspace(T, H, I, E, top_k, has_shared ? 1 : 0, nullptr, nullptr);
+}
+
+int phantom_moe_route(const void* x, int x_dtype, const float* router_w, const float* router_bias,
+                      int64_t T, int64_t H, int E, int top_k, int score_mode, int32_t* topk_idx,
+                      float* topk_w, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (int rc = check_route_shapes(x, x_dtype, router_w, T, H, E, top_k, score_mode)) return rc;
+  if (!topk_idx || !topk_w) return fail(PHANTOM_MOE_EINVAL, "topk_idx and topk_w must be non-null");
+  const size_t need = pmoe::plan_workspace(T, H, 0, E, top_k, 0, nullptr, nullptr);
+  if (!workspace || workspace_bytes < need)
+    return fail(PHANTOM_MOE_EWORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                workspace ? workspace_bytes : (size_t)0);
+  pmoe::Workspace ws;
+  pmoe::plan_workspace(T, H, 0, E, top_k, 0, workspace, &ws);
+  pmoe::RouteArgs r = {};
+  r.x = x;
+  r.x_dtype = x_dtype;
+  r.router_w = router_w;
+  r.router_bias = router_bias;
+  r.T = T;
+  r.H = H;
+  r.E = E;
+  r.k = top_k;
+  r.score_mode = score_mode;
+  r.topk_idx = topk_idx;
+  r.topk_w = topk_w;
+  r.prep_x = false;
+  r.do_permute = false;
+  return launch_status(pmoe::launch_route(r, ws, stream), "route");
+}
+
+int phantom_moe_permute(const int32_t* topk_idx, int64_t T, int top_k, int E, int32_t* expert_offsets,
+                        int32_t* sorted_slots, int32_t* slot_pos, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+  if (!topk_idx || !expert_offsets || !sorted_slots || !slot_pos)
+    return fail(PHANTOM_MOE_EINVAL, "permute: null pointer");
+  if (T < 1 || top_k < 1 || E < 1 || top_k > E)
+    return fail(PHANTOM_MOE_EINVAL, "permute: need T >= 1 and 1 <= top_k <= E");
+  if (E > pmoe::kMaxExperts) return fail(PHANTOM_MOE_EUNSUPPORTED, "permute: E above %d", pmoe::kMaxExperts);
+  if (T * (int64_t)top_k > ((int64_t)1 << 30)) return fail(PHANTOM_MOE_EUNSUPPORTED, "permute: T*top_k too large");
+  const size_t need = pmoe::plan_workspace(T, 32, 0, E, top_k, 0, nullptr, nullptr);
+  if (!workspace || workspace_bytes < need)
+    return fail(PHANTOM_MOE_EWORKSPACE, "workspace of %zu bytes required", need);
+  pmoe::Workspace ws;
+  pmoe::plan_workspace(T, 32, 0, E, top_k, 0, workspace, &ws);
+  return launch_status(
+      pmoe::launch_permute(topk_idx, T, top_k, E, 0, expert_offsets, sorted_slots, slot_pos, ws, stream),
+      "permute");
+}
+
+int phantom_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int E, int top_k,
+                        int score_mode, const float* router_w, const float* router_bias,
+                        const uint8_t* gate_nib, const uint16_t* gate_scale, const uint8_t* up_nib,
+                        const uint16_t* up_scale, const uint8_t* down_nib, const uint16_t* down_scale,
+                        const uint8_t* sh_gate_nib, const uint16_t* sh_gate_scale,
+                        const uint8_t* sh_up_nib, const uint16_t* sh_up_scale,
+                        const uint8_t* sh_down_nib, const uint16_t* sh_down_scale, float* y,
+                        int32_t* topk_idx, float* topk_w, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
+  if (int rc = check_route_shapes(x, x_dtype, router_w, T, H, E, top_k, score_mode)) return rc;
+  if (x_dtype != PHANTOM_MOE_X_BF16)
+    return fail(PHANTOM_MOE_EUNSUPPORTED, "phantom_moe_forward takes bf16 activations (x_dtype 0)");
+  if (I < 32 || I % 32) return fail(PHANTOM_MOE_EINVAL, "I must be a positive multiple of 32, got %lld", (long long)I);
+  if (!gate_nib || !gate_scale || !up_nib || !up_scale || !down_nib || !down_scale)
+    return fail(PHANTOM_MOE_EINVAL, "expert weight pointers must be non-null");
+  if (!y || !topk_idx || !topk_w) return fail(PHANTOM_MOE_EINVAL, "y, topk_idx and topk_w must be non-null");
+  const int n_sh = (sh_gate_nib != nullptr) + (sh_gate_scale != nullptr) + (sh_up_nib != nullptr) +
+                   (sh_up_scale != nullptr) + (sh_down_nib != nullptr) + (sh_down_scale != nullptr);
+  if (n_sh != 0 && n_sh != 6)
+    return fail(PHANTOM_MOE_EINVAL, "shared expert pointers must be all null or all non-null");
+  const int has_shared = n_sh == 6 ? 1 : 0;
+  const size_t need = pmoe::plan_workspace(T, H, I, E, top_k, has_shared, nullptr, nullptr);
+  if (!workspace || workspace_bytes < need)
+    return fail(PHANTOM_MOE_EWORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                workspace ? workspace_bytes : (size_t)0);
+  pmoe::Workspace ws;
+  pmoe::plan_workspace(T, H, I, E, top_k, has_shared, workspace, &ws);
+
+  pmoe::RouteArgs r = {};
+  r.x = x;
+  r.x_dtype = x_dtype;
+  r.router_w = router_w;
+  r.router_bias = router_bias;
+  r.T = T;
+  r.H = H;
+  r.E = E;
+  r.k = top_k;
+  r.score_mode = score_mode;
+  r.topk_idx = topk_idx;
+  r.topk_w = topk_w;
+  r.prep_x = true;
+  r.do_permute = true;
+  r.has_shared = has_shared;
+  if (int rc = launch_status(pmoe::launch_route(r, ws, stream), "route")) return rc;
+
+  pmoe::ExpertArgs a = {};
+  a.T = T;
+  a.H = H;
+  a.I = I;
+  a.E = E;
+  a.k = top_k;
+  a.has_shared = has_shared;
+  a.gate_nib = gate_nib;
+  a.gate_scale = gate_scale;
+  a.up_nib = up_nib;
+  a.up_scale = up_scale;
+  a.down_nib = down_nib;
+  a.down_scale = down_scale;
+  a.sh_gate_nib = sh_gate_nib;
+  a.sh_gate_scale = sh_gate_scale;
+  a.sh_up_nib = sh_up_nib;
+  a.sh_up_scale = sh_up_scale;
+  a.sh_down_nib = sh_down_nib;
+  a.sh_down_scale = sh_down_scale;
+  a.topk_w = topk_w;
+  a.y = y;
+  return launch_status(pmoe::launch_experts(a, ws, stream), "experts");
+}
+
+}  // extern "C"

@@ -1,0 +1,117 @@
+// moe_common.h -- shared device helpers for the gfx950 sparse-MoE kernels.
+//
+// Repacked Q4_0 layout (see phantom_q4_0_repack):
+//   A [rows, K] Q4_0 matrix is cut into row tiles of 16 rows and K quads of
+//   128 elements (4 Q4_0 groups).  One (row tile, quad) is 1 KiB of nibbles:
+//   lane l of a wave owns 16 bytes, which hold, for each of the quad's 4
+//   groups gi, the 4 qs bytes [4*p, 4*p+3] (p = l / 16) of row 16*rt + l%16.
+//   Its scales are 128 bytes: [16 rows][4 groups] fp16.
+//
+// MFMA operand mapping (v_mfma_f32_16x16x32_bf16):
+//   lane l holds 8 bf16 of A row (l % 16) and of B column (l % 16), both for
+//   the same 8 K positions of the 32-wide group, chosen by p = l / 16.  The 4
+//   qs bytes of part p expand (dequant_unit_bf16 / _f16) to the K positions
+//       kmap(p) = {4p, 4p+2, 16+4p, 18+4p, 4p+1, 4p+3, 17+4p, 19+4p}
+//   and activations are laid out in the same order, so the MFMA reduces over
+//   exactly the 32 elements of the group.
+//
+// Magic-number expansion: placing a nibble n in the top mantissa bits of the
+// constant 1.0 gives the exact value 1 + n/16 (bf16 pattern 0x3F80 | n << 3,
+// fp16 pattern 0x3C00 | n << 6), so 8 nibbles become MFMA operands with one
+// shift and one AND-OR per pair.  With q = n - 8,
+//     sum_k a_k q_k = 16 * sum_k a_k (1 + n_k/16) - 24 * sum_k a_k,
+// so each group's MFMA result is scaled by 16*d (exact) and the correction
+// 24 * d * S (S = group sum of the activations) is applied once per output
+// with an fp32 MFMA over groups.  The offset costs about 5x the signed
+// result's rounding error (mean |1 + n/16| / rms |q/16|), not more.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pmoe {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kRowTile = 16;
+constexpr int kQuad = 128;       // K elements per quad
+constexpr int kGroup = 32;       // Q4_0 group
+constexpr int kQuadNibBytes = 1024;
+constexpr int kQuadScales = 64;  // fp16 values per (row tile, quad)
+constexpr float kUnitScale = 16.0f;  // (1 + n/16) * 16 = n + 16
+constexpr float kUnitBias = 24.0f;   // 16 + 8: q = 16 (1 + n/16) - 24
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+// Position within a 32-group of element j (0..7) of MFMA part p (0..3).
+__host__ __device__ inline int kmap(int p, int j) {
+  // j: 0 1 2 3 4 5 6 7 -> 4p+{0, 2, 16, 18, 1, 3, 17, 19}
+  const int off[8] = {0, 2, 16, 18, 1, 3, 17, 19};
+  return 4 * p + off[j];
+}
+
+// 4 qs bytes (little endian word) -> 8 bf16 values 1 + n/16, in kmap order.
+__device__ inline u32x4 dequant_unit_bf16(uint32_t w) {
+  u32x4 r;
+  r.x = ((w << 3) & 0x00780078u) | 0x3F803F80u;
+  r.y = ((w >> 1) & 0x00780078u) | 0x3F803F80u;
+  r.z = ((w >> 5) & 0x00780078u) | 0x3F803F80u;
+  r.w = ((w >> 9) & 0x00780078u) | 0x3F803F80u;
+  return r;
+}
+
+// Same expansion as fp16 values 1 + n/16.
+__device__ inline u32x4 dequant_unit_f16(uint32_t w) {
+  u32x4 r;
+  r.x = ((w << 6) & 0x03C003C0u) | 0x3C003C00u;
+  r.y = ((w << 2) & 0x03C003C0u) | 0x3C003C00u;
+  r.z = ((w >> 2) & 0x03C003C0u) | 0x3C003C00u;
+  r.w = ((w >> 6) & 0x03C003C0u) | 0x3C003C00u;
+  return r;
+}
+
+__device__ inline f32x4 mfma_bf16_16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+__device__ inline f32x4 mfma_f16_16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+__device__ inline f32x4 mfma_f32_16x16x4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ inline float half_bits_to_float(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ inline float bf16_bits_to_float(uint32_t b) {
+  return __builtin_bit_cast(float, b << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits (finite inputs).
+__device__ inline uint32_t float_to_bf16_bits(float f) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f)));
+}
+
+__device__ inline uint32_t float_to_half_bits(float f) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f)));
+}
+
+__device__ inline float half_bits_to_float32(uint32_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+__device__ inline double shfl_xor_f64(double v, int mask) {
+  return __shfl_xor(v, mask, kWave);
+}
+
+}  // namespace pmoe

@@ -1,0 +1,89 @@
+// moe_launch.h -- host-side launch helpers and the workspace layout shared by
+// the kernel translation units and the C ABI (capi.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace pmoe {
+
+// Limits of this build (checked by the C ABI before any launch).
+constexpr int kMaxExperts = 512;  // router top-k keeps E/64 <= 8 logits per lane
+constexpr int kMaxTopK = 32;
+
+// Workspace carve-up.  Every region is 256-byte aligned.
+struct Workspace {
+  int32_t* counters = nullptr;      // [n_token_tiles + 1], zero between calls
+  double* logits = nullptr;         // [T, E]
+  uint16_t* xq = nullptr;           // [T, Kpad_h] bf16 bits, MFMA operand order
+  float* xs = nullptr;              // [T, Kpad_h / 32] group sums of x
+  int32_t* offsets = nullptr;       // [E + 2] segment offsets (+ shared segment)
+  int32_t* active = nullptr;        // [E + 1] active expert ids, ascending (+ shared = E)
+  int32_t* n_active = nullptr;      // [1]
+  int32_t* sorted_slots = nullptr;  // [T * k]
+  int32_t* slot_pos = nullptr;      // [T * k]
+  uint16_t* hq = nullptr;          // [rows, Kpad_I * 2] fp16 hi/lo of h, MFMA operand order
+  float* hs = nullptr;             // [rows, Kpad_I / 32, 2] half-group sums of h
+  float* outbuf = nullptr;          // [T*k + T*shared, H] expert outputs, segment order
+};
+
+size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared, void* base,
+                      Workspace* ws);
+
+// Router tiling: tokens per workgroup tile.
+int router_token_tile(int64_t T);
+
+hipError_t launch_q4_repack(const uint8_t* src, int64_t rows, int64_t K, uint8_t* nib,
+                            uint16_t* scale, hipStream_t stream);
+hipError_t launch_q4_unrepack(const uint8_t* nib, const uint16_t* scale, int64_t rows, int64_t K,
+                              uint8_t* dst, hipStream_t stream);
+hipError_t launch_q4_dequant_f32(const uint8_t* src, int64_t n_blocks, float* out,
+                                 hipStream_t stream);
+
+// Logits + top-k (+ optional MFMA-ordered copy of x and its group sums)
+// (+ optional permute), one launch.
+struct RouteArgs {
+  const void* x;
+  int x_dtype;
+  const float* router_w;
+  const float* router_bias;
+  int64_t T, H;
+  int E, k, score_mode;
+  int32_t* topk_idx;
+  float* topk_w;
+  bool prep_x;       // write ws.xq / ws.xs
+  bool do_permute;   // write offsets / sorted_slots / slot_pos / active
+  int has_shared;    // append the shared-expert segment to offsets / active
+  int32_t* offsets_out;       // optional user copy of offsets [E+1]
+  int32_t* sorted_slots_out;  // where to write sorted slots (default ws)
+  int32_t* slot_pos_out;      // where to write slot positions (default ws)
+};
+hipError_t launch_route(const RouteArgs& a, const Workspace& ws, hipStream_t stream);
+
+// Permute only (topk_idx given).
+hipError_t launch_permute(const int32_t* topk_idx, int64_t T, int k, int E, int has_shared,
+                          int32_t* offsets, int32_t* sorted_slots, int32_t* slot_pos,
+                          const Workspace& ws, hipStream_t stream);
+
+struct ExpertArgs {
+  int64_t T, H, I;
+  int E, k, has_shared;
+  const uint8_t* gate_nib;
+  const uint16_t* gate_scale;
+  const uint8_t* up_nib;
+  const uint16_t* up_scale;
+  const uint8_t* down_nib;
+  const uint16_t* down_scale;
+  const uint8_t* sh_gate_nib;
+  const uint16_t* sh_gate_scale;
+  const uint8_t* sh_up_nib;
+  const uint16_t* sh_up_scale;
+  const uint8_t* sh_down_nib;
+  const uint16_t* sh_down_scale;
+  const float* topk_w;
+  float* y;
+};
+hipError_t launch_experts(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);
+
+}  // namespace pmoe

@@ -1,0 +1,26 @@
+"""phantom_moe -- MI355X (gfx950) sparse-MoE layer for PHANTOM.
+
+Python surface over libphantom_moe.so (C ABI in include/phantom_moe.h):
+
+  PhantomTopKRouter   drop-in for the reference router module
+                      (tests/test_moe_routing.py:43-72)
+  moe_forward         router -> permute -> Q4_0 SwiGLU experts -> combine
+  route, permute      the first two stages on their own
+  MoEWeights          repacked Q4_0 expert weights resident in HBM
+  q4_0                GGUF Q4_0 pack / unpack / device repack
+"""
+from . import q4_0, synth
+from ._lib import PhantomMoEError
+from .ops import MoEWeights, moe_forward, permute, route
+from .router import PhantomTopKRouter
+
+__all__ = [
+    "PhantomTopKRouter",
+    "MoEWeights",
+    "moe_forward",
+    "route",
+    "permute",
+    "q4_0",
+    "synth",
+    "PhantomMoEError",
+]

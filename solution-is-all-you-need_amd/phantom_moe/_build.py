@@ -1,0 +1,60 @@
+"""In-tree build of libphantom_moe.so for gfx950 with hipcc.
+
+Every call compiles (no up-to-date check), so the library always matches the
+sources.  The output goes to ``phantom_moe/lib/``, which travels with the
+repository tree; nothing is installed into site-packages.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import tempfile
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG_DIR)
+CSRC = os.path.join(ROOT, "csrc")
+INCLUDE = os.path.join(os.path.dirname(ROOT), "include")
+SOURCES = ["q4_repack.hip", "router.hip", "expert_ffn.hip", "capi.hip"]
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-fvisibility=hidden",
+    # No packed fp32 VALU instructions anywhere in device code.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
+        if cand and (os.path.sep not in cand or os.path.exists(cand)):
+            return cand
+    return "hipcc"
+
+
+def build(verbose: bool = False) -> str:
+    """Compile all HIP sources into lib/libphantom_moe.so; returns its path."""
+    out_dir = os.path.join(PKG_DIR, "lib")
+    os.makedirs(out_dir, exist_ok=True)
+    out = os.path.join(out_dir, "libphantom_moe.so")
+    fd, tmp = tempfile.mkstemp(prefix="libphantom_moe.", suffix=".so.tmp", dir=out_dir)
+    os.close(fd)
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}"]
+    cmd += [os.path.join(CSRC, s) for s in SOURCES]
+    cmd += ["-o", tmp]
+    try:
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{res.stderr}")
+        if verbose and res.stderr:
+            print(res.stderr)
+        os.replace(tmp, out)
+    finally:
+        if os.path.exists(tmp):
+            os.unlink(tmp)
+    return out

@@ -1,0 +1,100 @@
+"""ctypes binding of libphantom_moe.so (declared in include/phantom_moe.h).
+
+The library is built in-tree by ``phantom_moe._build.build()`` into
+``phantom_moe/lib/libphantom_moe.so``.  There is no fallback: if the library
+is missing, every operator raises.
+
+torch is imported before the library is loaded.  torch ships its own HIP
+runtime (soname libamdhip64.so.7); loading torch first makes the dynamic
+linker bind our library's libamdhip64.so.7 dependency to that same runtime,
+so device pointers and streams from torch are valid in our calls.  The loader
+checks /proc/self/maps afterwards and refuses to run with two HIP runtimes.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must precede the CDLL, see module docstring)
+
+LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libphantom_moe.so")
+
+# Function name -> (restype, argtypes).  Mirrors include/phantom_moe.h.
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_sz = ctypes.c_size_t
+SIGNATURES = {
+    "phantom_moe_last_error": (ctypes.c_char_p, []),
+    "phantom_moe_version": (ctypes.c_char_p, []),
+    "phantom_q4_0_nib_bytes": (_i64, [_i64, _i64]),
+    "phantom_q4_0_scale_bytes": (_i64, [_i64, _i64]),
+    "phantom_q4_0_repack": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    "phantom_q4_0_unrepack": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "phantom_q4_0_dequant_f32": (_int, [_vp, _i64, _i64, _vp, _vp]),
+    "phantom_moe_workspace_bytes": (_sz, [_i64, _i64, _i64, _int, _int, _int]),
+    "phantom_moe_route": (_int, [_vp, _int, _vp, _vp, _i64, _i64, _int, _int, _int, _vp, _vp, _vp, _sz, _vp]),
+    "phantom_moe_permute": (_int, [_vp, _i64, _int, _int, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "phantom_moe_forward": (
+        _int,
+        [_vp, _int, _i64, _i64, _i64, _int, _int, _int, _vp, _vp]
+        + [_vp] * 6
+        + [_vp] * 6
+        + [_vp, _vp, _vp, _vp, _sz, _vp],
+    ),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class PhantomMoEError(RuntimeError):
+    """A libphantom_moe.so entry point returned a non-zero status."""
+
+
+def _hip_runtimes_mapped() -> set:
+    paths = set()
+    try:
+        with open("/proc/self/maps") as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) >= 6 and os.path.basename(parts[5]).startswith("libamdhip64.so"):
+                    paths.add(os.path.realpath(parts[5]))
+    except OSError:
+        pass
+    return paths
+
+
+def load(path: str = LIB_PATH):
+    """Load (once) and return the ctypes handle with typed signatures."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(path):
+            raise PhantomMoEError(
+                f"{path} is missing: build the HIP library first (python -c 'import __graft_entry__ as g; g.build()')"
+            )
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        runtimes = _hip_runtimes_mapped()
+        if len(runtimes) > 1:
+            raise PhantomMoEError(f"two HIP runtimes are mapped in this process: {sorted(runtimes)}")
+        _lib = lib
+        return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().phantom_moe_last_error().decode(errors="replace")
+        raise PhantomMoEError(f"{what} failed (status {rc}): {msg}")
+
+
+def stream_handle(device: torch.device | None = None) -> int:
+    """hipStream_t of torch's current stream on ``device`` (as an int)."""
+    return torch.cuda.current_stream(device).cuda_stream

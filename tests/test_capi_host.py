@@ -1,0 +1,158 @@
+"""Host-side checks of libphantom_moe.so that need no GPU: it loads, exports
+every entry point include/phantom_moe.h declares, reports sizes, and rejects
+invalid arguments with a status code (never an exit) before touching the
+device."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from phantom_moe import _lib, q4_0, synth
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "phantom_moe.h")
+EINVAL, EWORKSPACE, ELAUNCH, EUNSUPPORTED = -1, -2, -3, -4
+FAKE = 0x10000  # never dereferenced: every call below fails validation first
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return re.findall(r"PHANTOM_MOE_API\s+[\w\s\*]+?\b(phantom_\w+)\s*\(", text)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) >= 11
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in phantom_moe.h but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_version_and_sizes():
+    lib = _lib.load()
+    assert b"gfx950" in lib.phantom_moe_version()
+    assert q4_0.nib_bytes(768, 2048) == 768 * 2048 // 2
+    assert q4_0.scale_count(768, 2048) == 768 * 2048 // 32
+    # K padded to a multiple of 128
+    assert q4_0.nib_bytes(16, 96) == 16 * 128 // 2
+    with pytest.raises(ValueError):
+        q4_0.nib_bytes(15, 64)
+    with pytest.raises(ValueError):
+        q4_0.nib_bytes(16, 40)
+    a = lib.phantom_moe_workspace_bytes(32, 2048, 768, 128, 8, 0)
+    b = lib.phantom_moe_workspace_bytes(64, 2048, 768, 128, 8, 0)
+    c = lib.phantom_moe_workspace_bytes(32, 2048, 768, 128, 8, 1)
+    assert 0 < a < b and a < c
+    assert lib.phantom_moe_workspace_bytes(0, 2048, 768, 128, 8, 0) == 0
+
+
+def _route(**kw):
+    args = dict(x=FAKE, x_dtype=0, W=FAKE, b=None, T=4, H=256, E=8, k=2, score=0, idx=FAKE, w=FAKE, ws=None,
+                wsb=0, stream=None)
+    args.update(kw)
+    lib = _lib.load()
+    return lib.phantom_moe_route(args["x"], args["x_dtype"], args["W"], args["b"], args["T"], args["H"], args["E"],
+                                 args["k"], args["score"], args["idx"], args["w"], args["ws"], args["wsb"],
+                                 args["stream"])
+
+
+@pytest.mark.parametrize(
+    "kw,code",
+    [
+        (dict(x=None), EINVAL),
+        (dict(W=None), EINVAL),
+        (dict(x_dtype=2), EINVAL),
+        (dict(T=0), EINVAL),
+        (dict(H=100), EINVAL),
+        (dict(H=0), EINVAL),
+        (dict(k=9), EINVAL),
+        (dict(k=0), EINVAL),
+        (dict(E=0), EINVAL),
+        (dict(E=1000, k=2), EUNSUPPORTED),
+        (dict(E=64, k=40), EUNSUPPORTED),
+        (dict(score=3), EINVAL),
+        (dict(idx=None), EINVAL),
+        (dict(ws=None), EWORKSPACE),
+        (dict(ws=FAKE, wsb=16), EWORKSPACE),
+    ],
+)
+def test_route_validation(kw, code):
+    assert _route(**kw) == code
+    assert _lib.load().phantom_moe_last_error()
+
+
+def _forward(**kw):
+    a = dict(x=FAKE, xd=0, T=4, H=256, I=128, E=8, k=2, score=0, W=FAKE, b=None, w6=[FAKE] * 6, sh=[None] * 6,
+             y=FAKE, idx=FAKE, tw=FAKE, ws=None, wsb=0)
+    a.update(kw)
+    lib = _lib.load()
+    return lib.phantom_moe_forward(a["x"], a["xd"], a["T"], a["H"], a["I"], a["E"], a["k"], a["score"], a["W"],
+                                   a["b"], *a["w6"], *a["sh"], a["y"], a["idx"], a["tw"], a["ws"], a["wsb"], None)
+
+
+@pytest.mark.parametrize(
+    "kw,code",
+    [
+        (dict(xd=1), EUNSUPPORTED),
+        (dict(I=48), EINVAL),
+        (dict(I=0), EINVAL),
+        (dict(w6=[FAKE] * 5 + [None]), EINVAL),
+        (dict(sh=[FAKE] + [None] * 5), EINVAL),
+        (dict(y=None), EINVAL),
+        (dict(ws=None), EWORKSPACE),
+        (dict(T=-1), EINVAL),
+    ],
+)
+def test_forward_validation(kw, code):
+    assert _forward(**kw) == code
+
+
+def test_repack_and_permute_validation():
+    lib = _lib.load()
+    assert lib.phantom_q4_0_repack(FAKE, 15, 64, FAKE, FAKE, None) == EINVAL
+    assert lib.phantom_q4_0_repack(FAKE, 16, 40, FAKE, FAKE, None) == EINVAL
+    assert lib.phantom_q4_0_repack(None, 16, 64, FAKE, FAKE, None) == EINVAL
+    assert lib.phantom_q4_0_repack(FAKE, 16, 64, FAKE + 4, FAKE, None) == EINVAL  # misaligned nib
+    assert lib.phantom_q4_0_repack(None, 0, 64, None, None, None) == 0  # empty is a no-op
+    assert lib.phantom_q4_0_unrepack(FAKE, FAKE, 16, 33, FAKE, None) == EINVAL
+    assert lib.phantom_q4_0_dequant_f32(FAKE, 4, 31, FAKE, None) == EINVAL
+    assert lib.phantom_moe_permute(None, 4, 2, 8, FAKE, FAKE, FAKE, None, 0, None) == EINVAL
+    assert lib.phantom_moe_permute(FAKE, 4, 9, 8, FAKE, FAKE, FAKE, None, 0, None) == EINVAL
+    assert lib.phantom_moe_permute(FAKE, 4, 2, 8, FAKE, FAKE, FAKE, None, 0, None) == EWORKSPACE
+    assert lib.phantom_moe_permute(FAKE, 4, 2, 600, FAKE, FAKE, FAKE, None, 0, None) == EUNSUPPORTED
+
+
+def test_python_surface_rejects_cpu_tensors():
+    import torch
+
+    import phantom_moe
+
+    r = phantom_moe.PhantomTopKRouter(256, 8, 2)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        r(torch.randn(2, 4, 256))
+    with pytest.raises(TypeError):
+        q4_0.repack(torch.zeros(18, dtype=torch.uint8), 16, 32)
+
+
+def test_synth_configs_and_determinism():
+    c = synth.CONFIGS["qwen3_decode_t32_zipf"]
+    assert (c.H, c.I, c.E, c.k, c.T) == (2048, 768, 128, 8, 32)
+    assert c.expert_bytes() == 2654208
+    assert synth.CONFIGS["dsv3_decode_t1"].shared and synth.CONFIGS["dsv3_decode_t1"].score_mode == 1
+    small = synth.scaled(c, H=64, I=32, E=8, k=2, T=4)
+    a = synth.host_layer(small)
+    b = synth.host_layer(small)
+    assert np.array_equal(a.gate, b.gate) and np.array_equal(a.router_w, b.router_w)
+    bias = synth.zipf_bias(128, 1.1)
+    golden = np.load(os.path.join(os.path.dirname(__file__), "golden", "zipf_bias_e128_s1.1.npy"))
+    np.testing.assert_array_equal(bias, golden)
+    x = synth.activations(3, 64)
+    assert x.dtype == np.uint16
+    # bf16 rounding is round-to-nearest-even
+    np.testing.assert_array_equal(synth.f32_to_bf16_bits(np.array([1.0 + 2.0 ** -8], np.float32)),
+                                  np.array([0x3F80], np.uint16))
+    np.testing.assert_array_equal(synth.f32_to_bf16_bits(np.array([1.0 + 3 * 2.0 ** -8], np.float32)),
+                                  np.array([0x3F82], np.uint16))
