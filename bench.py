@@ -1,0 +1,274 @@
+#!/usr/bin/env python3
+"""MoE-layer throughput on one MI355X.
+
+A step is one forward of one sparse-MoE layer (router -> permute -> Q4_0
+SwiGLU experts -> weighted combine) over one batch of synthetic tokens.  The
+default workload is the Qwen3-30B-A3B-shaped layer (H=2048, I=768, E=128,
+top-8, softmax) at decode batch 32 with a fixed Zipf(1.1) router bias.  Steps
+rotate over --layers distinct layer instances (distinct weights and inputs,
+about 5.4 GB at 16 instances) so weight traffic comes from HBM, not from the
+256 MB last-level cache.  Everything the timed region touches is resident in
+HBM before it starts.
+
+Output: one JSON line with the whole-job tokens/s, the roofline of the
+dominant kernel (gate/up grouped GEMV, timed with HIP events recorded between
+kernels on the launch stream), and the CPU baseline (the reference's CPU MoE
+path, restated in oracle/ref_cpu_path.py, timed on this host on a bounded
+sample).
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "solution-is-all-you-need_amd"))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "gate_up_kernel_qwen3_decode_t32_zipf_pmc.json")
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--layers", type=int, default=16, help="distinct layer instances to rotate over")
+    p.add_argument("--workload", default="qwen3_decode_t32_zipf")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-stage-events", action="store_true", help="time without the per-stage events")
+    return p.parse_args()
+
+
+class HipEvents:
+    """Raw hipEvent_t handles from the HIP runtime torch loaded."""
+
+    def __init__(self):
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self, n):
+        out = []
+        for _ in range(n):
+            ev = ctypes.c_void_p()
+            rc = self.hip.hipEventCreateWithFlags(ctypes.byref(ev), 0)
+            if rc != 0:
+                raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+            out.append(ev.value)
+        return out
+
+    def elapsed_ms(self, a, b) -> float:
+        ms = ctypes.c_float()
+        rc = self.hip.hipEventElapsedTime(ctypes.byref(ms), ctypes.c_void_p(a), ctypes.c_void_p(b))
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return float(ms.value)
+
+    def destroy(self, evs):
+        for e in evs:
+            self.hip.hipEventDestroy(ctypes.c_void_p(e))
+
+
+def gate_up_bytes(cfg, U: int) -> int:
+    """Algorithmic HBM bytes of one gate/up launch: the Q4_0 gate and up
+    matrices of the U distinct active experts (plus the shared expert) and the
+    bf16 activations."""
+    per_expert = 2 * cfg.I * cfg.H * 18 // 32
+    return (U + (1 if cfg.shared else 0)) * per_expert + cfg.T * cfg.H * 2
+
+
+def layer_bytes(cfg, U: int) -> int:
+    """Algorithmic HBM bytes of one layer: expert weights of the U active
+    experts (+ shared), the fp32 router weight, bf16 x in and fp32 y out."""
+    experts = (U + (1 if cfg.shared else 0)) * 3 * cfg.H * cfg.I * 18 // 32
+    return experts + cfg.E * cfg.H * 4 + cfg.T * cfg.H * 2 + cfg.T * cfg.H * 4
+
+
+def layer_flops(cfg) -> int:
+    return 2 * cfg.T * (cfg.k + (1 if cfg.shared else 0)) * 3 * cfg.H * cfg.I + 2 * cfg.T * cfg.H * cfg.E
+
+
+def cpu_baseline(cfg, host_layer, budget_s: float):
+    """The reference CPU path on layer instance 0, timed on a bounded sample."""
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from oracle.ref_cpu_path import RefCPUMoE
+
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    router_w, bias, gate, up, down, shared, xb = host_layer
+    layer = RefCPUMoE(router_w, gate, up, down, cfg.H, cfg.I, cfg.k, cfg.score, bias, shared)
+    x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16)
+    layer(x)  # warm-up (allocator, oneDNN kernels)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        layer(x)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 50:
+            break
+    try:
+        cpu_model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except (OSError, StopIteration):
+        cpu_model = "unknown"
+    return {
+        "value": round(cfg.T * n / el, 3),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n} forwards of one {cfg.T}-token layer instance ({cfg.T * n} tokens, {el:.1f} s): torch fp32 "
+                  f"router, numpy Q4_0 dequant of every active expert on every call, torch bf16 SwiGLU, index_add_ "
+                  f"combine (oracle/ref_cpu_path.py)",
+        "cpu": cpu_model,
+    }
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); the sharding design is described in DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import phantom_moe
+    from phantom_moe import _lib, synth
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    cfg = synth.CONFIGS[args.workload]
+    L = max(1, args.layers)
+
+    # ---- resident inputs: L distinct layer instances --------------------
+    layers = []
+    host0 = None
+    for l in range(L):
+        dl = synth.device_layer(cfg, dev, layer=l)
+        ex = phantom_moe.MoEWeights.from_q4_0(dl.gate, dl.up, dl.down, cfg.H, cfg.I, cfg.E, shared=dl.shared)
+        xb = synth.activations(cfg.T, cfg.H, seed=42 + l)
+        x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).to(dev)
+        if l == 0 and not args.no_cpu_baseline:
+            host0 = (dl.router_w.cpu().numpy(), None if dl.router_bias is None else dl.router_bias.cpu().numpy(),
+                     dl.gate.cpu().numpy(), dl.up.cpu().numpy(), dl.down.cpu().numpy(),
+                     None if dl.shared is None else tuple(t.cpu().numpy() for t in dl.shared), xb)
+        layers.append(phantom_moe.PreparedForward(ex, dl.router_w, cfg.T, cfg.k, cfg.score, dl.router_bias, x=x))
+        del dl
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+    lib = _lib.load()
+    stream = _lib.stream_handle(dev)
+    for i in range(args.warmup):
+        layers[i % L](stream)
+    torch.cuda.synchronize()
+
+    use_events = not args.no_stage_events
+    ev = HipEvents()
+    n_ev = 5
+    events = ev.create(n_ev * args.steps) if use_events else []
+    arrays = [(ctypes.c_void_p * n_ev)(*events[i * n_ev:(i + 1) * n_ev]) for i in range(args.steps)] if use_events else []
+
+    # ---- timed region: exactly K steps between two synchronisations ------
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        if use_events:
+            lib.phantom_moe_set_profile_events(arrays[i], n_ev)
+        layers[i % L](stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    if use_events:
+        lib.phantom_moe_set_profile_events(None, 0)
+    elapsed = t1 - t0
+
+    # ---- per-stage times, U per instance ---------------------------------
+    U = [int(torch.unique(layers[l].topk_idx).numel()) for l in range(L)]
+    stages = {"route": [], "gate_up": [], "down": [], "combine": [], "layer": []}
+    if use_events:
+        for i in range(args.steps):
+            e = events[i * n_ev:(i + 1) * n_ev]
+            stages["route"].append(ev.elapsed_ms(e[0], e[1]))
+            stages["gate_up"].append(ev.elapsed_ms(e[1], e[2]))
+            stages["down"].append(ev.elapsed_ms(e[2], e[3]))
+            stages["combine"].append(ev.elapsed_ms(e[3], e[4]))
+            stages["layer"].append(ev.elapsed_ms(e[0], e[4]))
+        ev.destroy(events)
+    steps_U = [U[i % L] for i in range(args.steps)]
+
+    value = cfg.T * args.steps / elapsed
+    out = {
+        "metric": "MoE-layer decode tokens/s (Qwen3-30B-A3B-shaped layer, batch 32, Zipf-skewed routing)",
+        "value": round(value, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 activations x int4 (Q4_0) weights, fp32 accumulate; fp64 router logits",
+        "data": "synthetic (seeded): x ~ N(0,1) bf16, router N(0,0.02) fp32, Q4_0 q uniform [-8,7], d ~ |N(0,0.02)|",
+        "config": {
+            "workload": cfg.name,
+            "H": cfg.H, "I": cfg.I, "E": cfg.E, "top_k": cfg.k, "tokens_per_step": cfg.T,
+            "score": cfg.score, "zipf_bias_s": cfg.zipf, "shared_expert": cfg.shared,
+            "layer_instances": L, "weights_resident_gb": round(sum(x.experts.nbytes() for x in layers) / 1e9, 3),
+            "active_experts_per_step_mean": round(float(np.mean(steps_U)), 2),
+        },
+    }
+    if use_events:
+        gu_ms = float(np.sum(stages["gate_up"]))
+        gu_bytes = float(sum(gate_up_bytes(cfg, u) for u in steps_U))
+        achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
+        traffic = None
+        if os.path.exists(PMC_SUMMARY):
+            with open(PMC_SUMMARY) as f:
+                pmc = json.load(f)
+            if pmc.get("workload") == cfg.name:
+                traffic = pmc.get("hbm_bytes_per_launch")
+        out["roofline"] = {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "gate_up_kernel",
+            "algorithmic_bytes_per_launch": round(gu_bytes / args.steps),
+            "avg_launch_us": round(gu_ms * 1e3 / args.steps, 3),
+        }
+        lay_ms = float(np.sum(stages["layer"]))
+        lay_bytes = float(sum(layer_bytes(cfg, u) for u in steps_U))
+        out["layer"] = {
+            "gpu_us_per_step": round(lay_ms * 1e3 / args.steps, 3),
+            "stage_us": {k: round(float(np.mean(v)) * 1e3, 3) for k, v in stages.items() if k != "layer"},
+            "hbm_achieved_gbs": round(lay_bytes / (lay_ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(lay_bytes / (lay_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "tflops": round(layer_flops(cfg) * args.steps / (lay_ms * 1e-3) / 1e12, 3),
+        }
+    out["cpu_baseline"] = None
+    if host0 is not None:
+        out["cpu_baseline"] = cpu_baseline(cfg, host0, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

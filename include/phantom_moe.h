@@ -67,6 +67,15 @@ PHANTOM_MOE_API const char* phantom_moe_last_error(void);
 /* Library version string. */
 PHANTOM_MOE_API const char* phantom_moe_version(void);
 
+/* Stage timing.  With a non-null array of PHANTOM_MOE_PROFILE_EVENTS events
+ * set on the calling thread, phantom_moe_forward records events[0] before the
+ * router, [1] before gate/up, [2] before down, [3] before the combine and
+ * [4] after it, on the call's stream (no synchronisation).  NULL turns it
+ * off.  The non-blocking counterpart of the reference's per-call CudaTimer
+ * (kernels/common/cuda_utils.h:235-260, used at sparse_matmul.cu:256-257). */
+#define PHANTOM_MOE_PROFILE_EVENTS 5
+PHANTOM_MOE_API int phantom_moe_set_profile_events(hipEvent_t* events, int n_events);
+
 /* ---------------------------------------------------------------- */
 /* Q4_0 repack                                                       */
 /* ---------------------------------------------------------------- */
@@ -96,9 +105,9 @@ PHANTOM_MOE_API int phantom_q4_0_dequant_f32(const uint8_t* q4_0, int64_t rows, 
 /* ---------------------------------------------------------------- */
 
 /* Workspace bytes needed by phantom_moe_route / _permute / _forward for
- * these sizes.  The workspace must be zero-filled once before its first use;
- * the library leaves its internal counters at zero after every call.  One
- * workspace must not be used by calls that may run concurrently. */
+ * these sizes.  The workspace holds only per-call intermediates (no state
+ * carries between calls and no initial contents are required); one workspace
+ * must not be used by calls that may run concurrently. */
 PHANTOM_MOE_API size_t phantom_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int E, int top_k, int has_shared);
 
 /* Router: logits = x W^T (+ bias) under the fixed-order fp64 contract,

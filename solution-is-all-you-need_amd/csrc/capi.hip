@@ -17,6 +17,14 @@ namespace {
 
 thread_local char g_err[512] = "";
 
+// Optional stage events (phantom_moe_set_profile_events), per thread.
+thread_local hipEvent_t* g_prof_events = nullptr;
+
+hipError_t record_stage(int i, hipStream_t stream) {
+  if (!g_prof_events) return hipSuccess;
+  return hipEventRecord(g_prof_events[i], stream);
+}
+
 int fail(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -65,8 +73,6 @@ namespace pmoe {
 size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared, void* base,
                       Workspace* ws) {
   const int64_t Kpad = round_up(H, kQuad);
-  const int64_t TT = router_token_tile(T);
-  const int64_t n_ttiles = ceil_div(T, TT);
   const int64_t nslots = T * k;
   const int64_t rows = nslots + (has_shared ? T : 0);
   size_t off = 0;
@@ -75,22 +81,24 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
     off = align256(off + bytes);
     return o;
   };
-  const size_t o_cnt = take(sizeof(int32_t) * (size_t)(n_ttiles + 1));
   const size_t o_log = take(sizeof(double) * (size_t)(T * E));
-  const size_t o_xq = take(sizeof(uint16_t) * (size_t)(T * Kpad));
-  const size_t o_xs = take(sizeof(float) * (size_t)(T * (Kpad / kGroup)));
+  // x operand rows 0..T-1 plus an all-zero row T
+  const size_t o_xq = take(sizeof(uint16_t) * (size_t)((T + 1) * Kpad));
+  const size_t o_xs = take(sizeof(float) * (size_t)((T + 1) * (Kpad / kGroup)));
   const size_t o_off = take(sizeof(int32_t) * (size_t)(E + 2));
   const size_t o_act = take(sizeof(int32_t) * (size_t)(E + 1));
   const size_t o_nact = take(sizeof(int32_t));
   const size_t o_ss = take(sizeof(int32_t) * (size_t)nslots);
   const size_t o_sp = take(sizeof(int32_t) * (size_t)nslots);
+  const size_t o_desc = take(sizeof(int4) * (size_t)(E + 1));
+  const size_t o_tok = take(sizeof(int32_t) * (size_t)rows);
   const int64_t KpadI = I > 0 ? round_up(I, kQuad) : 0;
-  const size_t o_hq = take(sizeof(uint16_t) * (size_t)(rows * KpadI * 2));
-  const size_t o_hs = take(sizeof(float) * (size_t)(rows * (KpadI / kGroup) * 2));
+  // down operand rows plus an all-zero row
+  const size_t o_hq = take(sizeof(uint16_t) * (size_t)((rows + 1) * KpadI * 2));
+  const size_t o_hs = take(sizeof(float) * (size_t)((rows + 1) * (KpadI / kGroup) * 2));
   const size_t o_out = take(sizeof(float) * (size_t)(rows * (I > 0 ? H : 0)));
   if (ws && base) {
     char* b = static_cast<char*>(base);
-    ws->counters = reinterpret_cast<int32_t*>(b + o_cnt);
     ws->logits = reinterpret_cast<double*>(b + o_log);
     ws->xq = reinterpret_cast<uint16_t*>(b + o_xq);
     ws->xs = reinterpret_cast<float*>(b + o_xs);
@@ -99,6 +107,8 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
     ws->n_active = reinterpret_cast<int32_t*>(b + o_nact);
     ws->sorted_slots = reinterpret_cast<int32_t*>(b + o_ss);
     ws->slot_pos = reinterpret_cast<int32_t*>(b + o_sp);
+    ws->desc = reinterpret_cast<int4*>(b + o_desc);
+    ws->seg_tok = reinterpret_cast<int32_t*>(b + o_tok);
     ws->hq = reinterpret_cast<uint16_t*>(b + o_hq);
     ws->hs = reinterpret_cast<float*>(b + o_hs);
     ws->outbuf = reinterpret_cast<float*>(b + o_out);
@@ -113,6 +123,19 @@ extern "C" {
 const char* phantom_moe_last_error(void) { return g_err; }
 
 const char* phantom_moe_version(void) { return "phantom_moe 0.1.0 gfx950"; }
+
+int phantom_moe_set_profile_events(hipEvent_t* events, int n_events) {
+  if (events == nullptr) {
+    g_prof_events = nullptr;
+    return ok();
+  }
+  if (n_events < PHANTOM_MOE_PROFILE_EVENTS)
+    return fail(PHANTOM_MOE_EINVAL, "profile events: need %d events, got %d", PHANTOM_MOE_PROFILE_EVENTS, n_events);
+  for (int i = 0; i < PHANTOM_MOE_PROFILE_EVENTS; ++i)
+    if (!events[i]) return fail(PHANTOM_MOE_EINVAL, "profile events: event %d is null", i);
+  g_prof_events = events;
+  return ok();
+}
 
 int64_t phantom_q4_0_nib_bytes(int64_t rows, int64_t K) {
   if (rows < 0 || K < 0 || rows % 16 || K % 32) return -1;
@@ -248,6 +271,7 @@ int phantom_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_
   r.prep_x = true;
   r.do_permute = true;
   r.has_shared = has_shared;
+  if (int rc = launch_status(record_stage(0, stream), "profile event")) return rc;
   if (int rc = launch_status(pmoe::launch_route(r, ws, stream), "route")) return rc;
 
   pmoe::ExpertArgs a = {};
@@ -271,6 +295,15 @@ int phantom_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_
   a.sh_down_scale = sh_down_scale;
   a.topk_w = topk_w;
   a.y = y;
+  if (g_prof_events) {
+    if (int rc = launch_status(record_stage(1, stream), "profile event")) return rc;
+    if (int rc = launch_status(pmoe::launch_gate_up(a, ws, stream), "gate_up")) return rc;
+    if (int rc = launch_status(record_stage(2, stream), "profile event")) return rc;
+    if (int rc = launch_status(pmoe::launch_down(a, ws, stream), "down")) return rc;
+    if (int rc = launch_status(record_stage(3, stream), "profile event")) return rc;
+    if (int rc = launch_status(pmoe::launch_combine(a, ws, stream), "combine")) return rc;
+    return launch_status(record_stage(4, stream), "profile event");
+  }
   return launch_status(pmoe::launch_experts(a, ws, stream), "experts");
 }
 

@@ -5,14 +5,16 @@
 // projections, h = silu(g) * u in fp32, down projection) with the expert
 // weights of python/phantom/loader/gguf_loader.py:362-381 (Q4_0).
 //
-// Work decomposition.  Tokens are grouped per expert by the router's permute
-// (segment [offsets[e], offsets[e+1]) of sorted slots).  A workgroup of four
-// waves owns one 16-row tile of one active expert and walks that expert's
-// segment 16 tokens at a time; the four waves split K (quads q = w, w+4, ...)
-// and their partial tiles are summed in LDS in wave order, so the result does
-// not depend on timing.  Every weight byte of an active expert is read from
-// HBM by exactly one workgroup; the second and later 16-token tiles of a
-// segment re-read it from L2.
+// Work decomposition.  The router's permute groups tokens per expert into
+// segments and writes one descriptor {expert, begin, end} per launch slot
+// (expert -1 for slots beyond the active count).  A workgroup owns one 16-row
+// tile of one slot's expert and splits K across up to 16 waves, each issuing
+// the loads of its one to four quads at once; there are no loops over K and
+// no dependent chains beyond descriptor -> token id -> activation, so the
+// many short waves keep HBM busy the way a plain streaming read does.  Wave
+// partials are summed in LDS in wave order, so results do not depend on
+// timing.  Every weight byte of an active expert is read from HBM once; later
+// 16-token tiles of a long segment re-read it from L2.
 //
 // Arithmetic per 32-group g, token m, weight row n (see moe_common.h):
 //   P = mfma(a_m, 1 + nib_n / 16)               exact products, fp32 sums
@@ -25,23 +27,24 @@
 // kernel only loads operands (two fp16 MFMAs per group).  fp16 bounds |h| to
 // below 65504.
 #include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
 
 #include "moe_common.h"
 #include "moe_launch.h"
 
 namespace pmoe {
 
-struct SegmentK {
-  const int32_t* offsets;
-  const int32_t* active;
-  const int32_t* n_active;
-  const int32_t* sorted_slots;
-  int64_t T;
-  int k, E;
+struct SegSrc {
+  const int4* desc;        // [max_slots] {expert, begin, end, 0}; expert -1 = unused slot
+  const int32_t* seg_tok;  // token of each segment position
+  int E;
+  int max_slots;           // min(E, T*k) + shared
 };
 
 struct GateUpK {
-  SegmentK seg;
+  SegSrc seg;
+  int64_t T;  // tokens; row T of xq / xs is the all-zero activation row
   const uint16_t* xq;
   const float* xs;
   const uint8_t* gate_nib;
@@ -52,24 +55,26 @@ struct GateUpK {
   const uint16_t* sh_gate_sc;
   const uint8_t* sh_up_nib;
   const uint16_t* sh_up_sc;
-  int64_t I;   // rows of gate/up
-  int64_t Kq;  // quads of H
-  int64_t KqI; // quads of I (down operand layout)
-  uint16_t* hq;  // [rows][KqI][4 p][4 gi][hi, lo][8] fp16 bits
-  float* hs;     // [rows][KqI * 4 groups][2 halves] sums of hi + lo
+  int64_t I;    // rows of gate/up
+  int64_t Kq;   // quads of H
+  int64_t KqI;  // quads of I (down operand layout)
+  uint16_t* hq; // [rows + 1][KqI][4 p][4 gi][hi, lo][8] fp16 bits; row `zero_row` is zero
+  float* hs;    // [rows + 1][KqI * 4 groups][2 halves] sums of hi + lo
+  int64_t zero_row;
 };
 
 struct DownK {
-  SegmentK seg;
+  SegSrc seg;
   const uint16_t* hq;
   const float* hs;
   const uint8_t* down_nib;
   const uint16_t* down_sc;
   const uint8_t* sh_down_nib;
   const uint16_t* sh_down_sc;
-  int64_t H;   // rows of down
-  int64_t I;   // K of down
-  int64_t Kq;  // quads of I
+  int64_t H;         // rows of down
+  int64_t I;         // K of down
+  int64_t Kq;        // quads of I
+  int64_t zero_row;  // hq / hs row that holds zeros
   float* outbuf;
 };
 
@@ -80,203 +85,304 @@ __device__ inline void unpack_scales(uint2 s, float d[4]) {
   d[3] = half_bits_to_float((uint16_t)(s.y >> 16));
 }
 
-__device__ inline int64_t token_of(const SegmentK& s, int64_t pos) {
-  const int64_t nslots = s.T * s.k;
-  return (pos < nslots) ? (int64_t)(s.sorted_slots[pos] / s.k) : pos - nslots;
+// Copies the launch slots' segment descriptors into LDS; returns how many
+// slots are in use (they come first; unused slots carry expert -1).
+__device__ inline int load_descriptors(const SegSrc& seg, int4* s_desc, int* s_nact) {
+  if (threadIdx.x == 0) *s_nact = 0;
+  __syncthreads();
+  for (int u = threadIdx.x; u < seg.max_slots; u += blockDim.x) {
+    const int4 d = seg.desc[u];
+    s_desc[u] = d;
+    if (d.x >= 0 && (u + 1 == seg.max_slots || seg.desc[u + 1].x < 0)) *s_nact = u + 1;
+  }
+  __syncthreads();
+  return *s_nact;
 }
 
-__global__ __launch_bounds__(256) void gate_up_kernel(GateUpK a) {
-  const int u = blockIdx.y;
-  if (u >= *a.seg.n_active) return;
-  const int e = a.seg.active[u];
-  const int64_t seg_beg = a.seg.offsets[e];
-  const int64_t seg_end = a.seg.offsets[e + 1];
-  const int64_t nib_stride = a.I * a.Kq * 64;  // bytes per expert
-  const int64_t sc_stride = a.I * a.Kq * 4;    // fp16 scales per expert
-  const uint8_t* gnib;
-  const uint16_t* gsc;
-  const uint8_t* unib;
-  const uint16_t* usc;
-  if (e < a.seg.E) {
-    gnib = a.gate_nib + e * nib_stride;
-    gsc = a.gate_sc + e * sc_stride;
-    unib = a.up_nib + e * nib_stride;
-    usc = a.up_sc + e * sc_stride;
-  } else {
-    gnib = a.sh_gate_nib;
-    gsc = a.sh_gate_sc;
-    unib = a.sh_up_nib;
-    usc = a.sh_up_sc;
-  }
-  const int64_t rt = blockIdx.x;
+// ------------------------------------------------------------------ gate/up
+
+// Workgroup = (RT row tiles of one active expert) x (all of K).  Wave ks of
+// the ksplit waves takes quads ks, ks + ksplit, ... (NQ of them), issues all
+// their loads at once, and contributes a partial tile; partials are summed in
+// LDS in wave order.  The weight loads depend only on the segment descriptor
+// (one uniform load), the activation loads on one token-id load.
+// One item: RT row tiles starting at rt0 of the segment described by d.
+// Token tiles are taken TP at a time: each dequantised weight operand feeds
+// TP MFMAs, so the nibble expansion is paid once per 32 tokens.
+template <int RT, int NQ, int TP>
+__device__ inline void gate_up_pass(const GateUpK& a, const int e, const int64_t seg_end, const int64_t m0,
+                                    const int64_t rt0, float (*red)[2][2][16][16]) {
   const int lane = threadIdx.x % kWave;
-  const int w = threadIdx.x / kWave;
+  const int ks = threadIdx.x / kWave;
+  const int ksplit = blockDim.x / kWave;
   const int n = lane % 16;
   const int p = lane / 16;
-  __shared__ float red[4][2][16][16];
-
-  for (int64_t m0 = seg_beg; m0 < seg_end; m0 += 16) {
-    const int64_t pm = m0 + n;
-    const bool valid = pm < seg_end;
-    const int64_t tok = valid ? token_of(a.seg, pm) : 0;
-    f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = accg, cg = accg, cu = accg;
-    for (int64_t q = w; q < a.Kq; q += 4) {
-      const int64_t tq = rt * a.Kq + q;
-      const u32x4 gw = *reinterpret_cast<const u32x4*>(gnib + (tq * kWave + lane) * 16);
-      const u32x4 uw = *reinterpret_cast<const u32x4*>(unib + (tq * kWave + lane) * 16);
-      const uint2 gs = *reinterpret_cast<const uint2*>(gsc + tq * kQuadScales + n * 4);
-      const uint2 us = *reinterpret_cast<const uint2*>(usc + tq * kQuadScales + n * 4);
-      u32x4 xa[4];
-      float sx = 0.0f;
-      if (valid) {
-        const u32x4* xp = reinterpret_cast<const u32x4*>(a.xq + ((tok * a.Kq + q) * 16 + p * 4) * 8);
+  const uint32_t mask = vgpr_const(0x00780078u);
+  const int64_t nib_stride = a.I * a.Kq * 64;
+  const int64_t sc_stride = a.I * a.Kq * 4;
+  const uint8_t* gnib = e < a.seg.E ? a.gate_nib + e * nib_stride : a.sh_gate_nib;
+  const uint16_t* gsc = e < a.seg.E ? a.gate_sc + e * sc_stride : a.sh_gate_sc;
+  const uint8_t* unib = e < a.seg.E ? a.up_nib + e * nib_stride : a.sh_up_nib;
+  const uint16_t* usc = e < a.seg.E ? a.up_sc + e * sc_stride : a.sh_up_sc;
+  uint32_t xoff[TP];  // element offset of this lane's activation row
 #pragma unroll
-        for (int gi = 0; gi < 4; ++gi) xa[gi] = xp[gi];
-        sx = a.xs[tok * a.Kq * 4 + 4 * q + p];
-      } else {
-#pragma unroll
-        for (int gi = 0; gi < 4; ++gi) xa[gi] = u32x4{0u, 0u, 0u, 0u};
-      }
-      float dg[4], du[4];
-      unpack_scales(gs, dg);
-      unpack_scales(us, du);
-      const uint32_t gwv[4] = {gw.x, gw.y, gw.z, gw.w};
-      const uint32_t uwv[4] = {uw.x, uw.y, uw.z, uw.w};
-#pragma unroll
-      for (int gi = 0; gi < 4; ++gi) {
-        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-        const f32x4 pg = mfma_bf16_16x16x32(xa[gi], dequant_unit_bf16(gwv[gi]), z);
-        accg += (kUnitScale * dg[gi]) * pg;
-        const f32x4 pu = mfma_bf16_16x16x32(xa[gi], dequant_unit_bf16(uwv[gi]), z);
-        accu += (kUnitScale * du[gi]) * pu;
-      }
-      cg = mfma_f32_16x16x4(sx, dg[p], cg);
-      cu = mfma_f32_16x16x4(sx, du[p], cu);
-    }
-    const f32x4 rg = accg - kUnitBias * cg;
-    const f32x4 ru = accu - kUnitBias * cu;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      red[w][0][4 * p + r][n] = rg[r];
-      red[w][1][4 * p + r][n] = ru[r];
-    }
-    __syncthreads();
-    {
-      const int mm = threadIdx.x / 16;
-      const int nn = threadIdx.x % 16;
-      const float g = ((red[0][0][mm][nn] + red[1][0][mm][nn]) + red[2][0][mm][nn]) + red[3][0][mm][nn];
-      const float uu = ((red[0][1][mm][nn] + red[1][1][mm][nn]) + red[2][1][mm][nn]) + red[3][1][mm][nn];
-      const float h = g * (1.0f / (1.0f + expf(-g))) * uu;
-      // fp16 pair hi + lo of h, placed where the down kernel's MFMA operand
-      // for (token, group, part) expects element i of I.
-      const uint32_t hb = float_to_half_bits(h);
-      const float hf = half_bits_to_float32(hb);
-      const uint32_t lb = float_to_half_bits(h - hf);
-      const float lf = half_bits_to_float32(lb);
-      const int64_t pos = m0 + mm;
-      const int64_t i = rt * 16 + nn;
-      const int64_t g32 = i / kGroup;
-      const int c = (int)(i % kGroup);
-      const int half = c / 16;
-      const int pp = (c % 16) / 4;
-      const int r = c % 4;
-      // kmap(p, j) = 4p + {0, 2, 16, 18, 1, 3, 17, 19}[j], inverted per half
-      const int j = half == 0 ? ((r & 1) ? 4 : 0) + (r >> 1) : ((r & 1) ? 6 : 2) + (r >> 1);
-      if (pos < seg_end) {
-        uint16_t* dst = a.hq + (((pos * a.KqI + g32 / 4) * 16 + pp * 4 + (g32 % 4)) * 16);
-        dst[j] = (uint16_t)hb;
-        dst[8 + j] = (uint16_t)lb;
-      }
-      // The tile's 16 rows are one half of one group: sum hi + lo over them
-      // (16 consecutive lanes, fixed butterfly order).
-      float s = hf + lf;
-      s += __shfl_xor(s, 8, kWave);
-      s += __shfl_xor(s, 4, kWave);
-      s += __shfl_xor(s, 2, kWave);
-      s += __shfl_xor(s, 1, kWave);
-      if (nn == 0 && pos < seg_end) a.hs[(pos * a.KqI * 4 + g32) * 2 + half] = s;
-    }
-    __syncthreads();
+  for (int t = 0; t < TP; ++t) {
+    const int64_t pm = m0 + 16 * t + n;
+    const int64_t tok = pm < seg_end ? (int64_t)a.seg.seg_tok[pm] : a.T;  // row T is all zero
+    xoff[t] = (uint32_t)(tok * a.Kq);
   }
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  f32x4 ag[TP][RT], au[TP][RT], cg[TP][RT], cu[TP][RT];
+#pragma unroll
+  for (int t = 0; t < TP; ++t)
+#pragma unroll
+    for (int r = 0; r < RT; ++r) ag[t][r] = au[t][r] = cg[t][r] = cu[t][r] = z;
+  // quads ks, ks + ksplit, ... in chunks of NQ (one chunk for K <= 16 * NQ quads)
+  for (int64_t q0 = ks; q0 < a.Kq; q0 += (int64_t)NQ * ksplit) {
+    u32x4 gw[NQ][RT], uw[NQ][RT];
+    uint2 gs[NQ][RT], us[NQ][RT];
+    u32x4 xa[NQ][TP][4];
+    float sx[NQ][TP];
+    bool qok[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      int q = (int)(q0 + (int64_t)i * ksplit);
+      qok[i] = q < a.Kq;
+      q = qok[i] ? q : (int)a.Kq - 1;
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        const int64_t tq = (rt0 + r) * a.Kq + q;  // wave-uniform
+        const uint8_t* gb = gnib + tq * kQuadNibBytes;
+        const uint8_t* ub = unib + tq * kQuadNibBytes;
+        gw[i][r] = *reinterpret_cast<const u32x4*>(gb + lane * 16);
+        uw[i][r] = *reinterpret_cast<const u32x4*>(ub + lane * 16);
+        gs[i][r] = *reinterpret_cast<const uint2*>(gsc + tq * kQuadScales + n * 4);
+        us[i][r] = *reinterpret_cast<const uint2*>(usc + tq * kQuadScales + n * 4);
+      }
+#pragma unroll
+      for (int t = 0; t < TP; ++t) {
+        const u32x4* xp =
+            reinterpret_cast<const u32x4*>(a.xq + ((uint64_t)(xoff[t] + q) * 16 + p * 4) * 8);
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) xa[i][t][gi] = xp[gi];
+        sx[i][t] = a.xs[(uint64_t)(xoff[t] + q) * 4 + p];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      if (!qok[i]) continue;
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        float dg[4], du[4];
+        unpack_scales(gs[i][r], dg);
+        unpack_scales(us[i][r], du);
+        const uint32_t gwv[4] = {gw[i][r].x, gw[i][r].y, gw[i][r].z, gw[i][r].w};
+        const uint32_t uwv[4] = {uw[i][r].x, uw[i][r].y, uw[i][r].z, uw[i][r].w};
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const u32x4 bg = dequant_unit_bf16(gwv[gi], mask);
+          const u32x4 bu = dequant_unit_bf16(uwv[gi], mask);
+#pragma unroll
+          for (int t = 0; t < TP; ++t) {
+            ag[t][r] += dg[gi] * mfma_bf16_16x16x32(xa[i][t][gi], bg, z);
+            au[t][r] += du[gi] * mfma_bf16_16x16x32(xa[i][t][gi], bu, z);
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < TP; ++t) {
+          cg[t][r] = mfma_f32_16x16x4(sx[i][t], dg[p], cg[t][r]);
+          cu[t][r] = mfma_f32_16x16x4(sx[i][t], du[p], cu[t][r]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TP; ++t) {
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      // sum_g d * sum_k a (n - 8) = 16 * sum_g d P - 24 * sum_g d S
+      const f32x4 rg = kUnitScale * ag[t][r] - kUnitBias * cg[t][r];
+      const f32x4 ru = kUnitScale * au[t][r] - kUnitBias * cu[t][r];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        red[ks][t * RT + r][0][4 * p + j][n] = rg[j];
+        red[ks][t * RT + r][1][4 * p + j][n] = ru[j];
+      }
+    }
+  }
+  __syncthreads();
+  for (int o = threadIdx.x; o < TP * RT * 256; o += blockDim.x) {
+    const int tr = o / 256;
+    const int t = tr / RT;
+    const int r = tr % RT;
+    const int mm = (o % 256) / 16;
+    const int nn = o % 16;
+    float g = 0.0f, uu = 0.0f;
+    for (int s2 = 0; s2 < ksplit; ++s2) {
+      g += red[s2][tr][0][mm][nn];
+      uu += red[s2][tr][1][mm][nn];
+    }
+    const float h = g * (1.0f / (1.0f + expf(-g))) * uu;
+    // fp16 pair hi + lo of h, placed where the down kernel's MFMA operand
+    // for (segment position, group, part) expects element i of I.
+    const uint32_t hb = float_to_half_bits(h);
+    const float hf = half_bits_to_float32(hb);
+    const uint32_t lb = float_to_half_bits(h - hf);
+    const float lf = half_bits_to_float32(lb);
+    const int64_t pos = m0 + 16 * t + mm;
+    const bool ok = pos < seg_end;
+    const int64_t i = (rt0 + r) * 16 + nn;
+    const int64_t g32 = i / kGroup;
+    const int cc = (int)(i % kGroup);
+    const int half = cc / 16;
+    const int pp = (cc % 16) / 4;
+    const int rr = cc % 4;
+    // kmap(p, j) = 4p + {0, 2, 16, 18, 1, 3, 17, 19}[j], inverted per half
+    const int j = half == 0 ? ((rr & 1) ? 4 : 0) + (rr >> 1) : ((rr & 1) ? 6 : 2) + (rr >> 1);
+    if (ok) {
+      uint16_t* dst = a.hq + (((pos * a.KqI + g32 / 4) * 16 + pp * 4 + (g32 % 4)) * 16);
+      dst[j] = (uint16_t)hb;
+      dst[8 + j] = (uint16_t)lb;
+    }
+    // The tile's 16 rows are one half of one group: sum hi + lo over them
+    // (16 consecutive lanes, fixed butterfly order).
+    float sum = hf + lf;
+    sum += __shfl_xor(sum, 8, kWave);
+    sum += __shfl_xor(sum, 4, kWave);
+    sum += __shfl_xor(sum, 2, kWave);
+    sum += __shfl_xor(sum, 1, kWave);
+    if (nn == 0 && ok) a.hs[(pos * a.KqI * 4 + g32) * 2 + half] = sum;
+  }
+  __syncthreads();
 }
 
-__global__ __launch_bounds__(256) void down_kernel(DownK a) {
-  const int u = blockIdx.y;
-  if (u >= *a.seg.n_active) return;
-  const int e = a.seg.active[u];
-  const int64_t seg_beg = a.seg.offsets[e];
-  const int64_t seg_end = a.seg.offsets[e + 1];
+template <int RT, int NQ>
+__device__ inline void gate_up_item(const GateUpK& a, const int4 d, const int64_t rt0,
+                                    float (*red)[2][2][16][16]) {
+  const int e = __builtin_amdgcn_readfirstlane(d.x);
+  const int64_t beg = __builtin_amdgcn_readfirstlane(d.y);
+  const int64_t end = __builtin_amdgcn_readfirstlane(d.z);
+  int64_t m0 = beg;
+  for (; m0 + 16 < end; m0 += 32) gate_up_pass<RT, NQ, 2>(a, e, end, m0, rt0, red);
+  if (m0 < end) gate_up_pass<RT, NQ, 1>(a, e, end, m0, rt0, red);
+}
+
+template <int RT, int NQ>
+__global__ __launch_bounds__(1024) void gate_up_kernel(GateUpK a) {
+  __shared__ float red[16][2][2][16][16];  // [wave][token tile * RT + row tile][gate/up]
+  __shared__ int4 s_desc[kMaxExperts + 1];
+  __shared__ int s_nact;
+  const int lane = threadIdx.x % kWave;
+  const int ks = threadIdx.x / kWave;
+  const int ksplit = blockDim.x / kWave;
+  const int n = lane % 16;
+  const int p = lane / 16;
+  if (blockIdx.x == 0) {
+    // the all-zero down-operand row read for positions past a segment
+    for (int64_t i = threadIdx.x; i < a.KqI * 256; i += blockDim.x) a.hq[a.zero_row * a.KqI * 256 + i] = 0;
+    for (int64_t i = threadIdx.x; i < a.KqI * 8; i += blockDim.x) a.hs[a.zero_row * a.KqI * 8 + i] = 0.0f;
+  }
+  const int n_act = load_descriptors(a.seg, s_desc, &s_nact);
+  const int64_t n_cols = a.I / (kRowTile * RT);
+  for (int64_t item = blockIdx.x; item < (int64_t)n_act * n_cols; item += gridDim.x)
+    gate_up_item<RT, NQ>(a, s_desc[item / n_cols], (item % n_cols) * RT, red);
+}
+
+
+// ------------------------------------------------------------------ down
+
+// Same decomposition as gate_up_kernel: one 16-row tile of one expert per
+// workgroup, K split over its waves.  Positions past the segment read the
+// all-zero operand row of hq / hs.
+template <int NQ>
+__device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt, float (*red)[16][16]) {
+  const int lane = threadIdx.x % kWave;
+  const int ks = threadIdx.x / kWave;
+  const int ksplit = blockDim.x / kWave;
+  const int n = lane % 16;
+  const int p = lane / 16;
+  const int e = d.x;
   const int64_t nib_stride = a.H * a.Kq * 64;
   const int64_t sc_stride = a.H * a.Kq * 4;
-  const uint8_t* dnib;
-  const uint16_t* dsc;
-  if (e < a.seg.E) {
-    dnib = a.down_nib + e * nib_stride;
-    dsc = a.down_sc + e * sc_stride;
-  } else {
-    dnib = a.sh_down_nib;
-    dsc = a.sh_down_sc;
-  }
+  const uint8_t* dnib = e < a.seg.E ? a.down_nib + e * nib_stride : a.sh_down_nib;
+  const uint16_t* dsc = e < a.seg.E ? a.down_sc + e * sc_stride : a.sh_down_sc;
   const int64_t Kg = a.I / kGroup;
-  const int64_t rt = blockIdx.x;
-  const int lane = threadIdx.x % kWave;
-  const int w = threadIdx.x / kWave;
-  const int n = lane % 16;
-  const int p = lane / 16;
-  __shared__ float red[4][16][16];
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  const uint32_t mask = vgpr_const(0x03C003C0u);
 
-  for (int64_t m0 = seg_beg; m0 < seg_end; m0 += 16) {
-    const int64_t pm = m0 + n;
-    const bool valid = pm < seg_end;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f}, corr = acc;
-    for (int64_t q = w; q < a.Kq; q += 4) {
-      const int64_t tq = rt * a.Kq + q;
-      const u32x4 bw = *reinterpret_cast<const u32x4*>(dnib + (tq * kWave + lane) * 16);
-      const uint2 bs = *reinterpret_cast<const uint2*>(dsc + tq * kQuadScales + n * 4);
-      float dv[4];
-      unpack_scales(bs, dv);
-      const uint32_t bwv[4] = {bw.x, bw.y, bw.z, bw.w};
-      u32x4 ah[4], al[4];
-      float sp = 0.0f;
-      const u32x4 zero = {0u, 0u, 0u, 0u};
-      if (valid) {
+  for (int64_t m0 = d.y; m0 < d.z; m0 += 16) {
+    const int64_t pm0 = m0 + n;
+    const int64_t pm = pm0 < d.z ? pm0 : a.zero_row;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc = z, corr = z;
+    // quads ks, ks + ksplit, ... in chunks of NQ (one chunk for K <= 16 * NQ quads)
+    for (int64_t q0 = ks; q0 < a.Kq; q0 += (int64_t)NQ * ksplit) {
+      u32x4 bw[NQ];
+      uint2 bs[NQ];
+      u32x4 ah[NQ][4], al[NQ][4];
+      float sp[NQ];
+      bool qok[NQ];
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) {
+        int64_t q = q0 + (int64_t)i * ksplit;
+        qok[i] = q < a.Kq;
+        q = qok[i] ? q : a.Kq - 1;
+        const int64_t tq = rt * a.Kq + q;
+        bw[i] = *reinterpret_cast<const u32x4*>(dnib + (tq * kWave + lane) * 16);
+        bs[i] = *reinterpret_cast<const uint2*>(dsc + tq * kQuadScales + n * 4);
         const u32x4* src = reinterpret_cast<const u32x4*>(a.hq + ((pm * a.Kq + q) * 16 + p * 4) * 16);
 #pragma unroll
         for (int gi = 0; gi < 4; ++gi) {
           const bool real = 4 * q + gi < Kg;  // padded groups hold no h
-          ah[gi] = real ? src[2 * gi] : zero;
-          al[gi] = real ? src[2 * gi + 1] : zero;
+          const u32x4 h = src[2 * gi];
+          const u32x4 l = src[2 * gi + 1];
+          ah[i][gi] = real ? h : zero;
+          al[i][gi] = real ? l : zero;
         }
-        if (4 * q + p < Kg) {
-          const float* hsrc = a.hs + (pm * a.Kq * 4 + 4 * q + p) * 2;
-          sp = hsrc[0] + hsrc[1];
-        }
-      } else {
-#pragma unroll
-        for (int gi = 0; gi < 4; ++gi) ah[gi] = al[gi] = zero;
+        const float* hsrc = a.hs + (pm * a.Kq * 4 + 4 * q + p) * 2;
+        const float s0 = hsrc[0], s1 = hsrc[1];
+        sp[i] = (4 * q + p < Kg) ? s0 + s1 : 0.0f;
       }
 #pragma unroll
-      for (int gi = 0; gi < 4; ++gi) {
-        const u32x4 b = dequant_unit_f16(bwv[gi]);
-        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-        f32x4 pp = mfma_f16_16x16x32(ah[gi], b, z);
-        pp = mfma_f16_16x16x32(al[gi], b, pp);
-        acc += (kUnitScale * dv[gi]) * pp;
+      for (int i = 0; i < NQ; ++i) {
+        if (!qok[i]) continue;
+        float dv[4];
+        unpack_scales(bs[i], dv);
+        const uint32_t bwv[4] = {bw[i].x, bw[i].y, bw[i].z, bw[i].w};
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const u32x4 bb = dequant_unit_f16(bwv[gi], mask);
+          f32x4 pp = mfma_f16_16x16x32(ah[i][gi], bb, z);
+          pp = mfma_f16_16x16x32(al[i][gi], bb, pp);
+          acc += dv[gi] * pp;
+        }
+        corr = mfma_f32_16x16x4(sp[i], dv[p], corr);
       }
-      corr = mfma_f32_16x16x4(sp, dv[p], corr);
     }
-    const f32x4 res = acc - kUnitBias * corr;
+    const f32x4 res = kUnitScale * acc - kUnitBias * corr;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[w][4 * p + r][n] = res[r];
+    for (int j = 0; j < 4; ++j) red[ks][4 * p + j][n] = res[j];
     __syncthreads();
-    {
-      const int mm = threadIdx.x / 16;
-      const int nn = threadIdx.x % 16;
-      const float y = ((red[0][mm][nn] + red[1][mm][nn]) + red[2][mm][nn]) + red[3][mm][nn];
-      if (m0 + mm < seg_end) a.outbuf[(m0 + mm) * a.H + rt * 16 + nn] = y;
+    for (int o = threadIdx.x; o < 256; o += blockDim.x) {
+      const int mm = o / 16;
+      const int nn = o % 16;
+      float y = 0.0f;
+      for (int s2 = 0; s2 < ksplit; ++s2) y += red[s2][mm][nn];
+      if (m0 + mm < d.z) a.outbuf[(m0 + mm) * a.H + rt * 16 + nn] = y;
     }
     __syncthreads();
   }
+}
+
+template <int NQ>
+__global__ __launch_bounds__(1024) void down_kernel(DownK a) {
+  __shared__ float red[16][16][16];
+  __shared__ int4 s_desc[kMaxExperts + 1];
+  __shared__ int s_nact;
+  const int n_act = load_descriptors(a.seg, s_desc, &s_nact);
+  const int64_t n_rt = a.H / kRowTile;
+  for (int64_t item = blockIdx.x; item < (int64_t)n_act * n_rt; item += gridDim.x)
+    down_item<NQ>(a, s_desc[item / n_rt], item % n_rt, red);
 }
 
 // y[t] = sum_j w[t,j] * out[slot_pos[t*k+j]] (+ out[T*k + t] for the shared
@@ -313,20 +419,89 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   }
 }
 
-hipError_t launch_experts(const ExpertArgs& x, const Workspace& ws, hipStream_t stream) {
-  SegmentK seg;
-  seg.offsets = ws.offsets;
-  seg.active = ws.active;
-  seg.n_active = ws.n_active;
-  seg.sorted_slots = ws.sorted_slots;
-  seg.T = x.T;
-  seg.k = x.k;
-  seg.E = x.E;
+static unsigned max_active_experts(const ExpertArgs& x) {
   const int64_t nslots = x.T * x.k;
-  const int64_t max_active = ((nslots < x.E) ? nslots : x.E) + (x.has_shared ? 1 : 0);
+  return (unsigned)(((nslots < x.E) ? nslots : x.E) + (x.has_shared ? 1 : 0));
+}
 
+static SegSrc segments_of(const ExpertArgs& x, const Workspace& ws) {
+  SegSrc seg;
+  seg.desc = ws.desc;
+  seg.seg_tok = ws.seg_tok;
+  seg.E = x.E;
+  seg.max_slots = (int)max_active_experts(x);
+  return seg;
+}
+
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Workgroups for a strided item loop: those resident at once (occupancy of
+// this kernel at this block size, cached per kernel since the query is slow),
+// capped by the largest possible item count.
+template <typename Kernel>
+static unsigned resident_grid(Kernel kernel, int block, int64_t max_items) {
+  struct Entry {
+    const void* fn;
+    int block, per_cu;
+  };
+  static thread_local Entry cache[32];
+  static thread_local int n_cache = 0;
+  int per_cu = 0;
+  for (int i = 0; i < n_cache; ++i)
+    if (cache[i].fn == reinterpret_cast<const void*>(kernel) && cache[i].block == block) per_cu = cache[i].per_cu;
+  if (per_cu == 0) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess || per_cu < 1)
+      per_cu = 1;
+    if (n_cache < 32) cache[n_cache++] = Entry{reinterpret_cast<const void*>(kernel), block, per_cu};
+  }
+  int64_t g = (int64_t)device_cus() * per_cu;
+  if (g > max_items) g = max_items;
+  return (unsigned)(g < 1 ? 1 : g);
+}
+
+// K split: ksplit waves (at most 16) take about Kq / ksplit quads each, in
+// chunks of NQ <= max_nq issued together.
+struct Split {
+  int ksplit, nq;
+};
+
+static Split choose_split(int64_t Kq, int max_nq) {
+  Split s;
+  s.ksplit = (int)(Kq < 16 ? Kq : 16);
+  const int64_t qpw = ceil_div(Kq, s.ksplit);
+  s.nq = 1;
+  while (s.nq < qpw && s.nq < max_nq) s.nq *= 2;
+  return s;
+}
+
+// Optional override "ksplit,rt,nq" for tuning sweeps (PHANTOM_MOE_GATE_UP_TILING /
+// PHANTOM_MOE_DOWN_TILING); values outside the supported set are ignored.
+static void tiling_override(const char* name, int* ksplit, int* rt, int* nq) {
+  const char* v = getenv(name);
+  if (!v) return;
+  int a = 0, b = 0, c = 0;
+  if (sscanf(v, "%d,%d,%d", &a, &b, &c) == 3 && a >= 1 && a <= 16 && (b == 1 || b == 2) &&
+      (c == 1 || c == 2 || c == 4)) {
+    *ksplit = a;
+    *rt = b;
+    *nq = c;
+  }
+}
+
+hipError_t launch_gate_up(const ExpertArgs& x, const Workspace& ws, hipStream_t stream) {
   GateUpK g;
-  g.seg = seg;
+  g.seg = segments_of(x, ws);
+  g.T = x.T;
   g.xq = ws.xq;
   g.xs = ws.xs;
   g.gate_nib = x.gate_nib;
@@ -342,13 +517,26 @@ hipError_t launch_experts(const ExpertArgs& x, const Workspace& ws, hipStream_t 
   g.KqI = ceil_div(x.I, kQuad);
   g.hq = ws.hq;
   g.hs = ws.hs;
-  hipLaunchKernelGGL(gate_up_kernel, dim3((unsigned)(x.I / kRowTile), (unsigned)max_active),
-                     dim3(256), 0, stream, g);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
+  g.zero_row = x.T * x.k + (x.has_shared ? x.T : 0);
+  Split sp = choose_split(g.Kq, 1);
+  int rt = 1;
+  tiling_override("PHANTOM_MOE_GATE_UP_TILING", &sp.ksplit, &rt, &sp.nq);
+  if (sp.nq > 2) sp.nq = 2;
+  rt = 1;  // one row tile per item; token tiles are paired instead
+  const int block = kWave * sp.ksplit;
+  const int64_t max_items = (int64_t)max_active_experts(x) * (x.I / (kRowTile * rt));
+#define PMOE_GU(RT_, NQ_)                                                                               \
+  hipLaunchKernelGGL((gate_up_kernel<RT_, NQ_>), dim3(resident_grid(gate_up_kernel<RT_, NQ_>, block, max_items)), \
+                     dim3(block), 0, stream, g)
+  if (sp.nq == 1) PMOE_GU(1, 1);
+  else PMOE_GU(1, 2);
+#undef PMOE_GU
+  return hipGetLastError();
+}
 
+hipError_t launch_down(const ExpertArgs& x, const Workspace& ws, hipStream_t stream) {
   DownK d;
-  d.seg = seg;
+  d.seg = segments_of(x, ws);
   d.hq = ws.hq;
   d.hs = ws.hs;
   d.down_nib = x.down_nib;
@@ -358,18 +546,38 @@ hipError_t launch_experts(const ExpertArgs& x, const Workspace& ws, hipStream_t 
   d.H = x.H;
   d.I = x.I;
   d.Kq = ceil_div(x.I, kQuad);
+  d.zero_row = x.T * x.k + (x.has_shared ? x.T : 0);
   d.outbuf = ws.outbuf;
-  hipLaunchKernelGGL(down_kernel, dim3((unsigned)(x.H / kRowTile), (unsigned)max_active),
-                     dim3(256), 0, stream, d);
-  err = hipGetLastError();
-  if (err != hipSuccess) return err;
+  Split sp = choose_split(d.Kq, 2);
+  int rt = 1;
+  tiling_override("PHANTOM_MOE_DOWN_TILING", &sp.ksplit, &rt, &sp.nq);
+  if (sp.nq > 2) sp.nq = 2;
+  const int block = kWave * sp.ksplit;
+  const int64_t max_items = (int64_t)max_active_experts(x) * (x.H / kRowTile);
+  if (sp.nq == 1)
+    hipLaunchKernelGGL(down_kernel<1>, dim3(resident_grid(down_kernel<1>, block, max_items)), dim3(block), 0,
+                       stream, d);
+  else
+    hipLaunchKernelGGL(down_kernel<2>, dim3(resident_grid(down_kernel<2>, block, max_items)), dim3(block), 0,
+                       stream, d);
+  return hipGetLastError();
+}
 
+hipError_t launch_combine(const ExpertArgs& x, const Workspace& ws, hipStream_t stream) {
   const int64_t total = x.T * (x.H / 4);
   int64_t blocks = ceil_div(total, 256);
   if (blocks > 65536) blocks = 65536;
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, ws.outbuf,
                      ws.slot_pos, x.topk_w, x.T, x.k, x.H, x.has_shared, x.y);
   return hipGetLastError();
+}
+
+hipError_t launch_experts(const ExpertArgs& x, const Workspace& ws, hipStream_t stream) {
+  hipError_t err = launch_gate_up(x, ws, stream);
+  if (err != hipSuccess) return err;
+  err = launch_down(x, ws, stream);
+  if (err != hipSuccess) return err;
+  return launch_combine(x, ws, stream);
 }
 
 }  // namespace pmoe

@@ -55,23 +55,40 @@ __host__ __device__ inline int kmap(int p, int j) {
   return 4 * p + off[j];
 }
 
-// 4 qs bytes (little endian word) -> 8 bf16 values 1 + n/16, in kmap order.
-__device__ inline u32x4 dequant_unit_bf16(uint32_t w) {
-  u32x4 r;
-  r.x = ((w << 3) & 0x00780078u) | 0x3F803F80u;
-  r.y = ((w >> 1) & 0x00780078u) | 0x3F803F80u;
-  r.z = ((w >> 5) & 0x00780078u) | 0x3F803F80u;
-  r.w = ((w >> 9) & 0x00780078u) | 0x3F803F80u;
+// (a & m) | c in one VOP3 instruction.  gfx9 VOP3 reads at most one scalar
+// or literal operand, so the mask comes in a VGPR (hoisted out of loops by
+// the caller) and the constant in an SGPR.
+__device__ inline uint32_t and_or(uint32_t a, uint32_t m_vgpr, uint32_t c_sgpr) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m_vgpr), "s"(c_sgpr));
   return r;
 }
 
-// Same expansion as fp16 values 1 + n/16.
-__device__ inline u32x4 dequant_unit_f16(uint32_t w) {
+// 4 qs bytes (little endian word) -> 8 bf16 values 1 + n/16, in kmap order.
+// mask must hold 0x00780078 (in a VGPR).
+__device__ inline u32x4 dequant_unit_bf16(uint32_t w, uint32_t mask) {
   u32x4 r;
-  r.x = ((w << 6) & 0x03C003C0u) | 0x3C003C00u;
-  r.y = ((w << 2) & 0x03C003C0u) | 0x3C003C00u;
-  r.z = ((w >> 2) & 0x03C003C0u) | 0x3C003C00u;
-  r.w = ((w >> 6) & 0x03C003C0u) | 0x3C003C00u;
+  r.x = and_or(w << 3, mask, 0x3F803F80u);
+  r.y = and_or(w >> 1, mask, 0x3F803F80u);
+  r.z = and_or(w >> 5, mask, 0x3F803F80u);
+  r.w = and_or(w >> 9, mask, 0x3F803F80u);
+  return r;
+}
+
+// Same expansion as fp16 values 1 + n/16; mask must hold 0x03C003C0.
+__device__ inline u32x4 dequant_unit_f16(uint32_t w, uint32_t mask) {
+  u32x4 r;
+  r.x = and_or(w << 6, mask, 0x3C003C00u);
+  r.y = and_or(w << 2, mask, 0x3C003C00u);
+  r.z = and_or(w >> 2, mask, 0x3C003C00u);
+  r.w = and_or(w >> 6, mask, 0x3C003C00u);
+  return r;
+}
+
+// A value the compiler must keep in a VGPR (for and_or masks).
+__device__ inline uint32_t vgpr_const(uint32_t v) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "s"(v));
   return r;
 }
 

@@ -14,7 +14,6 @@ constexpr int kMaxTopK = 32;
 
 // Workspace carve-up.  Every region is 256-byte aligned.
 struct Workspace {
-  int32_t* counters = nullptr;      // [n_token_tiles + 1], zero between calls
   double* logits = nullptr;         // [T, E]
   uint16_t* xq = nullptr;           // [T, Kpad_h] bf16 bits, MFMA operand order
   float* xs = nullptr;              // [T, Kpad_h / 32] group sums of x
@@ -23,6 +22,8 @@ struct Workspace {
   int32_t* n_active = nullptr;      // [1]
   int32_t* sorted_slots = nullptr;  // [T * k]
   int32_t* slot_pos = nullptr;      // [T * k]
+  int4* desc = nullptr;             // [E + 1] {expert, begin, end, 0} per active segment
+  int32_t* seg_tok = nullptr;       // [T * k + T] token of each segment position
   uint16_t* hq = nullptr;          // [rows, Kpad_I * 2] fp16 hi/lo of h, MFMA operand order
   float* hs = nullptr;             // [rows, Kpad_I / 32, 2] half-group sums of h
   float* outbuf = nullptr;          // [T*k + T*shared, H] expert outputs, segment order
@@ -31,7 +32,7 @@ struct Workspace {
 size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared, void* base,
                       Workspace* ws);
 
-// Router tiling: tokens per workgroup tile.
+// Router tiling: tokens per logits workgroup tile.
 int router_token_tile(int64_t T);
 
 hipError_t launch_q4_repack(const uint8_t* src, int64_t rows, int64_t K, uint8_t* nib,
@@ -41,8 +42,9 @@ hipError_t launch_q4_unrepack(const uint8_t* nib, const uint16_t* scale, int64_t
 hipError_t launch_q4_dequant_f32(const uint8_t* src, int64_t n_blocks, float* out,
                                  hipStream_t stream);
 
-// Logits + top-k (+ optional MFMA-ordered copy of x and its group sums)
-// (+ optional permute), one launch.
+// Logits (+ optional MFMA-ordered copy of x and its group sums), top-k, and
+// optionally the permute: two launches for up to 16 tokens per select
+// workgroup, three beyond.
 struct RouteArgs {
   const void* x;
   int x_dtype;
@@ -84,6 +86,10 @@ struct ExpertArgs {
   const float* topk_w;
   float* y;
 };
+// The three expert stages; launch_experts runs them back to back.
+hipError_t launch_gate_up(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);
+hipError_t launch_down(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);
+hipError_t launch_combine(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);
 hipError_t launch_experts(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);
 
 }  // namespace pmoe

@@ -16,14 +16,18 @@
 // trades the other half with lane l ^ s, which yields exactly the tree above
 // while spending one shuffle-add per pair per lane in total.
 //
-// Top-k: the last workgroup to finish a token tile (atomic ticket after a
-// device-scope fence) selects for those tokens, one wave per token: k rounds
-// of a wave-wide arg-max over (logit desc, index asc).  The last token tile to
-// finish then runs the permute in one workgroup: per-wave expert counts,
-// an (expert, wave)-major exclusive scan, and a second pass that places every
-// slot at base + rank-within-round, where the rank comes from ballots over the
-// bits of the expert id.  Placement depends only on slot order, never on
-// atomics, so the permutation is deterministic and stable.
+// Launches.  route_logits_kernel computes logits (and the MFMA-ordered copy
+// of x) with no inter-workgroup communication.  route_select_kernel gives one
+// wave per token: k rounds of a wave-wide arg-max over (logit desc, index
+// asc), then the weights.  When the whole batch fits one workgroup (decode),
+// the same workgroup then runs the permute; otherwise permute_kernel does.
+// No device-scope fences anywhere: on a multi-XCD part an agent-scope release
+// writes back the XCD's L2, which costs microseconds per workgroup.
+// Permute: per-wave expert counts, an (expert, wave)-major exclusive scan, and
+// a second pass that places every slot at base + rank-within-round, where the
+// rank comes from ballots over the bits of the expert id.  Placement depends
+// only on slot order, never on atomics, so the permutation is deterministic
+// and stable.
 #include <float.h>
 #include <math.h>
 
@@ -41,8 +45,6 @@ struct RouteK {
   int32_t* topk_idx;
   float* topk_w;
   double* logits;
-  int32_t* counters;
-  int n_ttiles;
   // x preparation
   uint16_t* xq;
   float* xs;
@@ -57,6 +59,8 @@ struct RouteK {
   int32_t* n_active;
   int32_t* sorted_slots;
   int32_t* slot_pos;
+  int4* desc;        // [E + 1] {expert, begin, end, 0} per active segment, or null
+  int32_t* seg_tok;  // [T*k + T] token of each segment position, or null
 };
 
 __device__ inline bool ranks_before(double va, int ia, double vb, int ib) {
@@ -120,23 +124,31 @@ __device__ inline uint64_t match_expert(int e, bool valid, int nbits) {
   return m;
 }
 
-// Stable counting sort of n slots by expert, one workgroup of 256 threads.
-__device__ void block_permute(const int32_t* __restrict__ idx, int64_t n, int E, int64_t T,
+// Stable counting sort of n slots by expert, one workgroup of up to 1024
+// threads (NW = blockDim / 64 waves).
+//
+// Besides offsets / sorted_slots / slot_pos it can emit, for the expert
+// kernels, one descriptor {expert, begin, end} per active segment (the shared
+// expert last, covering positions [T*k, T*k + T)) and the token of every
+// segment position.
+__device__ void block_permute(const int32_t* __restrict__ idx, int64_t n, int k, int E, int64_t T,
                               int has_shared, int32_t* offsets, int32_t* offsets_user,
                               int32_t* active, int32_t* n_active, int32_t* sorted_slots,
-                              int32_t* slot_pos) {
-  __shared__ int s_cnt[4][kMaxExperts];
-  __shared__ int s_tmp[8];
+                              int32_t* slot_pos, int4* desc, int32_t* seg_tok) {
+  constexpr int kMaxWaves = 16;
+  __shared__ int s_cnt[kMaxWaves][kMaxExperts];
+  __shared__ int s_tmp[kMaxWaves];
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int w = tid / kWave;
+  const int NW = blockDim.x / kWave;
   int nbits = 1;
   while ((1 << nbits) < E) ++nbits;
 
-  for (int i = tid; i < 4 * kMaxExperts; i += blockDim.x) (&s_cnt[0][0])[i] = 0;
+  for (int i = tid; i < NW * kMaxExperts; i += blockDim.x) s_cnt[i / kMaxExperts][i % kMaxExperts] = 0;
   __syncthreads();
 
-  const int64_t chunk = round_up(ceil_div(n, 4), kWave);
+  const int64_t chunk = round_up(ceil_div(n, NW), kWave);
   const int64_t beg = w * chunk;
   const int64_t end = (beg + chunk < n) ? beg + chunk : n;
 
@@ -153,41 +165,63 @@ __device__ void block_permute(const int32_t* __restrict__ idx, int64_t n, int E,
   }
   __syncthreads();
 
-  // Scan: each thread owns experts 2*tid and 2*tid+1 (E <= 512).
-  int tot2[2], act2[2];
-  for (int i = 0; i < 2; ++i) {
-    const int e = 2 * tid + i;
+  // Scan over experts: thread t owns experts t, t + blockDim, ... (at most
+  // kMaxExperts / 256 = 2 per thread for 256 threads).
+  constexpr int kPer = kMaxExperts / 256;
+  int tot[kPer], act[kPer];
+  int my_tot = 0, my_act = 0;
+  for (int i = 0; i < kPer; ++i) {
+    const int e = tid * kPer + i;
     int t = 0;
-    if (e < E) t = s_cnt[0][e] + s_cnt[1][e] + s_cnt[2][e] + s_cnt[3][e];
-    tot2[i] = t;
-    act2[i] = (t > 0) ? 1 : 0;
+    if (e < E && tid * kPer < kMaxExperts) {
+      for (int ww = 0; ww < NW; ++ww) t += s_cnt[ww][e];
+    }
+    tot[i] = t;
+    act[i] = (t > 0) ? 1 : 0;
+    my_tot += t;
+    my_act += act[i];
   }
   int total = 0, total_act = 0;
-  const int ex = block_exclusive_scan(tot2[0] + tot2[1], s_tmp, &total);
-  const int ax = block_exclusive_scan(act2[0] + act2[1], s_tmp, &total_act);
+  const int ex = block_exclusive_scan(my_tot, s_tmp, &total);
+  const int ax = block_exclusive_scan(my_act, s_tmp, &total_act);
   int run = ex, arun = ax;
-  for (int i = 0; i < 2; ++i) {
-    const int e = 2 * tid + i;
+  for (int i = 0; i < kPer; ++i) {
+    const int e = tid * kPer + i;
     if (e < E) {
       offsets[e] = run;
       if (offsets_user) offsets_user[e] = run;
-      if (act2[i]) active[arun] = e;
+      if (act[i]) {
+        active[arun] = e;
+        if (desc) desc[arun] = make_int4(e, run, run + tot[i], 0);
+      }
       int b = run;
-      for (int ww = 0; ww < 4; ++ww) {
+      for (int ww = 0; ww < NW; ++ww) {
         const int c = s_cnt[ww][e];
         s_cnt[ww][e] = b;  // becomes the running base of (expert, wave)
         b += c;
       }
     }
-    run += tot2[i];
-    arun += act2[i];
+    run += tot[i];
+    arun += act[i];
   }
   if (tid == 0) {
     offsets[E] = total;
     if (offsets_user) offsets_user[E] = total;
     offsets[E + 1] = total + (has_shared ? (int)T : 0);
-    if (has_shared) active[total_act] = E;
+    if (has_shared) {
+      active[total_act] = E;
+      if (desc) desc[total_act] = make_int4(E, total, total + (int)T, 0);
+    }
     *n_active = total_act + (has_shared ? 1 : 0);
+  }
+  if (has_shared && seg_tok) {
+    for (int64_t t = tid; t < T; t += blockDim.x) seg_tok[n + t] = (int32_t)t;
+  }
+  if (desc) {
+    // unused slots up to the launch bound min(E, n) + shared carry expert -1
+    const int n_act = total_act + (has_shared ? 1 : 0);
+    const int max_active = (int)((n < E) ? n : E) + (has_shared ? 1 : 0);
+    for (int u = n_act + tid; u < max_active; u += blockDim.x) desc[u] = make_int4(-1, 0, 0, 0);
   }
   __syncthreads();
 
@@ -202,6 +236,7 @@ __device__ void block_permute(const int32_t* __restrict__ idx, int64_t n, int E,
       const int pos = s_cnt[w][e] + __popcll(below);
       sorted_slots[pos] = (int32_t)s;
       slot_pos[s] = pos;
+      if (seg_tok) seg_tok[pos] = (int32_t)(s / k);
       // Every lane of the group has read the base before the leader bumps
       // it: LDS operations of one wave complete in program order, and the
       // read above precedes this write in every lane's program.
@@ -212,96 +247,110 @@ __device__ void block_permute(const int32_t* __restrict__ idx, int64_t n, int E,
   }
 }
 
-// Wave-wide top-k for token t (called by all 64 lanes of one wave).
-__device__ void wave_topk(const RouteK& a, int64_t t, double* s_vals, int* s_idx, double* s_e) {
+// Order-preserving integer key of a logit: a > b (as numbers) iff
+// key(a) > key(b), -0.0 and +0.0 share a key, and NaN maps to 0, below every
+// number, so equal keys are exactly the ties the oracle breaks by index.
+__device__ inline uint64_t logit_key(double v) {
+  if (isnan(v)) return 0ull;
+  if (v == 0.0) v = 0.0;  // -0.0 -> +0.0
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
+}
+
+// Top-k of one token by rank counting (called by all 64 lanes of one wave).
+// The token's E keys sit in LDS; lane l ranks experts l, l + 64, ...:
+// rank(e) = #{e' : key(e') > key(e) or (key(e') == key(e) and e' < e)}, which
+// is e's position in (value desc, index asc) order.  Experts of rank < k are
+// written straight to their slot.  No cross-lane dependency chains: each
+// comparison reads a broadcast LDS word.
+template <int NV>
+__device__ void wave_topk(const RouteK& a, int64_t t, uint64_t* s_key, double* s_val, int* s_idx,
+                          double* s_e) {
   const int lane = threadIdx.x % kWave;
-  constexpr int NV = kMaxExperts / kWave;
-  double val[NV];
+  for (int e = lane; e < a.E; e += kWave) s_key[e] = logit_key(a.logits[t * a.E + e]);
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  uint64_t mine[NV];
+  int rank[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int e = lane + kWave * v;
-    val[v] = (e < a.E) ? a.logits[t * a.E + e] : 0.0;
+    mine[v] = e < a.E ? s_key[e] : 0ull;
+    rank[v] = 0;
   }
-  uint32_t taken = 0;
-  for (int j = 0; j < a.k; ++j) {
-    double bv = __builtin_nan("");
-    int bi = 0x7fffffff;
+  for (int e2 = 0; e2 < a.E; ++e2) {
+    const uint64_t k2 = s_key[e2];
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int e = lane + kWave * v;
-      if (e < a.E && !((taken >> v) & 1u) && ranks_before(val[v], e, bv, bi)) {
-        bv = val[v];
-        bi = e;
-      }
-    }
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) {
-      const double ov = shfl_xor_f64(bv, s);
-      const int oi = __shfl_xor(bi, s, kWave);
-      if (ranks_before(ov, oi, bv, bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if (bi != 0x7fffffff && (bi % kWave) == lane) taken |= 1u << (bi / kWave);
-    if (lane == 0) {
-      s_vals[j] = bv;
-      s_idx[j] = bi;
+      rank[v] += (k2 > mine[v] || (k2 == mine[v] && e2 < e)) ? 1 : 0;
     }
   }
-  // Weights: lane j (< k) owns slot j; every lane sums the k terms in slot
-  // order from LDS, so the normaliser is the same sequential fp64 sum as the
-  // oracle's.
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int e = lane + kWave * v;
+    if (e < a.E && rank[v] < a.k) {
+      s_idx[rank[v]] = e;
+      s_val[rank[v]] = a.logits[t * a.E + e];
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  // Weights: lane i (< k) owns slot i; every lane sums the k terms in slot
+  // order, so the normaliser is the same sequential fp64 sum as the oracle's.
   double ej = 0.0;
   if (lane < a.k) {
-    const double v = s_vals[lane];
-    ej = (a.score_mode == 0) ? exp(v - s_vals[0]) : 1.0 / (1.0 + exp(-v));
+    const double v = s_val[lane];
+    ej = (a.score_mode == 0) ? exp(v - s_val[0]) : 1.0 / (1.0 + exp(-v));
     s_e[lane] = ej;
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   if (lane < a.k) {
     double sum = 0.0;
-    for (int j = 0; j < a.k; ++j) sum += s_e[j];
+    for (int i = 0; i < a.k; ++i) sum += s_e[i];
     a.topk_idx[t * a.k + lane] = s_idx[lane];
     a.topk_w[t * a.k + lane] = (float)(ej / sum);
   }
+  __builtin_amdgcn_wave_barrier();
 }
 
 // MFMA-ordered copy of x (bf16) and fp32 group sums for tokens [t0, t0+TT).
+// Layout [t][q][p][gi][8]: one 16-byte chunk per (token, quad, part, group).
 __device__ void prep_x_tile(const RouteK& a, int64_t t0, int TT) {
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
-  const int64_t Kg = a.H / kGroup;
-  const int64_t chunks = (int64_t)TT * a.Kq * 16;  // (t, q, p, gi) -> 8 bf16
-  for (int64_t i = threadIdx.x; i < chunks; i += blockDim.x) {
-    const int gi = (int)(i % 4);
-    const int p = (int)((i / 4) % 4);
-    const int64_t q = (i / 16) % a.Kq;
-    const int64_t t = t0 + i / (16 * a.Kq);
-    if (t >= a.T) continue;
-    const int64_t g = 4 * q + gi;
-    uint32_t wds[4] = {0, 0, 0, 0};
-    if (g < Kg) {
-      const uint16_t* xr = x + t * a.H + g * kGroup;
-      for (int j = 0; j < 8; j += 2) {
-        wds[j / 2] = (uint32_t)xr[kmap(p, j)] | ((uint32_t)xr[kmap(p, j + 1)] << 16);
+  const int Kg = (int)(a.H / kGroup);
+  const int per_tok = (int)a.Kq * 16;
+  for (int ti = 0; ti < TT; ++ti) {
+    const int64_t t = t0 + ti;
+    if (t >= a.T) break;
+    const uint16_t* xt = x + t * a.H;
+    for (int c = threadIdx.x; c < per_tok; c += blockDim.x) {
+      const int gi = c & 3;
+      const int p = (c >> 2) & 3;
+      const int q = c >> 4;
+      const int g = 4 * q + gi;
+      uint32_t wds[4] = {0, 0, 0, 0};
+      if (g < Kg) {
+        const uint16_t* xr = xt + g * kGroup;
+        for (int j = 0; j < 8; j += 2) wds[j / 2] = (uint32_t)xr[kmap(p, j)] | ((uint32_t)xr[kmap(p, j + 1)] << 16);
       }
+      u32x4 v = {wds[0], wds[1], wds[2], wds[3]};
+      *reinterpret_cast<u32x4*>(a.xq + (t * a.Kq * 16 + c) * 8) = v;
     }
-    u32x4 v = {wds[0], wds[1], wds[2], wds[3]};
-    // layout [t][q][p][gi][8]
-    *reinterpret_cast<u32x4*>(a.xq + ((t * a.Kq + q) * 16 + p * 4 + gi) * 8) = v;
-  }
-  const int64_t ng = a.Kq * 4;
-  for (int64_t i = threadIdx.x; i < (int64_t)TT * ng; i += blockDim.x) {
-    const int64_t t = t0 + i / ng;
-    const int64_t g = i % ng;
-    if (t >= a.T) continue;
-    float s = 0.0f;
-    if (g < Kg) {
-      const uint16_t* xr = x + t * a.H + g * kGroup;
-      for (int j = 0; j < kGroup; ++j) s += bf16_bits_to_float(xr[j]);
+    const int ng = (int)a.Kq * 4;
+    for (int g = threadIdx.x; g < ng; g += blockDim.x) {
+      float sum = 0.0f;
+      if (g < Kg) {
+        const uint32_t* xr = reinterpret_cast<const uint32_t*>(xt + g * kGroup);
+        for (int j = 0; j < kGroup / 2; ++j) {
+          const uint32_t two = xr[j];
+          sum += bf16_bits_to_float(two & 0xffffu);
+          sum += bf16_bits_to_float(two >> 16);
+        }
+      }
+      a.xs[t * ng + g] = sum;
     }
-    a.xs[t * ng + g] = s;
   }
 }
 
@@ -345,8 +394,8 @@ __device__ inline int tree_pair_of_lane(int lane) {
   return pair;
 }
 
-template <typename XT, int TT, int EW>
-__global__ __launch_bounds__(256) void route_kernel(RouteK a) {
+template <typename XT, int TT, int EW, int CB>
+__global__ __launch_bounds__(256) void route_logits_kernel(RouteK a) {
   constexpr int P = TT * EW;
   static_assert((P & (P - 1)) == 0 && P <= 64, "pairs per wave must be a power of two <= 64");
   const int lane = threadIdx.x % kWave;
@@ -359,34 +408,48 @@ __global__ __launch_bounds__(256) void route_kernel(RouteK a) {
 #pragma unroll
   for (int i = 0; i < P; ++i) acc[i] = 0.0;
 
+  // Chunks are loaded CB at a time (all loads of a batch issued before its
+  // FMAs), then accumulated in increasing h as the contract requires.
   const int64_t nchunks = ceil_div(a.H, 256);
-  for (int64_t c = 0; c < nchunks; ++c) {
-    const int64_t h0 = c * 256 + 4 * lane;
-    if (h0 < a.H) {
-      float wv[EW][4];
+  for (int64_t c0 = 0; c0 < nchunks; c0 += CB) {
+    float wv[CB][EW][4];
+    float xv[CB][TT][4];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const int64_t h0 = (c0 + cb) * 256 + 4 * lane;
+      const bool hok = (c0 + cb) < nchunks && h0 < a.H;
 #pragma unroll
       for (int ei = 0; ei < EW; ++ei) {
         const int e = e0 + ei;
-        if (e < a.E) {
+        if (hok && e < a.E) {
           const float4 r = *reinterpret_cast<const float4*>(a.W + (int64_t)e * a.H + h0);
-          wv[ei][0] = r.x;
-          wv[ei][1] = r.y;
-          wv[ei][2] = r.z;
-          wv[ei][3] = r.w;
+          wv[cb][ei][0] = r.x;
+          wv[cb][ei][1] = r.y;
+          wv[cb][ei][2] = r.z;
+          wv[cb][ei][3] = r.w;
         } else {
-          wv[ei][0] = wv[ei][1] = wv[ei][2] = wv[ei][3] = 0.0f;
+          wv[cb][ei][0] = wv[cb][ei][1] = wv[cb][ei][2] = wv[cb][ei][3] = 0.0f;
         }
       }
 #pragma unroll
       for (int ti = 0; ti < TT; ++ti) {
         const int64_t t = t0 + ti;
-        float xv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (t < a.T) load_x4<XT>(x, t * a.H + h0, xv);
+        if (hok && t < a.T) {
+          load_x4<XT>(x, t * a.H + h0, xv[cb][ti]);
+        } else {
+          xv[cb][ti][0] = xv[cb][ti][1] = xv[cb][ti][2] = xv[cb][ti][3] = 0.0f;
+        }
+      }
+    }
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+      for (int ti = 0; ti < TT; ++ti) {
 #pragma unroll
         for (int ei = 0; ei < EW; ++ei) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            acc[ti * EW + ei] += (double)xv[i] * (double)wv[ei][i];
+            acc[ti * EW + ei] += (double)xv[cb][ti][i] * (double)wv[cb][ei][i];
           }
         }
       }
@@ -411,51 +474,41 @@ __global__ __launch_bounds__(256) void route_kernel(RouteK a) {
   }
 
   if (a.prep_x && blockIdx.x == 0) prep_x_tile(a, t0, TT);
-
-  // Ticket: the last expert tile of this token tile selects its top-k.
-  __shared__ int s_last;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = atomicAdd(&a.counters[blockIdx.y], 1);
-    s_last = (prev == (int)gridDim.x - 1);
+  if (a.prep_x && blockIdx.x == 1 % gridDim.x && blockIdx.y == 0) {
+    // all-zero activation row T, read by expert lanes past a segment
+    for (int64_t i = threadIdx.x; i < a.Kq * 128; i += blockDim.x) a.xq[a.T * a.Kq * 128 + i] = 0;
+    for (int64_t i = threadIdx.x; i < a.Kq * 4; i += blockDim.x) a.xs[a.T * a.Kq * 4 + i] = 0.0f;
   }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  __shared__ double s_vals[4][kMaxTopK];
-  __shared__ double s_e[4][kMaxTopK];
-  __shared__ int s_idx[4][kMaxTopK];
-  for (int ti = w; ti < TT; ti += 4) {
-    const int64_t t = t0 + ti;
-    if (t < a.T) wave_topk(a, t, s_vals[w], s_idx[w], s_e[w]);
-  }
-  if (threadIdx.x == 0) a.counters[blockIdx.y] = 0;
-  if (!a.do_permute) return;
-
-  // Ticket: the last token tile runs the permute over all T*k slots.
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = atomicAdd(&a.counters[a.n_ttiles], 1);
-    s_last = (prev == a.n_ttiles - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  if (threadIdx.x == 0) a.counters[a.n_ttiles] = 0;
-  block_permute(a.topk_idx, a.T * a.k, a.E, a.T, a.has_shared, a.offsets, a.offsets_user, a.active,
-                a.n_active, a.sorted_slots, a.slot_pos);
 }
 
-__global__ __launch_bounds__(256) void permute_kernel(const int32_t* idx, int64_t T, int k, int E,
-                                                      int has_shared, int32_t* offsets,
-                                                      int32_t* offsets_user, int32_t* active,
-                                                      int32_t* n_active, int32_t* sorted_slots,
-                                                      int32_t* slot_pos) {
-  block_permute(idx, T * k, E, T, has_shared, offsets, offsets_user, active, n_active,
-                sorted_slots, slot_pos);
+// Top-k and weights, one wave per token (grid-stride); a launch with one
+// workgroup continues with the permute.
+constexpr int kSelectWaves = 4;
+
+template <int NV>
+__global__ __launch_bounds__(256) void route_select_kernel(RouteK a) {
+  __shared__ uint64_t s_key[kSelectWaves][kMaxExperts];
+  __shared__ double s_val[kSelectWaves][kMaxTopK];
+  __shared__ double s_e[kSelectWaves][kMaxTopK];
+  __shared__ int s_idx[kSelectWaves][kMaxTopK];
+  const int w = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  for (int64_t t = (int64_t)blockIdx.x * nw + w; t < a.T; t += (int64_t)gridDim.x * nw)
+    wave_topk<NV>(a, t, s_key[w], s_val[w], s_idx[w], s_e[w]);
+  if (!a.do_permute || gridDim.x != 1) return;
+  __syncthreads();
+  block_permute(a.topk_idx, a.T * a.k, a.k, a.E, a.T, a.has_shared, a.offsets, a.offsets_user, a.active,
+                a.n_active, a.sorted_slots, a.slot_pos, a.desc, a.seg_tok);
+}
+
+__global__ __launch_bounds__(1024) void permute_kernel(const int32_t* idx, int64_t T, int k, int E,
+                                                       int has_shared, int32_t* offsets,
+                                                       int32_t* offsets_user, int32_t* active,
+                                                       int32_t* n_active, int32_t* sorted_slots,
+                                                       int32_t* slot_pos, int4* desc,
+                                                       int32_t* seg_tok) {
+  block_permute(idx, T * k, k, E, T, has_shared, offsets, offsets_user, active, n_active,
+                sorted_slots, slot_pos, desc, seg_tok);
 }
 
 int router_token_tile(int64_t T) {
@@ -465,16 +518,16 @@ int router_token_tile(int64_t T) {
 }
 
 template <typename XT>
-static hipError_t launch_route_t(const RouteK& k, int TT, hipStream_t stream) {
+static hipError_t launch_logits_t(const RouteK& k, int TT, int n_ttiles, hipStream_t stream) {
   if (TT == 1) {
-    dim3 grid((unsigned)ceil_div(k.E, 4 * 1), (unsigned)k.n_ttiles);
-    hipLaunchKernelGGL((route_kernel<XT, 1, 1>), grid, dim3(256), 0, stream, k);
+    dim3 grid((unsigned)ceil_div(k.E, 4 * 1), (unsigned)n_ttiles);
+    hipLaunchKernelGGL((route_logits_kernel<XT, 1, 1, 8>), grid, dim3(256), 0, stream, k);
   } else if (TT == 4) {
-    dim3 grid((unsigned)ceil_div(k.E, 4 * 2), (unsigned)k.n_ttiles);
-    hipLaunchKernelGGL((route_kernel<XT, 4, 2>), grid, dim3(256), 0, stream, k);
+    dim3 grid((unsigned)ceil_div(k.E, 4 * 2), (unsigned)n_ttiles);
+    hipLaunchKernelGGL((route_logits_kernel<XT, 4, 2, 8>), grid, dim3(256), 0, stream, k);
   } else {
-    dim3 grid((unsigned)ceil_div(k.E, 4 * 4), (unsigned)k.n_ttiles);
-    hipLaunchKernelGGL((route_kernel<XT, 16, 4>), grid, dim3(256), 0, stream, k);
+    dim3 grid((unsigned)ceil_div(k.E, 4 * 4), (unsigned)n_ttiles);
+    hipLaunchKernelGGL((route_logits_kernel<XT, 16, 4, 1>), grid, dim3(256), 0, stream, k);
   }
   return hipGetLastError();
 }
@@ -492,9 +545,8 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
   k.topk_idx = r.topk_idx;
   k.topk_w = r.topk_w;
   k.logits = ws.logits;
-  k.counters = ws.counters;
   const int TT = router_token_tile(r.T);
-  k.n_ttiles = (int)ceil_div(r.T, TT);
+  const int n_ttiles = (int)ceil_div(r.T, TT);
   k.xq = ws.xq;
   k.xs = ws.xs;
   k.Kq = ceil_div(r.H, kQuad);
@@ -507,15 +559,34 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
   k.n_active = ws.n_active;
   k.sorted_slots = r.sorted_slots_out ? r.sorted_slots_out : ws.sorted_slots;
   k.slot_pos = r.slot_pos_out ? r.slot_pos_out : ws.slot_pos;
-  if (r.x_dtype == 0) return launch_route_t<uint16_t>(k, TT, stream);
-  return launch_route_t<float>(k, TT, stream);
+  k.desc = r.do_permute ? ws.desc : nullptr;
+  k.seg_tok = r.do_permute ? ws.seg_tok : nullptr;
+  hipError_t err = (r.x_dtype == 0) ? launch_logits_t<uint16_t>(k, TT, n_ttiles, stream)
+                                    : launch_logits_t<float>(k, TT, n_ttiles, stream);
+  if (err != hipSuccess) return err;
+  // One wave per token, four tokens per workgroup, so selection is spread
+  // over many CUs; the permute then runs in its own single-workgroup launch.
+  // A batch of at most four tokens is routed and permuted by one workgroup.
+  const unsigned sel_blocks = (unsigned)ceil_div(r.T, kSelectWaves);
+  const dim3 sb(kWave * kSelectWaves);
+  if (r.E <= 64) hipLaunchKernelGGL(route_select_kernel<1>, dim3(sel_blocks), sb, 0, stream, k);
+  else if (r.E <= 128) hipLaunchKernelGGL(route_select_kernel<2>, dim3(sel_blocks), sb, 0, stream, k);
+  else if (r.E <= 256) hipLaunchKernelGGL(route_select_kernel<4>, dim3(sel_blocks), sb, 0, stream, k);
+  else hipLaunchKernelGGL(route_select_kernel<8>, dim3(sel_blocks), sb, 0, stream, k);
+  err = hipGetLastError();
+  if (err != hipSuccess || !r.do_permute || sel_blocks == 1) return err;
+  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, k.topk_idx, r.T, r.k, r.E,
+                     r.has_shared, ws.offsets, r.offsets_out, ws.active, ws.n_active, k.sorted_slots,
+                     k.slot_pos, k.desc, k.seg_tok);
+  return hipGetLastError();
 }
 
 hipError_t launch_permute(const int32_t* topk_idx, int64_t T, int k, int E, int has_shared,
                           int32_t* offsets, int32_t* sorted_slots, int32_t* slot_pos,
                           const Workspace& ws, hipStream_t stream) {
-  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(256), 0, stream, topk_idx, T, k, E, has_shared,
-                     ws.offsets, offsets, ws.active, ws.n_active, sorted_slots, slot_pos);
+  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, topk_idx, T, k, E, has_shared,
+                     ws.offsets, offsets, ws.active, ws.n_active, sorted_slots, slot_pos,
+                     static_cast<int4*>(nullptr), static_cast<int32_t*>(nullptr));
   return hipGetLastError();
 }
 

@@ -11,12 +11,13 @@ Python surface over libphantom_moe.so (C ABI in include/phantom_moe.h):
 """
 from . import q4_0, synth
 from ._lib import PhantomMoEError
-from .ops import MoEWeights, moe_forward, permute, route
+from .ops import MoEWeights, PreparedForward, moe_forward, permute, route
 from .router import PhantomTopKRouter
 
 __all__ = [
     "PhantomTopKRouter",
     "MoEWeights",
+    "PreparedForward",
     "moe_forward",
     "route",
     "permute",

@@ -43,17 +43,16 @@ def _need_cuda(t: torch.Tensor, what: str) -> None:
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zero-filled workspace of at least nbytes for (device, current stream).
+    """Workspace of at least nbytes for (device, current stream).
 
-    Cached per (device, stream); grows when a larger one is asked for.  The
-    library keeps its counters at zero between calls, so a cached workspace
-    stays valid."""
+    Cached per (device, stream) so calls on one stream reuse it in order;
+    grows when a larger one is asked for.  It carries no state between calls."""
     stream = _lib.stream_handle(device)
     key = (device.index, stream)
     with _ws_lock:
         ws = _workspaces.get(key)
         if ws is None or ws.numel() < nbytes:
-            ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+            ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
             _workspaces[key] = ws
         return ws
 
@@ -210,3 +209,56 @@ def moe_forward(x: torch.Tensor, router_weight: torch.Tensor, experts: MoEWeight
     if return_routing:
         return y, w.reshape(*lead, top_k), idx.reshape(*lead, top_k)
     return y
+
+
+class PreparedForward:
+    """A ``moe_forward`` call with every pointer bound once.
+
+    For decode loops that call one layer repeatedly on fixed buffers: the
+    caller writes tokens into ``self.x`` and calls the object, which issues
+    the layer on the current stream of the device with one C call and no
+    allocation.  Outputs land in ``self.y`` (fp32 [T, H]), ``self.topk_w`` and
+    ``self.topk_idx``."""
+
+    def __init__(self, experts: MoEWeights, router_weight: torch.Tensor, T: int, top_k: int, score="softmax",
+                 router_bias=None, x: torch.Tensor | None = None):
+        import ctypes
+
+        dev = experts.device
+        H, I, E = experts.H, experts.I, experts.E
+        self.experts = experts
+        self.router_weight = router_weight.detach().to(device=dev, dtype=torch.float32).contiguous()
+        if tuple(self.router_weight.shape) != (E, H):
+            raise ValueError(f"router_weight must be [{E}, {H}]")
+        self.router_bias = None
+        if router_bias is not None:
+            self.router_bias = router_bias.detach().to(device=dev, dtype=torch.float32).contiguous()
+        self.x = x if x is not None else torch.zeros((T, H), dtype=torch.bfloat16, device=dev)
+        if self.x.dtype != torch.bfloat16 or tuple(self.x.shape) != (T, H) or not self.x.is_contiguous():
+            raise ValueError("x must be a contiguous bf16 [T, H] tensor")
+        self.y = torch.empty((T, H), dtype=torch.float32, device=dev)
+        self.topk_idx = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+        self.topk_w = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+        lib = _lib.load()
+        has_sh = experts.shared is not None
+        nbytes = lib.phantom_moe_workspace_bytes(T, H, I, E, top_k, int(has_sh))
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        sh = [t.data_ptr() for t in experts.shared] if has_sh else [None] * 6
+        self._fn = lib.phantom_moe_forward
+        self._args = [
+            self.x.data_ptr(), 0, T, H, I, E, top_k, _score_mode(score), self.router_weight.data_ptr(),
+            None if self.router_bias is None else self.router_bias.data_ptr(),
+            experts.gate_nib.data_ptr(), experts.gate_scale.data_ptr(), experts.up_nib.data_ptr(),
+            experts.up_scale.data_ptr(), experts.down_nib.data_ptr(), experts.down_scale.data_ptr(),
+            *sh, self.y.data_ptr(), self.topk_idx.data_ptr(), self.topk_w.data_ptr(),
+            self.workspace.data_ptr(), nbytes,
+        ]
+        self.device = dev
+        self._ctypes = ctypes
+
+    def __call__(self, stream: int | None = None) -> torch.Tensor:
+        s = _lib.stream_handle(self.device) if stream is None else stream
+        rc = self._fn(*self._args, s)
+        if rc:
+            _lib.check(rc, "phantom_moe_forward")
+        return self.y

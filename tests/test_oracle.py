@@ -332,3 +332,22 @@ def test_layer_token_subset_is_a_restriction():
     ys, idxs, ws = oracle.moe_forward(xb, L.router_w, L.gate, L.up, L.down, cfg.k, tokens=sub)
     np.testing.assert_array_equal(ys, y[sub])
     np.testing.assert_array_equal(idxs, idx[sub])
+
+
+def test_reference_cpu_path_port_agrees_with_oracle():
+    """oracle/ref_cpu_path.py (the timed CPU baseline) computes the same layer
+    up to its bf16 weight/matmul rounding."""
+    import torch
+
+    from oracle.ref_cpu_path import RefCPUMoE
+
+    cfg = synth.MoEConfig("t", H=256, I=128, E=16, k=4, T=12, zipf=1.1)
+    L = synth.host_layer(cfg)
+    xb = synth.activations(cfg.T, cfg.H)
+    y, idx, _ = oracle.moe_forward(xb, L.router_w, L.gate, L.up, L.down, cfg.k, 0, L.router_bias)
+    for pre in (False, True):
+        ref = RefCPUMoE(L.router_w, L.gate, L.up, L.down, cfg.H, cfg.I, cfg.k, "softmax", L.router_bias,
+                        predequant=pre)
+        yc = ref(torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16)).numpy()
+        rel = np.linalg.norm(yc - y) / np.linalg.norm(y)
+        assert rel < 2e-2, rel
