@@ -97,6 +97,7 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
   const size_t o_hq = take(sizeof(uint16_t) * (size_t)((rows + 1) * KpadI * 2));
   const size_t o_hs = take(sizeof(float) * (size_t)((rows + 1) * (KpadI / kGroup) * 2));
   const size_t o_out = take(sizeof(float) * (size_t)(rows * (I > 0 ? H : 0)));
+  const size_t o_cnt = take(sizeof(int32_t));
   if (ws && base) {
     char* b = static_cast<char*>(base);
     ws->logits = reinterpret_cast<double*>(b + o_log);
@@ -112,6 +113,7 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
     ws->hq = reinterpret_cast<uint16_t*>(b + o_hq);
     ws->hs = reinterpret_cast<float*>(b + o_hs);
     ws->outbuf = reinterpret_cast<float*>(b + o_out);
+    ws->counter = reinterpret_cast<int32_t*>(b + o_cnt);
   }
   return off;
 }

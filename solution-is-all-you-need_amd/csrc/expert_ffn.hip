@@ -101,17 +101,21 @@ __device__ inline int load_descriptors(const SegSrc& seg, int4* s_desc, int* s_n
 
 // ------------------------------------------------------------------ gate/up
 
-// Workgroup = (RT row tiles of one active expert) x (all of K).  Wave ks of
-// the ksplit waves takes quads ks, ks + ksplit, ... (NQ of them), issues all
-// their loads at once, and contributes a partial tile; partials are summed in
-// LDS in wave order.  The weight loads depend only on the segment descriptor
-// (one uniform load), the activation loads on one token-id load.
-// One item: RT row tiles starting at rt0 of the segment described by d.
-// Token tiles are taken TP at a time: each dequantised weight operand feeds
-// TP MFMAs, so the nibble expansion is paid once per 32 tokens.
-template <int RT, int NQ, int TP>
+// Workgroups of up to kGateUpWaves waves loop over items (active expert,
+// 16-row tile of I).  Wave ks of the ksplit waves takes quads ks,
+// ks + ksplit, ... of K in chunks of NQ, issuing all loads of a chunk at once,
+// and contributes a partial tile; partials are summed in LDS in wave order,
+// so results do not depend on timing.  The weight addresses depend only on
+// the descriptor (wave-uniform), the activation addresses on one token id.
+constexpr int kGateUpWaves = 8;
+
+// One 16-row tile, token tiles [m0, m0 + 16 TP) of the segment ending at
+// seg_end.  Token tiles are taken TP at a time: each dequantised weight
+// operand feeds TP MFMAs, so the nibble expansion is paid once per 16 TP
+// tokens.
+template <int NQ, int TP>
 __device__ inline void gate_up_pass(const GateUpK& a, const int e, const int64_t seg_end, const int64_t m0,
-                                    const int64_t rt0, float (*red)[2][2][16][16]) {
+                                    const int64_t rt, float (*red)[1][2][16][16]) {
   const int lane = threadIdx.x % kWave;
   const int ks = threadIdx.x / kWave;
   const int ksplit = blockDim.x / kWave;
@@ -132,15 +136,17 @@ __device__ inline void gate_up_pass(const GateUpK& a, const int e, const int64_t
     xoff[t] = (uint32_t)(tok * a.Kq);
   }
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-  f32x4 ag[TP][RT], au[TP][RT], cg[TP][RT], cu[TP][RT];
+  f32x4 ag[TP], au[TP], cg[TP], cu[TP];
 #pragma unroll
-  for (int t = 0; t < TP; ++t)
-#pragma unroll
-    for (int r = 0; r < RT; ++r) ag[t][r] = au[t][r] = cg[t][r] = cu[t][r] = z;
-  // quads ks, ks + ksplit, ... in chunks of NQ (one chunk for K <= 16 * NQ quads)
+  for (int t = 0; t < TP; ++t) ag[t] = au[t] = cg[t] = cu[t] = z;
+  // Each chunk of NQ quads is summed on its own and then added to the
+  // running totals, which keeps the fp32 chains short for long K.
   for (int64_t q0 = ks; q0 < a.Kq; q0 += (int64_t)NQ * ksplit) {
-    u32x4 gw[NQ][RT], uw[NQ][RT];
-    uint2 gs[NQ][RT], us[NQ][RT];
+    f32x4 pg[TP], pu[TP];
+#pragma unroll
+    for (int t = 0; t < TP; ++t) pg[t] = pu[t] = z;
+    u32x4 gw[NQ], uw[NQ];
+    uint2 gs[NQ], us[NQ];
     u32x4 xa[NQ][TP][4];
     float sx[NQ][TP];
     bool qok[NQ];
@@ -149,16 +155,11 @@ __device__ inline void gate_up_pass(const GateUpK& a, const int e, const int64_t
       int q = (int)(q0 + (int64_t)i * ksplit);
       qok[i] = q < a.Kq;
       q = qok[i] ? q : (int)a.Kq - 1;
-#pragma unroll
-      for (int r = 0; r < RT; ++r) {
-        const int64_t tq = (rt0 + r) * a.Kq + q;  // wave-uniform
-        const uint8_t* gb = gnib + tq * kQuadNibBytes;
-        const uint8_t* ub = unib + tq * kQuadNibBytes;
-        gw[i][r] = *reinterpret_cast<const u32x4*>(gb + lane * 16);
-        uw[i][r] = *reinterpret_cast<const u32x4*>(ub + lane * 16);
-        gs[i][r] = *reinterpret_cast<const uint2*>(gsc + tq * kQuadScales + n * 4);
-        us[i][r] = *reinterpret_cast<const uint2*>(usc + tq * kQuadScales + n * 4);
-      }
+      const int64_t tq = rt * a.Kq + q;  // wave-uniform
+      gw[i] = *reinterpret_cast<const u32x4*>(gnib + tq * kQuadNibBytes + lane * 16);
+      uw[i] = *reinterpret_cast<const u32x4*>(unib + tq * kQuadNibBytes + lane * 16);
+      gs[i] = *reinterpret_cast<const uint2*>(gsc + tq * kQuadScales + n * 4);
+      us[i] = *reinterpret_cast<const uint2*>(usc + tq * kQuadScales + n * 4);
 #pragma unroll
       for (int t = 0; t < TP; ++t) {
         const u32x4* xp =
@@ -171,56 +172,53 @@ __device__ inline void gate_up_pass(const GateUpK& a, const int e, const int64_t
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       if (!qok[i]) continue;
+      float dg[4], du[4];
+      unpack_scales(gs[i], dg);
+      unpack_scales(us[i], du);
+      const uint32_t gwv[4] = {gw[i].x, gw[i].y, gw[i].z, gw[i].w};
+      const uint32_t uwv[4] = {uw[i].x, uw[i].y, uw[i].z, uw[i].w};
 #pragma unroll
-      for (int r = 0; r < RT; ++r) {
-        float dg[4], du[4];
-        unpack_scales(gs[i][r], dg);
-        unpack_scales(us[i][r], du);
-        const uint32_t gwv[4] = {gw[i][r].x, gw[i][r].y, gw[i][r].z, gw[i][r].w};
-        const uint32_t uwv[4] = {uw[i][r].x, uw[i][r].y, uw[i][r].z, uw[i][r].w};
-#pragma unroll
-        for (int gi = 0; gi < 4; ++gi) {
-          const u32x4 bg = dequant_unit_bf16(gwv[gi], mask);
-          const u32x4 bu = dequant_unit_bf16(uwv[gi], mask);
-#pragma unroll
-          for (int t = 0; t < TP; ++t) {
-            ag[t][r] += dg[gi] * mfma_bf16_16x16x32(xa[i][t][gi], bg, z);
-            au[t][r] += du[gi] * mfma_bf16_16x16x32(xa[i][t][gi], bu, z);
-          }
-        }
+      for (int gi = 0; gi < 4; ++gi) {
+        const u32x4 bg = dequant_unit_bf16(gwv[gi], mask);
+        const u32x4 bu = dequant_unit_bf16(uwv[gi], mask);
 #pragma unroll
         for (int t = 0; t < TP; ++t) {
-          cg[t][r] = mfma_f32_16x16x4(sx[i][t], dg[p], cg[t][r]);
-          cu[t][r] = mfma_f32_16x16x4(sx[i][t], du[p], cu[t][r]);
+          pg[t] += dg[gi] * mfma_bf16_16x16x32(xa[i][t][gi], bg, z);
+          pu[t] += du[gi] * mfma_bf16_16x16x32(xa[i][t][gi], bu, z);
         }
       }
+#pragma unroll
+      for (int t = 0; t < TP; ++t) {
+        cg[t] = mfma_f32_16x16x4(sx[i][t], dg[p], cg[t]);
+        cu[t] = mfma_f32_16x16x4(sx[i][t], du[p], cu[t]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TP; ++t) {
+      ag[t] += pg[t];
+      au[t] += pu[t];
     }
   }
 #pragma unroll
   for (int t = 0; t < TP; ++t) {
+    // sum_g d * sum_k a (n - 8) = 16 * sum_g d P - 24 * sum_g d S
+    const f32x4 rg = kUnitScale * ag[t] - kUnitBias * cg[t];
+    const f32x4 ru = kUnitScale * au[t] - kUnitBias * cu[t];
 #pragma unroll
-    for (int r = 0; r < RT; ++r) {
-      // sum_g d * sum_k a (n - 8) = 16 * sum_g d P - 24 * sum_g d S
-      const f32x4 rg = kUnitScale * ag[t][r] - kUnitBias * cg[t][r];
-      const f32x4 ru = kUnitScale * au[t][r] - kUnitBias * cu[t][r];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        red[ks][t * RT + r][0][4 * p + j][n] = rg[j];
-        red[ks][t * RT + r][1][4 * p + j][n] = ru[j];
-      }
+    for (int j = 0; j < 4; ++j) {
+      red[ks][t][0][4 * p + j][n] = rg[j];
+      red[ks][t][1][4 * p + j][n] = ru[j];
     }
   }
   __syncthreads();
-  for (int o = threadIdx.x; o < TP * RT * 256; o += blockDim.x) {
-    const int tr = o / 256;
-    const int t = tr / RT;
-    const int r = tr % RT;
+  for (int o = threadIdx.x; o < TP * 256; o += blockDim.x) {
+    const int t = o / 256;
     const int mm = (o % 256) / 16;
     const int nn = o % 16;
     float g = 0.0f, uu = 0.0f;
     for (int s2 = 0; s2 < ksplit; ++s2) {
-      g += red[s2][tr][0][mm][nn];
-      uu += red[s2][tr][1][mm][nn];
+      g += red[s2][t][0][mm][nn];
+      uu += red[s2][t][1][mm][nn];
     }
     const float h = g * (1.0f / (1.0f + expf(-g))) * uu;
     // fp16 pair hi + lo of h, placed where the down kernel's MFMA operand
@@ -231,7 +229,7 @@ __device__ inline void gate_up_pass(const GateUpK& a, const int e, const int64_t
     const float lf = half_bits_to_float32(lb);
     const int64_t pos = m0 + 16 * t + mm;
     const bool ok = pos < seg_end;
-    const int64_t i = (rt0 + r) * 16 + nn;
+    const int64_t i = rt * 16 + nn;
     const int64_t g32 = i / kGroup;
     const int cc = (int)(i % kGroup);
     const int half = cc / 16;
@@ -256,52 +254,52 @@ __device__ inline void gate_up_pass(const GateUpK& a, const int e, const int64_t
   __syncthreads();
 }
 
-template <int RT, int NQ>
-__device__ inline void gate_up_item(const GateUpK& a, const int4 d, const int64_t rt0,
-                                    float (*red)[2][2][16][16]) {
+template <int NQ>
+__device__ inline void gate_up_item(const GateUpK& a, const int4 d, const int64_t rt,
+                                    float (*red)[1][2][16][16]) {
   const int e = __builtin_amdgcn_readfirstlane(d.x);
   const int64_t beg = __builtin_amdgcn_readfirstlane(d.y);
   const int64_t end = __builtin_amdgcn_readfirstlane(d.z);
-  int64_t m0 = beg;
-  for (; m0 + 16 < end; m0 += 32) gate_up_pass<RT, NQ, 2>(a, e, end, m0, rt0, red);
-  if (m0 < end) gate_up_pass<RT, NQ, 1>(a, e, end, m0, rt0, red);
+  // One 16-token tile at a time: a longer segment re-reads the tile's
+  // weights from L2, which costs less than the registers of a paired pass.
+  for (int64_t m0 = beg; m0 < end; m0 += 16) gate_up_pass<NQ, 1>(a, e, end, m0, rt, red);
 }
 
-template <int RT, int NQ>
-__global__ __launch_bounds__(1024) void gate_up_kernel(GateUpK a) {
-  __shared__ float red[16][2][2][16][16];  // [wave][token tile * RT + row tile][gate/up]
+template <int NQ>
+__global__ __launch_bounds__(kGateUpWaves * kWave, 4) void gate_up_kernel(GateUpK a) {
+  __shared__ float red[kGateUpWaves][1][2][16][16];  // [wave][token tile][gate/up]
   __shared__ int4 s_desc[kMaxExperts + 1];
   __shared__ int s_nact;
-  const int lane = threadIdx.x % kWave;
-  const int ks = threadIdx.x / kWave;
-  const int ksplit = blockDim.x / kWave;
-  const int n = lane % 16;
-  const int p = lane / 16;
   if (blockIdx.x == 0) {
     // the all-zero down-operand row read for positions past a segment
     for (int64_t i = threadIdx.x; i < a.KqI * 256; i += blockDim.x) a.hq[a.zero_row * a.KqI * 256 + i] = 0;
     for (int64_t i = threadIdx.x; i < a.KqI * 8; i += blockDim.x) a.hs[a.zero_row * a.KqI * 8 + i] = 0.0f;
   }
   const int n_act = load_descriptors(a.seg, s_desc, &s_nact);
-  const int64_t n_cols = a.I / (kRowTile * RT);
-  for (int64_t item = blockIdx.x; item < (int64_t)n_act * n_cols; item += gridDim.x)
-    gate_up_item<RT, NQ>(a, s_desc[item / n_cols], (item % n_cols) * RT, red);
+  const int64_t n_rt = a.I / kRowTile;
+  for (int64_t item = blockIdx.x; item < (int64_t)n_act * n_rt; item += gridDim.x)
+    gate_up_item<NQ>(a, s_desc[item / n_rt], item % n_rt, red);
 }
 
 
 // ------------------------------------------------------------------ down
 
-// Same decomposition as gate_up_kernel: one 16-row tile of one expert per
-// workgroup, K split over its waves.  Positions past the segment read the
-// all-zero operand row of hq / hs.
-template <int NQ>
-__device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt, float (*red)[16][16]) {
+// Same decomposition as gate_up_kernel with RT 16-row tiles of H per item:
+// the activation operand of a quad (16 positions x 128 of I as fp16 hi/lo)
+// is loaded once and used for all RT tiles.  Positions past the segment
+// read the all-zero operand row of hq / hs.
+constexpr int kDownWaves = 4;
+
+template <int NQ, int RT>
+__device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt0, float (*red)[RT][16][16]) {
   const int lane = threadIdx.x % kWave;
   const int ks = threadIdx.x / kWave;
   const int ksplit = blockDim.x / kWave;
   const int n = lane % 16;
   const int p = lane / 16;
-  const int e = d.x;
+  const int e = __builtin_amdgcn_readfirstlane(d.x);
+  const int64_t beg = __builtin_amdgcn_readfirstlane(d.y);
+  const int64_t end = __builtin_amdgcn_readfirstlane(d.z);
   const int64_t nib_stride = a.H * a.Kq * 64;
   const int64_t sc_stride = a.H * a.Kq * 4;
   const uint8_t* dnib = e < a.seg.E ? a.down_nib + e * nib_stride : a.sh_down_nib;
@@ -310,15 +308,16 @@ __device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt,
   const u32x4 zero = {0u, 0u, 0u, 0u};
   const uint32_t mask = vgpr_const(0x03C003C0u);
 
-  for (int64_t m0 = d.y; m0 < d.z; m0 += 16) {
+  for (int64_t m0 = beg; m0 < end; m0 += 16) {
     const int64_t pm0 = m0 + n;
-    const int64_t pm = pm0 < d.z ? pm0 : a.zero_row;
+    const int64_t pm = pm0 < end ? pm0 : a.zero_row;
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    f32x4 acc = z, corr = z;
-    // quads ks, ks + ksplit, ... in chunks of NQ (one chunk for K <= 16 * NQ quads)
+    f32x4 acc[RT], corr[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) acc[r] = corr[r] = z;
     for (int64_t q0 = ks; q0 < a.Kq; q0 += (int64_t)NQ * ksplit) {
-      u32x4 bw[NQ];
-      uint2 bs[NQ];
+      u32x4 bw[NQ][RT];
+      uint2 bs[NQ][RT];
       u32x4 ah[NQ][4], al[NQ][4];
       float sp[NQ];
       bool qok[NQ];
@@ -327,9 +326,12 @@ __device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt,
         int64_t q = q0 + (int64_t)i * ksplit;
         qok[i] = q < a.Kq;
         q = qok[i] ? q : a.Kq - 1;
-        const int64_t tq = rt * a.Kq + q;
-        bw[i] = *reinterpret_cast<const u32x4*>(dnib + (tq * kWave + lane) * 16);
-        bs[i] = *reinterpret_cast<const uint2*>(dsc + tq * kQuadScales + n * 4);
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+          const int64_t tq = (rt0 + r) * a.Kq + q;  // wave-uniform
+          bw[i][r] = *reinterpret_cast<const u32x4*>(dnib + (tq * kWave + lane) * 16);
+          bs[i][r] = *reinterpret_cast<const uint2*>(dsc + tq * kQuadScales + n * 4);
+        }
         const u32x4* src = reinterpret_cast<const u32x4*>(a.hq + ((pm * a.Kq + q) * 16 + p * 4) * 16);
 #pragma unroll
         for (int gi = 0; gi < 4; ++gi) {
@@ -343,46 +345,59 @@ __device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt,
         const float s0 = hsrc[0], s1 = hsrc[1];
         sp[i] = (4 * q + p < Kg) ? s0 + s1 : 0.0f;
       }
+      // per-chunk partials, added to the totals once (short fp32 chains)
+      f32x4 part[RT];
+#pragma unroll
+      for (int r = 0; r < RT; ++r) part[r] = z;
 #pragma unroll
       for (int i = 0; i < NQ; ++i) {
         if (!qok[i]) continue;
-        float dv[4];
-        unpack_scales(bs[i], dv);
-        const uint32_t bwv[4] = {bw[i].x, bw[i].y, bw[i].z, bw[i].w};
 #pragma unroll
-        for (int gi = 0; gi < 4; ++gi) {
-          const u32x4 bb = dequant_unit_f16(bwv[gi], mask);
-          f32x4 pp = mfma_f16_16x16x32(ah[i][gi], bb, z);
-          pp = mfma_f16_16x16x32(al[i][gi], bb, pp);
-          acc += dv[gi] * pp;
+        for (int r = 0; r < RT; ++r) {
+          float dv[4];
+          unpack_scales(bs[i][r], dv);
+          const uint32_t bwv[4] = {bw[i][r].x, bw[i][r].y, bw[i][r].z, bw[i][r].w};
+#pragma unroll
+          for (int gi = 0; gi < 4; ++gi) {
+            const u32x4 bb = dequant_unit_f16(bwv[gi], mask);
+            f32x4 pp = mfma_f16_16x16x32(ah[i][gi], bb, z);
+            pp = mfma_f16_16x16x32(al[i][gi], bb, pp);
+            part[r] += dv[gi] * pp;
+          }
+          corr[r] = mfma_f32_16x16x4(sp[i], dv[p], corr[r]);
         }
-        corr = mfma_f32_16x16x4(sp[i], dv[p], corr);
       }
-    }
-    const f32x4 res = kUnitScale * acc - kUnitBias * corr;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) red[ks][4 * p + j][n] = res[j];
+      for (int r = 0; r < RT; ++r) acc[r] += part[r];
+    }
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      const f32x4 res = kUnitScale * acc[r] - kUnitBias * corr[r];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) red[ks][r][4 * p + j][n] = res[j];
+    }
     __syncthreads();
-    for (int o = threadIdx.x; o < 256; o += blockDim.x) {
-      const int mm = o / 16;
+    for (int o = threadIdx.x; o < RT * 256; o += blockDim.x) {
+      const int r = o / 256;
+      const int mm = (o % 256) / 16;
       const int nn = o % 16;
       float y = 0.0f;
-      for (int s2 = 0; s2 < ksplit; ++s2) y += red[s2][mm][nn];
-      if (m0 + mm < d.z) a.outbuf[(m0 + mm) * a.H + rt * 16 + nn] = y;
+      for (int s2 = 0; s2 < ksplit; ++s2) y += red[s2][r][mm][nn];
+      if (m0 + mm < end) a.outbuf[(m0 + mm) * a.H + (rt0 + r) * 16 + nn] = y;
     }
     __syncthreads();
   }
 }
 
-template <int NQ>
-__global__ __launch_bounds__(1024) void down_kernel(DownK a) {
-  __shared__ float red[16][16][16];
+template <int NQ, int RT>
+__global__ __launch_bounds__(kDownWaves * kWave) void down_kernel(DownK a) {
+  __shared__ float red[kDownWaves][RT][16][16];
   __shared__ int4 s_desc[kMaxExperts + 1];
   __shared__ int s_nact;
   const int n_act = load_descriptors(a.seg, s_desc, &s_nact);
-  const int64_t n_rt = a.H / kRowTile;
-  for (int64_t item = blockIdx.x; item < (int64_t)n_act * n_rt; item += gridDim.x)
-    down_item<NQ>(a, s_desc[item / n_rt], item % n_rt, red);
+  const int64_t n_items = a.H / (kRowTile * RT);
+  for (int64_t item = blockIdx.x; item < (int64_t)n_act * n_items; item += gridDim.x)
+    down_item<NQ, RT>(a, s_desc[item / n_items], (item % n_items) * RT, red);
 }
 
 // y[t] = sum_j w[t,j] * out[slot_pos[t*k+j]] (+ out[T*k + t] for the shared
@@ -469,29 +484,29 @@ static unsigned resident_grid(Kernel kernel, int block, int64_t max_items) {
   return (unsigned)(g < 1 ? 1 : g);
 }
 
-// K split: ksplit waves (at most 16) take about Kq / ksplit quads each, in
-// chunks of NQ <= max_nq issued together.
+// K split: ksplit waves (at most max_waves) take about two quads each (few
+// waves per item keep the cross-wave reduction short; two quads in flight per
+// wave keep enough loads outstanding), issued NQ = 2 at a time.
 struct Split {
   int ksplit, nq;
 };
 
-static Split choose_split(int64_t Kq, int max_nq) {
+static Split choose_split(int64_t Kq, int max_waves) {
   Split s;
-  s.ksplit = (int)(Kq < 16 ? Kq : 16);
-  const int64_t qpw = ceil_div(Kq, s.ksplit);
-  s.nq = 1;
-  while (s.nq < qpw && s.nq < max_nq) s.nq *= 2;
+  const int64_t half = ceil_div(Kq, 2);
+  s.ksplit = (int)(half < max_waves ? half : max_waves);
+  s.nq = Kq > 1 ? 2 : 1;
   return s;
 }
 
 // Optional override "ksplit,rt,nq" for tuning sweeps (PHANTOM_MOE_GATE_UP_TILING /
 // PHANTOM_MOE_DOWN_TILING); values outside the supported set are ignored.
-static void tiling_override(const char* name, int* ksplit, int* rt, int* nq) {
+static void tiling_override(const char* name, int max_waves, int* ksplit, int* rt, int* nq) {
   const char* v = getenv(name);
   if (!v) return;
   int a = 0, b = 0, c = 0;
-  if (sscanf(v, "%d,%d,%d", &a, &b, &c) == 3 && a >= 1 && a <= 16 && (b == 1 || b == 2) &&
-      (c == 1 || c == 2 || c == 4)) {
+  if (sscanf(v, "%d,%d,%d", &a, &b, &c) == 3 && a >= 1 && a <= max_waves && (b == 1 || b == 2 || b == 4) &&
+      (c == 1 || c == 2)) {
     *ksplit = a;
     *rt = b;
     *nq = c;
@@ -518,19 +533,17 @@ hipError_t launch_gate_up(const ExpertArgs& x, const Workspace& ws, hipStream_t 
   g.hq = ws.hq;
   g.hs = ws.hs;
   g.zero_row = x.T * x.k + (x.has_shared ? x.T : 0);
-  Split sp = choose_split(g.Kq, 1);
+  Split sp = choose_split(g.Kq, kGateUpWaves);
   int rt = 1;
-  tiling_override("PHANTOM_MOE_GATE_UP_TILING", &sp.ksplit, &rt, &sp.nq);
-  if (sp.nq > 2) sp.nq = 2;
-  rt = 1;  // one row tile per item; token tiles are paired instead
+  tiling_override("PHANTOM_MOE_GATE_UP_TILING", kGateUpWaves, &sp.ksplit, &rt, &sp.nq);
   const int block = kWave * sp.ksplit;
-  const int64_t max_items = (int64_t)max_active_experts(x) * (x.I / (kRowTile * rt));
-#define PMOE_GU(RT_, NQ_)                                                                               \
-  hipLaunchKernelGGL((gate_up_kernel<RT_, NQ_>), dim3(resident_grid(gate_up_kernel<RT_, NQ_>, block, max_items)), \
-                     dim3(block), 0, stream, g)
-  if (sp.nq == 1) PMOE_GU(1, 1);
-  else PMOE_GU(1, 2);
-#undef PMOE_GU
+  const int64_t max_items = (int64_t)max_active_experts(x) * (x.I / kRowTile);
+  if (sp.nq == 1)
+    hipLaunchKernelGGL(gate_up_kernel<1>, dim3(resident_grid(gate_up_kernel<1>, block, max_items)), dim3(block),
+                       0, stream, g);
+  else
+    hipLaunchKernelGGL(gate_up_kernel<2>, dim3(resident_grid(gate_up_kernel<2>, block, max_items)), dim3(block),
+                       0, stream, g);
   return hipGetLastError();
 }
 
@@ -548,18 +561,26 @@ hipError_t launch_down(const ExpertArgs& x, const Workspace& ws, hipStream_t str
   d.Kq = ceil_div(x.I, kQuad);
   d.zero_row = x.T * x.k + (x.has_shared ? x.T : 0);
   d.outbuf = ws.outbuf;
-  Split sp = choose_split(d.Kq, 2);
-  int rt = 1;
-  tiling_override("PHANTOM_MOE_DOWN_TILING", &sp.ksplit, &rt, &sp.nq);
-  if (sp.nq > 2) sp.nq = 2;
+  Split sp = choose_split(d.Kq, kDownWaves);
+  sp.nq = 1;   // measured faster than NQ = 2 at the occupancy NQ = 1 allows
+  int rt = 2;  // H is a multiple of 32: an even number of 16-row tiles
+  tiling_override("PHANTOM_MOE_DOWN_TILING", kDownWaves, &sp.ksplit, &rt, &sp.nq);
+  if (rt == 4 && (x.H / kRowTile) % 4) rt = 2;
   const int block = kWave * sp.ksplit;
-  const int64_t max_items = (int64_t)max_active_experts(x) * (x.H / kRowTile);
-  if (sp.nq == 1)
-    hipLaunchKernelGGL(down_kernel<1>, dim3(resident_grid(down_kernel<1>, block, max_items)), dim3(block), 0,
-                       stream, d);
-  else
-    hipLaunchKernelGGL(down_kernel<2>, dim3(resident_grid(down_kernel<2>, block, max_items)), dim3(block), 0,
-                       stream, d);
+  const int64_t max_items = (int64_t)max_active_experts(x) * (x.H / (kRowTile * rt));
+#define PMOE_DOWN(NQ_, RT_)                                                                               \
+  hipLaunchKernelGGL((down_kernel<NQ_, RT_>), dim3(resident_grid(down_kernel<NQ_, RT_>, block, max_items)), \
+                     dim3(block), 0, stream, d)
+  if (sp.nq == 1) {
+    if (rt == 1) PMOE_DOWN(1, 1);
+    else if (rt == 2) PMOE_DOWN(1, 2);
+    else PMOE_DOWN(1, 4);
+  } else {
+    if (rt == 1) PMOE_DOWN(2, 1);
+    else if (rt == 2) PMOE_DOWN(2, 2);
+    else PMOE_DOWN(2, 4);
+  }
+#undef PMOE_DOWN
   return hipGetLastError();
 }
 

@@ -27,6 +27,7 @@ struct Workspace {
   uint16_t* hq = nullptr;          // [rows, Kpad_I * 2] fp16 hi/lo of h, MFMA operand order
   float* hs = nullptr;             // [rows, Kpad_I / 32, 2] half-group sums of h
   float* outbuf = nullptr;          // [T*k + T*shared, H] expert outputs, segment order
+  int32_t* counter = nullptr;       // [1] router hand-off counter (reset by every route launch)
 };
 
 size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared, void* base,
@@ -43,8 +44,8 @@ hipError_t launch_q4_dequant_f32(const uint8_t* src, int64_t n_blocks, float* ou
                                  hipStream_t stream);
 
 // Logits (+ optional MFMA-ordered copy of x and its group sums), top-k, and
-// optionally the permute: two launches for up to 16 tokens per select
-// workgroup, three beyond.
+// optionally the permute: two launches up to 64 tokens (the permute runs in
+// the select launch), three beyond.
 struct RouteArgs {
   const void* x;
   int x_dtype;

@@ -1,6 +1,5 @@
-// router.hip -- fused MoE router for gfx950: gate GEMV (fp64, fixed order),
-// top-k selection, softmax / sigmoid weights, and the stable expert permute,
-// in one launch.
+// router.hip -- MoE router for gfx950: gate GEMV (fp64, fixed order), top-k
+// selection, softmax / sigmoid weights, and the stable expert permute.
 //
 // Reference semantics: PhantomTopKRouter.forward, tests/test_moe_routing.py:56-72
 // (logits = x W^T; torch.topk(largest, sorted); softmax over the k selected).
@@ -16,13 +15,15 @@
 // trades the other half with lane l ^ s, which yields exactly the tree above
 // while spending one shuffle-add per pair per lane in total.
 //
-// Launches.  route_logits_kernel computes logits (and the MFMA-ordered copy
-// of x) with no inter-workgroup communication.  route_select_kernel gives one
-// wave per token: k rounds of a wave-wide arg-max over (logit desc, index
-// asc), then the weights.  When the whole batch fits one workgroup (decode),
-// the same workgroup then runs the permute; otherwise permute_kernel does.
-// No device-scope fences anywhere: on a multi-XCD part an agent-scope release
-// writes back the XCD's L2, which costs microseconds per workgroup.
+// Launches.  route_logits_kernel computes logits (and, spread over all its
+// workgroups, the MFMA-ordered copy of x) with no inter-workgroup
+// communication.  route_select_kernel gives one wave per token: a radix
+// descent over the 64-bit order keys finds the k-th largest key, the k
+// winners are ranked among themselves, then the weights.  For up to
+// kFusedSelectBlocks select workgroups (decode) the last workgroup to finish
+// runs the permute; beyond that permute_kernel does.  The hand-off costs one
+// agent-scope release per select workgroup (an L2 write-back on a multi-XCD
+// part), which is why it is reserved for small grids.
 // Permute: per-wave expert counts, an (expert, wave)-major exclusive scan, and
 // a second pass that places every slot at base + rank-within-round, where the
 // rank comes from ballots over the bits of the expert id.  Placement depends
@@ -61,6 +62,8 @@ struct RouteK {
   int32_t* slot_pos;
   int4* desc;        // [E + 1] {expert, begin, end, 0} per active segment, or null
   int32_t* seg_tok;  // [T*k + T] token of each segment position, or null
+  int32_t* counter;  // select workgroups finished (fused permute); zeroed by the logits launch
+  int fuse_permute;
 };
 
 __device__ inline bool ranks_before(double va, int ia, double vb, int ib) {
@@ -152,16 +155,33 @@ __device__ void block_permute(const int32_t* __restrict__ idx, int64_t n, int k,
   const int64_t beg = w * chunk;
   const int64_t end = (beg + chunk < n) ? beg + chunk : n;
 
+  // Expert ids of the wave's first kCached rounds are loaded together (from
+  // clamped indices, so no load sits under a branch) and kept for pass 2.
+  const uint64_t lt_mask = (1ull << lane) - 1ull;
+  constexpr int kCached = 4;
+  int cached[kCached];
+#pragma unroll
+  for (int i = 0; i < kCached; ++i) {
+    const int64_t sl = beg + (int64_t)i * kWave + lane;
+    const int v = idx[sl < n ? sl : n - 1];
+    cached[i] = sl < end ? v : -1;
+  }
+
   // Pass 1: per-wave counts.
-  for (int64_t r0 = beg; r0 < end; r0 += kWave) {
-    const int64_t s = r0 + lane;
-    int e = (s < end) ? idx[s] : -1;
+  for (int64_t r0 = beg, i = 0; r0 < end; r0 += kWave, ++i) {
+    int e;
+    if (i < kCached) {
+      e = cached[0];
+#pragma unroll
+      for (int j = 1; j < kCached; ++j) e = (i == j) ? cached[j] : e;
+    } else {
+      const int64_t sl = r0 + lane;
+      const int v = idx[sl < end ? sl : end - 1];
+      e = sl < end ? v : -1;
+    }
     const bool valid = (e >= 0 && e < E);
     const uint64_t m = match_expert(e, valid, nbits);
-    if (valid) {
-      const uint64_t below = m & ((1ull << lane) - 1ull);
-      if (below == 0) s_cnt[w][e] += __popcll(m);
-    }
+    if (valid && (m & lt_mask) == 0) s_cnt[w][e] += __popcll(m);
   }
   __syncthreads();
 
@@ -226,73 +246,116 @@ __device__ void block_permute(const int32_t* __restrict__ idx, int64_t n, int k,
   __syncthreads();
 
   // Pass 2: placement.
-  for (int64_t r0 = beg; r0 < end; r0 += kWave) {
-    const int64_t s = r0 + lane;
-    int e = (s < end) ? idx[s] : -1;
+  for (int64_t r0 = beg, i = 0; r0 < end; r0 += kWave, ++i) {
+    const int64_t sl = r0 + lane;
+    int e;
+    if (i < kCached) {
+      e = cached[0];
+#pragma unroll
+      for (int j = 1; j < kCached; ++j) e = (i == j) ? cached[j] : e;
+    } else {
+      const int v = idx[sl < end ? sl : end - 1];
+      e = sl < end ? v : -1;
+    }
     const bool valid = (e >= 0 && e < E);
     const uint64_t m = match_expert(e, valid, nbits);
     if (valid) {
-      const uint64_t below = m & ((1ull << lane) - 1ull);
+      const uint64_t below = m & lt_mask;
       const int pos = s_cnt[w][e] + __popcll(below);
-      sorted_slots[pos] = (int32_t)s;
-      slot_pos[s] = pos;
-      if (seg_tok) seg_tok[pos] = (int32_t)(s / k);
+      sorted_slots[pos] = (int32_t)sl;
+      slot_pos[sl] = pos;
+      if (seg_tok) seg_tok[pos] = (int32_t)(sl / k);
       // Every lane of the group has read the base before the leader bumps
       // it: LDS operations of one wave complete in program order, and the
       // read above precedes this write in every lane's program.
       if (below == 0) s_cnt[w][e] = s_cnt[w][e] + __popcll(m);
-    } else if (s < end) {
-      slot_pos[s] = -1;
+    } else if (sl < end) {
+      slot_pos[sl] = -1;
     }
   }
 }
 
 // Order-preserving integer key of a logit: a > b (as numbers) iff
-// key(a) > key(b), -0.0 and +0.0 share a key, and NaN maps to 0, below every
-// number, so equal keys are exactly the ties the oracle breaks by index.
+// key(a) > key(b), -0.0 and +0.0 share a key, and NaN maps to 1, below every
+// number (-inf has key 0x000F...F), so equal keys are exactly the ties the
+// oracle breaks by index.  Key 0 is left for padding lanes.
 __device__ inline uint64_t logit_key(double v) {
-  if (isnan(v)) return 0ull;
+  if (isnan(v)) return 1ull;
   if (v == 0.0) v = 0.0;  // -0.0 -> +0.0
   const uint64_t b = __builtin_bit_cast(uint64_t, v);
   return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
 }
 
-// Top-k of one token by rank counting (called by all 64 lanes of one wave).
-// The token's E keys sit in LDS; lane l ranks experts l, l + 64, ...:
-// rank(e) = #{e' : key(e') > key(e) or (key(e') == key(e) and e' < e)}, which
-// is e's position in (value desc, index asc) order.  Experts of rank < k are
-// written straight to their slot.  No cross-lane dependency chains: each
-// comparison reads a broadcast LDS word.
+// Top-k of one token (called by all 64 lanes of one wave); lane l holds
+// experts l, l + 64, ... in registers.
+//  1. Radix descent over the key bits towards the largest x with
+//     #{key >= x} >= k, the k-th largest key (one ballot + popcount per bit
+//     and per register), stopping early at any x with exactly k keys >= x.
+//  2. Winners: every key > x, then keys == x in increasing expert index until
+//     k are taken -- the (value desc, index asc) order's first k.
+//  3. The k winners are compacted to LDS in index order and lane i < k ranks
+//     winner i among them; rank r goes to slot r.
 template <int NV>
-__device__ void wave_topk(const RouteK& a, int64_t t, uint64_t* s_key, double* s_val, int* s_idx,
-                          double* s_e) {
+__device__ void wave_topk(const RouteK& a, int64_t t, uint64_t* s_ck, double* s_cv, int* s_ci,
+                          double* s_val, int* s_idx, double* s_e) {
   const int lane = threadIdx.x % kWave;
-  for (int e = lane; e < a.E; e += kWave) s_key[e] = logit_key(a.logits[t * a.E + e]);
+  const uint64_t lt_mask = (1ull << lane) - 1ull;
+  uint64_t key[NV];
+  double val[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int e = lane + kWave * v;
+    const double lv = a.logits[t * a.E + (e < a.E ? e : a.E - 1)];  // unconditional load
+    val[v] = e < a.E ? lv : 0.0;
+    key[v] = e < a.E ? logit_key(lv) : 0ull;
+  }
+  // Invariant: #{key >= kth} >= k.  Once it is exactly k the winners are
+  // known (every other key is below kth), so the descent stops there --
+  // usually at the first bit that separates the k-th and (k+1)-th keys.
+  uint64_t kth = 0;
+  int at_kth = kWave * NV;
+  for (int bit = 63; bit >= 0 && at_kth != a.k; --bit) {
+    const uint64_t cand = kth | (1ull << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) cnt += __popcll(__ballot(key[v] >= cand));
+    if (cnt >= a.k) {
+      kth = cand;
+      at_kth = cnt;
+    }
+  }
+  int n_gt = 0;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) n_gt += __popcll(__ballot(key[v] > kth));
+  const int take_eq = a.k - n_gt;  // >= 1 by the choice of kth
+  int eq_before = 0, sel_before = 0;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const bool eq = key[v] == kth;
+    const uint64_t meq = __ballot(eq);
+    const bool sel = key[v] > kth || (eq && eq_before + __popcll(meq & lt_mask) < take_eq);
+    const uint64_t msel = __ballot(sel);
+    if (sel) {
+      const int pos = sel_before + __popcll(msel & lt_mask);
+      s_ck[pos] = key[v];
+      s_cv[pos] = val[v];
+      s_ci[pos] = lane + kWave * v;
+    }
+    eq_before += __popcll(meq);
+    sel_before += __popcll(msel);
+  }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  uint64_t mine[NV];
-  int rank[NV];
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int e = lane + kWave * v;
-    mine[v] = e < a.E ? s_key[e] : 0ull;
-    rank[v] = 0;
-  }
-  for (int e2 = 0; e2 < a.E; ++e2) {
-    const uint64_t k2 = s_key[e2];
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int e = lane + kWave * v;
-      rank[v] += (k2 > mine[v] || (k2 == mine[v] && e2 < e)) ? 1 : 0;
+  if (lane < a.k) {
+    const uint64_t mk = s_ck[lane];
+    const int me = s_ci[lane];
+    int r = 0;
+    for (int j = 0; j < a.k; ++j) {
+      const uint64_t kj = s_ck[j];
+      r += (kj > mk || (kj == mk && s_ci[j] < me)) ? 1 : 0;
     }
-  }
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int e = lane + kWave * v;
-    if (e < a.E && rank[v] < a.k) {
-      s_idx[rank[v]] = e;
-      s_val[rank[v]] = a.logits[t * a.E + e];
-    }
+    s_idx[r] = me;
+    s_val[r] = s_cv[lane];
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -315,41 +378,48 @@ __device__ void wave_topk(const RouteK& a, int64_t t, uint64_t* s_key, double* s
   __builtin_amdgcn_wave_barrier();
 }
 
-// MFMA-ordered copy of x (bf16) and fp32 group sums for tokens [t0, t0+TT).
-// Layout [t][q][p][gi][8]: one 16-byte chunk per (token, quad, part, group).
+// MFMA-ordered copy of x (bf16) and fp32 group sums for tokens [t0, t0+TT),
+// spread over the gridDim.x workgroups that share this token tile.
+// Layout [t][q][p][gi][8]: one 16-byte chunk per (token, quad, part, group);
+// chunk (p, gi) of quad q holds elements kmap(p, 0..7) of group 4q + gi, read
+// as two 8-byte runs (4p..4p+3 and 4p+16..4p+19).  A group's sum adds its
+// four parts' 8-element sums by an xor butterfly over p (lanes 4 and 8 apart).
 __device__ void prep_x_tile(const RouteK& a, int64_t t0, int TT) {
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
   const int Kg = (int)(a.H / kGroup);
   const int per_tok = (int)a.Kq * 16;
-  for (int ti = 0; ti < TT; ++ti) {
+  const int n = TT * per_tok;
+  const int lane = threadIdx.x % kWave;
+  const int wave0 = (int)(blockIdx.x * blockDim.x) + (int)(threadIdx.x / kWave) * kWave;
+  for (int c0 = wave0; c0 < n; c0 += (int)(gridDim.x * blockDim.x)) {  // wave-uniform
+    const int c = c0 + lane;
+    const int ti = c / per_tok;
+    const int cc = c - ti * per_tok;
     const int64_t t = t0 + ti;
-    if (t >= a.T) break;
-    const uint16_t* xt = x + t * a.H;
-    for (int c = threadIdx.x; c < per_tok; c += blockDim.x) {
-      const int gi = c & 3;
-      const int p = (c >> 2) & 3;
-      const int q = c >> 4;
-      const int g = 4 * q + gi;
-      uint32_t wds[4] = {0, 0, 0, 0};
-      if (g < Kg) {
-        const uint16_t* xr = xt + g * kGroup;
-        for (int j = 0; j < 8; j += 2) wds[j / 2] = (uint32_t)xr[kmap(p, j)] | ((uint32_t)xr[kmap(p, j + 1)] << 16);
-      }
-      u32x4 v = {wds[0], wds[1], wds[2], wds[3]};
-      *reinterpret_cast<u32x4*>(a.xq + (t * a.Kq * 16 + c) * 8) = v;
+    const bool valid = c < n && t < a.T;
+    const int gi = cc & 3;
+    const int p = (cc >> 2) & 3;
+    const int g = 4 * (cc >> 4) + gi;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    float sum = 0.0f;
+    if (valid && g < Kg) {
+      const uint16_t* xr = x + t * a.H + (int64_t)g * kGroup + 4 * p;
+      const uint2 lo = *reinterpret_cast<const uint2*>(xr);
+      const uint2 hi = *reinterpret_cast<const uint2*>(xr + 16);
+      v.x = (lo.x & 0xffffu) | (lo.y << 16);
+      v.y = (hi.x & 0xffffu) | (hi.y << 16);
+      v.z = (lo.x >> 16) | (lo.y & 0xffff0000u);
+      v.w = (hi.x >> 16) | (hi.y & 0xffff0000u);
+      sum = ((bf16_bits_to_float(lo.x & 0xffffu) + bf16_bits_to_float(lo.x >> 16)) +
+             (bf16_bits_to_float(lo.y & 0xffffu) + bf16_bits_to_float(lo.y >> 16))) +
+            ((bf16_bits_to_float(hi.x & 0xffffu) + bf16_bits_to_float(hi.x >> 16)) +
+             (bf16_bits_to_float(hi.y & 0xffffu) + bf16_bits_to_float(hi.y >> 16)));
     }
-    const int ng = (int)a.Kq * 4;
-    for (int g = threadIdx.x; g < ng; g += blockDim.x) {
-      float sum = 0.0f;
-      if (g < Kg) {
-        const uint32_t* xr = reinterpret_cast<const uint32_t*>(xt + g * kGroup);
-        for (int j = 0; j < kGroup / 2; ++j) {
-          const uint32_t two = xr[j];
-          sum += bf16_bits_to_float(two & 0xffffu);
-          sum += bf16_bits_to_float(two >> 16);
-        }
-      }
-      a.xs[t * ng + g] = sum;
+    sum += __shfl_xor(sum, 4, kWave);
+    sum += __shfl_xor(sum, 8, kWave);
+    if (valid) {
+      *reinterpret_cast<u32x4*>(a.xq + (t * per_tok + cc) * 8) = v;
+      if (p == 0) a.xs[t * a.Kq * 4 + g] = sum;
     }
   }
 }
@@ -403,13 +473,24 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteK a) {
   const int64_t t0 = (int64_t)blockIdx.y * TT;
   const int e0 = blockIdx.x * (4 * EW) + w * EW;
   const XT* x = static_cast<const XT*>(a.x);
+  if (a.prep_x) prep_x_tile(a, t0, TT);
+  if (a.counter && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *a.counter = 0;
+  // The bias of the expert this lane may write, fetched ahead of the GEMV.
+  float bias_e = 0.0f;
+  if (a.bias) {
+    const int e = e0 + tree_pair_of_lane<P>(lane) % EW;
+    bias_e = a.bias[e < a.E ? e : a.E - 1];
+  }
 
   double acc[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) acc[i] = 0.0;
 
   // Chunks are loaded CB at a time (all loads of a batch issued before its
-  // FMAs), then accumulated in increasing h as the contract requires.
+  // FMAs), then accumulated in increasing h as the contract requires.  Loads
+  // are unconditional, from clamped addresses, and out-of-range values are
+  // zeroed afterwards: a load under a branch gets its own vmcnt(0) wait,
+  // which would serialise the batch.
   const int64_t nchunks = ceil_div(a.H, 256);
   for (int64_t c0 = 0; c0 < nchunks; c0 += CB) {
     float wv[CB][EW][4];
@@ -418,27 +499,27 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteK a) {
     for (int cb = 0; cb < CB; ++cb) {
       const int64_t h0 = (c0 + cb) * 256 + 4 * lane;
       const bool hok = (c0 + cb) < nchunks && h0 < a.H;
+      const int64_t hc = hok ? h0 : 0;
 #pragma unroll
       for (int ei = 0; ei < EW; ++ei) {
         const int e = e0 + ei;
-        if (hok && e < a.E) {
-          const float4 r = *reinterpret_cast<const float4*>(a.W + (int64_t)e * a.H + h0);
-          wv[cb][ei][0] = r.x;
-          wv[cb][ei][1] = r.y;
-          wv[cb][ei][2] = r.z;
-          wv[cb][ei][3] = r.w;
-        } else {
-          wv[cb][ei][0] = wv[cb][ei][1] = wv[cb][ei][2] = wv[cb][ei][3] = 0.0f;
-        }
+        const bool ok = hok && e < a.E;
+        const int64_t ec = e < a.E ? e : a.E - 1;
+        const float4 r = *reinterpret_cast<const float4*>(a.W + ec * a.H + hc);
+        wv[cb][ei][0] = ok ? r.x : 0.0f;
+        wv[cb][ei][1] = ok ? r.y : 0.0f;
+        wv[cb][ei][2] = ok ? r.z : 0.0f;
+        wv[cb][ei][3] = ok ? r.w : 0.0f;
       }
 #pragma unroll
       for (int ti = 0; ti < TT; ++ti) {
         const int64_t t = t0 + ti;
-        if (hok && t < a.T) {
-          load_x4<XT>(x, t * a.H + h0, xv[cb][ti]);
-        } else {
-          xv[cb][ti][0] = xv[cb][ti][1] = xv[cb][ti][2] = xv[cb][ti][3] = 0.0f;
-        }
+        const bool ok = hok && t < a.T;
+        const int64_t tc = t < a.T ? t : a.T - 1;
+        float v4[4];
+        load_x4<XT>(x, tc * a.H + hc, v4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xv[cb][ti][i] = ok ? v4[i] : 0.0f;
       }
     }
 #pragma unroll
@@ -467,13 +548,12 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteK a) {
       const int e = e0 + ei;
       if (t < a.T && e < a.E) {
         double v = tot;
-        if (a.bias) v = v + (double)a.bias[e];
+        if (a.bias) v = v + (double)bias_e;
         a.logits[t * a.E + e] = v;
       }
     }
   }
 
-  if (a.prep_x && blockIdx.x == 0) prep_x_tile(a, t0, TT);
   if (a.prep_x && blockIdx.x == 1 % gridDim.x && blockIdx.y == 0) {
     // all-zero activation row T, read by expert lanes past a segment
     for (int64_t i = threadIdx.x; i < a.Kq * 128; i += blockDim.x) a.xq[a.T * a.Kq * 128 + i] = 0;
@@ -481,21 +561,40 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteK a) {
   }
 }
 
-// Top-k and weights, one wave per token (grid-stride); a launch with one
-// workgroup continues with the permute.
+// Top-k and weights, one wave per token (grid-stride).  With do_permute, a
+// launch of one workgroup continues with the permute, and a fused launch hands
+// the permute to the last workgroup to finish.
 constexpr int kSelectWaves = 4;
+constexpr int kFusedSelectBlocks = 16;
 
 template <int NV>
 __global__ __launch_bounds__(256) void route_select_kernel(RouteK a) {
-  __shared__ uint64_t s_key[kSelectWaves][kMaxExperts];
+  __shared__ uint64_t s_ck[kSelectWaves][kMaxTopK];
+  __shared__ double s_cv[kSelectWaves][kMaxTopK];
+  __shared__ int s_ci[kSelectWaves][kMaxTopK];
   __shared__ double s_val[kSelectWaves][kMaxTopK];
   __shared__ double s_e[kSelectWaves][kMaxTopK];
   __shared__ int s_idx[kSelectWaves][kMaxTopK];
+  __shared__ int s_last;
   const int w = threadIdx.x / kWave;
   const int nw = blockDim.x / kWave;
   for (int64_t t = (int64_t)blockIdx.x * nw + w; t < a.T; t += (int64_t)gridDim.x * nw)
-    wave_topk<NV>(a, t, s_key[w], s_val[w], s_idx[w], s_e[w]);
-  if (!a.do_permute || gridDim.x != 1) return;
+    wave_topk<NV>(a, t, s_ck[w], s_cv[w], s_ci[w], s_val[w], s_idx[w], s_e[w]);
+  if (!a.do_permute) return;
+  if (gridDim.x > 1) {
+    if (!a.fuse_permute) return;
+    // Every wave's top-k stores have reached L2 before the barrier; thread 0
+    // then writes the XCD's L2 back (agent-scope release) and counts in.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      __threadfence();
+      s_last = atomicAdd(a.counter, 1) == (int)gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();  // acquire: the other workgroups' top-k
+  }
   __syncthreads();
   block_permute(a.topk_idx, a.T * a.k, a.k, a.E, a.T, a.has_shared, a.offsets, a.offsets_user, a.active,
                 a.n_active, a.sorted_slots, a.slot_pos, a.desc, a.seg_tok);
@@ -561,20 +660,22 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
   k.slot_pos = r.slot_pos_out ? r.slot_pos_out : ws.slot_pos;
   k.desc = r.do_permute ? ws.desc : nullptr;
   k.seg_tok = r.do_permute ? ws.seg_tok : nullptr;
+  const unsigned sel_blocks = (unsigned)ceil_div(r.T, kSelectWaves);
+  k.fuse_permute = (r.do_permute && sel_blocks > 1 && sel_blocks <= kFusedSelectBlocks) ? 1 : 0;
+  k.counter = k.fuse_permute ? ws.counter : nullptr;
   hipError_t err = (r.x_dtype == 0) ? launch_logits_t<uint16_t>(k, TT, n_ttiles, stream)
                                     : launch_logits_t<float>(k, TT, n_ttiles, stream);
   if (err != hipSuccess) return err;
   // One wave per token, four tokens per workgroup, so selection is spread
-  // over many CUs; the permute then runs in its own single-workgroup launch.
-  // A batch of at most four tokens is routed and permuted by one workgroup.
-  const unsigned sel_blocks = (unsigned)ceil_div(r.T, kSelectWaves);
+  // over many CUs.  The permute runs in the select launch up to
+  // kFusedSelectBlocks workgroups, in its own single-workgroup launch beyond.
   const dim3 sb(kWave * kSelectWaves);
   if (r.E <= 64) hipLaunchKernelGGL(route_select_kernel<1>, dim3(sel_blocks), sb, 0, stream, k);
   else if (r.E <= 128) hipLaunchKernelGGL(route_select_kernel<2>, dim3(sel_blocks), sb, 0, stream, k);
   else if (r.E <= 256) hipLaunchKernelGGL(route_select_kernel<4>, dim3(sel_blocks), sb, 0, stream, k);
   else hipLaunchKernelGGL(route_select_kernel<8>, dim3(sel_blocks), sb, 0, stream, k);
   err = hipGetLastError();
-  if (err != hipSuccess || !r.do_permute || sel_blocks == 1) return err;
+  if (err != hipSuccess || !r.do_permute || sel_blocks == 1 || k.fuse_permute) return err;
   hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, k.topk_idx, r.T, r.k, r.E,
                      r.has_shared, ws.offsets, r.offsets_out, ws.active, ws.n_active, k.sorted_slots,
                      k.slot_pos, k.desc, k.seg_tok);

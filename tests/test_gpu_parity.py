@@ -109,6 +109,30 @@ def test_route_random_vs_oracle(dev, T, H, E, k, score, xdt):
     np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("E,k", [(7, 7), (32, 32), (64, 4), (128, 8), (200, 32), (256, 16)])
+def test_route_special_values(dev, E, k):
+    """NaN, +-inf, +-0 and exactly tied logits: NaN ranks below every number,
+    -0 ties +0, ties go to the lower expert index (the oracle's ranks_before)."""
+    rng = np.random.default_rng(1000 + E)
+    T, H = 9, 64
+    xb = synth.f32_to_bf16_bits(rng.standard_normal((T, H), dtype=np.float32))
+    W = (rng.standard_normal((E, H), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    W[1::5] = 0.0  # logit exactly +0 (plus bias)
+    n3 = len(W[3::7])
+    W[3::7] = W[2::7][:n3]  # duplicated rows: exact ties at distinct indices
+    bias = np.zeros(E, np.float32)
+    bias[::11] = np.nan
+    if E >= 200:
+        bias[4::13] = np.inf  # +inf in the top-k: softmax weights are NaN, selection still exact
+    bias[6::13] = -np.inf
+    bias[8::17] = -0.0
+    x = to_bf16_tensor(xb, dev)
+    w, idx = phantom_moe.route(x, torch.from_numpy(W).to(dev), k, 0, torch.from_numpy(bias).to(dev))
+    ridx, rw = oracle.route(xb, W, k, 0, bias)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-6, atol=1e-7, equal_nan=True)
+
+
 @pytest.mark.parametrize("name", list(synth.CONFIGS))
 def test_route_full_size_configs(dev, name):
     cfg = synth.CONFIGS[name]
