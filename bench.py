@@ -11,8 +11,8 @@ about 5.4 GB at 16 instances) so weight traffic comes from HBM, not from the
 HBM before it starts.
 
 Output: one JSON line with the whole-job tokens/s, the roofline of the
-dominant kernel (gate/up grouped GEMV, timed with HIP events recorded between
-kernels on the launch stream), and the CPU baseline (the reference's CPU MoE
+dominant kernel (gate/up grouped GEMV, one launch between two HIP events on
+its stream), and the CPU baseline (the reference's CPU MoE
 path, restated in oracle/ref_cpu_path.py, timed on this host on a bounded
 sample).
 
@@ -31,6 +31,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "solution-is-all-you-need_amd"))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+# Stage events of phantom_moe_set_profile_events (include/phantom_moe.h): before
+# the router, gate/up, down and combine, and after the combine.
+STAGES = ("route", "gate_up", "down", "combine")
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000  # a record needs no system-scope release
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "gate_up_kernel_qwen3_decode_t32_zipf_pmc.json")
 
@@ -45,6 +49,9 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-stage-events", action="store_true", help="time without the per-stage events")
+    p.add_argument("--copy-bytes", type=int, default=0,
+                   help="after the timed region, one plain device copy of this many bytes (the calibration "
+                        "dispatch for FETCH_SIZE / WRITE_SIZE counter runs)")
     return p.parse_args()
 
 
@@ -61,7 +68,7 @@ class HipEvents:
         out = []
         for _ in range(n):
             ev = ctypes.c_void_p()
-            rc = self.hip.hipEventCreateWithFlags(ctypes.byref(ev), 0)
+            rc = self.hip.hipEventCreateWithFlags(ctypes.byref(ev), HIP_EVENT_DISABLE_SYSTEM_FENCE)
             if rc != 0:
                 raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
             out.append(ev.value)
@@ -181,7 +188,7 @@ def main():
 
     use_events = not args.no_stage_events
     ev = HipEvents()
-    n_ev = 5
+    n_ev = len(STAGES) + 1
     events = ev.create(n_ev * args.steps) if use_events else []
     arrays = [(ctypes.c_void_p * n_ev)(*events[i * n_ev:(i + 1) * n_ev]) for i in range(args.steps)] if use_events else []
 
@@ -198,17 +205,24 @@ def main():
         lib.phantom_moe_set_profile_events(None, 0)
     elapsed = t1 - t0
 
-    # ---- per-stage times, U per instance ---------------------------------
+    if args.copy_bytes > 0:
+        src = torch.ones(args.copy_bytes, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    # ---- per-kernel and per-layer times, U per instance --------------------
     U = [int(torch.unique(layers[l].topk_idx).numel()) for l in range(L)]
-    stages = {"route": [], "gate_up": [], "down": [], "combine": [], "layer": []}
+    stages = {name: [] for name in STAGES}
+    layer_ms = []
     if use_events:
         for i in range(args.steps):
             e = events[i * n_ev:(i + 1) * n_ev]
-            stages["route"].append(ev.elapsed_ms(e[0], e[1]))
-            stages["gate_up"].append(ev.elapsed_ms(e[1], e[2]))
-            stages["down"].append(ev.elapsed_ms(e[2], e[3]))
-            stages["combine"].append(ev.elapsed_ms(e[3], e[4]))
-            stages["layer"].append(ev.elapsed_ms(e[0], e[4]))
+            layer_ms.append(ev.elapsed_ms(e[0], e[-1]))
+            for j, name in enumerate(STAGES):
+                stages[name].append(ev.elapsed_ms(e[j], e[j + 1]))
         ev.destroy(events)
     steps_U = [U[i % L] for i in range(args.steps)]
 
@@ -255,11 +269,11 @@ def main():
             "algorithmic_bytes_per_launch": round(gu_bytes / args.steps),
             "avg_launch_us": round(gu_ms * 1e3 / args.steps, 3),
         }
-        lay_ms = float(np.sum(stages["layer"]))
+        lay_ms = float(np.sum(layer_ms))
         lay_bytes = float(sum(layer_bytes(cfg, u) for u in steps_U))
         out["layer"] = {
             "gpu_us_per_step": round(lay_ms * 1e3 / args.steps, 3),
-            "stage_us": {k: round(float(np.mean(v)) * 1e3, 3) for k, v in stages.items() if k != "layer"},
+            "stage_us": {k: round(float(np.mean(v)) * 1e3, 3) for k, v in stages.items()},
             "hbm_achieved_gbs": round(lay_bytes / (lay_ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(lay_bytes / (lay_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "tflops": round(layer_flops(cfg) * args.steps / (lay_ms * 1e-3) / 1e12, 3),

@@ -70,8 +70,11 @@ PHANTOM_MOE_API const char* phantom_moe_version(void);
 /* Stage timing.  With a non-null array of PHANTOM_MOE_PROFILE_EVENTS events
  * set on the calling thread, phantom_moe_forward records events[0] before the
  * router, [1] before gate/up, [2] before down, [3] before the combine and
- * [4] after it, on the call's stream (no synchronisation).  NULL turns it
- * off.  The non-blocking counterpart of the reference's per-call CudaTimer
+ * [4] after it, on the call's stream (no synchronisation).  The gate/up and
+ * down stages are one kernel each, so [1]-[2] and [2]-[3] bracket single
+ * launches.  The array is read by every later call on the thread, so it must
+ * stay valid until it is replaced or cleared; NULL turns timing off.  The
+ * non-blocking counterpart of the reference's per-call CudaTimer
  * (kernels/common/cuda_utils.h:235-260, used at sparse_matmul.cu:256-257). */
 #define PHANTOM_MOE_PROFILE_EVENTS 5
 PHANTOM_MOE_API int phantom_moe_set_profile_events(hipEvent_t* events, int n_events);

@@ -139,12 +139,7 @@ __device__ inline void gate_up_pass(const GateUpK& a, const int e, const int64_t
   f32x4 ag[TP], au[TP], cg[TP], cu[TP];
 #pragma unroll
   for (int t = 0; t < TP; ++t) ag[t] = au[t] = cg[t] = cu[t] = z;
-  // Each chunk of NQ quads is summed on its own and then added to the
-  // running totals, which keeps the fp32 chains short for long K.
   for (int64_t q0 = ks; q0 < a.Kq; q0 += (int64_t)NQ * ksplit) {
-    f32x4 pg[TP], pu[TP];
-#pragma unroll
-    for (int t = 0; t < TP; ++t) pg[t] = pu[t] = z;
     u32x4 gw[NQ], uw[NQ];
     uint2 gs[NQ], us[NQ];
     u32x4 xa[NQ][TP][4];
@@ -183,8 +178,8 @@ __device__ inline void gate_up_pass(const GateUpK& a, const int e, const int64_t
         const u32x4 bu = dequant_unit_bf16(uwv[gi], mask);
 #pragma unroll
         for (int t = 0; t < TP; ++t) {
-          pg[t] += dg[gi] * mfma_bf16_16x16x32(xa[i][t][gi], bg, z);
-          pu[t] += du[gi] * mfma_bf16_16x16x32(xa[i][t][gi], bu, z);
+          ag[t] += dg[gi] * mfma_bf16_16x16x32(xa[i][t][gi], bg, z);
+          au[t] += du[gi] * mfma_bf16_16x16x32(xa[i][t][gi], bu, z);
         }
       }
 #pragma unroll
@@ -192,11 +187,6 @@ __device__ inline void gate_up_pass(const GateUpK& a, const int e, const int64_t
         cg[t] = mfma_f32_16x16x4(sx[i][t], dg[p], cg[t]);
         cu[t] = mfma_f32_16x16x4(sx[i][t], du[p], cu[t]);
       }
-    }
-#pragma unroll
-    for (int t = 0; t < TP; ++t) {
-      ag[t] += pg[t];
-      au[t] += pu[t];
     }
   }
 #pragma unroll
@@ -539,11 +529,11 @@ hipError_t launch_gate_up(const ExpertArgs& x, const Workspace& ws, hipStream_t 
   const int block = kWave * sp.ksplit;
   const int64_t max_items = (int64_t)max_active_experts(x) * (x.I / kRowTile);
   if (sp.nq == 1)
-    hipLaunchKernelGGL(gate_up_kernel<1>, dim3(resident_grid(gate_up_kernel<1>, block, max_items)), dim3(block),
-                       0, stream, g);
+    hipLaunchKernelGGL(gate_up_kernel<1>, dim3(resident_grid(gate_up_kernel<1>, block, max_items)), dim3(block), 0,
+                stream, g);
   else
-    hipLaunchKernelGGL(gate_up_kernel<2>, dim3(resident_grid(gate_up_kernel<2>, block, max_items)), dim3(block),
-                       0, stream, g);
+    hipLaunchKernelGGL(gate_up_kernel<2>, dim3(resident_grid(gate_up_kernel<2>, block, max_items)), dim3(block), 0,
+                stream, g);
   return hipGetLastError();
 }
 
@@ -568,9 +558,9 @@ hipError_t launch_down(const ExpertArgs& x, const Workspace& ws, hipStream_t str
   if (rt == 4 && (x.H / kRowTile) % 4) rt = 2;
   const int block = kWave * sp.ksplit;
   const int64_t max_items = (int64_t)max_active_experts(x) * (x.H / (kRowTile * rt));
-#define PMOE_DOWN(NQ_, RT_)                                                                               \
-  hipLaunchKernelGGL((down_kernel<NQ_, RT_>), dim3(resident_grid(down_kernel<NQ_, RT_>, block, max_items)), \
-                     dim3(block), 0, stream, d)
+#define PMOE_DOWN(NQ_, RT_)                                                                             \
+  hipLaunchKernelGGL((down_kernel<NQ_, RT_>),                                          \
+              dim3(resident_grid(down_kernel<NQ_, RT_>, block, max_items)), dim3(block), 0, stream, d)
   if (sp.nq == 1) {
     if (rt == 1) PMOE_DOWN(1, 1);
     else if (rt == 2) PMOE_DOWN(1, 2);
@@ -589,7 +579,7 @@ hipError_t launch_combine(const ExpertArgs& x, const Workspace& ws, hipStream_t 
   int64_t blocks = ceil_div(total, 256);
   if (blocks > 65536) blocks = 65536;
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, ws.outbuf,
-                     ws.slot_pos, x.topk_w, x.T, x.k, x.H, x.has_shared, x.y);
+              static_cast<const int32_t*>(ws.slot_pos), x.topk_w, x.T, x.k, x.H, x.has_shared, x.y);
   return hipGetLastError();
 }
 

@@ -676,9 +676,9 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
   else hipLaunchKernelGGL(route_select_kernel<8>, dim3(sel_blocks), sb, 0, stream, k);
   err = hipGetLastError();
   if (err != hipSuccess || !r.do_permute || sel_blocks == 1 || k.fuse_permute) return err;
-  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, k.topk_idx, r.T, r.k, r.E,
-                     r.has_shared, ws.offsets, r.offsets_out, ws.active, ws.n_active, k.sorted_slots,
-                     k.slot_pos, k.desc, k.seg_tok);
+  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, k.topk_idx, r.T, r.k,
+              r.E, r.has_shared, ws.offsets, r.offsets_out, ws.active, ws.n_active, k.sorted_slots, k.slot_pos,
+              k.desc, k.seg_tok);
   return hipGetLastError();
 }
 

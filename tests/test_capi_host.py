@@ -156,3 +156,16 @@ def test_synth_configs_and_determinism():
                                   np.array([0x3F80], np.uint16))
     np.testing.assert_array_equal(synth.f32_to_bf16_bits(np.array([1.0 + 3 * 2.0 ** -8], np.float32)),
                                   np.array([0x3F82], np.uint16))
+
+
+def test_profile_events_validation():
+    """The timing hook takes the documented number of non-null events or NULL."""
+    lib = _lib.load()
+    hdr = open(os.path.join(os.path.dirname(__file__), "..", "include", "phantom_moe.h")).read()
+    n = int(re.search(r"#define PHANTOM_MOE_PROFILE_EVENTS (\d+)", hdr).group(1))
+    assert lib.phantom_moe_set_profile_events(None, 0) == 0
+    short = (ctypes.c_void_p * n)(*([FAKE] * n))
+    assert lib.phantom_moe_set_profile_events(short, n - 1) == EINVAL
+    holes = (ctypes.c_void_p * n)(*([FAKE] * (n - 1) + [None]))
+    assert lib.phantom_moe_set_profile_events(holes, n) == EINVAL
+    assert lib.phantom_moe_set_profile_events(None, 0) == 0

@@ -268,3 +268,40 @@ def test_layer_properties(dev):
                                            torch.from_numpy(down2).to(dev), cfg.H, cfg.I, cfg.E)
     y3 = phantom_moe.moe_forward(x, W, ex2, cfg.k)
     assert torch.equal(y3, 2 * y1)
+
+
+def test_profiled_forward_is_identical(dev):
+    """Stage timing changes no output bit and brackets every stage."""
+    import ctypes
+
+    from phantom_moe import _lib
+
+    cfg = synth.CONFIGS["qwen3_decode_t32_zipf"]
+    dl = synth.device_layer(cfg, dev)
+    ex = phantom_moe.MoEWeights.from_q4_0(dl.gate, dl.up, dl.down, cfg.H, cfg.I, cfg.E)
+    x = to_bf16_tensor(synth.activations(cfg.T, cfg.H), dev)
+    y0 = phantom_moe.moe_forward(x, dl.router_w, ex, cfg.k, cfg.score, dl.router_bias)
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+    hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    n = 5
+    evs = []
+    for _ in range(n):
+        e = ctypes.c_void_p()
+        assert hip.hipEventCreateWithFlags(ctypes.byref(e), 0) == 0
+        evs.append(e.value)
+    arr = (ctypes.c_void_p * n)(*evs)
+    lib = _lib.load()
+    try:
+        assert lib.phantom_moe_set_profile_events(arr, n) == 0
+        y1 = phantom_moe.moe_forward(x, dl.router_w, ex, cfg.k, cfg.score, dl.router_bias)
+    finally:
+        assert lib.phantom_moe_set_profile_events(None, 0) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)
+    ms = ctypes.c_float()
+    for i in range(n - 1):
+        assert hip.hipEventElapsedTime(ctypes.byref(ms), evs[i], evs[i + 1]) == 0 and ms.value > 0, i
+    for e in evs:
+        hip.hipEventDestroy(ctypes.c_void_p(e))
