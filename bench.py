@@ -36,7 +36,19 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 STAGES = ("route", "gate_up", "down", "combine")
 HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000  # a record needs no system-scope release
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
-PMC_SUMMARY = os.path.join(ROOT, "profiles", "gate_up_kernel_qwen3_decode_t32_zipf_pmc.json")
+PREFILL_T = 1024  # from this batch on, a workload is priced against the MFMA roofline
+
+
+def pmc_summary(workload: str) -> str:
+    return os.path.join(ROOT, "profiles", f"gate_up_kernel_{workload}_pmc.json")
+
+
+def metric_name(cfg) -> str:
+    shape = {2048: "Qwen3-30B-A3B-shaped", 4096: "Mixtral-8x7B-shaped", 7168: "DeepSeek-V3-style"}.get(
+        cfg.H, f"H={cfg.H}")
+    regime = "prefill" if cfg.T >= PREFILL_T else "decode"
+    extra = ", Zipf-skewed routing" if cfg.zipf else ""
+    return f"MoE-layer {regime} tokens/s ({shape} layer, batch {cfg.T}{extra})"
 
 
 def parse_args():
@@ -99,6 +111,10 @@ def layer_bytes(cfg, U: int) -> int:
     experts (+ shared), the fp32 router weight, bf16 x in and fp32 y out."""
     experts = (U + (1 if cfg.shared else 0)) * 3 * cfg.H * cfg.I * 18 // 32
     return experts + cfg.E * cfg.H * 4 + cfg.T * cfg.H * 2 + cfg.T * cfg.H * 4
+
+
+def gate_up_flops(cfg) -> int:
+    return 2 * cfg.T * (cfg.k + (1 if cfg.shared else 0)) * 2 * cfg.H * cfg.I
 
 
 def layer_flops(cfg) -> int:
@@ -228,7 +244,7 @@ def main():
 
     value = cfg.T * args.steps / elapsed
     out = {
-        "metric": "MoE-layer decode tokens/s (Qwen3-30B-A3B-shaped layer, batch 32, Zipf-skewed routing)",
+        "metric": metric_name(cfg),
         "value": round(value, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -253,22 +269,24 @@ def main():
         gu_bytes = float(sum(gate_up_bytes(cfg, u) for u in steps_U))
         achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
         traffic = None
-        if os.path.exists(PMC_SUMMARY):
-            with open(PMC_SUMMARY) as f:
+        if os.path.exists(pmc_summary(cfg.name)):
+            with open(pmc_summary(cfg.name)) as f:
                 pmc = json.load(f)
             if pmc.get("workload") == cfg.name:
                 traffic = pmc.get("hbm_bytes_per_launch")
-        out["roofline"] = {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
+        if cfg.T >= PREFILL_T:
+            tf = gate_up_flops(cfg) * args.steps / (gu_ms * 1e-3) / 1e12
+            out["roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
+                               "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
+                               "algorithmic_flops_per_launch": gate_up_flops(cfg)}
+        else:
+            out["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                               "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
+        out["roofline"].update({
             "kernel": "gate_up_kernel",
             "algorithmic_bytes_per_launch": round(gu_bytes / args.steps),
             "avg_launch_us": round(gu_ms * 1e3 / args.steps, 3),
-        }
+        })
         lay_ms = float(np.sum(layer_ms))
         lay_bytes = float(sum(layer_bytes(cfg, u) for u in steps_U))
         out["layer"] = {

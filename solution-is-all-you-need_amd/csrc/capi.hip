@@ -270,7 +270,9 @@ int phantom_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_
   r.score_mode = score_mode;
   r.topk_idx = topk_idx;
   r.topk_w = topk_w;
+  const bool gemm = pmoe::gemm_regime(T, top_k, E);
   r.prep_x = true;
+  r.prep_fp16 = gemm;
   r.do_permute = true;
   r.has_shared = has_shared;
   if (int rc = launch_status(record_stage(0, stream), "profile event")) return rc;
@@ -297,16 +299,17 @@ int phantom_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_
   a.sh_down_scale = sh_down_scale;
   a.topk_w = topk_w;
   a.y = y;
-  if (g_prof_events) {
-    if (int rc = launch_status(record_stage(1, stream), "profile event")) return rc;
-    if (int rc = launch_status(pmoe::launch_gate_up(a, ws, stream), "gate_up")) return rc;
-    if (int rc = launch_status(record_stage(2, stream), "profile event")) return rc;
-    if (int rc = launch_status(pmoe::launch_down(a, ws, stream), "down")) return rc;
-    if (int rc = launch_status(record_stage(3, stream), "profile event")) return rc;
-    if (int rc = launch_status(pmoe::launch_combine(a, ws, stream), "combine")) return rc;
-    return launch_status(record_stage(4, stream), "profile event");
-  }
-  return launch_status(pmoe::launch_experts(a, ws, stream), "experts");
+  if (int rc = launch_status(record_stage(1, stream), "profile event")) return rc;
+  if (int rc = launch_status(gemm ? pmoe::launch_gemm_gate_up(a, ws, stream) : pmoe::launch_gate_up(a, ws, stream),
+                             "gate_up"))
+    return rc;
+  if (int rc = launch_status(record_stage(2, stream), "profile event")) return rc;
+  if (int rc = launch_status(gemm ? pmoe::launch_gemm_down(a, ws, stream) : pmoe::launch_down(a, ws, stream),
+                             "down"))
+    return rc;
+  if (int rc = launch_status(record_stage(3, stream), "profile event")) return rc;
+  if (int rc = launch_status(pmoe::launch_combine(a, ws, stream), "combine")) return rc;
+  return launch_status(record_stage(4, stream), "profile event");
 }
 
 }  // extern "C"

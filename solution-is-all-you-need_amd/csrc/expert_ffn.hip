@@ -30,17 +30,11 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include "expert_common.h"
 #include "moe_common.h"
 #include "moe_launch.h"
 
 namespace pmoe {
-
-struct SegSrc {
-  const int4* desc;        // [max_slots] {expert, begin, end, 0}; expert -1 = unused slot
-  const int32_t* seg_tok;  // token of each segment position
-  int E;
-  int max_slots;           // min(E, T*k) + shared
-};
 
 struct GateUpK {
   SegSrc seg;
@@ -77,27 +71,6 @@ struct DownK {
   int64_t zero_row;  // hq / hs row that holds zeros
   float* outbuf;
 };
-
-__device__ inline void unpack_scales(uint2 s, float d[4]) {
-  d[0] = half_bits_to_float((uint16_t)(s.x & 0xffffu));
-  d[1] = half_bits_to_float((uint16_t)(s.x >> 16));
-  d[2] = half_bits_to_float((uint16_t)(s.y & 0xffffu));
-  d[3] = half_bits_to_float((uint16_t)(s.y >> 16));
-}
-
-// Copies the launch slots' segment descriptors into LDS; returns how many
-// slots are in use (they come first; unused slots carry expert -1).
-__device__ inline int load_descriptors(const SegSrc& seg, int4* s_desc, int* s_nact) {
-  if (threadIdx.x == 0) *s_nact = 0;
-  __syncthreads();
-  for (int u = threadIdx.x; u < seg.max_slots; u += blockDim.x) {
-    const int4 d = seg.desc[u];
-    s_desc[u] = d;
-    if (d.x >= 0 && (u + 1 == seg.max_slots || seg.desc[u + 1].x < 0)) *s_nact = u + 1;
-  }
-  __syncthreads();
-  return *s_nact;
-}
 
 // ------------------------------------------------------------------ gate/up
 
@@ -422,56 +395,6 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     }
     *reinterpret_cast<float4*>(y + t * H + c) = acc;
   }
-}
-
-static unsigned max_active_experts(const ExpertArgs& x) {
-  const int64_t nslots = x.T * x.k;
-  return (unsigned)(((nslots < x.E) ? nslots : x.E) + (x.has_shared ? 1 : 0));
-}
-
-static SegSrc segments_of(const ExpertArgs& x, const Workspace& ws) {
-  SegSrc seg;
-  seg.desc = ws.desc;
-  seg.seg_tok = ws.seg_tok;
-  seg.E = x.E;
-  seg.max_slots = (int)max_active_experts(x);
-  return seg;
-}
-
-static int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
-// Workgroups for a strided item loop: those resident at once (occupancy of
-// this kernel at this block size, cached per kernel since the query is slow),
-// capped by the largest possible item count.
-template <typename Kernel>
-static unsigned resident_grid(Kernel kernel, int block, int64_t max_items) {
-  struct Entry {
-    const void* fn;
-    int block, per_cu;
-  };
-  static thread_local Entry cache[32];
-  static thread_local int n_cache = 0;
-  int per_cu = 0;
-  for (int i = 0; i < n_cache; ++i)
-    if (cache[i].fn == reinterpret_cast<const void*>(kernel) && cache[i].block == block) per_cu = cache[i].per_cu;
-  if (per_cu == 0) {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess || per_cu < 1)
-      per_cu = 1;
-    if (n_cache < 32) cache[n_cache++] = Entry{reinterpret_cast<const void*>(kernel), block, per_cu};
-  }
-  int64_t g = (int64_t)device_cus() * per_cu;
-  if (g > max_items) g = max_items;
-  return (unsigned)(g < 1 ? 1 : g);
 }
 
 // K split: ksplit waves (at most max_waves) take about two quads each (few

@@ -1,0 +1,460 @@
+// expert_gemm.hip -- grouped int4 (Q4_0) expert SwiGLU FFN for gfx950,
+// prefill regime: each expert segment is dense enough (tens to hundreds of
+// tokens) to be a real GEMM, so the work runs on the matrix cores.
+//
+// Reference operator: kernels/sparse_moe/sparse_matmul.cu:120-215 and its
+// dense branch (:322-365, cuBLAS GEMMs for gate/up and down, SwiGLU between),
+// with the expert weights of python/phantom/loader/gguf_loader.py:362-381.
+//
+// Operands are exact, as in the decode regime, and fp16 for
+// v_mfma_f32_16x16x32_f16, so the products are exact and only the fp32
+// accumulation rounds:
+//   A  gate/up: x rounded bf16 -> fp16 by the router's prep (exact for
+//      2^-17 <= |x| < 65504, the fp16 range a bf16 value fits); down: h as
+//      the fp16 pair hi + lo written by the gate/up epilogue.
+//   B  the weight q * d with q = n - 8 and the fp16 scale split d = dh + dl,
+//      dh = d with its 3 low mantissa bits cleared: q has at most 3
+//      significant bits, so q * dh (<= 11 bits) and q * dl (<= 6 bits) are
+//      both exact fp16 values (for normal d and |q d| < 65504).  The nibble
+//      becomes the fp16 value 1024 + n (one v_and_or_b32 per pair), one
+//      v_pk_add_f16 gives q, two v_pk_mul_f16 give the two operands.
+// gate/up: acc += A.Bh + A.Bl (2 MFMAs per group, chained in the
+// accumulators).  down: acc += hi.Bh + hi.Bl + lo.Bh (3 MFMAs; lo.Bl is below
+// 2^-20 of the product and dropped).  The scale lives inside the operands, so
+// there is no per-group vector-ALU work on the accumulators.
+//
+// Tiling.  A workgroup of kGemmWaves waves owns BM consecutive positions of
+// one expert segment and a block of weight rows.  Per K quad (128), the
+// positions' A rows are staged in LDS (double-buffered; 16-byte units XOR-
+// swizzled by row so the ds_read_b128 of 16 rows hit distinct banks) and every
+// wave multiplies them with kGemmNB weight row tiles of its own, dequantised
+// from its own 128-bit loads (the repacked layout hands each lane exactly its
+// B operand).  Each B operand feeds BM / 16 MFMAs.
+//   gate/up (BM 128): wave w takes one 32-row group of I (two 16-row tiles)
+//            for both gate and up (4 B operands), so its SwiGLU epilogue
+//            produces whole down-operand chunks (hi + lo, written via LDS).
+//   down (BM 64): wave w takes four 16-row tiles of H.
+#include <math.h>
+
+#include "expert_common.h"
+#include "moe_common.h"
+#include "moe_launch.h"
+
+namespace pmoe {
+
+constexpr int kGemmWaves = 4;
+constexpr int kGemmNB = 4;                     // B operands per wave per group
+constexpr int kGemmBMGateUp = 128;             // segment positions per gate/up tile
+constexpr int kGemmBMDown = 64;                // segment positions per down tile
+constexpr int kGemmRowsGU = kGemmWaves * 32;   // rows of I per gate/up workgroup
+constexpr int kGemmRowsDown = kGemmWaves * 64; // rows of H per down workgroup
+// LDS bytes of the double-buffered A tile: BM rows x 16 chunks x AW x 16 B
+constexpr int kGemmLdsA = 2 * kGemmBMGateUp * 16 * 16;
+static_assert(kGemmLdsA == 2 * kGemmBMDown * 32 * 16, "both tiles use the same LDS");
+
+struct GemmK {
+  SegSrc seg;
+  const uint16_t* a_src;  // fp16 rows [rows][Kq][16 chunks][AW x 8] in MFMA operand order
+  int64_t a_zero_row;     // an all-zero row of a_src
+  int a_by_token;         // 1: A row = token of the position (x); 0: A row = position (h)
+  int64_t Kq;             // quads of K
+  int64_t Kg;             // real 32-groups of K (padded groups of a_src are ignored)
+  int64_t N;              // rows of the weight matrices (I for gate/up, H for down)
+  // weights: [E][N/16][Kq][1 KiB] nibbles, [E][N/16][Kq][64] fp16 scales;
+  // w1 = gate (or down), w2 = up (gate/up only); sh_* the shared expert's
+  const uint8_t* nib1;
+  const uint16_t* sc1;
+  const uint8_t* nib2;
+  const uint16_t* sc2;
+  const uint8_t* sh_nib1;
+  const uint16_t* sh_sc1;
+  const uint8_t* sh_nib2;
+  const uint16_t* sh_sc2;
+  // gate/up output: h as fp16 hi + lo [rows + 1][KqI][16 chunks][hi 8, lo 8],
+  // the decode regime's down operand (its half-group sums are not written)
+  uint16_t* hq16;
+  int64_t KqI;
+  int64_t h_zero_row;
+  // down output: fp32 [rows][H]
+  float* outbuf;
+};
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+// B operands of one 32-group: the lane's four nibble bytes w (bytes 4p..4p+3
+// of the group's qs for its row) and the group's fp16 scale bits d -> the
+// eight q * dh and the eight q * dl, fp16, in kmap order.
+__device__ inline void dequant_split_f16(uint32_t w, uint32_t d, uint32_t mask, u32x4& bh, u32x4& bl) {
+  const h2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
+  const uint32_t dh = d & 0xFFF8u;
+  const _Float16 dlv = __builtin_bit_cast(_Float16, (uint16_t)d) - __builtin_bit_cast(_Float16, (uint16_t)dh);
+  const h2_t dh2 = __builtin_bit_cast(h2_t, dh | (dh << 16));
+  const h2_t dl2 = {dlv, dlv};
+  const uint32_t r[4] = {and_or(w, mask, 0x64006400u), and_or(w >> 4, mask, 0x64006400u),
+                         and_or(w >> 8, mask, 0x64006400u), and_or(w >> 12, mask, 0x64006400u)};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const h2_t q = __builtin_bit_cast(h2_t, r[i]) - off;  // n - 8, exact
+    bh[i] = __builtin_bit_cast(uint32_t, q * dh2);       // exact
+    bl[i] = __builtin_bit_cast(uint32_t, q * dl2);       // exact
+  }
+}
+
+// Item space: for each active segment u, ceil(len_u / BM) position blocks
+// times n_nb row blocks.  s_mb[u] = first position block of segment u (an
+// exclusive prefix over segments, computed by wave 0).
+template <int BM>
+__device__ inline int64_t plan_items(const int4* s_desc, int n_act, int* s_mb) {
+  if (threadIdx.x < kWave) {
+    const int lane = threadIdx.x;
+    int carry = 0;
+    for (int u0 = 0; u0 < n_act; u0 += kWave) {
+      const int u = u0 + lane;
+      const int len = u < n_act ? s_desc[u].z - s_desc[u].y : 0;
+      const int v = (len + BM - 1) / BM;
+      int inc = v;
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const int t = __shfl_up(inc, off, kWave);
+        if (lane >= off) inc += t;
+      }
+      if (u < n_act) s_mb[u] = carry + inc - v;
+      carry += __shfl(inc, kWave - 1, kWave);
+    }
+    if (lane == 0) s_mb[n_act] = carry;
+  }
+  __syncthreads();
+  return s_mb[n_act];
+}
+
+// Segment holding position block mb: the last u with s_mb[u] <= mb (binary
+// search; every lane computes the same answer).
+__device__ inline int segment_of_block(const int* s_mb, int n_act, int64_t mb) {
+  int lo = 0, hi = n_act - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (s_mb[mid] <= mb) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// One (segment, position block, row block) tile: acc[b][tt] += sum over K of
+// A(positions 16 tt ..) x B_b, B operand b of the wave being weight row tile
+// rt[b] of matrix (nib[b], sc[b]).  A rows hold AW 16-byte units per chunk
+// (1: fp16 x; 2: fp16 hi then lo of h).
+template <int BM, int AW>
+__device__ inline void gemm_tile(const GemmK& a, const int64_t* s_row, u32x4* lds_a,
+                                 const uint8_t* const nib[kGemmNB], const uint16_t* const sc[kGemmNB],
+                                 const int64_t rt[kGemmNB], f32x4 acc[kGemmNB][BM / 16]) {
+  constexpr int TT = BM / 16;
+  constexpr int PITCH = 16 * AW;          // 16-byte units per LDS row
+  constexpr int TPR = 256 / BM;           // staging threads per row, 8 units (128 B) each
+  // Unit u of row r is stored at u ^ swz(r): the 16 rows a ds_read_b128 of one
+  // 16-lane group touches then sit in 16 distinct bank quads.
+  auto swz = [](int row) { return (row & 15) * AW; };
+  static_assert(TPR * 8 == 16 * AW, "a thread stages 8 units of its row");
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int n = lane % 16;
+  const int p = lane / 16;
+  const uint32_t mask = vgpr_const(0x000F000Fu);
+  const int r = tid / TPR;
+  const int u0 = (tid % TPR) * 8;         // first unit of the row this thread moves
+  const uint16_t* arow = a.a_src + s_row[r] * a.Kq * (128 * AW) + u0 * 8;
+  u32x4 an[8];
+  u32x4 bw[kGemmNB], bn[kGemmNB];
+  uint2 bs[kGemmNB], bsn[kGemmNB];
+  auto load_a = [&](int64_t q) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) an[i] = reinterpret_cast<const u32x4*>(arow + q * (128 * AW))[i];
+  };
+  auto store_a = [&](int64_t q, int buf) {
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    u32x4* dst = lds_a + (buf * BM + r) * PITCH;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int gi = ((u0 + i) / AW) % 4;  // chunk (p, gi): padded groups read 0
+      dst[(u0 + i) ^ swz(r)] = (4 * q + gi < a.Kg) ? an[i] : zero;
+    }
+  };
+  auto load_b = [&](int64_t q, u32x4* w, uint2* sv) {
+#pragma unroll
+    for (int b = 0; b < kGemmNB; ++b) {
+      const int64_t tq = rt[b] * a.Kq + q;
+      w[b] = *reinterpret_cast<const u32x4*>(nib[b] + tq * kQuadNibBytes + lane * 16);
+      sv[b] = *reinterpret_cast<const uint2*>(sc[b] + tq * kQuadScales + n * 4);
+    }
+  };
+  load_a(0);
+  load_b(0, bw, bs);
+  store_a(0, 0);
+  __syncthreads();
+  for (int64_t q = 0; q < a.Kq; ++q) {
+    const int cur = (int)(q & 1);
+    const bool more = q + 1 < a.Kq;
+    if (more) {
+      load_a(q + 1);
+      load_b(q + 1, bn, bsn);
+    }
+    const u32x4* la = lds_a + cur * BM * PITCH;
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+      u32x4 bh[kGemmNB], bl[kGemmNB];
+#pragma unroll
+      for (int b = 0; b < kGemmNB; ++b) {
+        const uint32_t s2 = gi < 2 ? bs[b].x : bs[b].y;
+        dequant_split_f16(bw[b][gi], (gi % 2) ? (s2 >> 16) : (s2 & 0xffffu), mask, bh[b], bl[b]);
+      }
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        const u32x4* row = la + (tt * 16 + n) * PITCH;
+        const int unit = (p * 4 + gi) * AW;
+        const u32x4 ah = row[unit ^ swz(n)];
+#pragma unroll
+        for (int b = 0; b < kGemmNB; ++b) {
+          acc[b][tt] = mfma_f16_16x16x32(ah, bh[b], acc[b][tt]);
+          acc[b][tt] = mfma_f16_16x16x32(ah, bl[b], acc[b][tt]);
+        }
+        if constexpr (AW == 2) {
+          const u32x4 al = row[(unit + 1) ^ swz(n)];
+#pragma unroll
+          for (int b = 0; b < kGemmNB; ++b) acc[b][tt] = mfma_f16_16x16x32(al, bh[b], acc[b][tt]);
+        }
+      }
+    }
+    if (more) {
+      store_a(q + 1, cur ^ 1);
+#pragma unroll
+      for (int b = 0; b < kGemmNB; ++b) {
+        bw[b] = bn[b];
+        bs[b] = bsn[b];
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Shared prologue of both kernels: descriptors, item plan, and the A row of
+// every position of the tile.
+struct TileCoord {
+  int e;
+  int64_t m0, end;
+  int64_t nb;
+};
+
+template <int BM>
+__device__ inline TileCoord tile_coord(const GemmK& a, const int4* s_desc, const int* s_mb, int n_act,
+                                       int64_t item, int64_t n_nb, int64_t* s_row) {
+  TileCoord c;
+  const int64_t mb = item / n_nb;
+  c.nb = item % n_nb;
+  const int u = segment_of_block(s_mb, n_act, mb);
+  const int4 d = s_desc[u];
+  c.e = __builtin_amdgcn_readfirstlane(d.x);
+  c.m0 = (int64_t)d.y + (mb - s_mb[u]) * BM;
+  c.end = d.z;
+  if (threadIdx.x < BM) {
+    const int64_t pos = c.m0 + threadIdx.x;
+    int64_t row = a.a_zero_row;
+    if (pos < c.end) row = a.a_by_token ? (int64_t)a.seg.seg_tok[pos] : pos;
+    s_row[threadIdx.x] = row;
+  }
+  __syncthreads();
+  return c;
+}
+
+__global__ __launch_bounds__(kGemmWaves * kWave) void gemm_gate_up_kernel(GemmK a) {
+  constexpr int BM = kGemmBMGateUp;
+  constexpr int TT = BM / 16;
+  __shared__ u32x4 lds_a[kGemmLdsA / 16];
+  __shared__ int4 s_desc[kMaxExperts + 1];
+  __shared__ int s_mb[kMaxExperts + 2];
+  __shared__ int64_t s_row[BM];
+  __shared__ int s_nact;
+  const int lane = threadIdx.x % kWave;
+  const int w = threadIdx.x / kWave;
+  const int n = lane % 16;
+  const int p = lane / 16;
+  if (blockIdx.x == 0) {
+    // the all-zero down-operand row read for positions past a segment
+    for (int64_t i = threadIdx.x; i < a.KqI * 256; i += blockDim.x) a.hq16[a.h_zero_row * a.KqI * 256 + i] = 0;
+  }
+  const int n_act = load_descriptors(a.seg, s_desc, &s_nact);
+  const int64_t n_mb = plan_items<BM>(s_desc, n_act, s_mb);
+  const int64_t n_nb = ceil_div(a.N, kGemmRowsGU);
+  const int64_t n_groups = a.N / kGroup;
+  for (int64_t item = blockIdx.x; item < n_mb * n_nb; item += gridDim.x) {
+    const TileCoord c = tile_coord<BM>(a, s_desc, s_mb, n_act, item, n_nb, s_row);
+    const int64_t g = c.nb * kGemmWaves + w;             // this wave's 32-row group of I
+    const int64_t gc = g < n_groups ? g : n_groups - 1;  // a group past I computes, unstored
+    const int64_t nib_stride = a.N * a.Kq * 64, sc_stride = a.N * a.Kq * 4;
+    const bool routed = c.e < a.seg.E;
+    const uint8_t* g_nib = routed ? a.nib1 + c.e * nib_stride : a.sh_nib1;
+    const uint16_t* g_sc = routed ? a.sc1 + c.e * sc_stride : a.sh_sc1;
+    const uint8_t* u_nib = routed ? a.nib2 + c.e * nib_stride : a.sh_nib2;
+    const uint16_t* u_sc = routed ? a.sc2 + c.e * sc_stride : a.sh_sc2;
+    const uint8_t* const nib[kGemmNB] = {g_nib, u_nib, g_nib, u_nib};
+    const uint16_t* const sc[kGemmNB] = {g_sc, u_sc, g_sc, u_sc};
+    const int64_t rt[kGemmNB] = {2 * gc, 2 * gc, 2 * gc + 1, 2 * gc + 1};
+    f32x4 acc[kGemmNB][TT];
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b = 0; b < kGemmNB; ++b)
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) acc[b][tt] = z;
+    gemm_tile<BM, 1>(a, s_row, lds_a, nib, sc, rt, acc);
+
+    // SwiGLU, then h as the fp16 pair hi + lo into this wave's LDS scratch in
+    // down-operand chunk order [position][part p'][hi 8, lo 8]: element
+    // cc = half * 16 + n of the group sits at j' = kmap^-1(p', cc).
+    uint16_t* hs = reinterpret_cast<uint16_t*>(lds_a) + w * BM * 64;
+    const int pp = n / 4;
+    const int rr = n % 4;
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = tt * 16 + 4 * p + j;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const float gv = acc[2 * half][tt][j];
+          const float uv = acc[2 * half + 1][tt][j];
+          const float hv = gv * (1.0f / (1.0f + expf(-gv))) * uv;
+          const uint32_t hb = float_to_half_bits(hv);
+          const uint32_t lb = float_to_half_bits(hv - half_bits_to_float32(hb));
+          const int jj = half == 0 ? ((rr & 1) ? 4 : 0) + (rr >> 1) : ((rr & 1) ? 6 : 2) + (rr >> 1);
+          hs[(m * 4 + pp) * 16 + jj] = (uint16_t)hb;
+          hs[(m * 4 + pp) * 16 + 8 + jj] = (uint16_t)lb;
+        }
+      }
+    }
+    __syncthreads();
+    if (g < n_groups) {
+      for (int cidx = lane; cidx < BM * 4; cidx += kWave) {
+        const int m = cidx / 4;
+        const int p2 = cidx % 4;
+        const int64_t pos = c.m0 + m;
+        if (pos < c.end) {
+          const u32x4* src = reinterpret_cast<const u32x4*>(hs + (m * 4 + p2) * 16);
+          u32x4* dst = reinterpret_cast<u32x4*>(a.hq16 + ((pos * a.KqI + g / 4) * 16 + p2 * 4 + g % 4) * 16);
+          dst[0] = src[0];
+          dst[1] = src[1];
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(kGemmWaves * kWave) void gemm_down_kernel(GemmK a) {
+  constexpr int BM = kGemmBMDown;
+  constexpr int TT = BM / 16;
+  __shared__ u32x4 lds_a[kGemmLdsA / 16];
+  __shared__ int4 s_desc[kMaxExperts + 1];
+  __shared__ int s_mb[kMaxExperts + 2];
+  __shared__ int64_t s_row[BM];
+  __shared__ int s_nact;
+  const int lane = threadIdx.x % kWave;
+  const int w = threadIdx.x / kWave;
+  const int n = lane % 16;
+  const int p = lane / 16;
+  const int n_act = load_descriptors(a.seg, s_desc, &s_nact);
+  const int64_t n_mb = plan_items<BM>(s_desc, n_act, s_mb);
+  const int64_t n_nb = ceil_div(a.N, kGemmRowsDown);
+  const int64_t n_tiles = a.N / kRowTile;
+  for (int64_t item = blockIdx.x; item < n_mb * n_nb; item += gridDim.x) {
+    const TileCoord c = tile_coord<BM>(a, s_desc, s_mb, n_act, item, n_nb, s_row);
+    const int64_t nib_stride = a.N * a.Kq * 64, sc_stride = a.N * a.Kq * 4;
+    const bool routed = c.e < a.seg.E;
+    const uint8_t* d_nib = routed ? a.nib1 + c.e * nib_stride : a.sh_nib1;
+    const uint16_t* d_sc = routed ? a.sc1 + c.e * sc_stride : a.sh_sc1;
+    const uint8_t* const nib[kGemmNB] = {d_nib, d_nib, d_nib, d_nib};
+    const uint16_t* const sc[kGemmNB] = {d_sc, d_sc, d_sc, d_sc};
+    int64_t rt[kGemmNB];
+#pragma unroll
+    for (int b = 0; b < kGemmNB; ++b) {
+      const int64_t t = (c.nb * kGemmWaves + w) * kGemmNB + b;
+      rt[b] = t < n_tiles ? t : n_tiles - 1;  // a tile past H computes, unstored
+    }
+    f32x4 acc[kGemmNB][TT];
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b = 0; b < kGemmNB; ++b)
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) acc[b][tt] = z;
+    gemm_tile<BM, 2>(a, s_row, lds_a, nib, sc, rt, acc);
+#pragma unroll
+    for (int b = 0; b < kGemmNB; ++b) {
+      const int64_t t = (c.nb * kGemmWaves + w) * kGemmNB + b;
+      if (t >= n_tiles) continue;
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t pos = c.m0 + tt * 16 + 4 * p + j;
+          if (pos < c.end) a.outbuf[pos * a.N + t * 16 + n] = acc[b][tt][j];
+        }
+      }
+    }
+  }
+}
+
+bool gemm_regime(int64_t T, int k, int E) {
+  const int64_t slots = T * k;
+  const int64_t seg_max = slots < E ? slots : E;
+  return slots >= kGemmMinSlotsPerExpert * seg_max;
+}
+
+static int64_t gemm_max_items(const ExpertArgs& x, int BM, int64_t n_nb) {
+  const int64_t rows = x.T * x.k + (x.has_shared ? x.T : 0);
+  return (ceil_div(rows, BM) + max_active_experts(x)) * n_nb;
+}
+
+hipError_t launch_gemm_gate_up(const ExpertArgs& x, const Workspace& ws, hipStream_t stream) {
+  GemmK g = {};
+  g.seg = segments_of(x, ws);
+  g.a_src = ws.xq;
+  g.a_zero_row = x.T;
+  g.a_by_token = 1;
+  g.Kq = ceil_div(x.H, kQuad);
+  g.Kg = x.H / kGroup;
+  g.N = x.I;
+  g.nib1 = x.gate_nib;
+  g.sc1 = x.gate_scale;
+  g.nib2 = x.up_nib;
+  g.sc2 = x.up_scale;
+  g.sh_nib1 = x.sh_gate_nib;
+  g.sh_sc1 = x.sh_gate_scale;
+  g.sh_nib2 = x.sh_up_nib;
+  g.sh_sc2 = x.sh_up_scale;
+  g.hq16 = ws.hq;
+  g.KqI = ceil_div(x.I, kQuad);
+  g.h_zero_row = x.T * x.k + (x.has_shared ? x.T : 0);
+  const int64_t max_items = gemm_max_items(x, kGemmBMGateUp, ceil_div(x.I, kGemmRowsGU));
+  hipLaunchKernelGGL(gemm_gate_up_kernel, dim3(resident_grid(gemm_gate_up_kernel, kGemmWaves * kWave, max_items)),
+                     dim3(kGemmWaves * kWave), 0, stream, g);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_down(const ExpertArgs& x, const Workspace& ws, hipStream_t stream) {
+  GemmK g = {};
+  g.seg = segments_of(x, ws);
+  g.a_src = ws.hq;
+  g.a_zero_row = x.T * x.k + (x.has_shared ? x.T : 0);
+  g.a_by_token = 0;
+  g.Kq = ceil_div(x.I, kQuad);
+  g.Kg = x.I / kGroup;
+  g.N = x.H;
+  g.nib1 = x.down_nib;
+  g.sc1 = x.down_scale;
+  g.sh_nib1 = x.sh_down_nib;
+  g.sh_sc1 = x.sh_down_scale;
+  g.outbuf = ws.outbuf;
+  const int64_t max_items = gemm_max_items(x, kGemmBMDown, ceil_div(x.H, kGemmRowsDown));
+  hipLaunchKernelGGL(gemm_down_kernel, dim3(resident_grid(gemm_down_kernel, kGemmWaves * kWave, max_items)),
+                     dim3(kGemmWaves * kWave), 0, stream, g);
+  return hipGetLastError();
+}
+
+}  // namespace pmoe

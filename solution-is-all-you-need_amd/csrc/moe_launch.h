@@ -56,6 +56,7 @@ struct RouteArgs {
   int32_t* topk_idx;
   float* topk_w;
   bool prep_x;       // write ws.xq / ws.xs
+  bool prep_fp16;    // ws.xq as fp16 (GEMM regime) instead of bf16 (GEMV regime)
   bool do_permute;   // write offsets / sorted_slots / slot_pos / active
   int has_shared;    // append the shared-expert segment to offsets / active
   int32_t* offsets_out;       // optional user copy of offsets [E+1]
@@ -87,6 +88,14 @@ struct ExpertArgs {
   const float* topk_w;
   float* y;
 };
+// Prefill regime: when the average segment holds at least this many slots,
+// the expert stages run as grouped MFMA GEMMs (expert_gemm.hip) on fp16
+// operands; below it, as the grouped GEMV (expert_ffn.hip).
+constexpr int kGemmMinSlotsPerExpert = 64;
+bool gemm_regime(int64_t T, int k, int E);
+hipError_t launch_gemm_gate_up(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);
+hipError_t launch_gemm_down(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);
+
 // The three expert stages; launch_experts runs them back to back.
 hipError_t launch_gate_up(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);
 hipError_t launch_down(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);

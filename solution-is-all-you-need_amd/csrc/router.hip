@@ -51,6 +51,7 @@ struct RouteK {
   float* xs;
   int64_t Kq;  // quads of H (padded)
   int prep_x;
+  int prep_fp16;  // xq holds fp16 (rounded from bf16) instead of bf16
   // permute
   int do_permute;
   int has_shared;
@@ -414,6 +415,14 @@ __device__ void prep_x_tile(const RouteK& a, int64_t t0, int TT) {
              (bf16_bits_to_float(lo.y & 0xffffu) + bf16_bits_to_float(lo.y >> 16))) +
             ((bf16_bits_to_float(hi.x & 0xffffu) + bf16_bits_to_float(hi.x >> 16)) +
              (bf16_bits_to_float(hi.y & 0xffffu) + bf16_bits_to_float(hi.y >> 16)));
+      if (a.prep_fp16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t b2 = v[i];
+          v[i] = float_to_half_bits(bf16_bits_to_float(b2 & 0xffffu)) |
+                 (float_to_half_bits(bf16_bits_to_float(b2 >> 16)) << 16);
+        }
+      }
     }
     sum += __shfl_xor(sum, 4, kWave);
     sum += __shfl_xor(sum, 8, kWave);
@@ -650,6 +659,7 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
   k.xs = ws.xs;
   k.Kq = ceil_div(r.H, kQuad);
   k.prep_x = r.prep_x ? 1 : 0;
+  k.prep_fp16 = r.prep_fp16 ? 1 : 0;
   k.do_permute = r.do_permute ? 1 : 0;
   k.has_shared = r.has_shared;
   k.offsets = ws.offsets;

@@ -205,6 +205,11 @@ SMALL_CASES = [
     synth.MoEConfig("sigmoid_shared", 512, 128, 32, 4, 12, score="sigmoid", shared=True),
     synth.MoEConfig("zipf", 1024, 256, 128, 8, 32, zipf=1.1),
     synth.MoEConfig("k1", 128, 32, 4, 1, 3),
+    # GEMM regime (T*k >= 64 * min(E, T*k)): fp16 operands, 128-position tiles
+    synth.MoEConfig("gemm_e4", 256, 128, 4, 2, 200),
+    synth.MoEConfig("gemm_multi_block", 256, 256, 2, 2, 300),
+    synth.MoEConfig("gemm_ragged_k_and_rows", 416, 96, 3, 1, 257),
+    synth.MoEConfig("gemm_sigmoid_shared", 512, 256, 8, 2, 300, score="sigmoid", shared=True),
 ]
 
 
