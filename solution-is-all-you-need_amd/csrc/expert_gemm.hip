@@ -27,13 +27,13 @@
 // one expert segment and a block of weight rows.  Per K quad (128), the
 // positions' A rows are staged in LDS (double-buffered; 16-byte units XOR-
 // swizzled by row so the ds_read_b128 of 16 rows hit distinct banks) and every
-// wave multiplies them with kGemmNB weight row tiles of its own, dequantised
+// wave multiplies them with NB weight row tiles of its own, dequantised
 // from its own 128-bit loads (the repacked layout hands each lane exactly its
 // B operand).  Each B operand feeds BM / 16 MFMAs.
 //   gate/up (BM 128): wave w takes one 32-row group of I (two 16-row tiles)
 //            for both gate and up (4 B operands), so its SwiGLU epilogue
 //            produces whole down-operand chunks (hi + lo, written via LDS).
-//   down (BM 64): wave w takes four 16-row tiles of H.
+//   down (BM 64): wave w takes two 16-row tiles of H.
 #include <math.h>
 
 #include "expert_common.h"
@@ -43,11 +43,14 @@
 namespace pmoe {
 
 constexpr int kGemmWaves = 4;
-constexpr int kGemmNB = 4;                     // B operands per wave per group
+constexpr int kGemmNBGateUp = 2;               // B operands per wave: gate and up of one 16-row tile
+constexpr int kGemmNBDown = 2;                 // B operands per wave: two 16-row tiles of H
 constexpr int kGemmBMGateUp = 128;             // segment positions per gate/up tile
 constexpr int kGemmBMDown = 64;                // segment positions per down tile
-constexpr int kGemmRowsGU = kGemmWaves * 32;   // rows of I per gate/up workgroup
-constexpr int kGemmRowsDown = kGemmWaves * 64; // rows of H per down workgroup
+constexpr int kGemmRowsGU = kGemmWaves * 16;   // rows of I per gate/up workgroup (two groups)
+constexpr int kGemmRowsDown = kGemmWaves * 32; // rows of H per down workgroup
+constexpr bool kGemmSplitGateUp = true;        // split-scale operands (else fp32 scaling)
+constexpr bool kGemmSplitDown = true;
 // LDS bytes of the double-buffered A tile: BM rows x 16 chunks x AW x 16 B
 constexpr int kGemmLdsA = 2 * kGemmBMGateUp * 16 * 16;
 static_assert(kGemmLdsA == 2 * kGemmBMDown * 32 * 16, "both tiles use the same LDS");
@@ -80,6 +83,18 @@ struct GemmK {
 };
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+// B operand of one 32-group: the lane's four nibble bytes w (bytes 4p..4p+3 of
+// the group's qs for its row) -> the eight fp16 integers n - 8 in kmap order.
+__device__ inline u32x4 dequant_int_f16(uint32_t w, uint32_t mask) {
+  const h2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
+  const uint32_t r[4] = {and_or(w, mask, 0x64006400u), and_or(w >> 4, mask, 0x64006400u),
+                         and_or(w >> 8, mask, 0x64006400u), and_or(w >> 12, mask, 0x64006400u)};
+  u32x4 out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) out[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, r[i]) - off);
+  return out;
+}
 
 // B operands of one 32-group: the lane's four nibble bytes w (bytes 4p..4p+3
 // of the group's qs for its row) and the group's fp16 scale bits d -> the
@@ -143,44 +158,45 @@ __device__ inline int segment_of_block(const int* s_mb, int n_act, int64_t mb) {
 // A(positions 16 tt ..) x B_b, B operand b of the wave being weight row tile
 // rt[b] of matrix (nib[b], sc[b]).  A rows hold AW 16-byte units per chunk
 // (1: fp16 x; 2: fp16 hi then lo of h).
-template <int BM, int AW>
+template <int BM, int AW, int NB, bool SPLIT>
 __device__ inline void gemm_tile(const GemmK& a, const int64_t* s_row, u32x4* lds_a,
-                                 const uint8_t* const nib[kGemmNB], const uint16_t* const sc[kGemmNB],
-                                 const int64_t rt[kGemmNB], f32x4 acc[kGemmNB][BM / 16]) {
+                                 const uint8_t* const nib[NB], const uint16_t* const sc[NB],
+                                 const int64_t rt[NB], f32x4 acc[NB][BM / 16]) {
   constexpr int TT = BM / 16;
   constexpr int PITCH = 16 * AW;          // 16-byte units per LDS row
-  constexpr int TPR = 256 / BM;           // staging threads per row, 8 units (128 B) each
+  constexpr int TPR = 256 / BM;           // staging threads per row
+  constexpr int UPT = 16 * AW / TPR;      // 16-byte units each staging thread moves
   // Unit u of row r is stored at u ^ swz(r): the 16 rows a ds_read_b128 of one
   // 16-lane group touches then sit in 16 distinct bank quads.
   auto swz = [](int row) { return (row & 15) * AW; };
-  static_assert(TPR * 8 == 16 * AW, "a thread stages 8 units of its row");
+  static_assert(TPR * UPT == 16 * AW && UPT >= 1, "staging threads cover a row");
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int n = lane % 16;
   const int p = lane / 16;
   const uint32_t mask = vgpr_const(0x000F000Fu);
   const int r = tid / TPR;
-  const int u0 = (tid % TPR) * 8;         // first unit of the row this thread moves
+  const int u0 = (tid % TPR) * UPT;       // first unit of the row this thread moves
   const uint16_t* arow = a.a_src + s_row[r] * a.Kq * (128 * AW) + u0 * 8;
-  u32x4 an[8];
-  u32x4 bw[kGemmNB], bn[kGemmNB];
-  uint2 bs[kGemmNB], bsn[kGemmNB];
+  u32x4 an[UPT];
+  u32x4 bw[NB], bn[NB];
+  uint2 bs[NB], bsn[NB];
   auto load_a = [&](int64_t q) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) an[i] = reinterpret_cast<const u32x4*>(arow + q * (128 * AW))[i];
+    for (int i = 0; i < UPT; ++i) an[i] = reinterpret_cast<const u32x4*>(arow + q * (128 * AW))[i];
   };
   auto store_a = [&](int64_t q, int buf) {
     const u32x4 zero = {0u, 0u, 0u, 0u};
     u32x4* dst = lds_a + (buf * BM + r) * PITCH;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < UPT; ++i) {
       const int gi = ((u0 + i) / AW) % 4;  // chunk (p, gi): padded groups read 0
       dst[(u0 + i) ^ swz(r)] = (4 * q + gi < a.Kg) ? an[i] : zero;
     }
   };
   auto load_b = [&](int64_t q, u32x4* w, uint2* sv) {
 #pragma unroll
-    for (int b = 0; b < kGemmNB; ++b) {
+    for (int b = 0; b < NB; ++b) {
       const int64_t tq = rt[b] * a.Kq + q;
       w[b] = *reinterpret_cast<const u32x4*>(nib[b] + tq * kQuadNibBytes + lane * 16);
       sv[b] = *reinterpret_cast<const uint2*>(sc[b] + tq * kQuadScales + n * 4);
@@ -198,41 +214,92 @@ __device__ inline void gemm_tile(const GemmK& a, const int64_t* s_row, u32x4* ld
       load_b(q + 1, bn, bsn);
     }
     const u32x4* la = lds_a + cur * BM * PITCH;
-#pragma unroll
+    // the scaled form keeps one group's MFMA results live at a time
+#pragma unroll(SPLIT ? 4 : 1)
     for (int gi = 0; gi < 4; ++gi) {
-      u32x4 bh[kGemmNB], bl[kGemmNB];
+      if constexpr (SPLIT) {
+        u32x4 bh[NB], bl[NB];
 #pragma unroll
-      for (int b = 0; b < kGemmNB; ++b) {
-        const uint32_t s2 = gi < 2 ? bs[b].x : bs[b].y;
-        dequant_split_f16(bw[b][gi], (gi % 2) ? (s2 >> 16) : (s2 & 0xffffu), mask, bh[b], bl[b]);
-      }
-#pragma unroll
-      for (int tt = 0; tt < TT; ++tt) {
-        const u32x4* row = la + (tt * 16 + n) * PITCH;
-        const int unit = (p * 4 + gi) * AW;
-        const u32x4 ah = row[unit ^ swz(n)];
-#pragma unroll
-        for (int b = 0; b < kGemmNB; ++b) {
-          acc[b][tt] = mfma_f16_16x16x32(ah, bh[b], acc[b][tt]);
-          acc[b][tt] = mfma_f16_16x16x32(ah, bl[b], acc[b][tt]);
+        for (int b = 0; b < NB; ++b) {
+          const uint32_t s2 = gi < 2 ? bs[b].x : bs[b].y;
+          dequant_split_f16(bw[b][gi], (gi % 2) ? (s2 >> 16) : (s2 & 0xffffu), mask, bh[b], bl[b]);
         }
-        if constexpr (AW == 2) {
-          const u32x4 al = row[(unit + 1) ^ swz(n)];
 #pragma unroll
-          for (int b = 0; b < kGemmNB; ++b) acc[b][tt] = mfma_f16_16x16x32(al, bh[b], acc[b][tt]);
+        for (int tt = 0; tt < TT; ++tt) {
+          const u32x4* row = la + (tt * 16 + n) * PITCH;
+          const int unit = (p * 4 + gi) * AW;
+          const u32x4 ah = row[unit ^ swz(n)];
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            acc[b][tt] = mfma_f16_16x16x32(ah, bh[b], acc[b][tt]);
+            acc[b][tt] = mfma_f16_16x16x32(ah, bl[b], acc[b][tt]);
+          }
+          if constexpr (AW == 2) {
+            const u32x4 al = row[(unit + 1) ^ swz(n)];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) acc[b][tt] = mfma_f16_16x16x32(al, bh[b], acc[b][tt]);
+          }
+        }
+      } else {
+        // exact group sums P = A . (n - 8), then acc += d * P in fp32
+        u32x4 bq[NB];
+        float d[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          float dv[4];
+          unpack_scales(bs[b], dv);
+          d[b] = dv[gi];
+          bq[b] = dequant_int_f16(bw[b][gi], mask);
+        }
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+          const u32x4* row = la + (tt * 16 + n) * PITCH;
+          const int unit = (p * 4 + gi) * AW;
+          const u32x4 ah = row[unit ^ swz(n)];
+          u32x4 al = ah;
+          if constexpr (AW == 2) al = row[(unit + 1) ^ swz(n)];
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            f32x4 pv = mfma_f16_16x16x32(ah, bq[b], z);
+            if constexpr (AW == 2) pv = mfma_f16_16x16x32(al, bq[b], pv);
+            acc[b][tt] += d[b] * pv;
+          }
         }
       }
     }
     if (more) {
       store_a(q + 1, cur ^ 1);
 #pragma unroll
-      for (int b = 0; b < kGemmNB; ++b) {
+      for (int b = 0; b < NB; ++b) {
         bw[b] = bn[b];
         bs[b] = bsn[b];
       }
     }
     __syncthreads();
   }
+}
+
+// XCD-aware item order.  Workgroups are dispatched to the 8 XCDs round-robin
+// (workgroup b on XCD b % 8), each XCD with its own L2.  Position block mb is
+// handled only by the workgroups of XCD mb % 8, all its row blocks by
+// neighbouring workgroups there, so the block's A rows come from HBM once and
+// then from that L2.  Blocks (not segments) are dealt out, so one large
+// segment still spreads over every XCD.
+struct XcdPlan {
+  int nx, x;
+  int64_t l, nl, n_items;
+};
+
+__device__ inline XcdPlan xcd_plan(int64_t n_mb, int64_t n_nb) {
+  XcdPlan q;
+  q.nx = gridDim.x < 8 ? (int)gridDim.x : 8;
+  q.x = (int)(blockIdx.x % q.nx);
+  q.l = blockIdx.x / q.nx;
+  q.nl = ((int64_t)gridDim.x - q.x + q.nx - 1) / q.nx;
+  const int64_t mbs = n_mb > q.x ? (n_mb - q.x + q.nx - 1) / q.nx : 0;  // blocks of this XCD
+  q.n_items = mbs * n_nb;
+  return q;
 }
 
 // Shared prologue of both kernels: descriptors, item plan, and the A row of
@@ -245,9 +312,9 @@ struct TileCoord {
 
 template <int BM>
 __device__ inline TileCoord tile_coord(const GemmK& a, const int4* s_desc, const int* s_mb, int n_act,
-                                       int64_t item, int64_t n_nb, int64_t* s_row) {
+                                       const XcdPlan& xp, int64_t item, int64_t n_nb, int64_t* s_row) {
   TileCoord c;
-  const int64_t mb = item / n_nb;
+  const int64_t mb = (item / n_nb) * xp.nx + xp.x;
   c.nb = item % n_nb;
   const int u = segment_of_block(s_mb, n_act, mb);
   const int4 d = s_desc[u];
@@ -283,64 +350,64 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void gemm_gate_up_kernel(GemmK 
   const int n_act = load_descriptors(a.seg, s_desc, &s_nact);
   const int64_t n_mb = plan_items<BM>(s_desc, n_act, s_mb);
   const int64_t n_nb = ceil_div(a.N, kGemmRowsGU);
-  const int64_t n_groups = a.N / kGroup;
-  for (int64_t item = blockIdx.x; item < n_mb * n_nb; item += gridDim.x) {
-    const TileCoord c = tile_coord<BM>(a, s_desc, s_mb, n_act, item, n_nb, s_row);
-    const int64_t g = c.nb * kGemmWaves + w;             // this wave's 32-row group of I
-    const int64_t gc = g < n_groups ? g : n_groups - 1;  // a group past I computes, unstored
+  const XcdPlan xp = xcd_plan(n_mb, n_nb);
+  for (int64_t item = xp.l; item < xp.n_items; item += xp.nl) {
+    const TileCoord c = tile_coord<BM>(a, s_desc, s_mb, n_act, xp, item, n_nb, s_row);
+    const int64_t n_tiles = a.N / kRowTile;
+    const int64_t t = c.nb * kGemmWaves + w;             // this wave's 16-row tile of I
+    const int64_t tc = t < n_tiles ? t : n_tiles - 1;    // a tile past I computes, unstored
     const int64_t nib_stride = a.N * a.Kq * 64, sc_stride = a.N * a.Kq * 4;
     const bool routed = c.e < a.seg.E;
-    const uint8_t* g_nib = routed ? a.nib1 + c.e * nib_stride : a.sh_nib1;
-    const uint16_t* g_sc = routed ? a.sc1 + c.e * sc_stride : a.sh_sc1;
-    const uint8_t* u_nib = routed ? a.nib2 + c.e * nib_stride : a.sh_nib2;
-    const uint16_t* u_sc = routed ? a.sc2 + c.e * sc_stride : a.sh_sc2;
-    const uint8_t* const nib[kGemmNB] = {g_nib, u_nib, g_nib, u_nib};
-    const uint16_t* const sc[kGemmNB] = {g_sc, u_sc, g_sc, u_sc};
-    const int64_t rt[kGemmNB] = {2 * gc, 2 * gc, 2 * gc + 1, 2 * gc + 1};
-    f32x4 acc[kGemmNB][TT];
+    const uint8_t* const nib[2] = {routed ? a.nib1 + c.e * nib_stride : a.sh_nib1,
+                                   routed ? a.nib2 + c.e * nib_stride : a.sh_nib2};
+    const uint16_t* const sc[2] = {routed ? a.sc1 + c.e * sc_stride : a.sh_sc1,
+                                   routed ? a.sc2 + c.e * sc_stride : a.sh_sc2};
+    const int64_t rt[2] = {tc, tc};
+    f32x4 acc[2][TT];
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int b = 0; b < kGemmNB; ++b)
+    for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) acc[b][tt] = z;
-    gemm_tile<BM, 1>(a, s_row, lds_a, nib, sc, rt, acc);
+    gemm_tile<BM, 1, 2, kGemmSplitGateUp>(a, s_row, lds_a, nib, sc, rt, acc);
 
-    // SwiGLU, then h as the fp16 pair hi + lo into this wave's LDS scratch in
-    // down-operand chunk order [position][part p'][hi 8, lo 8]: element
-    // cc = half * 16 + n of the group sits at j' = kmap^-1(p', cc).
-    uint16_t* hs = reinterpret_cast<uint16_t*>(lds_a) + w * BM * 64;
+    // SwiGLU, then h as the fp16 pair hi + lo into LDS in down-operand chunk
+    // order [group of the workgroup][position][part p'][hi 8, lo 8]: element
+    // cc = half * 16 + n of a group sits at j' = kmap^-1(p', cc), half = w % 2.
+    uint16_t* hs = reinterpret_cast<uint16_t*>(lds_a);
+    const int gl = w / 2;  // group of the workgroup this wave's tile belongs to
+    const int half = w % 2;
     const int pp = n / 4;
     const int rr = n % 4;
+    const int jj = half == 0 ? ((rr & 1) ? 4 : 0) + (rr >> 1) : ((rr & 1) ? 6 : 2) + (rr >> 1);
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int m = tt * 16 + 4 * p + j;
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const float gv = acc[2 * half][tt][j];
-          const float uv = acc[2 * half + 1][tt][j];
-          const float hv = gv * (1.0f / (1.0f + expf(-gv))) * uv;
-          const uint32_t hb = float_to_half_bits(hv);
-          const uint32_t lb = float_to_half_bits(hv - half_bits_to_float32(hb));
-          const int jj = half == 0 ? ((rr & 1) ? 4 : 0) + (rr >> 1) : ((rr & 1) ? 6 : 2) + (rr >> 1);
-          hs[(m * 4 + pp) * 16 + jj] = (uint16_t)hb;
-          hs[(m * 4 + pp) * 16 + 8 + jj] = (uint16_t)lb;
-        }
+        const float gv = acc[0][tt][j];
+        const float uv = acc[1][tt][j];
+        const float hv = gv * (1.0f / (1.0f + expf(-gv))) * uv;
+        const uint32_t hb = float_to_half_bits(hv);
+        const uint32_t lb = float_to_half_bits(hv - half_bits_to_float32(hb));
+        uint16_t* chunk = hs + ((gl * BM + m) * 4 + pp) * 16;
+        chunk[jj] = (uint16_t)hb;
+        chunk[8 + jj] = (uint16_t)lb;
       }
     }
     __syncthreads();
-    if (g < n_groups) {
-      for (int cidx = lane; cidx < BM * 4; cidx += kWave) {
-        const int m = cidx / 4;
-        const int p2 = cidx % 4;
-        const int64_t pos = c.m0 + m;
-        if (pos < c.end) {
-          const u32x4* src = reinterpret_cast<const u32x4*>(hs + (m * 4 + p2) * 16);
-          u32x4* dst = reinterpret_cast<u32x4*>(a.hq16 + ((pos * a.KqI + g / 4) * 16 + p2 * 4 + g % 4) * 16);
-          dst[0] = src[0];
-          dst[1] = src[1];
-        }
+    // the workgroup's two groups: BM positions x 4 parts x 2 groups chunks
+    for (int cidx = threadIdx.x; cidx < 2 * BM * 4; cidx += blockDim.x) {
+      const int g2 = cidx / (BM * 4);
+      const int m = (cidx / 4) % BM;
+      const int p2 = cidx % 4;
+      const int64_t g = c.nb * 2 + g2;  // group of I
+      const int64_t pos = c.m0 + m;
+      if (pos < c.end && 2 * g + 1 < n_tiles) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(hs + ((g2 * BM + m) * 4 + p2) * 16);
+        u32x4* dst = reinterpret_cast<u32x4*>(a.hq16 + ((pos * a.KqI + g / 4) * 16 + p2 * 4 + g % 4) * 16);
+        dst[0] = src[0];
+        dst[1] = src[1];
       }
     }
     __syncthreads();
@@ -363,30 +430,33 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void gemm_down_kernel(GemmK a) 
   const int64_t n_mb = plan_items<BM>(s_desc, n_act, s_mb);
   const int64_t n_nb = ceil_div(a.N, kGemmRowsDown);
   const int64_t n_tiles = a.N / kRowTile;
-  for (int64_t item = blockIdx.x; item < n_mb * n_nb; item += gridDim.x) {
-    const TileCoord c = tile_coord<BM>(a, s_desc, s_mb, n_act, item, n_nb, s_row);
+  const XcdPlan xp = xcd_plan(n_mb, n_nb);
+  for (int64_t item = xp.l; item < xp.n_items; item += xp.nl) {
+    const TileCoord c = tile_coord<BM>(a, s_desc, s_mb, n_act, xp, item, n_nb, s_row);
     const int64_t nib_stride = a.N * a.Kq * 64, sc_stride = a.N * a.Kq * 4;
     const bool routed = c.e < a.seg.E;
     const uint8_t* d_nib = routed ? a.nib1 + c.e * nib_stride : a.sh_nib1;
     const uint16_t* d_sc = routed ? a.sc1 + c.e * sc_stride : a.sh_sc1;
-    const uint8_t* const nib[kGemmNB] = {d_nib, d_nib, d_nib, d_nib};
-    const uint16_t* const sc[kGemmNB] = {d_sc, d_sc, d_sc, d_sc};
-    int64_t rt[kGemmNB];
+    const uint8_t* nib[kGemmNBDown];
+    const uint16_t* sc[kGemmNBDown];
+    int64_t rt[kGemmNBDown];
 #pragma unroll
-    for (int b = 0; b < kGemmNB; ++b) {
-      const int64_t t = (c.nb * kGemmWaves + w) * kGemmNB + b;
+    for (int b = 0; b < kGemmNBDown; ++b) {
+      nib[b] = d_nib;
+      sc[b] = d_sc;
+      const int64_t t = (c.nb * kGemmWaves + w) * kGemmNBDown + b;
       rt[b] = t < n_tiles ? t : n_tiles - 1;  // a tile past H computes, unstored
     }
-    f32x4 acc[kGemmNB][TT];
+    f32x4 acc[kGemmNBDown][TT];
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int b = 0; b < kGemmNB; ++b)
+    for (int b = 0; b < kGemmNBDown; ++b)
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) acc[b][tt] = z;
-    gemm_tile<BM, 2>(a, s_row, lds_a, nib, sc, rt, acc);
+    gemm_tile<BM, 2, kGemmNBDown, kGemmSplitDown>(a, s_row, lds_a, nib, sc, rt, acc);
 #pragma unroll
-    for (int b = 0; b < kGemmNB; ++b) {
-      const int64_t t = (c.nb * kGemmWaves + w) * kGemmNB + b;
+    for (int b = 0; b < kGemmNBDown; ++b) {
+      const int64_t t = (c.nb * kGemmWaves + w) * kGemmNBDown + b;
       if (t >= n_tiles) continue;
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) {
