@@ -86,113 +86,133 @@ constexpr int kGateUpWaves = 8;
 // seg_end.  Token tiles are taken TP at a time: each dequantised weight
 // operand feeds TP MFMAs, so the nibble expansion is paid once per 16 TP
 // tokens.
-template <int NQ, int TP>
-__device__ inline void gate_up_pass(const GateUpK& a, const int e, const int64_t seg_end, const int64_t m0,
-                                    const int64_t rt, float (*red)[1][2][16][16]) {
+// A pass is one 16-token tile of RT 16-row tiles of I of one segment.  Each
+// wave works a pass one quad of K at a time.  Passes are software-pipelined:
+// right after a pass's MFMAs, and before its epilogue, every wave issues the
+// loads of the next pass's first chunk, so their latency overlaps the
+// cross-wave reduction and the epilogue, and the epilogue's stores (younger
+// than those loads) never sit in the wait for them.
+struct GUPass {
+  int e;             // expert (E = the shared expert)
+  int64_t end;       // segment end position
+  int64_t m0;        // first position of the tile
+  int64_t rt;        // 16-row tile of I
+  uint32_t xoff;     // this lane's activation row (times Kq)
+};
+
+// One quad of K for RT row tiles: their gate and up nibbles and scales, and
+// the 16 tokens' activation operand they share.
+template <int RT>
+struct GUChunk {
+  u32x4 gw[RT], uw[RT];
+  uint2 gs[RT], us[RT];
+  u32x4 xa[4];
+  float sx;
+};
+
+template <bool TOK_LDS>
+__device__ __attribute__((always_inline)) inline GUPass gu_pass(const GateUpK& a, const int* s_tok, const int4 d, int64_t m0, int64_t rt) {
+  GUPass ps;
+  ps.e = __builtin_amdgcn_readfirstlane(d.x);
+  ps.end = __builtin_amdgcn_readfirstlane(d.z);
+  ps.m0 = m0;
+  ps.rt = rt;
+  // token of the lane's position: from the LDS copy when the kernel made
+  // one, else one unconditional global load (clamped index); row T is zero
+  const int64_t pm = m0 + threadIdx.x % 16;
+  const int64_t pc = pm < ps.end ? pm : ps.end - 1;
+  int64_t tv;
+  if constexpr (TOK_LDS) tv = s_tok[pc];
+  else tv = a.seg.seg_tok[pc];
+  ps.xoff = (uint32_t)((pm < ps.end ? tv : a.T) * a.Kq);
+  return ps;
+}
+
+// Loads of quad q of the pass's RT row tiles (rt0 .. rt0 + RT - 1).
+template <int RT>
+__device__ __attribute__((always_inline)) inline void gu_load(const GateUpK& a, const GUPass& ps, int64_t q, GUChunk<RT>& c) {
   const int lane = threadIdx.x % kWave;
-  const int ks = threadIdx.x / kWave;
-  const int ksplit = blockDim.x / kWave;
   const int n = lane % 16;
   const int p = lane / 16;
-  const uint32_t mask = vgpr_const(0x00780078u);
   const int64_t nib_stride = a.I * a.Kq * 64;
   const int64_t sc_stride = a.I * a.Kq * 4;
-  const uint8_t* gnib = e < a.seg.E ? a.gate_nib + e * nib_stride : a.sh_gate_nib;
-  const uint16_t* gsc = e < a.seg.E ? a.gate_sc + e * sc_stride : a.sh_gate_sc;
-  const uint8_t* unib = e < a.seg.E ? a.up_nib + e * nib_stride : a.sh_up_nib;
-  const uint16_t* usc = e < a.seg.E ? a.up_sc + e * sc_stride : a.sh_up_sc;
-  uint32_t xoff[TP];  // element offset of this lane's activation row
+  const bool routed = ps.e < a.seg.E;
+  const uint8_t* gnib = routed ? a.gate_nib + ps.e * nib_stride : a.sh_gate_nib;
+  const uint16_t* gsc = routed ? a.gate_sc + ps.e * sc_stride : a.sh_gate_sc;
+  const uint8_t* unib = routed ? a.up_nib + ps.e * nib_stride : a.sh_up_nib;
+  const uint16_t* usc = routed ? a.up_sc + ps.e * sc_stride : a.sh_up_sc;
+  // Wave-uniform bases plus 32-bit lane offsets: each load is one SGPR-base
+  // access with a single VGPR offset instead of a per-lane 64-bit address.
+  const uint32_t o_nib = (uint32_t)lane * 16u;
+  const uint32_t o_sc = (uint32_t)n * 8u;
 #pragma unroll
-  for (int t = 0; t < TP; ++t) {
-    const int64_t pm = m0 + 16 * t + n;
-    const int64_t tok = pm < seg_end ? (int64_t)a.seg.seg_tok[pm] : a.T;  // row T is all zero
-    xoff[t] = (uint32_t)(tok * a.Kq);
+  for (int r = 0; r < RT; ++r) {
+    const int64_t tq = (ps.rt + r) * a.Kq + q;  // wave-uniform
+    const char* gb = uniform_ptr(reinterpret_cast<const char*>(gnib) + tq * kQuadNibBytes);
+    const char* ub = uniform_ptr(reinterpret_cast<const char*>(unib) + tq * kQuadNibBytes);
+    const char* gsb = uniform_ptr(reinterpret_cast<const char*>(gsc) + tq * kQuadScales * 2);
+    const char* usb = uniform_ptr(reinterpret_cast<const char*>(usc) + tq * kQuadScales * 2);
+    c.gw[r] = *reinterpret_cast<const u32x4*>(gb + o_nib);
+    c.uw[r] = *reinterpret_cast<const u32x4*>(ub + o_nib);
+    c.gs[r] = *reinterpret_cast<const uint2*>(gsb + o_sc);
+    c.us[r] = *reinterpret_cast<const uint2*>(usb + o_sc);
   }
+  const uint32_t xrow = ps.xoff + (uint32_t)q;  // (token, quad) row of xq / xs
+  const char* xb = reinterpret_cast<const char*>(a.xq);
+  const uint32_t o_x = (xrow * 16u + (uint32_t)p * 4u) * 16u;
+#pragma unroll
+  for (int gi = 0; gi < 4; ++gi) c.xa[gi] = *reinterpret_cast<const u32x4*>(xb + (o_x + gi * 16u));
+  c.sx = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.xs) + (xrow * 4u + (uint32_t)p) * 4u);
+}
+
+template <int RT>
+__device__ __attribute__((always_inline)) inline void gu_math(const GUChunk<RT>& c, f32x4 (&ag)[RT], f32x4 (&au)[RT], f32x4 (&cg)[RT],
+                               f32x4 (&cu)[RT]) {
+  const int p = (threadIdx.x % kWave) / 16;
+  const uint32_t mask = vgpr_const(0x00780078u);
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-  f32x4 ag[TP], au[TP], cg[TP], cu[TP];
 #pragma unroll
-  for (int t = 0; t < TP; ++t) ag[t] = au[t] = cg[t] = cu[t] = z;
-  for (int64_t q0 = ks; q0 < a.Kq; q0 += (int64_t)NQ * ksplit) {
-    u32x4 gw[NQ], uw[NQ];
-    uint2 gs[NQ], us[NQ];
-    u32x4 xa[NQ][TP][4];
-    float sx[NQ][TP];
-    bool qok[NQ];
+  for (int r = 0; r < RT; ++r) {
+    float dg[4], du[4];
+    unpack_scales(c.gs[r], dg);
+    unpack_scales(c.us[r], du);
+    const uint32_t gwv[4] = {c.gw[r].x, c.gw[r].y, c.gw[r].z, c.gw[r].w};
+    const uint32_t uwv[4] = {c.uw[r].x, c.uw[r].y, c.uw[r].z, c.uw[r].w};
 #pragma unroll
-    for (int i = 0; i < NQ; ++i) {
-      int q = (int)(q0 + (int64_t)i * ksplit);
-      qok[i] = q < a.Kq;
-      q = qok[i] ? q : (int)a.Kq - 1;
-      const int64_t tq = rt * a.Kq + q;  // wave-uniform
-      gw[i] = *reinterpret_cast<const u32x4*>(gnib + tq * kQuadNibBytes + lane * 16);
-      uw[i] = *reinterpret_cast<const u32x4*>(unib + tq * kQuadNibBytes + lane * 16);
-      gs[i] = *reinterpret_cast<const uint2*>(gsc + tq * kQuadScales + n * 4);
-      us[i] = *reinterpret_cast<const uint2*>(usc + tq * kQuadScales + n * 4);
-#pragma unroll
-      for (int t = 0; t < TP; ++t) {
-        const u32x4* xp =
-            reinterpret_cast<const u32x4*>(a.xq + ((uint64_t)(xoff[t] + q) * 16 + p * 4) * 8);
-#pragma unroll
-        for (int gi = 0; gi < 4; ++gi) xa[i][t][gi] = xp[gi];
-        sx[i][t] = a.xs[(uint64_t)(xoff[t] + q) * 4 + p];
-      }
+    for (int gi = 0; gi < 4; ++gi) {
+      const u32x4 bg = dequant_unit_bf16(gwv[gi], mask);
+      const u32x4 bu = dequant_unit_bf16(uwv[gi], mask);
+      ag[r] += dg[gi] * mfma_bf16_16x16x32(c.xa[gi], bg, z);
+      au[r] += du[gi] * mfma_bf16_16x16x32(c.xa[gi], bu, z);
     }
-#pragma unroll
-    for (int i = 0; i < NQ; ++i) {
-      if (!qok[i]) continue;
-      float dg[4], du[4];
-      unpack_scales(gs[i], dg);
-      unpack_scales(us[i], du);
-      const uint32_t gwv[4] = {gw[i].x, gw[i].y, gw[i].z, gw[i].w};
-      const uint32_t uwv[4] = {uw[i].x, uw[i].y, uw[i].z, uw[i].w};
-#pragma unroll
-      for (int gi = 0; gi < 4; ++gi) {
-        const u32x4 bg = dequant_unit_bf16(gwv[gi], mask);
-        const u32x4 bu = dequant_unit_bf16(uwv[gi], mask);
-#pragma unroll
-        for (int t = 0; t < TP; ++t) {
-          ag[t] += dg[gi] * mfma_bf16_16x16x32(xa[i][t][gi], bg, z);
-          au[t] += du[gi] * mfma_bf16_16x16x32(xa[i][t][gi], bu, z);
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < TP; ++t) {
-        cg[t] = mfma_f32_16x16x4(sx[i][t], dg[p], cg[t]);
-        cu[t] = mfma_f32_16x16x4(sx[i][t], du[p], cu[t]);
-      }
-    }
+    cg[r] = mfma_f32_16x16x4(c.sx, dg[p], cg[r]);
+    cu[r] = mfma_f32_16x16x4(c.sx, du[p], cu[r]);
   }
-#pragma unroll
-  for (int t = 0; t < TP; ++t) {
-    // sum_g d * sum_k a (n - 8) = 16 * sum_g d P - 24 * sum_g d S
-    const f32x4 rg = kUnitScale * ag[t] - kUnitBias * cg[t];
-    const f32x4 ru = kUnitScale * au[t] - kUnitBias * cu[t];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      red[ks][t][0][4 * p + j][n] = rg[j];
-      red[ks][t][1][4 * p + j][n] = ru[j];
-    }
-  }
-  __syncthreads();
-  for (int o = threadIdx.x; o < TP * 256; o += blockDim.x) {
-    const int t = o / 256;
+}
+
+// SwiGLU of the pass from the wave partials in red, written as the down
+// kernel's operand: fp16 pair hi + lo of h in MFMA operand order, plus the
+// half-group sums of hi + lo.
+template <int RT>
+__device__ __attribute__((always_inline)) inline void gu_epilogue(const GateUpK& a, const GUPass& ps, float (*red)[RT][2][16][16]) {
+  const int ksplit = blockDim.x / kWave;
+  for (int o = threadIdx.x; o < RT * 256; o += blockDim.x) {
+    const int r = o / 256;
     const int mm = (o % 256) / 16;
     const int nn = o % 16;
     float g = 0.0f, uu = 0.0f;
     for (int s2 = 0; s2 < ksplit; ++s2) {
-      g += red[s2][t][0][mm][nn];
-      uu += red[s2][t][1][mm][nn];
+      g += red[s2][r][0][mm][nn];
+      uu += red[s2][r][1][mm][nn];
     }
     const float h = g * (1.0f / (1.0f + expf(-g))) * uu;
-    // fp16 pair hi + lo of h, placed where the down kernel's MFMA operand
-    // for (segment position, group, part) expects element i of I.
     const uint32_t hb = float_to_half_bits(h);
     const float hf = half_bits_to_float32(hb);
     const uint32_t lb = float_to_half_bits(h - hf);
     const float lf = half_bits_to_float32(lb);
-    const int64_t pos = m0 + 16 * t + mm;
-    const bool ok = pos < seg_end;
-    const int64_t i = rt * 16 + nn;
+    const int64_t pos = ps.m0 + mm;
+    const bool ok = pos < ps.end;
+    const int64_t i = (ps.rt + r) * 16 + nn;
     const int64_t g32 = i / kGroup;
     const int cc = (int)(i % kGroup);
     const int half = cc / 16;
@@ -214,34 +234,78 @@ __device__ inline void gate_up_pass(const GateUpK& a, const int e, const int64_t
     sum += __shfl_xor(sum, 1, kWave);
     if (nn == 0 && ok) a.hs[(pos * a.KqI * 4 + g32) * 2 + half] = sum;
   }
-  __syncthreads();
 }
 
-template <int NQ>
-__device__ inline void gate_up_item(const GateUpK& a, const int4 d, const int64_t rt,
-                                    float (*red)[1][2][16][16]) {
-  const int e = __builtin_amdgcn_readfirstlane(d.x);
-  const int64_t beg = __builtin_amdgcn_readfirstlane(d.y);
-  const int64_t end = __builtin_amdgcn_readfirstlane(d.z);
-  // One 16-token tile at a time: a longer segment re-reads the tile's
-  // weights from L2, which costs less than the registers of a paired pass.
-  for (int64_t m0 = beg; m0 < end; m0 += 16) gate_up_pass<NQ, 1>(a, e, end, m0, rt, red);
-}
+// Segment-position token ids kept in LDS when they fit (decode batches).
+constexpr int kTokLds = 2048;
 
-template <int NQ>
+template <int RT, bool TOK_LDS>
 __global__ __launch_bounds__(kGateUpWaves * kWave, 4) void gate_up_kernel(GateUpK a) {
-  __shared__ float red[kGateUpWaves][1][2][16][16];  // [wave][token tile][gate/up]
+  __shared__ float red[kGateUpWaves][RT][2][16][16];  // [wave][row tile][gate/up]
   __shared__ int4 s_desc[kMaxExperts + 1];
+  __shared__ int s_tok[TOK_LDS ? kTokLds : 1];
   __shared__ int s_nact;
+  const int lane = threadIdx.x % kWave;
+  const int ks = threadIdx.x / kWave;
+  const int ksplit = blockDim.x / kWave;
+  const int n = lane % 16;
+  const int p = lane / 16;
+  if constexpr (TOK_LDS) {
+    for (int64_t i = threadIdx.x; i < a.zero_row; i += blockDim.x) s_tok[i] = a.seg.seg_tok[i];
+  }
   if (blockIdx.x == 0) {
     // the all-zero down-operand row read for positions past a segment
     for (int64_t i = threadIdx.x; i < a.KqI * 256; i += blockDim.x) a.hq[a.zero_row * a.KqI * 256 + i] = 0;
     for (int64_t i = threadIdx.x; i < a.KqI * 8; i += blockDim.x) a.hs[a.zero_row * a.KqI * 8 + i] = 0.0f;
   }
   const int n_act = load_descriptors(a.seg, s_desc, &s_nact);
-  const int64_t n_rt = a.I / kRowTile;
-  for (int64_t item = blockIdx.x; item < (int64_t)n_act * n_rt; item += gridDim.x)
-    gate_up_item<NQ>(a, s_desc[item / n_rt], item % n_rt, red);
+  const int64_t n_blk = a.I / (kRowTile * RT);  // RT-tile blocks of I per expert
+  const int64_t n_items = (int64_t)n_act * n_blk;
+  int64_t item = blockIdx.x;
+  if (item >= n_items) return;
+  // this wave's quads of K: ks, ks + ksplit, ... (nch of them)
+  const int64_t nch = ks < a.Kq ? (a.Kq - ks + ksplit - 1) / ksplit : 0;
+  GUPass ps = gu_pass<TOK_LDS>(a, s_tok, s_desc[item / n_blk], s_desc[item / n_blk].y, (item % n_blk) * RT);
+  GUChunk<RT> ck;
+  if (nch > 0) gu_load<RT>(a, ps, ks, ck);
+  for (;;) {
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    f32x4 ag[RT], au[RT], cg[RT], cu[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) ag[r] = au[r] = cg[r] = cu[r] = z;
+    for (int64_t c = 0; c < nch; ++c) {
+      gu_math<RT>(ck, ag, au, cg, cu);
+      if (c + 1 < nch) gu_load<RT>(a, ps, ks + (c + 1) * ksplit, ck);
+    }
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      // sum_g d * sum_k a (n - 8) = 16 * sum_g d P - 24 * sum_g d S
+      const f32x4 rg = kUnitScale * ag[r] - kUnitBias * cg[r];
+      const f32x4 ru = kUnitScale * au[r] - kUnitBias * cu[r];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        red[ks][r][0][4 * p + j][n] = rg[j];
+        red[ks][r][1][4 * p + j][n] = ru[j];
+      }
+    }
+    __syncthreads();
+    // next pass: the segment's next token tile, else the next item
+    GUPass nx = ps;
+    bool more = true;
+    if (ps.m0 + 16 < ps.end) {
+      nx = gu_pass<TOK_LDS>(a, s_tok, s_desc[item / n_blk], ps.m0 + 16, ps.rt);
+    } else {
+      item += gridDim.x;
+      more = item < n_items;
+      if (more)
+        nx = gu_pass<TOK_LDS>(a, s_tok, s_desc[item / n_blk], s_desc[item / n_blk].y, (item % n_blk) * RT);
+    }
+    if (more && nch > 0) gu_load<RT>(a, nx, ks, ck);
+    gu_epilogue<RT>(a, ps, red);
+    __syncthreads();
+    if (!more) break;
+    ps = nx;
+  }
 }
 
 
@@ -446,17 +510,21 @@ hipError_t launch_gate_up(const ExpertArgs& x, const Workspace& ws, hipStream_t 
   g.hq = ws.hq;
   g.hs = ws.hs;
   g.zero_row = x.T * x.k + (x.has_shared ? x.T : 0);
-  Split sp = choose_split(g.Kq, kGateUpWaves);
-  int rt = 1;
-  tiling_override("PHANTOM_MOE_GATE_UP_TILING", kGateUpWaves, &sp.ksplit, &rt, &sp.nq);
-  const int block = kWave * sp.ksplit;
+  // K split: about four quads per wave (fewer waves per item keep more items
+  // in flight per CU), one quad of loads outstanding per wave at a time.
+  const int64_t q4 = ceil_div(g.Kq, 4);
+  int ksplit = (int)(q4 < kGateUpWaves ? q4 : kGateUpWaves);
+  int rt = 1, nq = 1;
+  tiling_override("PHANTOM_MOE_GATE_UP_TILING", kGateUpWaves, &ksplit, &rt, &nq);
+  const int block = kWave * ksplit;
   const int64_t max_items = (int64_t)max_active_experts(x) * (x.I / kRowTile);
-  if (sp.nq == 1)
-    hipLaunchKernelGGL(gate_up_kernel<1>, dim3(resident_grid(gate_up_kernel<1>, block, max_items)), dim3(block), 0,
-                stream, g);
+  // segment positions (T*k + shared T) = g.zero_row; their token ids go to LDS when they fit
+  if (g.zero_row <= kTokLds)
+    hipLaunchKernelGGL((gate_up_kernel<1, true>), dim3(resident_grid(gate_up_kernel<1, true>, block, max_items)),
+                       dim3(block), 0, stream, g);
   else
-    hipLaunchKernelGGL(gate_up_kernel<2>, dim3(resident_grid(gate_up_kernel<2>, block, max_items)), dim3(block), 0,
-                stream, g);
+    hipLaunchKernelGGL((gate_up_kernel<1, false>), dim3(resident_grid(gate_up_kernel<1, false>, block, max_items)),
+                       dim3(block), 0, stream, g);
   return hipGetLastError();
 }
 

@@ -86,6 +86,17 @@ __device__ inline u32x4 dequant_unit_f16(uint32_t w, uint32_t mask) {
 }
 
 // A value the compiler must keep in a VGPR (for and_or masks).
+// A pointer the compiler cannot prove wave-uniform, made uniform (it must
+// already hold the same value in every lane), so loads from it plus a 32-bit
+// lane offset use the SGPR-base form.
+template <typename T>
+__device__ inline const T* uniform_ptr(const T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const T*>(((uint64_t)hi << 32) | lo);
+}
+
 __device__ inline uint32_t vgpr_const(uint32_t v) {
   uint32_t r;
   asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "s"(v));
