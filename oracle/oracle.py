@@ -58,6 +58,19 @@ def lib():
         L.oracle_half_to_float.restype = ctypes.c_float
         L.oracle_bf16_to_float.argtypes = [_u16p, _i64, _f32p]
         L.oracle_bf16_to_float.restype = None
+        # legacy_oracle.c
+        L.oracle_lg_dot.argtypes = [_u16p, _u16p, _i64, _int]
+        L.oracle_lg_dot.restype = ctypes.c_float
+        L.oracle_lg_f2h.argtypes = [ctypes.c_float]
+        L.oracle_lg_f2h.restype = ctypes.c_uint16
+        L.oracle_lg_predict.argtypes = [_u16p, _u16p, _vp, _i64, _i64, _i64, ctypes.c_float, _int,
+                                        _f32p, _u8p, _i32p, _i32p]
+        L.oracle_lg_predict.restype = None
+        L.oracle_lg_sparse_mlp.argtypes = [_u16p, _u16p, _vp, _u16p, _vp, _u16p, _vp, _vp,
+                                           _i64, _i64, _i64, ctypes.c_float, _int, _u16p]
+        L.oracle_lg_sparse_mlp.restype = _int
+        L.oracle_lg_sparsity.argtypes = [_i32p, _i64, _i64]
+        L.oracle_lg_sparsity.restype = ctypes.c_float
         _lib = L
     return _lib
 
@@ -182,3 +195,64 @@ def moe_forward(x, router_w, gate_q4, up_q4, down_q4, top_k: int, score_mode: in
     if rc:
         raise ValueError(f"oracle_moe_forward rejected the arguments (rc={rc})")
     return y, idx, w
+
+
+# ---------------------------------------------------------------------------
+# legacy neuron-sparse FFN ABI (legacy_oracle.c).  fp16 arrays are passed as
+# numpy float16 or as their uint16 bit patterns; order 0 is this build's fixed
+# summation order, order 1 the reference kernels' sequential loops.
+
+
+def _h16(a) -> np.ndarray:
+    a = np.asarray(a)
+    if a.dtype == np.float16:
+        a = a.view(np.uint16)
+    return np.ascontiguousarray(a, dtype=np.uint16)
+
+
+def lg_dot(w, x, order: int = 0) -> np.float32:
+    w, x = _h16(w).reshape(-1), _h16(x).reshape(-1)
+    assert w.size == x.size
+    return np.float32(lib().oracle_lg_dot(w, x, w.size, order))
+
+
+def lg_f2h(f: float) -> np.uint16:
+    """fp32 -> fp16 bits, round to nearest even (the oracle's own conversion)."""
+    return np.uint16(lib().oracle_lg_f2h(float(np.float32(f))))
+
+
+def lg_predict(x, w, bias, threshold: float, order: int = 0):
+    """predict_active_neurons: returns (gate [B,Dffn] f32, mask [B,Dffn] u8,
+    indices [B,Dffn] i32 (first count[b] valid, rest -1), count [B] i32)."""
+    x, w = _h16(x), _h16(w)
+    B, D = x.shape
+    D_ffn = w.shape[0]
+    b = None if bias is None else _h16(bias).reshape(-1)
+    gate = np.empty((B, D_ffn), np.float32)
+    mask = np.empty((B, D_ffn), np.uint8)
+    idx = np.full((B, D_ffn), -1, np.int32)
+    cnt = np.empty(B, np.int32)
+    lib().oracle_lg_predict(x, w, _ptr(b), B, D, D_ffn, float(np.float32(threshold)), order, gate, mask, idx, cnt)
+    return gate, mask, idx, cnt
+
+
+def lg_sparse_mlp(x, wg, bg, wu, bu, wd, idx, count, sparsity_pct: float, order: int = 0) -> np.ndarray:
+    """sparse_mlp_forward: returns y [B, D] as fp16 bits (uint16)."""
+    x, wg, wu, wd = _h16(x), _h16(wg), _h16(wu), _h16(wd)
+    B, D = x.shape
+    D_ffn = wg.shape[0]
+    bg = None if bg is None else _h16(bg).reshape(-1)
+    bu = None if bu is None else _h16(bu).reshape(-1)
+    idx = None if idx is None else np.ascontiguousarray(idx, dtype=np.int32)
+    count = None if count is None else np.ascontiguousarray(count, dtype=np.int32)
+    y = np.empty((B, D), np.uint16)
+    rc = lib().oracle_lg_sparse_mlp(x, wg, _ptr(bg), wu, _ptr(bu), wd, _ptr(idx), _ptr(count),
+                                    B, D, D_ffn, float(np.float32(sparsity_pct)), order, y)
+    if rc:
+        raise ValueError("oracle_lg_sparse_mlp: sparsity_pct leaves no list position to compute")
+    return y
+
+
+def lg_sparsity(count, D_ffn: int) -> np.float32:
+    c = np.ascontiguousarray(count, dtype=np.int32).reshape(-1)
+    return np.float32(lib().oracle_lg_sparsity(c, c.size, D_ffn))

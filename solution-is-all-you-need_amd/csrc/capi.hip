@@ -70,6 +70,16 @@ int check_route_shapes(const void* x, int x_dtype, const float* router_w, int64_
 
 namespace pmoe {
 
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_error() { g_err[0] = '\0'; }
+
 size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared, void* base,
                       Workspace* ws) {
   const int64_t Kpad = round_up(H, kQuad);

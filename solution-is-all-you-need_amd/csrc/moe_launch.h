@@ -30,6 +30,11 @@ struct Workspace {
   int32_t* counter = nullptr;       // [1] router hand-off counter (reset by every route launch)
 };
 
+// The thread-local message behind phantom_moe_last_error(): set_error
+// formats it and returns `code`; clear_error empties it.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
 size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared, void* base,
                       Workspace* ws);
 

@@ -8,8 +8,11 @@ Python surface over libphantom_moe.so (C ABI in include/phantom_moe.h):
   route, permute      the first two stages on their own
   MoEWeights          repacked Q4_0 expert weights resident in HBM
   q4_0                GGUF Q4_0 pack / unpack / device repack
+  legacy              the reference's neuron-sparse fp16 FFN ABI
+                      (sparse_mlp_forward, predict_active_neurons,
+                      get_sparsity_stats; include/phantom_legacy.h)
 """
-from . import q4_0, synth
+from . import legacy, q4_0, synth
 from ._lib import PhantomMoEError
 from .ops import MoEWeights, PreparedForward, moe_forward, permute, route
 from .router import PhantomTopKRouter
@@ -22,6 +25,7 @@ __all__ = [
     "route",
     "permute",
     "q4_0",
+    "legacy",
     "synth",
     "PhantomMoEError",
 ]

@@ -21,11 +21,13 @@ import torch  # noqa: F401  (must precede the CDLL, see module docstring)
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libphantom_moe.so")
 
-# Function name -> (restype, argtypes).  Mirrors include/phantom_moe.h.
+# Function name -> (restype, argtypes).  Mirrors include/phantom_moe.h and
+# include/phantom_legacy.h.
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
 _sz = ctypes.c_size_t
+_f32 = ctypes.c_float
 SIGNATURES = {
     "phantom_moe_last_error": (ctypes.c_char_p, []),
     "phantom_moe_version": (ctypes.c_char_p, []),
@@ -45,6 +47,10 @@ SIGNATURES = {
         + [_vp] * 6
         + [_vp, _vp, _vp, _vp, _sz, _vp],
     ),
+    # include/phantom_legacy.h: the reference's own symbol names and order
+    "sparse_mlp_forward": (_f32, [_vp] * 9 + [_int, _int, _int, _f32, _vp]),
+    "predict_active_neurons": (_f32, [_vp] * 7 + [_int, _int, _int, _f32, _vp]),
+    "get_sparsity_stats": (_f32, [_vp, _int, _int, _vp]),
 }
 
 _lock = threading.Lock()

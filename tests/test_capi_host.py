@@ -16,19 +16,50 @@ EINVAL, EWORKSPACE, ELAUNCH, EUNSUPPORTED = -1, -2, -3, -4
 FAKE = 0x10000  # never dereferenced: every call below fails validation first
 
 
+LEGACY_HEADER = os.path.join(os.path.dirname(HEADER), "phantom_legacy.h")
+
+
 def declared_symbols():
     text = open(HEADER).read()
-    return re.findall(r"PHANTOM_MOE_API\s+[\w\s\*]+?\b(phantom_\w+)\s*\(", text)
+    names = re.findall(r"PHANTOM_MOE_API\s+[\w\s\*]+?\b(phantom_\w+)\s*\(", text)
+    legacy = re.findall(r"PHANTOM_LEGACY_API\s+[\w\s\*]+?\b(\w+)\s*\(", open(LEGACY_HEADER).read())
+    return names + legacy
 
 
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     names = declared_symbols()
-    assert len(names) >= 11
+    assert len(names) >= 14
+    assert {"sparse_mlp_forward", "predict_active_neurons", "get_sparsity_stats"} <= set(names)
     for n in names:
-        assert hasattr(lib, n), f"{n} declared in phantom_moe.h but not exported"
+        assert hasattr(lib, n), f"{n} declared in include/ but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_legacy_validation_returns_status_not_exit():
+    """The reference exits on these (kernels/common/cuda_utils.h:31-52); the
+    library returns the negative status as a float before any HIP call."""
+    lib = _lib.load()
+    F = FAKE
+    smf = lib.sparse_mlp_forward
+    assert smf(F, F, None, F, None, F, F, F, F, 0, 64, 128, 50.0, None) == EINVAL  # B = 0
+    assert smf(F, F, None, F, None, F, F, F, F, 1, -1, 128, 50.0, None) == EINVAL  # D < 0
+    assert smf(None, F, None, F, None, F, F, F, F, 1, 64, 128, 50.0, None) == EINVAL
+    assert smf(F, F, None, F, None, F, None, F, F, 1, 64, 128, 50.0, None) == EINVAL  # sparse needs lists
+    # 1000% sparsity: the reference grid would be empty (launch failure there)
+    assert smf(F, F, None, F, None, F, F, F, F, 1, 64, 128, 1000.0, None) == EINVAL
+    assert smf(F, F, None, F, None, F, F, F, F, 1, 64, 128, float("nan"), None) == EINVAL
+    pan = lib.predict_active_neurons
+    assert pan(F, F, None, F, F, F, None, 0, 64, 128, 0.5, None) == EINVAL
+    assert pan(F, F, None, None, F, F, None, 1, 64, 128, 0.5, None) == EINVAL
+    assert pan(F, F, None, F, F, F, None, 1, 64, 0, 0.5, None) == EINVAL
+    gss = lib.get_sparsity_stats
+    assert gss(F, -1, 128, None) == EINVAL
+    assert gss(None, 2, 128, None) == EINVAL
+    assert np.isnan(gss(None, 0, 128, None))  # 0 / 0, as the reference
+    msg = lib.phantom_moe_last_error().decode()
+    assert msg == "" or "get_sparsity_stats" in msg
 
 
 def test_version_and_sizes():
