@@ -158,6 +158,103 @@ def cpu_baseline(cfg, host_layer, budget_s: float):
     }
 
 
+# The reference's neuron-sparse fp16 FFN operator (legacy C ABI), B tokens of
+# a D x D_ffn SwiGLU FFN with half the neurons active.
+LEGACY_WORKLOADS = {
+    "legacy_ffn_b1": dict(B=1, D=4096, D_ffn=14336, sparsity=50.0),
+    "legacy_ffn_b8": dict(B=8, D=4096, D_ffn=14336, sparsity=50.0),
+}
+
+
+def bench_legacy(args):
+    """sparse_mlp_forward (include/phantom_legacy.h) on resident fp16 weights:
+    the call's own event timing (it waits for its stream, as the reference
+    does) is the GPU time; tokens/s is over the wall clock of the K calls."""
+    import numpy as np
+    import torch
+
+    from phantom_moe import legacy
+
+    w = LEGACY_WORKLOADS[args.workload]
+    B, D, Dffn, pct = w["B"], w["D"], w["D_ffn"], w["sparsity"]
+    dev = torch.device("cuda:0")
+    per_layer = 3 * Dffn * D * 2
+    L = max(1, min(args.layers, (4 << 30) // per_layer + 1))
+    gen = torch.Generator(device=dev)
+    layers = []
+    for l in range(L):
+        gen.manual_seed(1000 + l)
+        wg = (torch.randn(Dffn, D, device=dev, generator=gen) / D ** 0.5).half()
+        wu = (torch.randn(Dffn, D, device=dev, generator=gen) / D ** 0.5).half()
+        wd = (torch.randn(D, Dffn, device=dev, generator=gen) / Dffn ** 0.5).half()
+        bg = (torch.randn(Dffn, device=dev, generator=gen) * 0.1).half()
+        bu = (torch.randn(Dffn, device=dev, generator=gen) * 0.1).half()
+        x = torch.randn(B, D, device=dev, generator=gen).half()
+        on = torch.rand(B, Dffn, device=dev, generator=gen) < (1.0 - pct / 100.0)
+        idx = torch.zeros(B, Dffn, dtype=torch.int32, device=dev)
+        cnt = on.sum(1).to(torch.int32)
+        for b in range(B):
+            nz = torch.nonzero(on[b]).flatten().to(torch.int32)
+            idx[b, : nz.numel()] = nz
+        layers.append((x, wg, bg, wu, bu, wd, idx, cnt))
+    torch.cuda.synchronize()
+    for i in range(args.warmup):
+        legacy.sparse_mlp_forward(*layers[i % L], pct)
+    torch.cuda.synchronize()
+    gpu_ms = []
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        gpu_ms.append(legacy.sparse_mlp_forward(*layers[i % L], pct)[1])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    counts = [int(layers[i % L][7].sum()) for i in range(args.steps)]
+    # algorithmic bytes: the active rows of gate and up, the active columns of
+    # down, x in and y out (fp16)
+    alg = [3 * c * D * 2 + 2 * B * D * 2 for c in counts]
+    ms = float(np.sum(gpu_ms))
+    achieved = float(np.sum(alg)) / (ms * 1e-3) / 1e9
+    out = {
+        "metric": f"legacy sparse_mlp_forward tokens/s (fp16 SwiGLU FFN D={D}, D_ffn={Dffn}, batch {B}, "
+                  f"{pct:.0f}% neuron sparsity)",
+        "value": round(B * args.steps / elapsed, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 activations and weights, fp32 accumulate",
+        "data": "synthetic (seeded): x ~ N(0,1), weights N(0, 1/fan_in), random active sets",
+        "config": {"workload": args.workload, "B": B, "D": D, "D_ffn": Dffn, "sparsity_pct": pct,
+                   "layer_instances": L, "weights_resident_gb": round(L * per_layer / 1e9, 3),
+                   "active_neurons_mean": round(float(np.mean(counts)) / B, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "sparse_mlp_forward call (zero fill + lg_ffn_rows_kernel + lg_down_kernel)",
+                     "algorithmic_bytes_per_launch": round(float(np.mean(alg))),
+                     "avg_launch_us": round(ms * 1e3 / args.steps, 3)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, ROOT)
+        from oracle import oracle as O
+
+        x, wg, bg, wu, bu, wd, idx, cnt = (t.cpu().numpy() for t in layers[0])
+        n, t0 = 0, time.perf_counter()
+        while True:
+            O.lg_sparse_mlp(x, wg, bg, wu, bu, wd, idx, cnt, pct, order=1)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= min(args.cpu_seconds, 10.0) or n >= 20:
+                break
+        out["cpu_baseline"] = {"value": round(B * n / el, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+                               "sample": f"{n} calls on layer instance 0 ({el:.1f} s): the reference kernels' "
+                                         f"sequential fp32 loops restated in C (oracle/legacy_oracle.c, order 1)"}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -165,6 +262,8 @@ def main():
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}, "
               f"WORLD_SIZE={world}); the sharding design is described in DESIGN.md.", file=sys.stderr)
         sys.exit(2)
+    if args.workload in LEGACY_WORKLOADS:
+        return bench_legacy(args)
 
     import numpy as np
     import torch

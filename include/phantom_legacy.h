@@ -51,8 +51,12 @@
  *     partial sums, partial l adding, in increasing d and from +0.0, the
  *     products with (d mod 512) / 8 == l; partials combined by
  *     p[l] += p[l xor s] for s = 32, 16, 8, 4, 2, 1; then the bias added.
- *   - Down projection over list entries i: partial l takes the entries with
- *     (i mod 256) / 4 == l, same tree.
+ *   - Down projection: over the columns n of W_down, weighting act[n] by
+ *     m_n, the number of times n appears among the first active_count[b]
+ *     list entries (1 for every n in the dense branch); columns with m_n = 0
+ *     are skipped; partial l takes fmaf(W[d, n], m_n * act[n], .) for
+ *     (n mod 512) / 8 == l in increasing n, same tree.  In exact arithmetic
+ *     this is the reference's sum over list entries, duplicates included.
  *   - sigmoid(a) = (float)(1 / (1 + exp(-(double)a))); silu and the SwiGLU
  *     product in fp32 as sparse_matmul.cu:141-145; fp16 stores round to
  *     nearest even.

@@ -26,7 +26,12 @@
  *     partial l adding in increasing d, from +0.0, every product with
  *     (d mod 512) / 8 == l; partials combined by p[l] + p[l xor s] for
  *     s = 32, 16, 8, 4, 2, 1; then the bias (if any) added.  The down
- *     projection over list entries i: partial l takes (i mod 256) / 4 == l.
+ *     projection runs over the columns n of W_down with m_n, the number of
+ *     times n appears among the first count list entries (every n once in
+ *     the dense branch): columns with m_n = 0 are skipped, the others add
+ *     fmaf(W[d, n], m_n * act[n], p) to partial l = (n mod 512) / 8 in
+ *     increasing n; same tree.  This equals the sum over list entries in
+ *     exact arithmetic.
  *   order 1 (the reference kernels' own loops)
  *     acc starts at the bias (or 0) and adds the products one at a time in
  *     increasing d, or in list order for the down projection
@@ -163,6 +168,7 @@ ORACLE_API int oracle_lg_sparse_mlp(const uint16_t* x, const uint16_t* wg, const
     }
     uint16_t* act = (uint16_t*)calloc((size_t)(B * D_ffn), sizeof(uint16_t));
     int32_t* list = (int32_t*)malloc(sizeof(int32_t) * (size_t)D_ffn);
+    int32_t* mult = (int32_t*)malloc(sizeof(int32_t) * (size_t)D_ffn);
     for (int64_t b = 0; b < B; ++b) {
         const uint16_t* xb = x + b * D;
         uint16_t* ab = act + b * D_ffn;
@@ -184,6 +190,13 @@ ORACLE_API int oracle_lg_sparse_mlp(const uint16_t* x, const uint16_t* wg, const
             float u = lg_dot(wu + n * D, xb, D, order, dense ? 0.0f : lg_bias(bu, n));
             ab[n] = lg_swiglu(g, u, order);
         }
+        /* multiplicity of each neuron among the first lim list entries (the
+         * dense branch lists every neuron once) */
+        for (int64_t n = 0; n < D_ffn; ++n) mult[n] = 0;
+        for (int64_t i = 0; i < lim; ++i) {
+            int64_t n = list[i];
+            if (n >= 0 && n < D_ffn) mult[n] += 1;
+        }
         for (int64_t d = 0; d < D; ++d) {
             const uint16_t* wrow = wd + d * D_ffn;
             float out;
@@ -198,11 +211,11 @@ ORACLE_API int oracle_lg_sparse_mlp(const uint16_t* x, const uint16_t* wg, const
             } else {
                 float p[64];
                 for (int l = 0; l < 64; ++l) p[l] = 0.0f;
-                for (int64_t i = 0; i < lim; ++i) {
-                    int64_t n = list[i];
-                    if (n < 0 || n >= D_ffn) continue;
-                    int l = (int)((i % 256) / 4);
-                    p[l] = p[l] + lg_h2f(ab[n]) * lg_h2f(wrow[n]);
+                for (int64_t n = 0; n < D_ffn; ++n) {
+                    if (mult[n] == 0) continue;
+                    int l = (int)((n % 512) / 8);
+                    float a = (float)mult[n] * lg_h2f(ab[n]);
+                    p[l] = fmaf(lg_h2f(wrow[n]), a, p[l]);
                 }
                 for (int s = 32; s >= 1; s >>= 1) {
                     float q[64];
@@ -214,6 +227,7 @@ ORACLE_API int oracle_lg_sparse_mlp(const uint16_t* x, const uint16_t* wg, const
             y[b * D + d] = lg_f2h(out);
         }
     }
+    free(mult);
     free(list);
     free(act);
     return 0;

@@ -19,9 +19,10 @@
 //     positions of one batch row (sparse branch).
 //   - lg_compact_kernel: wave prefix sums over the mask, one workgroup per
 //     batch row, in increasing neuron order.
-//   - lg_down_kernel: one wave per 8 output rows; the lanes split the active
-//     list, gather the activations and weights of their entries, then the
-//     fixed xor tree.
+//   - lg_count_kernel + lg_down_kernel: the multiplicity of every neuron in
+//     the active list, then a GEMV over the columns of W_down against
+//     multiplicity x activation, streamed with the same coalesced 16-byte
+//     loads (one pass over W_down per tile of up to 8 batch rows).
 // Arithmetic: fp16 x fp16 products are exact in fp32, so each fmaf below is
 // one rounded fp32 addition; the summation order is fixed (header of
 // phantom_legacy.h), so results do not depend on timing.
@@ -38,9 +39,9 @@ namespace pmoe {
 constexpr int kLgWaves = 4;         // waves per workgroup
 constexpr int kLgChunk = kWave * 8; // dot-product elements per lane pass: 8 per lane
 constexpr int kLgRowsPredict = 8;   // predictor rows per wave
-constexpr int kLgRowsFfn = 4;       // gate (and up) rows per wave
-constexpr int kLgRowsDown = 8;      // down rows per wave
-constexpr int kLgDownChunk = kWave * 4;  // list entries per lane pass: 4 per lane
+constexpr int kLgRowsFfn = 4;       // dense branch: neurons (gate and up rows) per wave
+constexpr int kLgRowsSparse = 2;    // sparse branch: list positions per wave
+constexpr int kLgRowsDown = 4;      // down rows per wave
 constexpr int kLgCompactThreads = 1024;
 
 enum LgMode { kLgPredict = 0, kLgDense = 1, kLgSparse = 2 };
@@ -55,7 +56,7 @@ struct LgRowsK {
   const int32_t* count; // [B]
   int64_t B, D, D_ffn;
   int64_t cover;        // list positions the reference's grid covers (sparse mode)
-  bool vec;             // D % 8 == 0 and x / w rows 16-byte aligned
+  bool vec;             // D % 8 == 0 and x / w rows 16-byte aligned (picks the VEC kernels)
   float threshold;
   float* gate_out;      // [B, D_ffn] or null (predict)
   uint8_t* mask;        // [B, D_ffn] (predict)
@@ -66,30 +67,32 @@ __device__ inline float lg_sigmoid(float a) {
   return static_cast<float>(1.0 / (1.0 + exp(-static_cast<double>(a))));
 }
 
-// Eight fp16 values of a row starting at element d0 (zeros past D).  The
-// address is clamped so the load itself is unconditional.
-__device__ inline void lg_load8(const uint16_t* row, int64_t d0, int64_t D, bool vec, float out[8]) {
-  if (vec) {
+// Eight fp16 values of a row starting at element d0, as raw bits (zeros past
+// D).  The address is clamped so the load itself is unconditional.  VEC:
+// D % 8 == 0 and 16-byte aligned rows, one 128-bit load; else eight element
+// loads.
+template <bool VEC>
+__device__ inline uint4 lg_load8(const uint16_t* row, int64_t d0, int64_t D) {
+  if (VEC) {
     const int64_t dc = d0 < D ? d0 : D - 8;
     const uint4 v = *reinterpret_cast<const uint4*>(row + dc);
-    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      out[2 * j] = half_bits_to_float32(u[j] & 0xffffu);
-      out[2 * j + 1] = half_bits_to_float32(u[j] >> 16);
-    }
-    if (d0 >= D) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) out[j] = 0.0f;
-    }
+    return d0 < D ? v : make_uint4(0u, 0u, 0u, 0u);
   } else {
+    uint32_t h[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int64_t d = d0 + j;
-      const float v = half_bits_to_float(row[d < D ? d : D - 1]);
-      out[j] = d < D ? v : 0.0f;
+      const uint32_t v = row[d < D ? d : D - 1];
+      h[j] = d < D ? v : 0u;
     }
+    return make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
   }
+}
+
+// Element j (0..7) of eight packed fp16 values, as fp32.
+__device__ inline float lg_elem(const uint4& v, int j) {
+  const uint32_t w = j < 2 ? v.x : (j < 4 ? v.y : (j < 6 ? v.z : v.w));
+  return half_bits_to_float32((j & 1) ? (w >> 16) : (w & 0xffffu));
 }
 
 __device__ inline float lg_tree(float v) {
@@ -104,29 +107,36 @@ __device__ inline float lg_bias(const uint16_t* b, int64_t n) {
 
 // NR weight rows x BT batch rows of dot products over D, in the fixed order:
 // lane l adds elements d = 512 c + 8 l + j in increasing (c, j), then the
-// xor tree.  Every lane returns every sum.
-template <int NR, int BT>
+// xor tree.  Every lane returns every sum.  U chunks are loaded before any of
+// them is summed (chunks past D load as zeros, which add nothing to a
+// partial that started at +0.0).
+template <int NR, int BT, bool VEC, int U>
 __device__ inline void lg_dots(const uint16_t* const (&rows)[NR], const uint16_t* const (&xr)[BT], int64_t D,
-                               bool vec, float (&acc)[NR][BT]) {
+                               float (&acc)[NR][BT]) {
   const int lane = threadIdx.x % kWave;
 #pragma unroll
   for (int r = 0; r < NR; ++r)
 #pragma unroll
     for (int b = 0; b < BT; ++b) acc[r][b] = 0.0f;
-  for (int64_t c0 = 0; c0 < D; c0 += kLgChunk) {
-    const int64_t d0 = c0 + 8 * lane;
-    float xv[BT][8];
+  for (int64_t c0 = 0; c0 < D; c0 += U * kLgChunk) {
+    uint4 xv[U][BT], wv[U][NR];
 #pragma unroll
-    for (int b = 0; b < BT; ++b) lg_load8(xr[b], d0, D, vec, xv[b]);
+    for (int u = 0; u < U; ++u) {
+      const int64_t d0 = c0 + u * kLgChunk + 8 * lane;
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      float wv[8];
-      lg_load8(rows[r], d0, D, vec, wv);
+      for (int b = 0; b < BT; ++b) xv[u][b] = lg_load8<VEC>(xr[b], d0, D);
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int b = 0; b < BT; ++b) acc[r][b] = fmaf(wv[j], xv[b][j], acc[r][b]);
+      for (int r = 0; r < NR; ++r) wv[u][r] = lg_load8<VEC>(rows[r], d0, D);
     }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int b = 0; b < BT; ++b)
+            acc[r][b] = fmaf(lg_elem(wv[u][r], j), lg_elem(xv[u][b], j), acc[r][b]);
   }
 #pragma unroll
   for (int r = 0; r < NR; ++r)
@@ -164,7 +174,7 @@ __device__ inline float lg_pick(const float (&acc)[NR][BT], int i) {
 }
 
 // Predictor: R consecutive neurons x BT batch rows per wave.
-template <int BT>
+template <int BT, bool VEC, int U>
 __global__ __launch_bounds__(kLgWaves* kWave) void lg_predict_kernel(LgRowsK p) {
   constexpr int R = kLgRowsPredict;
   const int lane = threadIdx.x % kWave;
@@ -181,7 +191,7 @@ __global__ __launch_bounds__(kLgWaves* kWave) void lg_predict_kernel(LgRowsK p) 
 #pragma unroll
   for (int b = 0; b < BT; ++b) xr[b] = p.x + (b0 + b < p.B ? b0 + b : p.B - 1) * p.D;
   float acc[R][BT];
-  lg_dots<R, BT>(rows, xr, p.D, p.vec, acc);
+  lg_dots<R, BT, VEC, U>(rows, xr, p.D, acc);
   if (lane < R * BT) {
     const int r = lane / BT, b = lane % BT;
     const int64_t n = n0 + r, bb = b0 + b;
@@ -197,9 +207,8 @@ __global__ __launch_bounds__(kLgWaves* kWave) void lg_predict_kernel(LgRowsK p) 
 
 // FFN gate + up + SwiGLU.  Dense: R consecutive neurons x BT batch rows, no
 // biases.  Sparse: R list positions of one batch row, with biases.
-template <int MODE, int BT>
+template <int MODE, int R, int BT, bool VEC, int U>
 __global__ __launch_bounds__(kLgWaves* kWave) void lg_ffn_rows_kernel(LgRowsK p) {
-  constexpr int R = kLgRowsFfn;
   const int lane = threadIdx.x % kWave;
   const int64_t i0 = ((int64_t)blockIdx.x * kLgWaves + threadIdx.x / kWave) * R;
   const int64_t b0 = (int64_t)blockIdx.y * BT;
@@ -234,7 +243,7 @@ __global__ __launch_bounds__(kLgWaves* kWave) void lg_ffn_rows_kernel(LgRowsK p)
 #pragma unroll
   for (int b = 0; b < BT; ++b) xr[b] = p.x + (b0 + b < p.B ? b0 + b : p.B - 1) * p.D;
   float acc[2 * R][BT];
-  lg_dots<2 * R, BT>(rows, xr, p.D, p.vec, acc);
+  lg_dots<2 * R, BT, VEC, U>(rows, xr, p.D, acc);
   if (lane < R * BT) {
     const int r = lane / BT, b = lane % BT;
     // gate rows are 0..R-1 and up rows R..2R-1 of acc: pick both for (r, b)
@@ -265,64 +274,124 @@ __global__ __launch_bounds__(kLgWaves* kWave) void lg_ffn_rows_kernel(LgRowsK p)
   }
 }
 
-// y[b, d] = sum over list entries i < lim of act[b, n_i] * Wd[d, n_i]; lane l
-// takes entries i = 256 c + 4 l + j in increasing (c, j), then the xor tree.
-template <int MODE>
+// Multiplicity of every neuron in the first count[b] list entries of batch
+// row b (sparse branch): the down projection sums over list entries, so a
+// neuron listed twice contributes twice.  Integer atomics, so the counts do
+// not depend on timing.
+__global__ __launch_bounds__(256) void lg_count_kernel(const int32_t* __restrict__ idx,
+                                                        const int32_t* __restrict__ count,
+                                                        int32_t* __restrict__ mult, int64_t D_ffn) {
+  const int64_t b = blockIdx.y;
+  int64_t lim = count[b];
+  lim = lim < 0 ? 0 : (lim > D_ffn ? D_ffn : lim);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < lim; i += (int64_t)gridDim.x * blockDim.x) {
+    const int32_t n = idx[b * D_ffn + i];
+    if (n >= 0 && n < D_ffn) atomicAdd(&mult[b * D_ffn + n], 1);
+  }
+}
+
+// m_n * act[n] as fp32, and whether column n takes part (m_n > 0; dense
+// branch: every column, m_n = 1).
+template <int MODE, bool VEC>
+__device__ inline void lg_down_operand(const uint16_t* arow, const int32_t* mrow, int64_t n0, int64_t D_ffn,
+                                       float a[8], bool on[8]) {
+  const uint4 av = lg_load8<VEC>(arow, n0, D_ffn);
+  if (MODE == kLgSparse) {
+    int32_t m[8];
+    if (VEC) {
+      const int64_t nc = n0 < D_ffn ? n0 : D_ffn - 8;
+      const int4 m0 = *reinterpret_cast<const int4*>(mrow + nc);
+      const int4 m1 = *reinterpret_cast<const int4*>(mrow + nc + 4);
+      const int32_t mm[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m[j] = n0 < D_ffn ? mm[j] : 0;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t n = n0 + j;
+        const int32_t v = mrow[n < D_ffn ? n : D_ffn - 1];
+        m[j] = n < D_ffn ? v : 0;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      on[j] = m[j] > 0;
+      a[j] = (float)m[j] * lg_elem(av, j);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      on[j] = n0 + j < D_ffn;
+      a[j] = lg_elem(av, j);
+    }
+  }
+}
+
+// y[b, d] = sum over columns n of Wd[d, n] * (m_n act[b, n]), columns with
+// m_n = 0 skipped; lane l adds the columns with (n mod 512) / 8 == l in
+// increasing n (the predictor's order), then the xor tree.  R output rows x
+// BT batch rows per wave: each 16-byte weight load serves BT batch rows, so
+// W_down is streamed once per batch tile with coalesced loads, whatever the
+// active lists look like (a row-major W_down has every 64-column line touched
+// by any list denser than a few percent anyway).
+template <int MODE, int R, int BT, bool VEC, int U>
 __global__ __launch_bounds__(kLgWaves* kWave) void lg_down_kernel(const uint16_t* __restrict__ act,
+                                                                  const int32_t* __restrict__ mult,
                                                                   const uint16_t* __restrict__ wd,
-                                                                  const int32_t* __restrict__ idx,
-                                                                  const int32_t* __restrict__ count,
-                                                                  uint16_t* __restrict__ y, int64_t D,
+                                                                  uint16_t* __restrict__ y, int64_t B, int64_t D,
                                                                   int64_t D_ffn) {
-  constexpr int R = kLgRowsDown;
   const int lane = threadIdx.x % kWave;
   const int64_t d0 = ((int64_t)blockIdx.x * kLgWaves + threadIdx.x / kWave) * R;
-  const int64_t b = blockIdx.y;
+  const int64_t b0 = (int64_t)blockIdx.y * BT;
   if (d0 >= D) return;
-  int64_t lim = D_ffn;
-  if (MODE == kLgSparse) {
-    int64_t c = count[b];
-    lim = c < 0 ? 0 : (c > D_ffn ? D_ffn : c);
-  }
-  const uint16_t* arow = act + b * D_ffn;
   const uint16_t* wrow[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) wrow[r] = wd + (d0 + r < D ? d0 + r : D - 1) * D_ffn;
-  float acc[R];
+  const uint16_t* arow[BT];
+  const int32_t* mrow[BT];
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-  for (int64_t c0 = 0; c0 < lim; c0 += kLgDownChunk) {
-    int64_t n[4];
-    float a[4];
-    bool ok[4];
+  for (int b = 0; b < BT; ++b) {
+    const int64_t bb = b0 + b < B ? b0 + b : B - 1;
+    arow[b] = act + bb * D_ffn;
+    mrow[b] = mult + bb * D_ffn;
+  }
+  float acc[R][BT];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t i = c0 + 4 * lane + j;
-      const bool in = i < lim;
-      int64_t v = i;
-      if (MODE == kLgSparse) v = idx[b * D_ffn + (in ? i : lim - 1)];
-      ok[j] = in && v >= 0 && v < D_ffn;
-      n[j] = ok[j] ? v : 0;
-      const float av = half_bits_to_float(arow[n[j]]);
-      a[j] = ok[j] ? av : 0.0f;
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int b = 0; b < BT; ++b) acc[r][b] = 0.0f;
+  for (int64_t c0 = 0; c0 < D_ffn; c0 += U * kLgChunk) {
+    uint4 wv[U][R];
+    float a[U][BT][8];
+    bool on[U][BT][8];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t n0 = c0 + u * kLgChunk + 8 * lane;
+#pragma unroll
+      for (int r = 0; r < R; ++r) wv[u][r] = lg_load8<VEC>(wrow[r], n0, D_ffn);
+#pragma unroll
+      for (int b = 0; b < BT; ++b) lg_down_operand<MODE, VEC>(arow[b], mrow[b], n0, D_ffn, a[u][b], on[u][b]);
     }
-    // skipped entries add an exact +0 product, which leaves a partial that
-    // started at +0.0 unchanged
+    // skipped columns add an exact +0 product (their activation is zero),
+    // which leaves a partial that started at +0.0 unchanged
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float w = half_bits_to_float(wrow[r][n[j]]);
-        acc[r] = fmaf(ok[j] ? w : 0.0f, a[j], acc[r]);
-      }
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float w = lg_elem(wv[u][r], j);
+#pragma unroll
+          for (int b = 0; b < BT; ++b) acc[r][b] = fmaf(on[u][b][j] ? w : 0.0f, a[u][b][j], acc[r][b]);
+        }
   }
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = lg_tree(acc[r]);
-  if (lane < R && d0 + lane < D) {
-    float v = acc[0];
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int r = 1; r < R; ++r) v = lane == r ? acc[r] : v;
-    y[b * D + d0 + lane] = static_cast<uint16_t>(float_to_half_bits(v));
+    for (int b = 0; b < BT; ++b) acc[r][b] = lg_tree(acc[r][b]);
+  if (lane < R * BT) {
+    const int r = lane / BT, b = lane % BT;
+    if (d0 + r < D && b0 + b < B) y[(b0 + b) * D + d0 + r] = static_cast<uint16_t>(float_to_half_bits(lg_pick<R, BT>(acc, lane)));
   }
 }
 
@@ -384,19 +453,55 @@ namespace {
 
 int batch_tile(int64_t B) { return B >= 8 ? 8 : (B >= 4 ? 4 : (B >= 2 ? 2 : 1)); }
 
-template <int BT>
+// Loads in flight per lane: U chunks x (rows + batch rows) x 16 bytes.
+template <int BT, bool VEC>
 hipError_t launch_predict_bt(const LgRowsK& p, hipStream_t s) {
+  constexpr int U = BT == 1 ? 2 : 1;
   const dim3 grid((unsigned)ceil_div(p.D_ffn, (int64_t)kLgWaves * kLgRowsPredict), (unsigned)ceil_div(p.B, BT));
-  hipLaunchKernelGGL(lg_predict_kernel<BT>, grid, dim3(kLgWaves * kWave), 0, s, p);
+  hipLaunchKernelGGL((lg_predict_kernel<BT, VEC, U>), grid, dim3(kLgWaves * kWave), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int MODE, int BT, bool VEC>
+hipError_t launch_ffn_rows_bt(const LgRowsK& p, hipStream_t s) {
+  // sparse: one batch row, few list positions per wave and deep loads;
+  // dense: neighbouring neurons of several batch rows share each row load
+  constexpr int R = MODE == kLgSparse ? kLgRowsSparse : kLgRowsFfn;
+  constexpr int U = MODE == kLgSparse ? 4 : (BT == 1 ? 2 : 1);
+  const int64_t rows = MODE == kLgSparse ? (p.cover < p.D_ffn ? p.cover : p.D_ffn) : p.D_ffn;
+  const dim3 grid((unsigned)ceil_div(rows, (int64_t)kLgWaves * R), (unsigned)ceil_div(p.B, BT));
+  hipLaunchKernelGGL((lg_ffn_rows_kernel<MODE, R, BT, VEC, U>), grid, dim3(kLgWaves * kWave), 0, s, p);
   return hipGetLastError();
 }
 
 template <int MODE, int BT>
-hipError_t launch_ffn_rows_bt(const LgRowsK& p, hipStream_t s) {
-  const int64_t rows = MODE == kLgSparse ? (p.cover < p.D_ffn ? p.cover : p.D_ffn) : p.D_ffn;
-  const dim3 grid((unsigned)ceil_div(rows, (int64_t)kLgWaves * kLgRowsFfn), (unsigned)ceil_div(p.B, BT));
-  hipLaunchKernelGGL((lg_ffn_rows_kernel<MODE, BT>), grid, dim3(kLgWaves * kWave), 0, s, p);
+hipError_t launch_ffn_rows(const LgRowsK& p, hipStream_t s) {
+  return p.vec ? launch_ffn_rows_bt<MODE, BT, true>(p, s) : launch_ffn_rows_bt<MODE, BT, false>(p, s);
+}
+
+template <int MODE, int BT, bool VEC>
+hipError_t launch_down_bt(const uint16_t* act, const int32_t* mult, const uint16_t* wd, uint16_t* y, int64_t B,
+                          int64_t D, int64_t D_ffn, hipStream_t s) {
+  constexpr int U = BT == 1 ? 2 : 1;
+  const dim3 grid((unsigned)ceil_div(D, (int64_t)kLgWaves * kLgRowsDown), (unsigned)ceil_div(B, BT));
+  hipLaunchKernelGGL((lg_down_kernel<MODE, kLgRowsDown, BT, VEC, U>), grid, dim3(kLgWaves * kWave), 0, s, act, mult,
+                     wd, y, B, D, D_ffn);
   return hipGetLastError();
+}
+
+template <int MODE>
+hipError_t launch_down(const uint16_t* act, const int32_t* mult, const uint16_t* wd, uint16_t* y, int64_t B,
+                       int64_t D, int64_t D_ffn, bool vec, hipStream_t s) {
+  switch (batch_tile(B)) {
+    case 8: return vec ? launch_down_bt<MODE, 8, true>(act, mult, wd, y, B, D, D_ffn, s)
+                       : launch_down_bt<MODE, 8, false>(act, mult, wd, y, B, D, D_ffn, s);
+    case 4: return vec ? launch_down_bt<MODE, 4, true>(act, mult, wd, y, B, D, D_ffn, s)
+                       : launch_down_bt<MODE, 4, false>(act, mult, wd, y, B, D, D_ffn, s);
+    case 2: return vec ? launch_down_bt<MODE, 2, true>(act, mult, wd, y, B, D, D_ffn, s)
+                       : launch_down_bt<MODE, 2, false>(act, mult, wd, y, B, D, D_ffn, s);
+    default: return vec ? launch_down_bt<MODE, 1, true>(act, mult, wd, y, B, D, D_ffn, s)
+                        : launch_down_bt<MODE, 1, false>(act, mult, wd, y, B, D, D_ffn, s);
+  }
 }
 
 // Per-device state of the legacy entry points: the activation buffer and the
@@ -450,13 +555,18 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 }  // namespace
 
-hipError_t launch_lg_predict(const LgRowsK& p, hipStream_t s) {
+template <bool VEC>
+hipError_t launch_lg_predict_v(const LgRowsK& p, hipStream_t s) {
   switch (batch_tile(p.B)) {
-    case 8: return launch_predict_bt<8>(p, s);
-    case 4: return launch_predict_bt<4>(p, s);
-    case 2: return launch_predict_bt<2>(p, s);
-    default: return launch_predict_bt<1>(p, s);
+    case 8: return launch_predict_bt<8, VEC>(p, s);
+    case 4: return launch_predict_bt<4, VEC>(p, s);
+    case 2: return launch_predict_bt<2, VEC>(p, s);
+    default: return launch_predict_bt<1, VEC>(p, s);
   }
+}
+
+hipError_t launch_lg_predict(const LgRowsK& p, hipStream_t s) {
+  return p.vec ? launch_lg_predict_v<true>(p, s) : launch_lg_predict_v<false>(p, s);
 }
 
 }  // namespace pmoe
@@ -528,7 +638,10 @@ PHANTOM_LEGACY_API float sparse_mlp_forward(const phantom_half* d_input, const p
   std::lock_guard<std::mutex> lock(g_lg_mutex);
   LgCall call;
   if (const char* m = lg_begin(stream, &call)) return (float)set_error(PHANTOM_MOE_ELAUNCH, "sparse_mlp_forward: %s", m);
-  const size_t need = (size_t)round_up((int64_t)B * D_ffn, 8) * sizeof(uint16_t);
+  // pool: act fp16 [B, D_ffn] (16-byte rows padded as a whole), then the
+  // neuron multiplicities int32 [B, D_ffn]
+  const size_t act_bytes = (size_t)round_up((int64_t)B * D_ffn, 8) * sizeof(uint16_t);
+  const size_t need = act_bytes + (size_t)round_up((int64_t)B * D_ffn, 4) * sizeof(int32_t);
   if (call.dev->act_bytes < need) {
     if (!call.timed)
       return (float)set_error(PHANTOM_MOE_EUNSUPPORTED, "sparse_mlp_forward: activation buffer must grow; call once outside stream capture first");
@@ -542,6 +655,7 @@ PHANTOM_LEGACY_API float sparse_mlp_forward(const phantom_half* d_input, const p
       return (float)set_error(PHANTOM_MOE_ELAUNCH, "sparse_mlp_forward: cannot allocate %zu bytes", bytes);
     call.dev->act_bytes = bytes;
   }
+  int32_t* mult = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(call.dev->act) + act_bytes);
   LgRowsK p{};
   p.x = d_input;
   p.w1 = d_gate_weight;
@@ -559,26 +673,26 @@ PHANTOM_LEGACY_API float sparse_mlp_forward(const phantom_half* d_input, const p
   hipError_t e = hipSuccess;
   if (dense) {
     switch (batch_tile(B)) {
-      case 8: e = launch_ffn_rows_bt<kLgDense, 8>(p, stream); break;
-      case 4: e = launch_ffn_rows_bt<kLgDense, 4>(p, stream); break;
-      case 2: e = launch_ffn_rows_bt<kLgDense, 2>(p, stream); break;
-      default: e = launch_ffn_rows_bt<kLgDense, 1>(p, stream); break;
+      case 8: e = launch_ffn_rows<kLgDense, 8>(p, stream); break;
+      case 4: e = launch_ffn_rows<kLgDense, 4>(p, stream); break;
+      case 2: e = launch_ffn_rows<kLgDense, 2>(p, stream); break;
+      default: e = launch_ffn_rows<kLgDense, 1>(p, stream); break;
     }
   } else {
     hipLaunchKernelGGL(lg_zero_kernel, dim3(1024), dim3(256), 0, stream, reinterpret_cast<uint4*>(p.act),
                        (int64_t)(need / 16));
     e = hipGetLastError();
-    if (e == hipSuccess) e = launch_ffn_rows_bt<kLgSparse, 1>(p, stream);
+    if (e == hipSuccess) {
+      hipLaunchKernelGGL(lg_count_kernel, dim3((unsigned)ceil_div(D_ffn, 256), (unsigned)B), dim3(256), 0, stream,
+                         d_active_indices, d_active_count, mult, (int64_t)D_ffn);
+      e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = launch_ffn_rows<kLgSparse, 1>(p, stream);
   }
   if (e == hipSuccess && D > 0) {
-    const dim3 grid((unsigned)ceil_div(D, (int64_t)kLgWaves * kLgRowsDown), (unsigned)B);
-    if (dense)
-      hipLaunchKernelGGL(lg_down_kernel<kLgDense>, grid, dim3(kLgWaves * kWave), 0, stream, p.act, d_down_weight,
-                         d_active_indices, d_active_count, d_output, (int64_t)D, (int64_t)D_ffn);
-    else
-      hipLaunchKernelGGL(lg_down_kernel<kLgSparse>, grid, dim3(kLgWaves * kWave), 0, stream, p.act, d_down_weight,
-                         d_active_indices, d_active_count, d_output, (int64_t)D, (int64_t)D_ffn);
-    e = hipGetLastError();
+    const bool dvec = D_ffn % 8 == 0 && aligned16(d_down_weight);
+    e = dense ? launch_down<kLgDense>(p.act, mult, d_down_weight, d_output, B, D, D_ffn, dvec, stream)
+              : launch_down<kLgSparse>(p.act, mult, d_down_weight, d_output, B, D, D_ffn, dvec, stream);
   }
   if (e != hipSuccess) return (float)set_error(PHANTOM_MOE_ELAUNCH, "sparse_mlp_forward: %s", hipGetErrorString(e));
   const float ms = lg_end(stream, call);
