@@ -11,8 +11,11 @@ Python surface over libphantom_moe.so (C ABI in include/phantom_moe.h):
   legacy              the reference's neuron-sparse fp16 FFN ABI
                       (sparse_mlp_forward, predict_active_neurons,
                       get_sparsity_stats; include/phantom_legacy.h)
+  gguf                GGUF reader; a layer's Q4_0 experts straight to HBM
+  hf                  transformers MoE blocks routed through moe_forward
+                      (imported on demand: ``from phantom_moe import hf``)
 """
-from . import legacy, q4_0, synth
+from . import gguf, legacy, q4_0, synth
 from ._lib import PhantomMoEError
 from .ops import MoEWeights, PreparedForward, moe_forward, permute, route
 from .router import PhantomTopKRouter
@@ -26,6 +29,7 @@ __all__ = [
     "permute",
     "q4_0",
     "legacy",
+    "gguf",
     "synth",
     "PhantomMoEError",
 ]
