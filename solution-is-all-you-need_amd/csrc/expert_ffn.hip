@@ -152,10 +152,12 @@ __device__ __attribute__((always_inline)) inline void gu_load(const GateUpK& a, 
     const char* ub = uniform_ptr(reinterpret_cast<const char*>(unib) + tq * kQuadNibBytes);
     const char* gsb = uniform_ptr(reinterpret_cast<const char*>(gsc) + tq * kQuadScales * 2);
     const char* usb = uniform_ptr(reinterpret_cast<const char*>(usc) + tq * kQuadScales * 2);
-    c.gw[r] = *reinterpret_cast<const u32x4*>(gb + o_nib);
-    c.uw[r] = *reinterpret_cast<const u32x4*>(ub + o_nib);
-    c.gs[r] = *reinterpret_cast<const uint2*>(gsb + o_sc);
-    c.us[r] = *reinterpret_cast<const uint2*>(usb + o_sc);
+    // explicitly global: the routed / shared pointer select would make these
+    // flat loads, after which every wait is a wait for all outstanding loads
+    c.gw[r] = gload<u32x4>(gb + o_nib);
+    c.uw[r] = gload<u32x4>(ub + o_nib);
+    c.gs[r] = gload_u2(gsb + o_sc);
+    c.us[r] = gload_u2(usb + o_sc);
   }
   const uint32_t xrow = ps.xoff + (uint32_t)q;  // (token, quad) row of xq / xs
   const char* xb = reinterpret_cast<const char*>(a.xq);

@@ -138,6 +138,23 @@ __device__ inline float half_bits_to_float32(uint32_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
 }
 
+// A load through an explicitly global (address space 1) pointer.  A pointer
+// chosen with ?: between two kernel arguments, one of which may be null, is
+// generic to the compiler; generic (flat) loads count against both vmcnt and
+// lgkmcnt, so every wait after one becomes a wait for all outstanding loads.
+template <typename T>
+__device__ inline T gload(const void* ptr) {
+  typedef const __attribute__((address_space(1))) T* global_ptr;
+  return *(global_ptr)ptr;
+}
+
+// The 8-byte case as one 64-bit load (a uint2 struct load through the cast
+// pointer is lowered as a generic copy).
+__device__ inline uint2 gload_u2(const void* ptr) {
+  const uint64_t v = gload<uint64_t>(ptr);
+  return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+}
+
 __device__ inline double shfl_xor_f64(double v, int mask) {
   return __shfl_xor(v, mask, kWave);
 }

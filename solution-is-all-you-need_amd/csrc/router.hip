@@ -619,10 +619,127 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* idx, int64
                 sorted_slots, slot_pos, desc, seg_tok);
 }
 
+// Logits for many tokens (prefill): the same per-lane partials and tree as
+// route_logits_kernel, with TT tokens x EW experts per wave and the loads of
+// chunk c + 1 in flight while chunk c is summed.  x stays packed (bf16 pairs)
+// in registers until its FMAs, so two chunks of operands fit beside the
+// 2 * TT * EW fp64 accumulators.
+// tokens x experts per wave of the many-token logits kernel
+constexpr int kBigTT = 8;
+constexpr int kBigEW = 4;
+
+template <typename XT>
+struct XRaw;
+template <>
+struct XRaw<uint16_t> {
+  uint2 v;
+  __device__ inline void load(const uint16_t* x, int64_t off) { v = *reinterpret_cast<const uint2*>(x + off); }
+  __device__ inline float get(int i) const {
+    const uint32_t w = i < 2 ? v.x : v.y;
+    return bf16_bits_to_float((i & 1) ? (w >> 16) : (w & 0xffffu));
+  }
+};
+template <>
+struct XRaw<float> {
+  float4 v;
+  __device__ inline void load(const float* x, int64_t off) { v = *reinterpret_cast<const float4*>(x + off); }
+  __device__ inline float get(int i) const { return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w)); }
+};
+
+template <typename XT, int TT, int EW>
+struct LogitsChunk {
+  float4 w[EW];
+  XRaw<XT> x[TT];
+  bool hok;
+};
+
+template <typename XT, int TT, int EW>
+__device__ inline void logits_load(const RouteK& a, const XT* x, int64_t c, int64_t nchunks, int64_t t0, int e0,
+                                   LogitsChunk<XT, TT, EW>& k) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t h0 = c * 256 + 4 * lane;
+  k.hok = c < nchunks && h0 < a.H;
+  const int64_t hc = k.hok ? h0 : 0;
+#pragma unroll
+  for (int ei = 0; ei < EW; ++ei) {
+    const int64_t ec = e0 + ei < a.E ? e0 + ei : a.E - 1;
+    k.w[ei] = *reinterpret_cast<const float4*>(a.W + ec * a.H + hc);
+  }
+#pragma unroll
+  for (int ti = 0; ti < TT; ++ti) {
+    const int64_t tc = t0 + ti < a.T ? t0 + ti : a.T - 1;
+    k.x[ti].load(x, tc * a.H + hc);
+  }
+}
+
+template <typename XT, int TT, int EW>
+__global__ __launch_bounds__(256) void route_logits_big_kernel(RouteK a) {
+  constexpr int P = TT * EW;
+  static_assert((P & (P - 1)) == 0 && P <= 64, "pairs per wave must be a power of two <= 64");
+  const int lane = threadIdx.x % kWave;
+  const int w = threadIdx.x / kWave;
+  const int64_t t0 = (int64_t)blockIdx.y * TT;
+  const int e0 = blockIdx.x * (4 * EW) + w * EW;
+  const XT* x = static_cast<const XT*>(a.x);
+  if (a.prep_x) prep_x_tile(a, t0, TT);
+  if (a.counter && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *a.counter = 0;
+  float bias_e = 0.0f;
+  if (a.bias) {
+    const int e = e0 + tree_pair_of_lane<P>(lane) % EW;
+    bias_e = a.bias[e < a.E ? e : a.E - 1];
+  }
+  double acc[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) acc[i] = 0.0;
+  const int64_t nchunks = ceil_div(a.H, 256);
+  LogitsChunk<XT, TT, EW> cur, nxt;
+  logits_load<XT, TT, EW>(a, x, 0, nchunks, t0, e0, cur);
+  for (int64_t c = 0; c < nchunks; ++c) {
+    logits_load<XT, TT, EW>(a, x, c + 1, nchunks, t0, e0, nxt);
+    // out-of-range experts and tokens are never stored, so only the h range
+    // needs masking (both operands, so a non-finite weight read from the
+    // clamped address adds nothing); partials add in increasing h as the
+    // contract requires
+    float4 wm[EW];
+#pragma unroll
+    for (int ei = 0; ei < EW; ++ei)
+      wm[ei] = cur.hok ? cur.w[ei] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int ti = 0; ti < TT; ++ti) {
+      double xd[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xd[i] = cur.hok ? (double)cur.x[ti].get(i) : 0.0;
+#pragma unroll
+      for (int ei = 0; ei < EW; ++ei) {
+        const float4 wv = wm[ei];
+        acc[ti * EW + ei] += xd[0] * (double)wv.x;
+        acc[ti * EW + ei] += xd[1] * (double)wv.y;
+        acc[ti * EW + ei] += xd[2] * (double)wv.z;
+        acc[ti * EW + ei] += xd[3] * (double)wv.w;
+      }
+    }
+    cur = nxt;
+  }
+  const double tot = tree_reduce_pairs<P>(acc);
+  {
+    constexpr int kLowBits = (P == 1) ? 6 : (P == 2) ? 5 : (P == 4) ? 4 : (P == 8) ? 3 : (P == 16) ? 2 : (P == 32) ? 1 : 0;
+    if ((lane & ((1 << kLowBits) - 1)) == 0) {
+      const int pair = tree_pair_of_lane<P>(lane);
+      const int64_t t = t0 + pair / EW;
+      const int e = e0 + pair % EW;
+      if (t < a.T && e < a.E) {
+        double v = tot;
+        if (a.bias) v = v + (double)bias_e;
+        a.logits[t * a.E + e] = v;
+      }
+    }
+  }
+}
+
 int router_token_tile(int64_t T) {
   if (T <= 1) return 1;
   if (T <= 64) return 4;
-  return 16;
+  return kBigTT;
 }
 
 template <typename XT>
@@ -634,8 +751,8 @@ static hipError_t launch_logits_t(const RouteK& k, int TT, int n_ttiles, hipStre
     dim3 grid((unsigned)ceil_div(k.E, 4 * 2), (unsigned)n_ttiles);
     hipLaunchKernelGGL((route_logits_kernel<XT, 4, 2, 8>), grid, dim3(256), 0, stream, k);
   } else {
-    dim3 grid((unsigned)ceil_div(k.E, 4 * 4), (unsigned)n_ttiles);
-    hipLaunchKernelGGL((route_logits_kernel<XT, 16, 4, 1>), grid, dim3(256), 0, stream, k);
+    dim3 grid((unsigned)ceil_div(k.E, 4 * kBigEW), (unsigned)n_ttiles);
+    hipLaunchKernelGGL((route_logits_big_kernel<XT, kBigTT, kBigEW>), grid, dim3(256), 0, stream, k);
   }
   return hipGetLastError();
 }
