@@ -11,6 +11,7 @@
  *   sparse_mlp_forward      kernels/sparse_moe/sparse_matmul.cu:240-255
  *   predict_active_neurons  kernels/sparse_moe/gate_predict.cu:200-213
  *   get_sparsity_stats      kernels/sparse_moe/gate_predict.cu:253-258
+ *   calibrate_sparsity_gate kernels/sparse_moe/gate_calibrate.cu:228-240
  *
  * Behaviour kept from the reference:
  *   - sparse_mlp_forward and predict_active_neurons time themselves with two
@@ -64,6 +65,7 @@
 #ifndef PHANTOM_LEGACY_H
 #define PHANTOM_LEGACY_H
 
+#include <stdbool.h>
 #include <stdint.h>
 
 #include <hip/hip_runtime_api.h>
@@ -101,6 +103,24 @@ PHANTOM_LEGACY_API float predict_active_neurons(const phantom_half* d_input, con
 /* Mean sparsity in percent over the B counts (blocks on the stream).
  * Replaces kernels/sparse_moe/gate_predict.cu:253-271. */
 PHANTOM_LEGACY_API float get_sparsity_stats(const int* d_active_count, int B, int D_ffn, hipStream_t stream);
+
+/* Trains the predictor gates of one FFN layer (blocks on the stream).
+ * d_inputs [N, D] fp32, d_mlp_activations [N, D_ffn] fp32; writes
+ * d_gate_w [D_ffn, D] and d_gate_b [D_ffn] (fp32, device) and, on the host,
+ * *h_enabled (F1 >= 0.70), *h_f1_score and *h_sparsity (percent of inactive
+ * neurons).  A neuron is active on a sample when |activation| >= 0.01 *
+ * max(row max |activation|, 1e-10); the gates start at zero and take 50
+ * full-batch gradient steps of binary cross-entropy at lr 1e-3; F1 compares
+ * gate >= 0.5 with the masks.  Arithmetic: the forward dot products in the
+ * fixed order above with fmaf on fp32 operands, then the bias; gradients
+ * summed over samples in order with fmaf, divided by N, applied as
+ * w = fmaf(-lr, g, w); the sigmoid as above, clamped to [1e-7, 1 - 1e-7].
+ * Returns 0 or a negative PHANTOM_MOE_E* status; the reference returns void
+ * (so its callers ignore the status), prints progress and exits on error.
+ * Replaces kernels/sparse_moe/gate_calibrate.cu:228-340. */
+PHANTOM_LEGACY_API int calibrate_sparsity_gate(const float* d_inputs, const float* d_mlp_activations, int N_samples,
+                                               int D, int D_ffn, float* d_gate_w, float* d_gate_b, bool* h_enabled,
+                                               float* h_f1_score, float* h_sparsity, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -239,3 +239,90 @@ ORACLE_API float oracle_lg_sparsity(const int32_t* count, int64_t B, int64_t D_f
     float avg_active = total_active / (float)B;
     return (1.0f - avg_active / (float)D_ffn) * 100.0f;
 }
+
+/* ---------------------------------------------------------------------- */
+/* oracle_lg_calibrate: kernels/sparse_moe/gate_calibrate.cu:54-85 (masks),
+ * :105-210 (forward, gradient step), :228-340 (driver: zero start, `epochs`
+ * full-batch steps at lr 1e-3, final forward, baseline sparsity and F1 on
+ * the host).  order 0: this build's forward order (64 partials over
+ * (d mod 512) / 8, fmaf, tree, then the bias) and fp64-based sigmoid;
+ * order 1: the reference's loops (bias first, sequential fmaf) with this C
+ * library's expf.  Both: gradients summed over samples in order with fmaf,
+ * divided by N, applied as w = fmaf(-lr, g, w); predictions clamped to
+ * [1e-7, 1 - 1e-7]. */
+static float cal_dot0(const float* w, const float* x, int64_t D) {
+    float p[64];
+    for (int l = 0; l < 64; ++l) p[l] = 0.0f;
+    for (int64_t d = 0; d < D; ++d) {
+        int l = (int)((d % 512) / 8);
+        p[l] = fmaf(w[d], x[d], p[l]);
+    }
+    for (int s = 32; s >= 1; s >>= 1) {
+        float q[64];
+        for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ s];
+        memcpy(p, q, sizeof(p));
+    }
+    return p[0];
+}
+
+ORACLE_API void oracle_lg_calibrate(const float* x, const float* act, int64_t N, int64_t D, int64_t D_ffn, int order,
+                                    int epochs, float* w, float* b, uint8_t* masks, float* pred, int* enabled,
+                                    float* f1_out, float* sparsity_out) {
+    const float lr = 1e-3f;
+    long long active_total = 0;
+    for (int64_t s = 0; s < N; ++s) {
+        const float* row = act + s * D_ffn;
+        float m = 0.0f;
+        for (int64_t i = 0; i < D_ffn; ++i) m = fmaxf(m, fabsf(row[i]));
+        m = fmaxf(m, 1e-10f);
+        const float thr = 0.01f * m;
+        for (int64_t i = 0; i < D_ffn; ++i) {
+            masks[s * D_ffn + i] = fabsf(row[i]) >= thr ? 1 : 0;
+            active_total += masks[s * D_ffn + i];
+        }
+    }
+    *sparsity_out = (1.0f - (float)active_total / ((float)N * (float)D_ffn)) * 100.0f;
+    for (int64_t i = 0; i < D_ffn * D; ++i) w[i] = 0.0f;
+    for (int64_t n = 0; n < D_ffn; ++n) b[n] = 0.0f;
+    for (int ep = 0; ep <= epochs; ++ep) {
+        for (int64_t s = 0; s < N; ++s)
+            for (int64_t n = 0; n < D_ffn; ++n) {
+                const float* wr = w + n * D;
+                const float* xs = x + s * D;
+                float a, p;
+                if (order == 1) {
+                    a = b[n];
+                    for (int64_t d = 0; d < D; ++d) a = fmaf(xs[d], wr[d], a);
+                    p = 1.0f / (1.0f + expf(-a));
+                } else {
+                    a = cal_dot0(wr, xs, D) + b[n];
+                    p = (float)(1.0 / (1.0 + exp(-(double)a)));
+                }
+                pred[s * D_ffn + n] = fmaxf(1e-7f, fminf(1.0f - 1e-7f, p));
+            }
+        if (ep == epochs) break; /* the final forward only */
+        for (int64_t n = 0; n < D_ffn; ++n) {
+            float gb = 0.0f;
+            for (int64_t s = 0; s < N; ++s) gb += pred[s * D_ffn + n] - (float)masks[s * D_ffn + n];
+            for (int64_t d = 0; d < D; ++d) {
+                float gw = 0.0f;
+                for (int64_t s = 0; s < N; ++s)
+                    gw = fmaf(pred[s * D_ffn + n] - (float)masks[s * D_ffn + n], x[s * D + d], gw);
+                w[n * D + d] = fmaf(-lr, gw / (float)N, w[n * D + d]);
+            }
+            b[n] = fmaf(-lr, gb / (float)N, b[n]);
+        }
+    }
+    long long tp = 0, fp = 0, fn = 0;
+    for (int64_t i = 0; i < N * D_ffn; ++i) {
+        int pr = pred[i] >= 0.5f, ac = masks[i] > 0;
+        if (pr && ac) ++tp;
+        else if (pr && !ac) ++fp;
+        else if (!pr && ac) ++fn;
+    }
+    float precision = (tp + fp > 0) ? (float)tp / (float)(tp + fp) : 0.0f;
+    float recall = (tp + fn > 0) ? (float)tp / (float)(tp + fn) : 0.0f;
+    float f1 = (precision + recall > 0) ? 2.0f * precision * recall / (precision + recall) : 0.0f;
+    *f1_out = f1;
+    *enabled = f1 >= 0.70f;
+}

@@ -71,6 +71,9 @@ def lib():
         L.oracle_lg_sparse_mlp.restype = _int
         L.oracle_lg_sparsity.argtypes = [_i32p, _i64, _i64]
         L.oracle_lg_sparsity.restype = ctypes.c_float
+        L.oracle_lg_calibrate.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _int, _int, _f32p, _f32p, _u8p, _f32p,
+                                          _vp, _vp, _vp]
+        L.oracle_lg_calibrate.restype = None
         _lib = L
     return _lib
 
@@ -256,3 +259,20 @@ def lg_sparse_mlp(x, wg, bg, wu, bu, wd, idx, count, sparsity_pct: float, order:
 def lg_sparsity(count, D_ffn: int) -> np.float32:
     c = np.ascontiguousarray(count, dtype=np.int32).reshape(-1)
     return np.float32(lib().oracle_lg_sparsity(c, c.size, D_ffn))
+
+
+def lg_calibrate(x, act, order: int = 0, epochs: int = 50):
+    """calibrate_sparsity_gate: returns (w [D_ffn, D], b [D_ffn], masks, final
+    predictions [N, D_ffn], enabled, f1, sparsity_pct)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    act = np.ascontiguousarray(act, dtype=np.float32)
+    N, D = x.shape
+    D_ffn = act.shape[1]
+    w = np.empty((D_ffn, D), np.float32)
+    b = np.empty(D_ffn, np.float32)
+    masks = np.empty((N, D_ffn), np.uint8)
+    pred = np.empty((N, D_ffn), np.float32)
+    en, f1, sp = ctypes.c_int(0), ctypes.c_float(0), ctypes.c_float(0)
+    lib().oracle_lg_calibrate(x, act, N, D, D_ffn, order, epochs, w, b, masks, pred, ctypes.byref(en),
+                              ctypes.byref(f1), ctypes.byref(sp))
+    return w, b, masks, pred, bool(en.value), np.float32(f1.value), np.float32(sp.value)

@@ -14,7 +14,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(ROOT, "csrc")
 INCLUDE = os.path.join(os.path.dirname(ROOT), "include")
-SOURCES = ["q4_repack.hip", "router.hip", "expert_ffn.hip", "expert_gemm.hip", "legacy_ffn.hip", "capi.hip"]
+SOURCES = ["q4_repack.hip", "router.hip", "expert_ffn.hip", "expert_gemm.hip", "legacy_ffn.hip", "gate_calibrate.hip", "capi.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

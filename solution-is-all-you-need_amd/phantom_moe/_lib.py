@@ -51,6 +51,7 @@ SIGNATURES = {
     "sparse_mlp_forward": (_f32, [_vp] * 9 + [_int, _int, _int, _f32, _vp]),
     "predict_active_neurons": (_f32, [_vp] * 7 + [_int, _int, _int, _f32, _vp]),
     "get_sparsity_stats": (_f32, [_vp, _int, _int, _vp]),
+    "calibrate_sparsity_gate": (_int, [_vp, _vp, _int, _int, _int, _vp, _vp, _vp, _vp, _vp, _vp]),
 }
 
 _lock = threading.Lock()

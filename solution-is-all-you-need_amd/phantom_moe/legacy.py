@@ -92,3 +92,24 @@ def get_sparsity_stats(active_count: torch.Tensor, D_ffn: int) -> float:
     if ret != ret:  # NaN: B == 0, as the reference's 0 / 0
         return ret
     return _check(ret, "get_sparsity_stats")
+
+
+def calibrate_sparsity_gate(inputs: torch.Tensor, mlp_activations: torch.Tensor):
+    """inputs [N, D] fp32, mlp_activations [N, D_ffn] fp32 (on the GPU).
+
+    Returns (gate_w [D_ffn, D] fp32, gate_b [D_ffn] fp32, enabled, f1, sparsity_pct)."""
+    import ctypes
+
+    N, D = inputs.shape
+    if mlp_activations.shape[0] != N:
+        raise _lib.PhantomMoEError("inputs and mlp_activations must have the same number of rows")
+    D_ffn = mlp_activations.shape[1]
+    w = torch.empty((D_ffn, D), dtype=torch.float32, device=inputs.device)
+    b = torch.empty((D_ffn,), dtype=torch.float32, device=inputs.device)
+    en, f1, sp = ctypes.c_bool(False), ctypes.c_float(0.0), ctypes.c_float(0.0)
+    rc = _lib.load().calibrate_sparsity_gate(
+        _dev(inputs, "inputs", torch.float32), _dev(mlp_activations, "mlp_activations", torch.float32), N, D, D_ffn,
+        w.data_ptr(), b.data_ptr(), ctypes.addressof(en), ctypes.addressof(f1), ctypes.addressof(sp),
+        _lib.stream_handle(inputs.device))
+    _lib.check(rc, "calibrate_sparsity_gate")
+    return w, b, bool(en.value), float(f1.value), float(sp.value)

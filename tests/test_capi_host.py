@@ -60,6 +60,10 @@ def test_legacy_validation_returns_status_not_exit():
     assert np.isnan(gss(None, 0, 128, None))  # 0 / 0, as the reference
     msg = lib.phantom_moe_last_error().decode()
     assert msg == "" or "get_sparsity_stats" in msg
+    cal = lib.calibrate_sparsity_gate
+    assert cal(F, F, 0, 8, 8, F, F, F, F, F, None) == EINVAL
+    assert cal(F, None, 4, 8, 8, F, F, F, F, F, None) == EINVAL
+    assert "calibrate_sparsity_gate" in lib.phantom_moe_last_error().decode()
 
 
 def test_version_and_sizes():

@@ -192,3 +192,34 @@ def test_errors_raise_not_exit(dev):
     with pytest.raises(RuntimeError, match="float16"):
         legacy.sparse_mlp_forward(T(x, dev).float(), T(wg, dev), None, T(wu, dev), None, T(wd, dev),
                                   None, None, 0.0)
+
+
+# ------------------------------------------------------------ gate calibration
+
+
+@pytest.mark.parametrize("N,D,Dffn", [(37, 200, 96), (8, 512, 1000), (1, 64, 33), (64, 1031, 130)])
+def test_calibrate_matches_oracle(dev, N, D, Dffn):
+    rng = np.random.default_rng(N * 7 + D + Dffn)
+    x = rng.standard_normal((N, D)).astype(np.float32)
+    W = (rng.standard_normal((Dffn, D)) / np.sqrt(D)).astype(np.float32)
+    act = np.maximum(x @ W.T, 0).astype(np.float32) * rng.random((N, Dffn)).astype(np.float32)
+    w, b, en, f1, sp = legacy.calibrate_sparsity_gate(T(x, dev), T(act, dev))
+    w0, b0, m0, p0, en0, f10, sp0 = O.lg_calibrate(x, act, 0)
+    assert np.float32(sp) == sp0
+    # same order, same fused operations: bit-exact unless an fp64 exp of the
+    # device library and of the C library round apart in one sigmoid
+    np.testing.assert_allclose(w.cpu().numpy(), w0, rtol=1e-6, atol=1e-12)
+    np.testing.assert_allclose(b.cpu().numpy(), b0, rtol=1e-6, atol=1e-12)
+    assert abs(f1 - float(f10)) <= 1e-6 and en == en0
+    # against the reference's loops: weights agree to fp32 rounding
+    w1, b1, _, _, en1, f11, _ = O.lg_calibrate(x, act, 1)
+    np.testing.assert_allclose(w.cpu().numpy(), w1, rtol=1e-4, atol=1e-7)
+    assert abs(f1 - float(f11)) <= 1e-2
+
+
+def test_calibrate_errors(dev):
+    x = torch.zeros((4, 8), dtype=torch.float32, device=dev)
+    with pytest.raises(RuntimeError, match="same number of rows"):
+        legacy.calibrate_sparsity_gate(x, torch.zeros((3, 8), dtype=torch.float32, device=dev))
+    with pytest.raises(RuntimeError, match="float32"):
+        legacy.calibrate_sparsity_gate(x.half(), torch.zeros((4, 8), dtype=torch.float32, device=dev))

@@ -261,3 +261,48 @@ def test_sparsity_stats_closed_form():
     want = np.float32((np.float32(1.0) - np.float32(c.sum()) / np.float32(4) / np.float32(1024)) * np.float32(100))
     assert O.lg_sparsity(c, 1024) == want
     assert O.lg_sparsity(np.array([512], np.int32), 1024) == np.float32(50.0)
+
+
+# --- gate calibration ------------------------------------------------------------
+
+def test_calibration_mask_rule():
+    """gate_calibrate.cu:54-85: active iff |a| >= 0.01 * max(row max |a|, 1e-10);
+    NaN is never active (fmaxf ignores it in the max)."""
+    act = np.array([[0.5, -0.004, 0.006, np.nan, 0.0, -0.005],
+                    [0.0, 0.0, 0.0, 0.0, 0.0, 0.0]], np.float32)
+    x = np.zeros((2, 8), np.float32)
+    _, _, masks, _, _, _, sp = O.lg_calibrate(x, act, 0, epochs=0)
+    np.testing.assert_array_equal(masks, [[1, 0, 1, 0, 0, 1], [0, 0, 0, 0, 0, 0]])
+    assert sp == np.float32((1.0 - 3 / 12) * 100)
+
+
+def test_calibration_first_step_closed_form():
+    """From zero weights every prediction is sigmoid(0) = 1/2, so one step is
+    w = -lr * mean_s((1/2 - y_s) x_s), b = -lr * mean_s(1/2 - y_s)."""
+    rng = np.random.default_rng(20)
+    x = rng.standard_normal((13, 40)).astype(np.float32)
+    act = rng.standard_normal((13, 24)).astype(np.float32)
+    w, b, masks, _, _, _, _ = O.lg_calibrate(x, act, 0, epochs=1)
+    e = 0.5 - masks.astype(np.float64)
+    w_ref = -1e-3 * (e.T @ x.astype(np.float64)) / 13
+    b_ref = -1e-3 * e.mean(0)
+    np.testing.assert_allclose(w, w_ref, rtol=1e-5, atol=1e-9)
+    np.testing.assert_allclose(b, b_ref, rtol=1e-5, atol=1e-9)
+
+
+def test_calibration_f1_and_orders():
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((30, 64)).astype(np.float32)
+    W = (rng.standard_normal((48, 64)) * 0.3).astype(np.float32)
+    act = np.maximum(x @ W.T, 0).astype(np.float32)
+    w0, b0, m0, p0, en0, f10, sp0 = O.lg_calibrate(x, act, 0)
+    pr, ac = p0 >= np.float32(0.5), m0 > 0
+    tp, fp, fn = int((pr & ac).sum()), int((pr & ~ac).sum()), int((~pr & ac).sum())
+    prec, rec = np.float32(tp) / np.float32(tp + fp), np.float32(tp) / np.float32(tp + fn)
+    assert f10 == np.float32(np.float32(2.0) * prec * rec / (prec + rec))
+    assert en0 == (f10 >= np.float32(0.70))
+    w1, b1, m1, _, en1, f11, sp1 = O.lg_calibrate(x, act, 1)
+    np.testing.assert_array_equal(m0, m1)
+    assert sp0 == sp1
+    np.testing.assert_allclose(w0, w1, rtol=1e-4, atol=1e-7)
+    assert abs(f10 - f11) <= 1e-2
