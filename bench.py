@@ -14,7 +14,9 @@ Output: one JSON line with the whole-job tokens/s, the roofline of the
 dominant kernel (gate/up grouped GEMV, one launch between two HIP events on
 its stream), and the CPU baseline (the reference's CPU MoE
 path, restated in oracle/ref_cpu_path.py, timed on this host on a bounded
-sample).
+sample).  The K timed steps run twice: eagerly with per-stage events (the
+stage and roofline figures), then as one HIP graph replay of the same K
+launches (value and ms_per_step; --no-graph keeps the eager timing).
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
 """
@@ -61,6 +63,8 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-stage-events", action="store_true", help="time without the per-stage events")
+    p.add_argument("--no-graph", action="store_true",
+                   help="time eager launches instead of a HIP graph replay of the K steps")
     p.add_argument("--copy-bytes", type=int, default=0,
                    help="after the timed region, one plain device copy of this many bytes (the calibration "
                         "dispatch for FETCH_SIZE / WRITE_SIZE counter runs)")
@@ -320,6 +324,24 @@ def main():
         lib.phantom_moe_set_profile_events(None, 0)
     elapsed = t1 - t0
 
+    # ---- the same K steps captured in one HIP graph and replayed --------
+    # (value and ms_per_step come from the replay unless --no-graph; the
+    # stage events above stay eager, one event pair per stage)
+    graph_elapsed = None
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            gstream = _lib.stream_handle(dev)
+            for i in range(args.steps):
+                layers[i % L](gstream)
+        graph.replay()  # untimed warm-up replay
+        torch.cuda.synchronize()
+        g0 = time.perf_counter()
+        graph.replay()
+        torch.cuda.synchronize()
+        graph_elapsed = time.perf_counter() - g0
+        del graph
+
     if args.copy_bytes > 0:
         src = torch.ones(args.copy_bytes, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -341,6 +363,9 @@ def main():
         ev.destroy(events)
     steps_U = [U[i % L] for i in range(args.steps)]
 
+    eager_elapsed = elapsed
+    if graph_elapsed is not None:
+        elapsed = graph_elapsed
     value = cfg.T * args.steps / elapsed
     out = {
         "metric": metric_name(cfg),
@@ -361,8 +386,12 @@ def main():
             "score": cfg.score, "zipf_bias_s": cfg.zipf, "shared_expert": cfg.shared,
             "layer_instances": L, "weights_resident_gb": round(sum(x.experts.nbytes() for x in layers) / 1e9, 3),
             "active_experts_per_step_mean": round(float(np.mean(steps_U)), 2),
+            "timing": "one HIP graph replay of the K steps" if graph_elapsed is not None else "eager launches",
         },
     }
+    if graph_elapsed is not None:
+        out["eager"] = {"tokens_per_s": round(cfg.T * args.steps / eager_elapsed, 2),
+                        "ms_per_step": round(eager_elapsed * 1e3 / args.steps, 5)}
     if use_events:
         gu_ms = float(np.sum(stages["gate_up"]))
         gu_bytes = float(sum(gate_up_bytes(cfg, u) for u in steps_U))
