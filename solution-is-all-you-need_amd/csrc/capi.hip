@@ -102,6 +102,8 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
   const size_t o_sp = take(sizeof(int32_t) * (size_t)nslots);
   const size_t o_desc = take(sizeof(int4) * (size_t)(E + 1));
   const size_t o_tok = take(sizeof(int32_t) * (size_t)rows);
+  const size_t o_tiles = take(sizeof(int32_t) * (size_t)(max_token_tiles(T, k, E, has_shared) * kTileWords));
+  const size_t o_ntiles = take(sizeof(int32_t));
   const int64_t KpadI = I > 0 ? round_up(I, kQuad) : 0;
   // down operand rows plus an all-zero row
   const size_t o_hq = take(sizeof(uint16_t) * (size_t)((rows + 1) * KpadI * 2));
@@ -120,6 +122,8 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
     ws->slot_pos = reinterpret_cast<int32_t*>(b + o_sp);
     ws->desc = reinterpret_cast<int4*>(b + o_desc);
     ws->seg_tok = reinterpret_cast<int32_t*>(b + o_tok);
+    ws->tiles = reinterpret_cast<int32_t*>(b + o_tiles);
+    ws->n_tiles = reinterpret_cast<int32_t*>(b + o_ntiles);
     ws->hq = reinterpret_cast<uint16_t*>(b + o_hq);
     ws->hs = reinterpret_cast<float*>(b + o_hs);
     ws->outbuf = reinterpret_cast<float*>(b + o_out);
@@ -285,6 +289,7 @@ int phantom_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_
   r.prep_fp16 = gemm;
   r.do_permute = true;
   r.has_shared = has_shared;
+  r.want_tiles = !gemm && pmoe::gate_up_tile_regime(T, H, I, E, top_k, has_shared);
   if (int rc = launch_status(record_stage(0, stream), "profile event")) return rc;
   if (int rc = launch_status(pmoe::launch_route(r, ws, stream), "route")) return rc;
 

@@ -29,6 +29,7 @@
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include "expert_common.h"
 #include "moe_common.h"
@@ -55,6 +56,8 @@ struct GateUpK {
   uint16_t* hq; // [rows + 1][KqI][4 p][4 gi][hi, lo][8] fp16 bits; row `zero_row` is zero
   float* hs;    // [rows + 1][KqI * 4 groups][2 halves] sums of hi + lo
   int64_t zero_row;
+  const int32_t* tiles;    // token tiles of the segments (router permute), or null
+  const int32_t* n_tiles;
 };
 
 struct DownK {
@@ -310,6 +313,262 @@ __global__ __launch_bounds__(kGateUpWaves * kWave, 4) void gate_up_kernel(GateUp
   }
 }
 
+// ------------------------------------------------------- gate/up, token tiles
+//
+// A workgroup takes one token tile of the router's tile table (16 positions
+// of one segment) and a block of its 16-row tiles of I.  It gathers the
+// tile's activation operand for all of K into LDS once, in MFMA operand order
+// ([quad][group][lane] 16-byte pieces, conflict-free reads), with
+// direct-to-LDS loads, so neighbouring waves no longer each gather the same
+// 16 scattered token rows per quad.  Each wave owns whole row tiles (all of K,
+// no cross-wave reduction) and streams their weights through a ring of D
+// chunk buffers in registers: after the math of chunk j it issues the loads
+// of chunk j + D, which may belong to its next row tile.  Loads go through
+// buffer resources, so a chunk costs no vector address arithmetic.
+// Two workgroups fit a CU's LDS at H = 2048, so two waves per SIMD: the
+// register budget is 256.
+constexpr int kTileWaves = 4;
+
+struct WChunk {  // one quad of one row tile: gate and up nibbles and scales
+  u32x4 gw, uw;
+  uint2 gs, us;
+};
+
+struct WSrc {  // weight resources of one expert
+  BufRsrc g, u, gs, us;
+};
+
+__device__ inline void dma_b128(BufRsrc r, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, (int)voff,
+                                           (int)soff, 0, 0);
+}
+
+__device__ inline void dma_b32(BufRsrc r, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, (int)voff,
+                                           (int)soff, 0, 0);
+}
+
+__device__ __attribute__((always_inline)) inline void wchunk_load(const WSrc& s, uint32_t tq_in, WChunk& c) {
+  // wave-uniform already; the compiler is told so (a buffer offset it takes
+  // for divergent would be issued once per distinct value)
+  const uint32_t tq = (uint32_t)__builtin_amdgcn_readfirstlane((int)tq_in);
+  const int lane = threadIdx.x % kWave;
+  const uint32_t o_nib = (uint32_t)lane * 16u;
+  const uint32_t o_sc = (uint32_t)(lane % 16) * 8u;
+  c.gw = buf_load_b128(s.g, o_nib, tq * kQuadNibBytes);
+  c.uw = buf_load_b128(s.u, o_nib, tq * kQuadNibBytes);
+  c.gs = buf_load_b64(s.gs, o_sc, tq * (kQuadScales * 2));
+  c.us = buf_load_b64(s.us, o_sc, tq * (kQuadScales * 2));
+}
+
+// The math of gu_math for one row tile, the activation operand of quad q
+// read from LDS.
+__device__ __attribute__((always_inline)) inline void wchunk_math(const WChunk& c, const u32x4* s_xq, const float* s_sxq,
+                                                                  f32x4& ag, f32x4& au, f32x4& cg, f32x4& cu) {
+  const int lane = threadIdx.x % kWave;
+  const int p = lane / 16;
+  const uint32_t mask = vgpr_const(0x00780078u);
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  float dg[4], du[4];
+  unpack_scales(c.gs, dg);
+  unpack_scales(c.us, du);
+  const uint32_t gwv[4] = {c.gw.x, c.gw.y, c.gw.z, c.gw.w};
+  const uint32_t uwv[4] = {c.uw.x, c.uw.y, c.uw.z, c.uw.w};
+#pragma unroll
+  for (int gi = 0; gi < 4; ++gi) {
+    const u32x4 xa = s_xq[gi * kWave + lane];
+    const u32x4 bg = dequant_unit_bf16(gwv[gi], mask);
+    const u32x4 bu = dequant_unit_bf16(uwv[gi], mask);
+    ag += dg[gi] * mfma_bf16_16x16x32(xa, bg, z);
+    au += du[gi] * mfma_bf16_16x16x32(xa, bu, z);
+  }
+  const float sx = s_sxq[lane];
+  cg = mfma_f32_16x16x4(sx, dg[p], cg);
+  cu = mfma_f32_16x16x4(sx, du[p], cu);
+}
+
+// SwiGLU of one row tile rt of the token tile [m0, end) from the wave's own
+// accumulators (lane (n, p) holds positions m0 + 4p + j of row n), stored as
+// the down kernel's operand.
+__device__ inline void tile_epilogue(const GateUpK& a, BufRsrc hqr, BufRsrc hsr, int64_t m0, int64_t end, uint32_t rt,
+                                     const f32x4& ag, const f32x4& au, const f32x4& cg, const f32x4& cu) {
+  const int lane = threadIdx.x % kWave;
+  const int n = lane % 16;
+  const int p = lane / 16;
+  const uint32_t pos_bytes = (uint32_t)(a.KqI * 512);  // hq bytes per position
+  const f32x4 rg = kUnitScale * ag - kUnitBias * cg;
+  const f32x4 ru = kUnitScale * au - kUnitBias * cu;
+  const uint32_t i = rt * 16u + (uint32_t)n;  // row of I
+  const uint32_t g32 = i / kGroup;
+  const int half = (int)((i % kGroup) / 16);
+  const int pp = n / 4, rr = n % 4;
+  // kmap(p, j) = 4p + {0, 2, 16, 18, 1, 3, 17, 19}[j], inverted per half
+  const int j = half == 0 ? ((rr & 1) ? 4 : 0) + (rr >> 1) : ((rr & 1) ? 6 : 2) + (rr >> 1);
+  const uint32_t o_row = ((((g32 / 4) * 16 + pp * 4 + (g32 % 4)) * 16) + j) * 2;
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const float g = rg[jj], u = ru[jj];
+    const float h = g * (1.0f / (1.0f + expf(-g))) * u;
+    const uint32_t hb = float_to_half_bits(h);
+    const float hf = half_bits_to_float32(hb);
+    const uint32_t lb = float_to_half_bits(h - hf);
+    const float lf = half_bits_to_float32(lb);
+    const int64_t pos = m0 + 4 * p + jj;
+    const bool ok = pos < end;
+    const uint32_t o = (uint32_t)pos * pos_bytes + o_row;
+    if (ok) {
+      __builtin_amdgcn_raw_buffer_store_b16((unsigned short)hb, hqr, (int)o, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16((unsigned short)lb, hqr, (int)(o + 16u), 0, 0);
+    }
+    // the 16 rows of the tile are one half of one group: sum hi + lo over
+    // them (16 consecutive lanes, fixed butterfly order)
+    float sum = hf + lf;
+    sum += __shfl_xor(sum, 8, kWave);
+    sum += __shfl_xor(sum, 4, kWave);
+    sum += __shfl_xor(sum, 2, kWave);
+    sum += __shfl_xor(sum, 1, kWave);
+    if (n == 0 && ok)
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum), hsr,
+                                            (int)((((uint32_t)pos * (uint32_t)a.KqI * 4u + g32) * 2u + half) * 4u), 0, 0);
+  }
+}
+
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima), gfx9 encoding.
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Dynamic LDS: x operand [Kq][4 groups][64 lanes] x 16 bytes, then group sums
+// [Kq][64 lanes] floats.
+inline size_t tile_lds_bytes(int64_t Kq) { return (size_t)Kq * (256 * 16 + 64 * 4); }
+
+template <int D>
+__global__ __launch_bounds__(kTileWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void gate_up_tile_kernel(GateUpK a) {
+  extern __shared__ u32x4 s_x[];
+  const int lane = threadIdx.x % kWave;
+  const int p = lane / 16;
+  const uint32_t w = (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t Kq = (uint32_t)a.Kq;
+  float* s_sx = reinterpret_cast<float*>(s_x + Kq * 256);
+  if (blockIdx.x == 0) {
+    // the all-zero down-operand row read for positions past a segment
+    for (int64_t i = threadIdx.x; i < a.KqI * 256; i += blockDim.x) a.hq[a.zero_row * a.KqI * 256 + i] = 0;
+    for (int64_t i = threadIdx.x; i < a.KqI * 8; i += blockDim.x) a.hs[a.zero_row * a.KqI * 8 + i] = 0.0f;
+  }
+  const uint32_t n_tiles = (uint32_t)__builtin_amdgcn_readfirstlane(*a.n_tiles);
+  const uint32_t n_rt = (uint32_t)(a.I / kRowTile);
+  // row tiles per wave and job: enough that the jobs about fill the grid
+  uint32_t M = (n_tiles * n_rt + kTileWaves * gridDim.x - 1) / (kTileWaves * gridDim.x);
+  M = M < 1 ? 1 : M;
+  const uint32_t per_job = kTileWaves * M;
+  const uint32_t jpt = (n_rt + per_job - 1) / per_job;  // jobs per token tile
+  const uint32_t n_jobs = n_tiles * jpt;
+
+  const BufRsrc xr = buf_rsrc(a.xq, (uint32_t)((a.T + 1) * a.Kq * 256));
+  const BufRsrc xsr = buf_rsrc(a.xs, (uint32_t)((a.T + 1) * a.Kq * 16));
+  const BufRsrc hqr = buf_rsrc(a.hq, (uint32_t)((a.zero_row + 1) * a.KqI * 512));
+  const BufRsrc hsr = buf_rsrc(a.hs, (uint32_t)((a.zero_row + 1) * a.KqI * 32));
+  const uint32_t nib_bytes = (uint32_t)(a.I * a.Kq * 64);
+  const uint32_t sc_bytes = (uint32_t)(a.I * a.Kq * 8);
+
+  for (uint32_t job = blockIdx.x; job < n_jobs; job += gridDim.x) {
+    const uint32_t gt = job / jpt;
+    const uint32_t part = job - gt * jpt;
+    const int32_t* tw = a.tiles + (int64_t)gt * kTileWords;
+    const int tok_w = tw[4 + lane % 16];
+    const int e = __builtin_amdgcn_readfirstlane(tw[0]);
+    const int64_t m0 = __builtin_amdgcn_readfirstlane(tw[1]);
+    const int64_t end = __builtin_amdgcn_readfirstlane(tw[2]);
+    // token of the lane's A-operand row; positions past the segment read the
+    // all-zero row T
+    const int tok = m0 + lane % 16 < end ? tok_w : (int)a.T;
+    const bool routed = e < a.seg.E;
+    WSrc ws;
+    ws.g = buf_rsrc(routed ? a.gate_nib + (int64_t)e * nib_bytes : a.sh_gate_nib, nib_bytes);
+    ws.u = buf_rsrc(routed ? a.up_nib + (int64_t)e * nib_bytes : a.sh_up_nib, nib_bytes);
+    ws.gs = buf_rsrc(routed ? reinterpret_cast<const uint8_t*>(a.gate_sc) + (int64_t)e * sc_bytes
+                            : reinterpret_cast<const uint8_t*>(a.sh_gate_sc), sc_bytes);
+    ws.us = buf_rsrc(routed ? reinterpret_cast<const uint8_t*>(a.up_sc) + (int64_t)e * sc_bytes
+                            : reinterpret_cast<const uint8_t*>(a.sh_up_sc), sc_bytes);
+    // this wave's row tiles: rt0 + kTileWaves * i, i < n_mine
+    const uint32_t rt0 = part * per_job + w;
+    const uint32_t left = rt0 < n_rt ? (n_rt - rt0 + kTileWaves - 1) / kTileWaves : 0;
+    const uint32_t n_mine = left < M ? left : M;
+    const int64_t total = (int64_t)n_mine * Kq;  // chunks of this wave in this job
+
+    // the tile's activation operand -> LDS (every wave takes a share)
+    {
+      const uint32_t row = (uint32_t)tok * Kq;
+      const uint32_t xv = row * 256u + (uint32_t)p * 64u;
+      const uint32_t sv = row * 16u + (uint32_t)p * 4u;
+      for (uint32_t b = w; b < Kq * 4; b += kTileWaves)
+        dma_b128(xr, s_x + b * kWave, xv, (b / 4) * 256u + (b % 4) * 16u);
+      for (uint32_t q = w; q < Kq; q += kTileWaves) dma_b32(xsr, s_sx + q * kWave, sv, q * 16u);
+    }
+    asm volatile("" ::: "memory");  // the operand loads stay older than the weight loads below
+
+    // ring prologue (the load cursor stops at the last chunk; refills past
+    // the end reload it and are never used)
+    uint32_t li = 0, lq = 0;
+    int64_t loaded = 0;
+    auto advance = [&]() {
+      if (loaded + 1 < total) {
+        ++loaded;
+        if (++lq == Kq) {
+          lq = 0;
+          ++li;
+        }
+      }
+    };
+    WChunk buf[D];
+    if (total > 0) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        wchunk_load(ws, (rt0 + kTileWaves * li) * Kq + lq, buf[d]);
+        advance();
+      }
+      // the DMA is older than the D chunks just issued
+      wait_vmcnt<4 * D>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    // every wave's share of the operand is in LDS; no LDS access may move
+    // across the barrier
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+
+    uint32_t ci = 0, cq = 0;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    f32x4 ag = z, au = z, cg = z, cu = z;
+    auto consume = [&](WChunk& c, bool refill) {
+      wchunk_math(c, s_x + cq * 256, s_sx + cq * kWave, ag, au, cg, cu);
+      if (refill) {
+        wchunk_load(ws, (rt0 + kTileWaves * li) * Kq + lq, c);
+        advance();
+      }
+      if (++cq == Kq) {
+        tile_epilogue(a, hqr, hsr, m0, end, rt0 + kTileWaves * ci, ag, au, cg, cu);
+        ag = au = cg = cu = z;
+        cq = 0;
+        ++ci;
+      }
+    };
+    const int64_t n_full = total / D;
+    for (int64_t j = 0; j < n_full; ++j) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) consume(buf[d], true);
+    }
+    const int rem = (int)(total - n_full * D);
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d)
+      if (d < rem) consume(buf[d], false);
+    __syncthreads();  // the operand is read by every wave before the next job overwrites it
+  }
+}
+
 
 // ------------------------------------------------------------------ down
 
@@ -492,6 +751,62 @@ static void tiling_override(const char* name, int max_waves, int* ksplit, int* r
   }
 }
 
+// The token-tile kernel needs the tile table (written by the permute in the
+// decode regime), the tile's operand in LDS, and every buffer it reads or
+// writes addressable with 32-bit offsets.
+// PHANTOM_MOE_GATE_UP_KERNEL=classic selects the K-split kernel instead.
+bool gate_up_tile_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared) {
+  const char* v = getenv("PHANTOM_MOE_GATE_UP_KERNEL");
+  if (v && strcmp(v, "classic") == 0) return false;
+  const int64_t lim = (int64_t)1 << 31;
+  const int64_t Kq = ceil_div(H, kQuad), KqI = ceil_div(I, kQuad);
+  const int64_t rows = T * k + (has_shared ? T : 0);
+  // one wave per row tile of a token tile: with fewer row tiles than four
+  // per CU (a single token, few experts) the K-split kernel fills the chip
+  const int64_t row_items = max_token_tiles(T, k, E, has_shared) * (I / kRowTile);
+  return row_items >= 4 * (int64_t)device_cus() && tile_lds_bytes(Kq) <= 160 * 1024 && I % kRowTile == 0 &&
+         (T + 1) * Kq * 256 < lim && I * Kq * 64 < lim && (rows + 1) * KqI * 512 < lim;
+}
+
+static bool tile_fits(const ExpertArgs& x, const GateUpK& g) {
+  return g.tiles != nullptr && gate_up_tile_regime(x.T, x.H, x.I, x.E, x.k, x.has_shared);
+}
+
+// PHANTOM_MOE_GATE_UP_DEPTH=2..4 overrides the ring depth for tuning sweeps.
+static hipError_t launch_gate_up_tile(const ExpertArgs& x, const GateUpK& g, hipStream_t stream) {
+  int depth = 3;
+  if (const char* v = getenv("PHANTOM_MOE_GATE_UP_DEPTH")) {
+    const int d = atoi(v);
+    if (d >= 2 && d <= 4) depth = d;
+  }
+  const size_t lds = tile_lds_bytes(g.Kq);
+  const int block = kTileWaves * kWave;
+  const int64_t max_jobs = max_token_tiles(x.T, x.k, x.E, x.has_shared) * ceil_div(x.I / kRowTile, kTileWaves);
+#define PMOE_TILE(D_)                                                                                    \
+  do {                                                                                                   \
+    static bool attr_set = false;                                                                        \
+    if (!attr_set) {                                                                                     \
+      hipError_t e_ = hipFuncSetAttribute(reinterpret_cast<const void*>(&gate_up_tile_kernel<D_>),       \
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);       \
+      if (e_ != hipSuccess) return e_;                                                                   \
+      attr_set = true;                                                                                   \
+    }                                                                                                    \
+    int per_cu = 0;                                                                                      \
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gate_up_tile_kernel<D_>, block, lds) !=    \
+            hipSuccess || per_cu < 1)                                                                    \
+      per_cu = 1;                                                                                        \
+    int64_t grid = (int64_t)device_cus() * per_cu;                                                       \
+    if (grid > max_jobs) grid = max_jobs;                                                                \
+    hipLaunchKernelGGL((gate_up_tile_kernel<D_>), dim3((unsigned)(grid < 1 ? 1 : grid)), dim3(block), lds, \
+                       stream, g);                                                                       \
+  } while (0)
+  if (depth == 2) PMOE_TILE(2);
+  else if (depth == 3) PMOE_TILE(3);
+  else PMOE_TILE(4);
+#undef PMOE_TILE
+  return hipGetLastError();
+}
+
 hipError_t launch_gate_up(const ExpertArgs& x, const Workspace& ws, hipStream_t stream) {
   GateUpK g;
   g.seg = segments_of(x, ws);
@@ -512,6 +827,9 @@ hipError_t launch_gate_up(const ExpertArgs& x, const Workspace& ws, hipStream_t 
   g.hq = ws.hq;
   g.hs = ws.hs;
   g.zero_row = x.T * x.k + (x.has_shared ? x.T : 0);
+  g.tiles = ws.tiles;
+  g.n_tiles = ws.n_tiles;
+  if (tile_fits(x, g)) return launch_gate_up_tile(x, g, stream);
   // K split: about four quads per wave (fewer waves per item keep more items
   // in flight per CU), one quad of loads outstanding per wave at a time.
   const int64_t q4 = ceil_div(g.Kq, 4);

@@ -215,7 +215,8 @@ __device__ inline void gemm_tile(const GemmK& a, const int64_t* s_row, u32x4* ld
     }
     const u32x4* la = lds_a + cur * BM * PITCH;
     // the scaled form keeps one group's MFMA results live at a time
-#pragma unroll(SPLIT ? 4 : 1)
+    constexpr int kGroupUnroll = SPLIT ? 4 : 1;
+#pragma unroll kGroupUnroll
     for (int gi = 0; gi < 4; ++gi) {
       if constexpr (SPLIT) {
         u32x4 bh[NB], bl[NB];

@@ -159,4 +159,28 @@ __device__ inline double shfl_xor_f64(double v, int mask) {
   return __shfl_xor(v, mask, kWave);
 }
 
+// Raw buffer access: a 128-bit resource (base, size in bytes) held in SGPRs,
+// a per-lane 32-bit offset and a wave-uniform 32-bit offset.  A load whose
+// lane offsets are fixed for many chunks then costs no vector address
+// arithmetic per chunk; accesses at or past `bytes` read zero and do not
+// write.  Word 3 is the gfx9 raw-buffer format (32-bit data).
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+
+__device__ inline BufRsrc buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+__device__ inline u32x4 buf_load_b128(BufRsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+}
+
+__device__ inline uint2 buf_load_b64(BufRsrc r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+  return make_uint2(v[0], v[1]);
+}
+
+__device__ inline float buf_load_f32(BufRsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+
 }  // namespace pmoe

@@ -12,6 +12,16 @@ namespace pmoe {
 constexpr int kMaxExperts = 512;  // router top-k keeps E/64 <= 8 logits per lane
 constexpr int kMaxTopK = 32;
 
+// Token tiles: the permute cuts every segment into tiles of 16 positions and
+// writes, per tile, {expert, first position, segment end, 0} followed by the
+// token of each of the 16 positions (T, the all-zero activation row, past the
+// segment end).  Routed segments come in expert order, the shared one last.
+constexpr int kTileWords = 20;
+inline int64_t max_token_tiles(int64_t T, int k, int E, int has_shared) {
+  const int64_t nslots = T * k;
+  return (nslots + 15) / 16 + (nslots < E ? nslots : E) + (has_shared ? (T + 15) / 16 : 0);
+}
+
 // Workspace carve-up.  Every region is 256-byte aligned.
 struct Workspace {
   double* logits = nullptr;         // [T, E]
@@ -24,6 +34,8 @@ struct Workspace {
   int32_t* slot_pos = nullptr;      // [T * k]
   int4* desc = nullptr;             // [E + 1] {expert, begin, end, 0} per active segment
   int32_t* seg_tok = nullptr;       // [T * k + T] token of each segment position
+  int32_t* tiles = nullptr;         // [max_token_tiles][kTileWords] 16-position tiles of the segments
+  int32_t* n_tiles = nullptr;       // [1]
   uint16_t* hq = nullptr;          // [rows, Kpad_I * 2] fp16 hi/lo of h, MFMA operand order
   float* hs = nullptr;             // [rows, Kpad_I / 32, 2] half-group sums of h
   float* outbuf = nullptr;          // [T*k + T*shared, H] expert outputs, segment order
@@ -64,6 +76,7 @@ struct RouteArgs {
   bool prep_fp16;    // ws.xq as fp16 (GEMM regime) instead of bf16 (GEMV regime)
   bool do_permute;   // write offsets / sorted_slots / slot_pos / active
   int has_shared;    // append the shared-expert segment to offsets / active
+  bool want_tiles;   // write ws.tiles / ws.n_tiles (the token-tile gate/up kernel reads them)
   int32_t* offsets_out;       // optional user copy of offsets [E+1]
   int32_t* sorted_slots_out;  // where to write sorted slots (default ws)
   int32_t* slot_pos_out;      // where to write slot positions (default ws)
@@ -100,6 +113,10 @@ constexpr int kGemmMinSlotsPerExpert = 64;
 bool gemm_regime(int64_t T, int k, int E);
 hipError_t launch_gemm_gate_up(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);
 hipError_t launch_gemm_down(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);
+
+// Whether the decode-regime gate/up stage runs as the token-tile kernel (which
+// needs the permute's token tiles) for this shape.
+bool gate_up_tile_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
 
 // The three expert stages; launch_experts runs them back to back.
 hipError_t launch_gate_up(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);

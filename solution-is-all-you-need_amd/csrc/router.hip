@@ -63,6 +63,8 @@ struct RouteK {
   int32_t* slot_pos;
   int4* desc;        // [E + 1] {expert, begin, end, 0} per active segment, or null
   int32_t* seg_tok;  // [T*k + T] token of each segment position, or null
+  int32_t* tiles;    // token tiles (see kTileWords), or null
+  int32_t* n_tiles;
   int32_t* counter;  // select workgroups finished (fused permute); zeroed by the logits launch
   int fuse_permute;
 };
@@ -117,6 +119,46 @@ __device__ inline int block_exclusive_scan(int v, int* s_tmp, int* total) {
   return prefix + inc - v;
 }
 
+// The same for three values at once (one pair of barriers); s_tmp holds 3
+// ints per wave.
+__device__ inline int3 block_exclusive_scan3(int3 v, int* s_tmp, int3* total) {
+  const int lane = threadIdx.x % kWave;
+  const int w = threadIdx.x / kWave;
+  int3 inc = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int nx = __shfl_up(inc.x, off, kWave);
+    const int ny = __shfl_up(inc.y, off, kWave);
+    const int nz = __shfl_up(inc.z, off, kWave);
+    if (lane >= off) {
+      inc.x += nx;
+      inc.y += ny;
+      inc.z += nz;
+    }
+  }
+  if (lane == kWave - 1) {
+    s_tmp[3 * w] = inc.x;
+    s_tmp[3 * w + 1] = inc.y;
+    s_tmp[3 * w + 2] = inc.z;
+  }
+  __syncthreads();
+  int3 prefix = make_int3(0, 0, 0), tot = make_int3(0, 0, 0);
+  for (int i = 0; i < (int)(blockDim.x / kWave); ++i) {
+    const int3 s = make_int3(s_tmp[3 * i], s_tmp[3 * i + 1], s_tmp[3 * i + 2]);
+    if (i < w) {
+      prefix.x += s.x;
+      prefix.y += s.y;
+      prefix.z += s.z;
+    }
+    tot.x += s.x;
+    tot.y += s.y;
+    tot.z += s.z;
+  }
+  __syncthreads();
+  *total = tot;
+  return make_int3(prefix.x + inc.x - v.x, prefix.y + inc.y - v.y, prefix.z + inc.z - v.z);
+}
+
 // Lanes of the wave holding the same expert id as this lane (valid lanes only).
 __device__ inline uint64_t match_expert(int e, bool valid, int nbits) {
   uint64_t m = __ballot(valid);
@@ -133,15 +175,18 @@ __device__ inline uint64_t match_expert(int e, bool valid, int nbits) {
 //
 // Besides offsets / sorted_slots / slot_pos it can emit, for the expert
 // kernels, one descriptor {expert, begin, end} per active segment (the shared
-// expert last, covering positions [T*k, T*k + T)) and the token of every
-// segment position.
-__device__ void block_permute(const int32_t* __restrict__ idx, int64_t n, int k, int E, int64_t T,
+// expert last, covering positions [T*k, T*k + T)), the token of every
+// segment position, and the segments' 16-position token tiles.
+__device__ __attribute__((always_inline)) inline void block_permute(const int32_t* __restrict__ idx, int64_t n, int k, int E, int64_t T,
                               int has_shared, int32_t* offsets, int32_t* offsets_user,
                               int32_t* active, int32_t* n_active, int32_t* sorted_slots,
-                              int32_t* slot_pos, int4* desc, int32_t* seg_tok) {
+                              int32_t* slot_pos, int4* desc, int32_t* seg_tok, int32_t* tiles,
+                              int32_t* n_tiles) {
   constexpr int kMaxWaves = 16;
   __shared__ int s_cnt[kMaxWaves][kMaxExperts];
-  __shared__ int s_tmp[kMaxWaves];
+  __shared__ int s_tmp[3 * kMaxWaves];
+  __shared__ int s_tb[kMaxExperts];   // first token tile of each expert's segment
+  __shared__ int s_beg[kMaxExperts];  // first position of each expert's segment
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int w = tid / kWave;
@@ -191,6 +236,7 @@ __device__ void block_permute(const int32_t* __restrict__ idx, int64_t n, int k,
   constexpr int kPer = kMaxExperts / 256;
   int tot[kPer], act[kPer];
   int my_tot = 0, my_act = 0;
+#pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int e = tid * kPer + i;
     int t = 0;
@@ -202,10 +248,15 @@ __device__ void block_permute(const int32_t* __restrict__ idx, int64_t n, int k,
     my_tot += t;
     my_act += act[i];
   }
-  int total = 0, total_act = 0;
-  const int ex = block_exclusive_scan(my_tot, s_tmp, &total);
-  const int ax = block_exclusive_scan(my_act, s_tmp, &total_act);
-  int run = ex, arun = ax;
+  int my_tc = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) my_tc += (tot[i] + 15) / 16;
+  // positions, active experts and token tiles before this thread's experts
+  int3 tot3;
+  const int3 ex3 = block_exclusive_scan3(make_int3(my_tot, my_act, my_tc), s_tmp, &tot3);
+  const int total = tot3.x, total_act = tot3.y, total_tiles = tot3.z;
+  int run = ex3.x, arun = ex3.y, trun = ex3.z;
+#pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int e = tid * kPer + i;
     if (e < E) {
@@ -215,6 +266,15 @@ __device__ void block_permute(const int32_t* __restrict__ idx, int64_t n, int k,
         active[arun] = e;
         if (desc) desc[arun] = make_int4(e, run, run + tot[i], 0);
       }
+      s_tb[e] = trun;
+      s_beg[e] = run;
+      if (tiles) {
+        // headers (pass 2 writes the tokens; words past the segment end are
+        // left as they are and never read)
+        for (int j = 0; j < (tot[i] + 15) / 16; ++j)
+          *reinterpret_cast<int4*>(tiles + (int64_t)(trun + j) * kTileWords) = make_int4(e, run + 16 * j, run + tot[i], 0);
+      }
+      trun += (tot[i] + 15) / 16;
       int b = run;
       for (int ww = 0; ww < NW; ++ww) {
         const int c = s_cnt[ww][e];
@@ -237,6 +297,15 @@ __device__ void block_permute(const int32_t* __restrict__ idx, int64_t n, int k,
   }
   if (has_shared && seg_tok) {
     for (int64_t t = tid; t < T; t += blockDim.x) seg_tok[n + t] = (int32_t)t;
+  }
+  if (tiles) {
+    const int64_t n_sh = has_shared ? (T + 15) / 16 : 0;
+    for (int64_t j = tid; j < n_sh; j += blockDim.x) {
+      int32_t* tw = tiles + (total_tiles + j) * kTileWords;
+      *reinterpret_cast<int4*>(tw) = make_int4(E, total + (int)(16 * j), total + (int)T, 0);
+      for (int jj = 0; jj < 16 && 16 * j + jj < T; ++jj) tw[4 + jj] = (int32_t)(16 * j + jj);
+    }
+    if (tid == 0) *n_tiles = total_tiles + (int)n_sh;
   }
   if (desc) {
     // unused slots up to the launch bound min(E, n) + shared carry expert -1
@@ -266,6 +335,10 @@ __device__ void block_permute(const int32_t* __restrict__ idx, int64_t n, int k,
       sorted_slots[pos] = (int32_t)sl;
       slot_pos[sl] = pos;
       if (seg_tok) seg_tok[pos] = (int32_t)(sl / k);
+      if (tiles) {
+        const int rel = pos - s_beg[e];
+        tiles[(int64_t)(s_tb[e] + rel / 16) * kTileWords + 4 + rel % 16] = (int32_t)(sl / k);
+      }
       // Every lane of the group has read the base before the leader bumps
       // it: LDS operations of one wave complete in program order, and the
       // read above precedes this write in every lane's program.
@@ -606,7 +679,7 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteK a) {
   }
   __syncthreads();
   block_permute(a.topk_idx, a.T * a.k, a.k, a.E, a.T, a.has_shared, a.offsets, a.offsets_user, a.active,
-                a.n_active, a.sorted_slots, a.slot_pos, a.desc, a.seg_tok);
+                a.n_active, a.sorted_slots, a.slot_pos, a.desc, a.seg_tok, a.tiles, a.n_tiles);
 }
 
 __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* idx, int64_t T, int k, int E,
@@ -614,9 +687,9 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* idx, int64
                                                        int32_t* offsets_user, int32_t* active,
                                                        int32_t* n_active, int32_t* sorted_slots,
                                                        int32_t* slot_pos, int4* desc,
-                                                       int32_t* seg_tok) {
+                                                       int32_t* seg_tok, int32_t* tiles, int32_t* n_tiles) {
   block_permute(idx, T * k, k, E, T, has_shared, offsets, offsets_user, active, n_active,
-                sorted_slots, slot_pos, desc, seg_tok);
+                sorted_slots, slot_pos, desc, seg_tok, tiles, n_tiles);
 }
 
 // Logits for many tokens (prefill): the same per-lane partials and tree as
@@ -787,6 +860,10 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
   k.slot_pos = r.slot_pos_out ? r.slot_pos_out : ws.slot_pos;
   k.desc = r.do_permute ? ws.desc : nullptr;
   k.seg_tok = r.do_permute ? ws.seg_tok : nullptr;
+  // the token tiles feed the token-tile gate/up kernel only
+  const bool want_tiles = r.do_permute && r.want_tiles;
+  k.tiles = want_tiles ? ws.tiles : nullptr;
+  k.n_tiles = want_tiles ? ws.n_tiles : nullptr;
   const unsigned sel_blocks = (unsigned)ceil_div(r.T, kSelectWaves);
   k.fuse_permute = (r.do_permute && sel_blocks > 1 && sel_blocks <= kFusedSelectBlocks) ? 1 : 0;
   k.counter = k.fuse_permute ? ws.counter : nullptr;
@@ -805,7 +882,7 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
   if (err != hipSuccess || !r.do_permute || sel_blocks == 1 || k.fuse_permute) return err;
   hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, k.topk_idx, r.T, r.k,
               r.E, r.has_shared, ws.offsets, r.offsets_out, ws.active, ws.n_active, k.sorted_slots, k.slot_pos,
-              k.desc, k.seg_tok);
+              k.desc, k.seg_tok, k.tiles, k.n_tiles);
   return hipGetLastError();
 }
 
@@ -814,7 +891,8 @@ hipError_t launch_permute(const int32_t* topk_idx, int64_t T, int k, int E, int 
                           const Workspace& ws, hipStream_t stream) {
   hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, topk_idx, T, k, E, has_shared,
                      ws.offsets, offsets, ws.active, ws.n_active, sorted_slots, slot_pos,
-                     static_cast<int4*>(nullptr), static_cast<int32_t*>(nullptr));
+                     static_cast<int4*>(nullptr), static_cast<int32_t*>(nullptr), static_cast<int32_t*>(nullptr),
+                     static_cast<int32_t*>(nullptr));
   return hipGetLastError();
 }
 

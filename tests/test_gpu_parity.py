@@ -310,3 +310,41 @@ def test_profiled_forward_is_identical(dev):
         assert hip.hipEventElapsedTime(ctypes.byref(ms), evs[i], evs[i + 1]) == 0 and ms.value > 0, i
     for e in evs:
         hip.hipEventDestroy(ctypes.c_void_p(e))
+
+
+TILE_CASES = [
+    synth.MoEConfig("tile_sigmoid_shared", 512, 512, 64, 8, 40, score="sigmoid", shared=True),
+    synth.MoEConfig("tile_ragged_h", 416, 512, 32, 4, 60),
+    synth.MoEConfig("tile_zipf", 1024, 768, 128, 8, 32, zipf=1.1),
+]
+
+
+@pytest.mark.parametrize("cfg", TILE_CASES, ids=lambda c: c.name)
+def test_gate_up_kernels_agree(dev, cfg, monkeypatch):
+    """The decode gate/up stage has two kernels: the token-tile kernel (operand
+    of a 16-position tile gathered into LDS once, one wave per row tile) where
+    the row tiles of all token tiles give at least four waves per CU, else the
+    K-split kernel.  These shapes are in the token-tile regime; both kernels
+    (the K-split one forced by PHANTOM_MOE_GATE_UP_KERNEL=classic) must meet
+    the layer tolerance against the oracle, shared expert and a ragged last
+    quad of K included."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    n_slots = cfg.T * cfg.k
+    max_tiles = -(-n_slots // 16) + min(n_slots, cfg.E) + (-(-cfg.T // 16) if cfg.shared else 0)
+    assert max_tiles * (cfg.I // 16) >= 4 * cus, "shape not in the token-tile regime"
+    L = synth.host_layer(cfg)
+    xb = synth.activations(cfg.T, cfg.H, seed=7)
+    ex = dev_weights(L, dev)
+    b = None if L.router_bias is None else torch.from_numpy(L.router_bias).to(dev)
+    W = torch.from_numpy(L.router_w).to(dev)
+    x = to_bf16_tensor(xb, dev)
+    ry, ridx, _ = oracle.moe_forward(xb, L.router_w, L.gate, L.up, L.down, cfg.k, cfg.score_mode,
+                                     L.router_bias, shared=L.shared)
+    y_tile, _, idx_tile = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b, return_routing=True)
+    monkeypatch.setenv("PHANTOM_MOE_GATE_UP_KERNEL", "classic")
+    y_cls, _, idx_cls = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b, return_routing=True)
+    monkeypatch.delenv("PHANTOM_MOE_GATE_UP_KERNEL")
+    np.testing.assert_array_equal(idx_tile.cpu().numpy(), ridx)
+    np.testing.assert_array_equal(idx_cls.cpu().numpy(), ridx)
+    check_y(y_tile.cpu().numpy(), ry, cfg.name + " token-tile")
+    check_y(y_cls.cpu().numpy(), ry, cfg.name + " K-split")
