@@ -289,7 +289,8 @@ int phantom_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_
   r.prep_fp16 = gemm;
   r.do_permute = true;
   r.has_shared = has_shared;
-  r.want_tiles = !gemm && pmoe::gate_up_tile_regime(T, H, I, E, top_k, has_shared);
+  r.want_tiles = !gemm && (pmoe::gate_up_tile_regime(T, H, I, E, top_k, has_shared) ||
+                           pmoe::down_tile_regime(T, H, I, E, top_k, has_shared));
   if (int rc = launch_status(record_stage(0, stream), "profile event")) return rc;
   if (int rc = launch_status(pmoe::launch_route(r, ws, stream), "route")) return rc;
 

@@ -73,6 +73,8 @@ struct DownK {
   int64_t Kq;        // quads of I
   int64_t zero_row;  // hq / hs row that holds zeros
   float* outbuf;
+  const int32_t* tiles;  // token tiles of the segments (router permute), or null
+  const int32_t* n_tiles;
 };
 
 // ------------------------------------------------------------------ gate/up
@@ -688,6 +690,161 @@ __global__ __launch_bounds__(kDownWaves * kWave) void down_kernel(DownK a) {
     down_item<NQ, RT>(a, s_desc[item / n_items], (item % n_items) * RT, red);
 }
 
+// --------------------------------------------------------- down, token tiles
+//
+// As gate_up_tile_kernel, for the down projection: a workgroup takes one token
+// tile (16 consecutive segment positions) and a block of the 16-row tiles of
+// H.  The tile's activation operand (fp16 hi and lo of h for all of I, plus the
+// half-group sums) is copied into LDS once with direct-to-LDS loads, in MFMA
+// operand order; each wave streams whole row tiles of W_down (all of I)
+// through a ring of D chunks and writes its expert-output rows.  Positions
+// past the segment read the all-zero operand row, and groups of the padded
+// last quad of I are zeroed at use.
+struct DChunk {  // one quad of one row tile of W_down
+  u32x4 w;
+  uint2 s;
+};
+
+// Dynamic LDS: operand [KqI][4 groups][hi, lo][64 lanes] x 16 bytes, then the
+// half-group sums [KqI][2 halves][64 lanes] floats.
+inline size_t down_tile_lds_bytes(int64_t KqI) { return (size_t)KqI * (8 * 64 * 16 + 2 * 64 * 4); }
+
+template <int D>
+__global__ __launch_bounds__(kTileWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void down_tile_kernel(DownK a) {
+  extern __shared__ u32x4 s_h[];
+  const int lane = threadIdx.x % kWave;
+  const int n = lane % 16;
+  const int p = lane / 16;
+  const uint32_t w = (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t Kq = (uint32_t)a.Kq;  // quads of I
+  const int64_t Kg = a.I / kGroup;
+  float* s_hs = reinterpret_cast<float*>(s_h + Kq * 512);
+  const uint32_t n_tiles = (uint32_t)__builtin_amdgcn_readfirstlane(*a.n_tiles);
+  const uint32_t n_rt = (uint32_t)(a.H / kRowTile);
+  uint32_t M = (n_tiles * n_rt + kTileWaves * gridDim.x - 1) / (kTileWaves * gridDim.x);
+  M = M < 1 ? 1 : M;
+  const uint32_t per_job = kTileWaves * M;
+  const uint32_t jpt = (n_rt + per_job - 1) / per_job;
+  const uint32_t n_jobs = n_tiles * jpt;
+
+  const BufRsrc hqr = buf_rsrc(a.hq, (uint32_t)((a.zero_row + 1) * a.Kq * 512));
+  const BufRsrc hsr = buf_rsrc(a.hs, (uint32_t)((a.zero_row + 1) * a.Kq * 32));
+  const uint32_t nib_bytes = (uint32_t)(a.H * a.Kq * 64);
+  const uint32_t sc_bytes = (uint32_t)(a.H * a.Kq * 8);
+  const uint32_t mask = vgpr_const(0x03C003C0u);
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
+
+  for (uint32_t job = blockIdx.x; job < n_jobs; job += gridDim.x) {
+    const uint32_t gt = job / jpt;
+    const uint32_t part = job - gt * jpt;
+    const int32_t* tw = a.tiles + (int64_t)gt * kTileWords;
+    const int e = __builtin_amdgcn_readfirstlane(tw[0]);
+    const int64_t m0 = __builtin_amdgcn_readfirstlane(tw[1]);
+    const int64_t end = __builtin_amdgcn_readfirstlane(tw[2]);
+    const bool routed = e < a.seg.E;
+    const BufRsrc wr = buf_rsrc(routed ? a.down_nib + (int64_t)e * nib_bytes : a.sh_down_nib, nib_bytes);
+    const BufRsrc sr = buf_rsrc(routed ? reinterpret_cast<const uint8_t*>(a.down_sc) + (int64_t)e * sc_bytes
+                                       : reinterpret_cast<const uint8_t*>(a.sh_down_sc), sc_bytes);
+    const uint32_t rt0 = part * per_job + w;
+    const uint32_t left = rt0 < n_rt ? (n_rt - rt0 + kTileWaves - 1) / kTileWaves : 0;
+    const uint32_t n_mine = left < M ? left : M;
+    const int64_t total = (int64_t)n_mine * Kq;
+
+    // the tile's operand -> LDS: block b = (q, gi, h) is one 16-byte piece per lane
+    {
+      const int64_t pos = m0 + n < end ? m0 + n : a.zero_row;
+      const uint32_t hv = (uint32_t)pos * Kq * 512u + (uint32_t)p * 128u;
+      const uint32_t sv = (uint32_t)pos * Kq * 32u + (uint32_t)p * 8u;
+      for (uint32_t b = w; b < Kq * 8; b += kTileWaves)
+        dma_b128(hqr, s_h + b * kWave, hv, (b / 8) * 512u + ((b / 2) % 4) * 32u + (b % 2) * 16u);
+      for (uint32_t b = w; b < Kq * 2; b += kTileWaves) dma_b32(hsr, s_hs + b * kWave, sv, (b / 2) * 32u + (b % 2) * 4u);
+    }
+    asm volatile("" ::: "memory");  // the operand loads stay older than the weight loads below
+
+    uint32_t li = 0, lq = 0;
+    int64_t loaded = 0;
+    auto advance = [&]() {
+      if (loaded + 1 < total) {
+        ++loaded;
+        if (++lq == Kq) {
+          lq = 0;
+          ++li;
+        }
+      }
+    };
+    auto load = [&](DChunk& c) {
+      const uint32_t tq = (uint32_t)__builtin_amdgcn_readfirstlane((int)((rt0 + kTileWaves * li) * Kq + lq));
+      c.w = buf_load_b128(wr, (uint32_t)lane * 16u, tq * kQuadNibBytes);
+      c.s = buf_load_b64(sr, (uint32_t)n * 8u, tq * (kQuadScales * 2));
+    };
+    DChunk buf[D];
+    if (total > 0) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        load(buf[d]);
+        advance();
+      }
+      wait_vmcnt<2 * D>();  // the operand copies are older than the D chunks
+    } else {
+      wait_vmcnt<0>();
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+
+    uint32_t ci = 0, cq = 0;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc = z, corr = z;
+    auto consume = [&](DChunk& c, bool refill) {
+      float dv[4];
+      unpack_scales(c.s, dv);
+      const uint32_t bwv[4] = {c.w.x, c.w.y, c.w.z, c.w.w};
+      const u32x4* hq_q = s_h + cq * 512;
+      f32x4 part_acc = z;
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const bool real = 4 * (int64_t)cq + gi < Kg;  // padded groups hold no h
+        const u32x4 ah = real ? hq_q[(gi * 2) * kWave + lane] : zero4;
+        const u32x4 al = real ? hq_q[(gi * 2 + 1) * kWave + lane] : zero4;
+        const u32x4 bb = dequant_unit_f16(bwv[gi], mask);
+        f32x4 pp = mfma_f16_16x16x32(ah, bb, z);
+        pp = mfma_f16_16x16x32(al, bb, pp);
+        part_acc += dv[gi] * pp;
+      }
+      const float sp = (4 * (int64_t)cq + p < Kg) ? s_hs[(cq * 2) * kWave + lane] + s_hs[(cq * 2 + 1) * kWave + lane] : 0.0f;
+      corr = mfma_f32_16x16x4(sp, dv[p], corr);
+      acc += part_acc;
+      if (refill) {
+        load(c);
+        advance();
+      }
+      if (++cq == Kq) {
+        const f32x4 res = kUnitScale * acc - kUnitBias * corr;
+        const uint32_t rt = rt0 + kTileWaves * ci;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t pos = m0 + 4 * p + j;
+          if (pos < end) a.outbuf[pos * a.H + rt * 16 + n] = res[j];
+        }
+        acc = corr = z;
+        cq = 0;
+        ++ci;
+      }
+    };
+    const int64_t n_full = total / D;
+    for (int64_t j = 0; j < n_full; ++j) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) consume(buf[d], true);
+    }
+    const int rem = (int)(total - n_full * D);
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d)
+      if (d < rem) consume(buf[d], false);
+    __syncthreads();  // the operand is read by every wave before the next job overwrites it
+  }
+}
+
+
 // y[t] = sum_j w[t,j] * out[slot_pos[t*k+j]] (+ out[T*k + t] for the shared
 // expert), j in slot order, fp32.
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ outbuf,
@@ -848,6 +1005,56 @@ hipError_t launch_gate_up(const ExpertArgs& x, const Workspace& ws, hipStream_t 
   return hipGetLastError();
 }
 
+bool down_tile_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared) {
+  const char* v = getenv("PHANTOM_MOE_DOWN_KERNEL");
+  if (v && strcmp(v, "classic") == 0) return false;
+  const int64_t lim = (int64_t)1 << 31;
+  const int64_t KqI = ceil_div(I, kQuad);
+  const int64_t rows = T * k + (has_shared ? T : 0);
+  // Its waves stream short rows (I / 128 chunks of 1 KB each), so it needs
+  // two workgroups per CU (operand within half the LDS) and at least eight
+  // row tiles per CU to beat the K-split kernel (measured at H 7168, I 2048:
+  // one workgroup per CU, 2.8x slower; at a single token of Qwen3, 7% slower).
+  const int64_t row_items = max_token_tiles(T, k, E, has_shared) * (H / kRowTile);
+  return row_items >= 8 * (int64_t)device_cus() && down_tile_lds_bytes(KqI) <= 80 * 1024 && H % kRowTile == 0 &&
+         H * KqI * 64 < lim && (rows + 1) * KqI * 512 < lim;
+}
+
+// PHANTOM_MOE_DOWN_DEPTH=2, 4 or 6 overrides the ring depth for tuning sweeps.
+static hipError_t launch_down_tile(const ExpertArgs& x, const DownK& d, hipStream_t stream) {
+  int depth = 2;
+  if (const char* v = getenv("PHANTOM_MOE_DOWN_DEPTH")) {
+    const int dd = atoi(v);
+    if (dd == 2 || dd == 4 || dd == 6) depth = dd;
+  }
+  const size_t lds = down_tile_lds_bytes(d.Kq);
+  const int block = kTileWaves * kWave;
+  const int64_t max_jobs = max_token_tiles(x.T, x.k, x.E, x.has_shared) * ceil_div(x.H / kRowTile, kTileWaves);
+#define PMOE_DTILE(D_)                                                                                   \
+  do {                                                                                                   \
+    static bool attr_set = false;                                                                        \
+    if (!attr_set) {                                                                                     \
+      hipError_t e_ = hipFuncSetAttribute(reinterpret_cast<const void*>(&down_tile_kernel<D_>),          \
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);       \
+      if (e_ != hipSuccess) return e_;                                                                   \
+      attr_set = true;                                                                                   \
+    }                                                                                                    \
+    int per_cu = 0;                                                                                      \
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, down_tile_kernel<D_>, block, lds) !=       \
+            hipSuccess || per_cu < 1)                                                                    \
+      per_cu = 1;                                                                                        \
+    int64_t grid = (int64_t)device_cus() * per_cu;                                                       \
+    if (grid > max_jobs) grid = max_jobs;                                                                \
+    hipLaunchKernelGGL((down_tile_kernel<D_>), dim3((unsigned)(grid < 1 ? 1 : grid)), dim3(block), lds,  \
+                       stream, d);                                                                       \
+  } while (0)
+  if (depth == 2) PMOE_DTILE(2);
+  else if (depth == 4) PMOE_DTILE(4);
+  else PMOE_DTILE(6);
+#undef PMOE_DTILE
+  return hipGetLastError();
+}
+
 hipError_t launch_down(const ExpertArgs& x, const Workspace& ws, hipStream_t stream) {
   DownK d;
   d.seg = segments_of(x, ws);
@@ -862,6 +1069,9 @@ hipError_t launch_down(const ExpertArgs& x, const Workspace& ws, hipStream_t str
   d.Kq = ceil_div(x.I, kQuad);
   d.zero_row = x.T * x.k + (x.has_shared ? x.T : 0);
   d.outbuf = ws.outbuf;
+  d.tiles = ws.tiles;
+  d.n_tiles = ws.n_tiles;
+  if (d.tiles && down_tile_regime(x.T, x.H, x.I, x.E, x.k, x.has_shared)) return launch_down_tile(x, d, stream);
   Split sp = choose_split(d.Kq, kDownWaves);
   sp.nq = 1;   // measured faster than NQ = 2 at the occupancy NQ = 1 allows
   int rt = 2;  // H is a multiple of 32: an even number of 16-row tiles

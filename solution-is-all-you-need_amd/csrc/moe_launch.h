@@ -117,6 +117,8 @@ hipError_t launch_gemm_down(const ExpertArgs& a, const Workspace& ws, hipStream_
 // Whether the decode-regime gate/up stage runs as the token-tile kernel (which
 // needs the permute's token tiles) for this shape.
 bool gate_up_tile_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
+// The same for the down stage.
+bool down_tile_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
 
 // The three expert stages; launch_experts runs them back to back.
 hipError_t launch_gate_up(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);

@@ -314,24 +314,27 @@ def test_profiled_forward_is_identical(dev):
 
 TILE_CASES = [
     synth.MoEConfig("tile_sigmoid_shared", 512, 512, 64, 8, 40, score="sigmoid", shared=True),
-    synth.MoEConfig("tile_ragged_h", 416, 512, 32, 4, 60),
+    synth.MoEConfig("tile_ragged_h", 416, 512, 64, 8, 60),
+    synth.MoEConfig("tile_ragged_i", 512, 480, 64, 8, 40),
     synth.MoEConfig("tile_zipf", 1024, 768, 128, 8, 32, zipf=1.1),
 ]
 
 
 @pytest.mark.parametrize("cfg", TILE_CASES, ids=lambda c: c.name)
-def test_gate_up_kernels_agree(dev, cfg, monkeypatch):
-    """The decode gate/up stage has two kernels: the token-tile kernel (operand
-    of a 16-position tile gathered into LDS once, one wave per row tile) where
-    the row tiles of all token tiles give at least four waves per CU, else the
-    K-split kernel.  These shapes are in the token-tile regime; both kernels
-    (the K-split one forced by PHANTOM_MOE_GATE_UP_KERNEL=classic) must meet
-    the layer tolerance against the oracle, shared expert and a ragged last
-    quad of K included."""
+def test_expert_kernels_agree(dev, cfg, monkeypatch):
+    """Each decode expert stage has two kernels: the token-tile kernel (the
+    operand of a 16-position tile copied into LDS once, one wave per row tile)
+    where the row tiles of all token tiles give at least four waves per CU
+    (eight for down), else the K-split kernel.  These shapes are in the
+    token-tile regime of both stages; both kernel pairs (the K-split ones forced by
+    PHANTOM_MOE_GATE_UP_KERNEL / PHANTOM_MOE_DOWN_KERNEL=classic) must meet the
+    layer tolerance against the oracle, shared expert and ragged last quads of
+    H and of I included."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     n_slots = cfg.T * cfg.k
     max_tiles = -(-n_slots // 16) + min(n_slots, cfg.E) + (-(-cfg.T // 16) if cfg.shared else 0)
-    assert max_tiles * (cfg.I // 16) >= 4 * cus, "shape not in the token-tile regime"
+    assert max_tiles * (cfg.I // 16) >= 4 * cus, "shape not in the gate/up token-tile regime"
+    assert max_tiles * (cfg.H // 16) >= 8 * cus, "shape not in the down token-tile regime"
     L = synth.host_layer(cfg)
     xb = synth.activations(cfg.T, cfg.H, seed=7)
     ex = dev_weights(L, dev)
@@ -342,8 +345,10 @@ def test_gate_up_kernels_agree(dev, cfg, monkeypatch):
                                      L.router_bias, shared=L.shared)
     y_tile, _, idx_tile = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b, return_routing=True)
     monkeypatch.setenv("PHANTOM_MOE_GATE_UP_KERNEL", "classic")
+    monkeypatch.setenv("PHANTOM_MOE_DOWN_KERNEL", "classic")
     y_cls, _, idx_cls = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b, return_routing=True)
     monkeypatch.delenv("PHANTOM_MOE_GATE_UP_KERNEL")
+    monkeypatch.delenv("PHANTOM_MOE_DOWN_KERNEL")
     np.testing.assert_array_equal(idx_tile.cpu().numpy(), ridx)
     np.testing.assert_array_equal(idx_cls.cpu().numpy(), ridx)
     check_y(y_tile.cpu().numpy(), ry, cfg.name + " token-tile")
