@@ -41,8 +41,8 @@ BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PREFILL_T = 1024  # from this batch on, a workload is priced against the MFMA roofline
 
 
-def pmc_summary(workload: str) -> str:
-    return os.path.join(ROOT, "profiles", f"gate_up_kernel_{workload}_pmc.json")
+def pmc_summary(kernel: str, workload: str) -> str:
+    return os.path.join(ROOT, "profiles", f"{kernel}_{workload}_pmc.json")
 
 
 def metric_name(cfg) -> str:
@@ -396,11 +396,15 @@ def main():
         gu_ms = float(np.sum(stages["gate_up"]))
         gu_bytes = float(sum(gate_up_bytes(cfg, u) for u in steps_U))
         achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
+        # the kernel the gate/up stage launches at this shape
+        names = dict(kv.split("=") for kv in _lib.load().phantom_moe_expert_kernels(
+            cfg.T, cfg.H, cfg.I, cfg.E, cfg.k, int(cfg.shared)).decode().split(";"))
+        gu_kernel = names["gate_up"]
         traffic = None
-        if os.path.exists(pmc_summary(cfg.name)):
-            with open(pmc_summary(cfg.name)) as f:
+        if os.path.exists(pmc_summary(gu_kernel, cfg.name)):
+            with open(pmc_summary(gu_kernel, cfg.name)) as f:
                 pmc = json.load(f)
-            if pmc.get("workload") == cfg.name:
+            if pmc.get("workload") == cfg.name and pmc.get("kernel") == gu_kernel:
                 traffic = pmc.get("hbm_bytes_per_launch")
         if cfg.T >= PREFILL_T:
             tf = gate_up_flops(cfg) * args.steps / (gu_ms * 1e-3) / 1e12
@@ -411,7 +415,8 @@ def main():
             out["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
         out["roofline"].update({
-            "kernel": "gate_up_kernel",
+            "kernel": gu_kernel,
+            "down_kernel": names["down"],
             "algorithmic_bytes_per_launch": round(gu_bytes / args.steps),
             "avg_launch_us": round(gu_ms * 1e3 / args.steps, 3),
         })

@@ -79,6 +79,13 @@ PHANTOM_MOE_API const char* phantom_moe_version(void);
 #define PHANTOM_MOE_PROFILE_EVENTS 5
 PHANTOM_MOE_API int phantom_moe_set_profile_events(hipEvent_t* events, int n_events);
 
+/* Names of the kernels phantom_moe_forward launches for the gate/up and down
+ * stages at this shape, as "gate_up=<kernel>;down=<kernel>" (thread-local
+ * storage, valid until the next call on the thread), so a profile can be
+ * matched to its launches.  Diagnostic only: no counterpart in the reference. */
+PHANTOM_MOE_API const char* phantom_moe_expert_kernels(int64_t T, int64_t H, int64_t I, int E, int top_k,
+                                                       int has_shared);
+
 /* ---------------------------------------------------------------- */
 /* Q4_0 repack                                                       */
 /* ---------------------------------------------------------------- */

@@ -140,6 +140,20 @@ const char* phantom_moe_last_error(void) { return g_err; }
 
 const char* phantom_moe_version(void) { return "phantom_moe 0.1.0 gfx950"; }
 
+const char* phantom_moe_expert_kernels(int64_t T, int64_t H, int64_t I, int E, int top_k, int has_shared) {
+  static thread_local char buf[96];
+  const char *gu, *dn;
+  if (pmoe::gemm_regime(T, top_k, E)) {
+    gu = "gemm_gate_up_kernel";
+    dn = "gemm_down_kernel";
+  } else {
+    gu = pmoe::gate_up_tile_regime(T, H, I, E, top_k, has_shared) ? "gate_up_tile_kernel" : "gate_up_kernel";
+    dn = pmoe::down_tile_regime(T, H, I, E, top_k, has_shared) ? "down_tile_kernel" : "down_kernel";
+  }
+  snprintf(buf, sizeof(buf), "gate_up=%s;down=%s", gu, dn);
+  return buf;
+}
+
 int phantom_moe_set_profile_events(hipEvent_t* events, int n_events) {
   if (events == nullptr) {
     g_prof_events = nullptr;

@@ -32,6 +32,7 @@ SIGNATURES = {
     "phantom_moe_last_error": (ctypes.c_char_p, []),
     "phantom_moe_version": (ctypes.c_char_p, []),
     "phantom_moe_set_profile_events": (_int, [_vp, _int]),
+    "phantom_moe_expert_kernels": (ctypes.c_char_p, [_i64, _i64, _i64, _int, _int, _int]),
     "phantom_q4_0_nib_bytes": (_i64, [_i64, _i64]),
     "phantom_q4_0_scale_bytes": (_i64, [_i64, _i64]),
     "phantom_q4_0_repack": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
