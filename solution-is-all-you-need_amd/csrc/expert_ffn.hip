@@ -1073,8 +1073,12 @@ hipError_t launch_down(const ExpertArgs& x, const Workspace& ws, hipStream_t str
   d.n_tiles = ws.n_tiles;
   if (d.tiles && down_tile_regime(x.T, x.H, x.I, x.E, x.k, x.has_shared)) return launch_down_tile(x, d, stream);
   Split sp = choose_split(d.Kq, kDownWaves);
-  sp.nq = 1;   // measured faster than NQ = 2 at the occupancy NQ = 1 allows
   int rt = 2;  // H is a multiple of 32: an even number of 16-row tiles
+  // Two quads of loads in flight per wave pay off only when items are few
+  // (one token: 7.7 vs 8.4 us at Qwen3 shape, 28.6 vs 29.8 at H 7168, I 2048);
+  // with many items the occupancy NQ = 1 allows wins (158 vs 162 us at 8 tokens).
+  const int64_t items = (int64_t)max_active_experts(x) * (x.H / (kRowTile * rt));
+  sp.nq = items <= 4096 ? 2 : 1;
   tiling_override("PHANTOM_MOE_DOWN_TILING", kDownWaves, &sp.ksplit, &rt, &sp.nq);
   if (rt == 4 && (x.H / kRowTile) % 4) rt = 2;
   const int block = kWave * sp.ksplit;

@@ -96,31 +96,19 @@ __device__ inline void load_x4<float>(const float* x, int64_t off, float v[4]) {
   v[3] = r.w;
 }
 
-// Block-wide exclusive scan for 256 threads.  Returns the exclusive prefix and
-// writes the block total to *total.
-__device__ inline int block_exclusive_scan(int v, int* s_tmp, int* total) {
-  const int lane = threadIdx.x % kWave;
-  const int w = threadIdx.x / kWave;
-  int inc = v;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int n = __shfl_up(inc, off, kWave);
-    if (lane >= off) inc += n;
-  }
-  if (lane == kWave - 1) s_tmp[w] = inc;
-  __syncthreads();
-  int prefix = 0, tot = 0;
-  for (int i = 0; i < (int)(blockDim.x / kWave); ++i) {
-    if (i < w) prefix += s_tmp[i];
-    tot += s_tmp[i];
-  }
-  __syncthreads();
-  *total = tot;
-  return prefix + inc - v;
+// Workgroup barrier for LDS data only: waits for this wave's LDS accesses,
+// not for its outstanding global stores (which no wave of the workgroup reads
+// back), as a __syncthreads() fence would.
+__device__ inline void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt not waited for
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
-// The same for three values at once (one pair of barriers); s_tmp holds 3
-// ints per wave.
+// Block-wide exclusive scan of three values at once (256 threads or more,
+// one pair of barriers); s_tmp holds 3 ints per wave.  Returns the exclusive
+// prefixes and writes the block totals to *total.
 __device__ inline int3 block_exclusive_scan3(int3 v, int* s_tmp, int3* total) {
   const int lane = threadIdx.x % kWave;
   const int w = threadIdx.x / kWave;
@@ -141,7 +129,7 @@ __device__ inline int3 block_exclusive_scan3(int3 v, int* s_tmp, int3* total) {
     s_tmp[3 * w + 1] = inc.y;
     s_tmp[3 * w + 2] = inc.z;
   }
-  __syncthreads();
+  lds_barrier();
   int3 prefix = make_int3(0, 0, 0), tot = make_int3(0, 0, 0);
   for (int i = 0; i < (int)(blockDim.x / kWave); ++i) {
     const int3 s = make_int3(s_tmp[3 * i], s_tmp[3 * i + 1], s_tmp[3 * i + 2]);
@@ -154,7 +142,7 @@ __device__ inline int3 block_exclusive_scan3(int3 v, int* s_tmp, int3* total) {
     tot.y += s.y;
     tot.z += s.z;
   }
-  __syncthreads();
+  lds_barrier();
   *total = tot;
   return make_int3(prefix.x + inc.x - v.x, prefix.y + inc.y - v.y, prefix.z + inc.z - v.z);
 }
@@ -195,7 +183,7 @@ __device__ __attribute__((always_inline)) inline void block_permute(const int32_
   while ((1 << nbits) < E) ++nbits;
 
   for (int i = tid; i < NW * kMaxExperts; i += blockDim.x) s_cnt[i / kMaxExperts][i % kMaxExperts] = 0;
-  __syncthreads();
+  lds_barrier();
 
   const int64_t chunk = round_up(ceil_div(n, NW), kWave);
   const int64_t beg = w * chunk;
@@ -229,7 +217,7 @@ __device__ __attribute__((always_inline)) inline void block_permute(const int32_
     const uint64_t m = match_expert(e, valid, nbits);
     if (valid && (m & lt_mask) == 0) s_cnt[w][e] += __popcll(m);
   }
-  __syncthreads();
+  lds_barrier();
 
   // Scan over experts: thread t owns experts t, t + blockDim, ... (at most
   // kMaxExperts / 256 = 2 per thread for 256 threads).
@@ -313,7 +301,7 @@ __device__ __attribute__((always_inline)) inline void block_permute(const int32_
     const int max_active = (int)((n < E) ? n : E) + (has_shared ? 1 : 0);
     for (int u = n_act + tid; u < max_active; u += blockDim.x) desc[u] = make_int4(-1, 0, 0, 0);
   }
-  __syncthreads();
+  lds_barrier();
 
   // Pass 2: placement.
   for (int64_t r0 = beg, i = 0; r0 < end; r0 += kWave, ++i) {
@@ -371,7 +359,7 @@ __device__ inline uint64_t logit_key(double v) {
 //     winner i among them; rank r goes to slot r.
 template <int NV>
 __device__ void wave_topk(const RouteK& a, int64_t t, uint64_t* s_ck, double* s_cv, int* s_ci,
-                          double* s_val, int* s_idx, double* s_e) {
+                          double* s_val, int* s_idx, double* s_e, int* s_out) {
   const int lane = threadIdx.x % kWave;
   const uint64_t lt_mask = (1ull << lane) - 1ull;
   uint64_t key[NV];
@@ -447,6 +435,7 @@ __device__ void wave_topk(const RouteK& a, int64_t t, uint64_t* s_ck, double* s_
     double sum = 0.0;
     for (int i = 0; i < a.k; ++i) sum += s_e[i];
     a.topk_idx[t * a.k + lane] = s_idx[lane];
+    if (s_out) s_out[t * a.k + lane] = s_idx[lane];
     a.topk_w[t * a.k + lane] = (float)(ej / sum);
   }
   __builtin_amdgcn_wave_barrier();
@@ -555,7 +544,6 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteK a) {
   const int64_t t0 = (int64_t)blockIdx.y * TT;
   const int e0 = blockIdx.x * (4 * EW) + w * EW;
   const XT* x = static_cast<const XT*>(a.x);
-  if (a.prep_x) prep_x_tile(a, t0, TT);
   if (a.counter && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *a.counter = 0;
   // The bias of the expert this lane may write, fetched ahead of the GEMV.
   float bias_e = 0.0f;
@@ -604,6 +592,8 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteK a) {
         for (int i = 0; i < 4; ++i) xv[cb][ti][i] = ok ? v4[i] : 0.0f;
       }
     }
+    // the MFMA-ordered copy of x, its loads in flight with the first batch's
+    if (c0 == 0 && a.prep_x) prep_x_tile(a, t0, TT);
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
 #pragma unroll
@@ -657,12 +647,21 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteK a) {
   __shared__ double s_val[kSelectWaves][kMaxTopK];
   __shared__ double s_e[kSelectWaves][kMaxTopK];
   __shared__ int s_idx[kSelectWaves][kMaxTopK];
+  __shared__ int s_sel[kSelectWaves * kMaxTopK];  // one workgroup: every token's selection, for the permute
   __shared__ int s_last;
   const int w = threadIdx.x / kWave;
   const int nw = blockDim.x / kWave;
+  const bool single = gridDim.x == 1 && a.T <= kSelectWaves;
   for (int64_t t = (int64_t)blockIdx.x * nw + w; t < a.T; t += (int64_t)gridDim.x * nw)
-    wave_topk<NV>(a, t, s_ck[w], s_cv[w], s_ci[w], s_val[w], s_idx[w], s_e[w]);
+    wave_topk<NV>(a, t, s_ck[w], s_cv[w], s_ci[w], s_val[w], s_idx[w], s_e[w], single ? s_sel : nullptr);
   if (!a.do_permute) return;
+  if (single) {
+    // the selection reaches the permute through LDS, not a global round trip
+    lds_barrier();
+    block_permute(s_sel, a.T * a.k, a.k, a.E, a.T, a.has_shared, a.offsets, a.offsets_user, a.active,
+                  a.n_active, a.sorted_slots, a.slot_pos, a.desc, a.seg_tok, a.tiles, a.n_tiles);
+    return;
+  }
   if (gridDim.x > 1) {
     if (!a.fuse_permute) return;
     // Every wave's top-k stores have reached L2 before the barrier; thread 0
