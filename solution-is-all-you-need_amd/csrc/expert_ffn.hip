@@ -340,16 +340,6 @@ struct WSrc {  // weight resources of one expert
   BufRsrc g, u, gs, us;
 };
 
-__device__ inline void dma_b128(BufRsrc r, void* lds, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, (int)voff,
-                                           (int)soff, 0, 0);
-}
-
-__device__ inline void dma_b32(BufRsrc r, void* lds, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, (int)voff,
-                                           (int)soff, 0, 0);
-}
-
 __device__ __attribute__((always_inline)) inline void wchunk_load(const WSrc& s, uint32_t tq_in, WChunk& c) {
   // wave-uniform already; the compiler is told so (a buffer offset it takes
   // for divergent would be issued once per distinct value)
@@ -433,13 +423,6 @@ __device__ inline void tile_epilogue(const GateUpK& a, BufRsrc hqr, BufRsrc hsr,
       __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum), hsr,
                                             (int)((((uint32_t)pos * (uint32_t)a.KqI * 4u + g32) * 2u + half) * 4u), 0, 0);
   }
-}
-
-// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima), gfx9 encoding.
-template <int N>
-__device__ inline void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
 // Dynamic LDS: x operand [Kq][4 groups][64 lanes] x 16 bytes, then group sums

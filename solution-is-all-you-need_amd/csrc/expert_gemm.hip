@@ -23,6 +23,11 @@
 // 2^-20 of the product and dropped).  The scale lives inside the operands, so
 // there is no per-group vector-ALU work on the accumulators.
 //
+// Two tile pipelines share these tiles and this arithmetic.  The default,
+// gemm_tile3 (gemm_*_kernel2, 8 waves), stages both operands into a 3-stage
+// LDS ring with direct-to-LDS loads two quads ahead; gemm_tile (4 waves,
+// PHANTOM_MOE_GEMM_KERNEL=v1) stages A through registers one quad ahead.
+//
 // Tiling.  A workgroup of kGemmWaves waves owns BM consecutive positions of
 // one expert segment and a block of weight rows.  Per K quad (128), the
 // positions' A rows are staged in LDS (double-buffered; 16-byte units XOR-
@@ -35,6 +40,8 @@
 //            produces whole down-operand chunks (hi + lo, written via LDS).
 //   down (BM 64): wave w takes two 16-row tiles of H.
 #include <math.h>
+#include <stdlib.h>
+#include <string.h>
 
 #include "expert_common.h"
 #include "moe_common.h"
@@ -471,10 +478,298 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void gemm_down_kernel(GemmK a) 
   }
 }
 
+// ------------------------------------------------- tile pipeline, LDS ring
+//
+// The same tiles and arithmetic as gemm_tile, with both operands staged by
+// direct-to-LDS loads into a ring of kG2Stages LDS stages two quads ahead of
+// the MFMAs: per quad and wave, the wave's share of the A rows and its own B
+// operands (nibbles and scales).  The loads are issued from inline assembly
+// (dma_b128_unseen), so the compiler adds no waits of its own; per quad there
+// is one workgroup barrier, preceded by a wait for the wave's copies of the
+// quad about to be read (the newer quad's copies stay in flight), which also
+// guarantees every wave has left the stage about to be refilled.  A rows are
+// stored with unit s of row r at s ^ (r & 15), so the 16 rows one
+// ds_read_b128 group touches fall in distinct banks for both operand widths.
+// Padded groups of K (I not a multiple of 128 in the down projection, whose
+// operand rows leave them unwritten) are skipped.
+constexpr int kG2Waves = 8;
+constexpr int kG2Stages = 3;
+constexpr int kG2AUnits = 2048;  // 16-byte units of A per stage: BM x 16 x AW (128 x 16, 64 x 32)
+constexpr int kG2NB = 2;         // B operands per wave in both kernels
+constexpr int kG2BUnits = kG2Waves * kG2NB * kWave;  // nibbles: one 1 KiB unit row per operand
+constexpr int kG2SUnits = kG2Waves * kG2NB * 8;      // scales: 128 B per operand
+constexpr int kG2StageUnits = kG2AUnits + kG2BUnits + kG2SUnits;
+constexpr int kG2LoadsPerQuad = kG2AUnits / kWave / kG2Waves + 2 * kG2NB;  // per wave
+
+// s_waitcnt vmcnt(N) lgkmcnt(0), gfx9 encoding.
+template <int N>
+__device__ inline void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));
+}
+
+// Active segment count (active slots come first; wave 0 scans, the others
+// wait at the barrier) without copying the descriptors to LDS.
+__device__ inline int count_active(const SegSrc& seg, int* s_nact) {
+  if (threadIdx.x < kWave) {
+    int cnt = 0;
+    for (int u0 = 0; u0 < seg.max_slots; u0 += kWave) {
+      const int u = u0 + (int)threadIdx.x;
+      const bool act = u < seg.max_slots && seg.desc[u < seg.max_slots ? u : 0].x >= 0;
+      cnt += __popcll(__ballot(act));
+    }
+    if (threadIdx.x == 0) *s_nact = cnt;
+  }
+  __syncthreads();
+  return *s_nact;
+}
+
+template <int BM, int AW>
+__device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* lds, const i32x4& ar,
+                                  const i32x4 (&nr)[kG2NB], const i32x4 (&sr)[kG2NB], const int64_t (&rt)[kG2NB],
+                                  f32x4 acc[kG2NB][BM / 16]) {
+  constexpr int NB = kG2NB;
+  constexpr int TT = BM / 16;
+  constexpr int UPR = 16 * AW;                // 16-byte units per A row
+  constexpr int RPD = kWave / UPR;            // A rows per direct-to-LDS load
+  constexpr int ND = kG2AUnits / kWave / kG2Waves;  // A loads per wave per quad
+  static_assert(BM * UPR == kG2AUnits && ND >= 1, "one stage holds the tile");
+  const int lane = threadIdx.x % kWave;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int n = lane % 16;
+  const int p = lane / 16;
+  const uint32_t mask = vgpr_const(0x000F000Fu);
+  const uint32_t row_bytes = (uint32_t)(a.Kq * 256 * AW);
+  // this wave's A loads j = w + kG2Waves * i: lane l fills slot l % UPR of row
+  // j * RPD + l / UPR with logical unit (slot ^ (row & 15))
+  uint32_t voff[ND];
+#pragma unroll
+  for (int i = 0; i < ND; ++i) {
+    const int j = w + kG2Waves * i;
+    const int row = j * RPD + lane / UPR;
+    const int unit = (lane % UPR) ^ (row & 15);
+    voff[i] = (uint32_t)s_row[row] * row_bytes + (uint32_t)unit * 16u;
+  }
+  const uint32_t lds0 = lds_addr(lds);
+  auto uni = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
+  auto copy = [&](int64_t q) {
+    const uint32_t st = lds0 + (uint32_t)(q % kG2Stages) * (kG2StageUnits * 16);
+    const uint32_t aoff = uni((uint32_t)q * 256u * AW);
+#pragma unroll
+    for (int i = 0; i < ND; ++i)
+      dma_b128_unseen(ar, uni(st + (uint32_t)(w + kG2Waves * i) * kWave * 16), voff[i], aoff);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const uint32_t tq = uni((uint32_t)(rt[b] * a.Kq + q));
+      dma_b128_unseen(nr[b], uni(st + (uint32_t)(kG2AUnits + (w * NB + b) * kWave) * 16), (uint32_t)lane * 16u,
+                      tq * kQuadNibBytes);
+      // the 128 scale bytes: eight lanes
+      if (lane < 8)
+        dma_b128_unseen(sr[b], uni(st + (uint32_t)(kG2AUnits + kG2BUnits + (w * NB + b) * 8) * 16),
+                        (uint32_t)lane * 16u, tq * (kQuadScales * 2));
+    }
+  };
+  copy(0);
+  if (a.Kq > 1) copy(1);
+  for (int64_t q = 0; q < a.Kq; ++q) {
+    asm volatile("" ::: "memory");
+    if (q + 1 < a.Kq) wait_vm_lgkm0<kG2LoadsPerQuad>();  // quad q's copies done, q + 1's may fly
+    else wait_vm_lgkm0<0>();
+    __builtin_amdgcn_s_barrier();  // every wave's copies are in; stage (q - 1) % 3 is free
+    asm volatile("" ::: "memory");
+    if (q + 2 < a.Kq) copy(q + 2);
+    const u32x4* st = lds + (q % kG2Stages) * kG2StageUnits;
+    const u32x4* la = st;
+    u32x4 bw[NB];
+    uint2 bs[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      bw[b] = st[kG2AUnits + (w * NB + b) * kWave + lane];
+      bs[b] = reinterpret_cast<const uint2*>(st + kG2AUnits + kG2BUnits + (w * NB + b) * 8)[n];
+    }
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+      if (4 * q + gi >= a.Kg) continue;  // padded group (uniform)
+      u32x4 bh[NB], bl[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const uint32_t s2 = gi < 2 ? bs[b].x : bs[b].y;
+        dequant_split_f16(bw[b][gi], (gi % 2) ? (s2 >> 16) : (s2 & 0xffffu), mask, bh[b], bl[b]);
+      }
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        const u32x4* row = la + (tt * 16 + n) * UPR;
+        const int unit = (p * 4 + gi) * AW;
+        const u32x4 ah = row[unit ^ n];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          acc[b][tt] = mfma_f16_16x16x32(ah, bh[b], acc[b][tt]);
+          acc[b][tt] = mfma_f16_16x16x32(ah, bl[b], acc[b][tt]);
+        }
+        if constexpr (AW == 2) {
+          const u32x4 al = row[(unit + 1) ^ n];
+#pragma unroll
+          for (int b = 0; b < NB; ++b) acc[b][tt] = mfma_f16_16x16x32(al, bh[b], acc[b][tt]);
+        }
+      }
+    }
+  }
+  lds_barrier();  // every wave has left the ring before it is reused
+}
+
+__global__ __launch_bounds__(kG2Waves * kWave) void gemm_gate_up_kernel2(GemmK a) {
+  constexpr int BM = kGemmBMGateUp;
+  constexpr int TT = BM / 16;
+  constexpr int kRows = kG2Waves * 16;  // rows of I per workgroup (kG2Waves / 2 groups)
+  __shared__ u32x4 lds_a[kG2Stages * kG2StageUnits];
+  __shared__ int s_mb[kMaxExperts + 2];
+  __shared__ int64_t s_row[BM];
+  __shared__ int s_nact;
+  const int lane = threadIdx.x % kWave;
+  const int w = threadIdx.x / kWave;
+  const int n = lane % 16;
+  const int p = lane / 16;
+  if (blockIdx.x == 0) {
+    for (int64_t i = threadIdx.x; i < a.KqI * 256; i += blockDim.x) a.hq16[a.h_zero_row * a.KqI * 256 + i] = 0;
+  }
+  const i32x4 ar = buf_rsrc_words(a.a_src, (uint32_t)((a.a_zero_row + 1) * a.Kq * 256));
+  const int n_act = count_active(a.seg, &s_nact);
+  const int64_t n_mb = plan_items<BM>(a.seg.desc, n_act, s_mb);
+  const int64_t n_nb = ceil_div(a.N, kRows);
+  const XcdPlan xp = xcd_plan(n_mb, n_nb);
+  const uint32_t nib_bytes = (uint32_t)(a.N * a.Kq * 64), sc_bytes = (uint32_t)(a.N * a.Kq * 8);
+  for (int64_t item = xp.l; item < xp.n_items; item += xp.nl) {
+    const TileCoord c = tile_coord<BM>(a, a.seg.desc, s_mb, n_act, xp, item, n_nb, s_row);
+    const int64_t n_tiles = a.N / kRowTile;
+    const int64_t t = c.nb * kG2Waves + w;
+    const int64_t tc = t < n_tiles ? t : n_tiles - 1;
+    const bool routed = c.e < a.seg.E;
+    const i32x4 nr[2] = {buf_rsrc_words(routed ? a.nib1 + (int64_t)c.e * nib_bytes : a.sh_nib1, nib_bytes),
+                         buf_rsrc_words(routed ? a.nib2 + (int64_t)c.e * nib_bytes : a.sh_nib2, nib_bytes)};
+    const i32x4 sr[2] = {
+        buf_rsrc_words(routed ? reinterpret_cast<const uint8_t*>(a.sc1) + (int64_t)c.e * sc_bytes
+                              : reinterpret_cast<const uint8_t*>(a.sh_sc1), sc_bytes),
+        buf_rsrc_words(routed ? reinterpret_cast<const uint8_t*>(a.sc2) + (int64_t)c.e * sc_bytes
+                              : reinterpret_cast<const uint8_t*>(a.sh_sc2), sc_bytes)};
+    const int64_t rt[2] = {tc, tc};
+    f32x4 acc[2][TT];
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) acc[b][tt] = z;
+    gemm_tile3<BM, 1>(a, s_row, lds_a, ar, nr, sr, rt, acc);
+
+    // SwiGLU, h as fp16 hi + lo into LDS in down-operand chunk order, as in
+    // gemm_gate_up_kernel (kG2Waves / 2 groups of I per workgroup)
+    uint16_t* hs = reinterpret_cast<uint16_t*>(lds_a);
+    const int gl = w / 2;
+    const int half = w % 2;
+    const int pp = n / 4;
+    const int rr = n % 4;
+    const int jj = half == 0 ? ((rr & 1) ? 4 : 0) + (rr >> 1) : ((rr & 1) ? 6 : 2) + (rr >> 1);
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = tt * 16 + 4 * p + j;
+        const float gv = acc[0][tt][j];
+        const float uv = acc[1][tt][j];
+        const float hv = gv * (1.0f / (1.0f + expf(-gv))) * uv;
+        const uint32_t hb = float_to_half_bits(hv);
+        const uint32_t lb = float_to_half_bits(hv - half_bits_to_float32(hb));
+        uint16_t* chunk = hs + ((gl * BM + m) * 4 + pp) * 16;
+        chunk[jj] = (uint16_t)hb;
+        chunk[8 + jj] = (uint16_t)lb;
+      }
+    }
+    lds_barrier();
+    constexpr int kGroups = kG2Waves / 2;
+    for (int cidx = threadIdx.x; cidx < kGroups * BM * 4; cidx += blockDim.x) {
+      const int g2 = cidx / (BM * 4);
+      const int m = (cidx / 4) % BM;
+      const int p2 = cidx % 4;
+      const int64_t g = c.nb * kGroups + g2;  // group of I
+      const int64_t pos = c.m0 + m;
+      if (pos < c.end && 2 * g + 1 < n_tiles) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(hs + ((g2 * BM + m) * 4 + p2) * 16);
+        u32x4* dst = reinterpret_cast<u32x4*>(a.hq16 + ((pos * a.KqI + g / 4) * 16 + p2 * 4 + g % 4) * 16);
+        dst[0] = src[0];
+        dst[1] = src[1];
+      }
+    }
+    lds_barrier();
+  }
+}
+
+__global__ __launch_bounds__(kG2Waves * kWave) void gemm_down_kernel2(GemmK a) {
+  constexpr int BM = kGemmBMDown;
+  constexpr int TT = BM / 16;
+  constexpr int NB = kG2NB;
+  constexpr int kRows = kG2Waves * 16 * NB;  // rows of H per workgroup
+  __shared__ u32x4 lds_a[kG2Stages * kG2StageUnits];
+  __shared__ int s_mb[kMaxExperts + 2];
+  __shared__ int64_t s_row[BM];
+  __shared__ int s_nact;
+  const int lane = threadIdx.x % kWave;
+  const int w = threadIdx.x / kWave;
+  const int n = lane % 16;
+  const int p = lane / 16;
+  const i32x4 ar = buf_rsrc_words(a.a_src, (uint32_t)((a.a_zero_row + 1) * a.Kq * 512));
+  const int n_act = count_active(a.seg, &s_nact);
+  const int64_t n_mb = plan_items<BM>(a.seg.desc, n_act, s_mb);
+  const int64_t n_nb = ceil_div(a.N, kRows);
+  const int64_t n_tiles = a.N / kRowTile;
+  const XcdPlan xp = xcd_plan(n_mb, n_nb);
+  const uint32_t nib_bytes = (uint32_t)(a.N * a.Kq * 64), sc_bytes = (uint32_t)(a.N * a.Kq * 8);
+  for (int64_t item = xp.l; item < xp.n_items; item += xp.nl) {
+    const TileCoord c = tile_coord<BM>(a, a.seg.desc, s_mb, n_act, xp, item, n_nb, s_row);
+    const bool routed = c.e < a.seg.E;
+    const i32x4 nw = buf_rsrc_words(routed ? a.nib1 + (int64_t)c.e * nib_bytes : a.sh_nib1, nib_bytes);
+    const i32x4 sw = buf_rsrc_words(routed ? reinterpret_cast<const uint8_t*>(a.sc1) + (int64_t)c.e * sc_bytes
+                                           : reinterpret_cast<const uint8_t*>(a.sh_sc1), sc_bytes);
+    const i32x4 nr[NB] = {nw, nw};
+    const i32x4 sr[NB] = {sw, sw};
+    int64_t rt[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int64_t t = (c.nb * kG2Waves + w) * NB + b;
+      rt[b] = t < n_tiles ? t : n_tiles - 1;
+    }
+    f32x4 acc[NB][TT];
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) acc[b][tt] = z;
+    gemm_tile3<BM, 2>(a, s_row, lds_a, ar, nr, sr, rt, acc);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int64_t t = (c.nb * kG2Waves + w) * NB + b;
+      if (t >= n_tiles) continue;
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t pos = c.m0 + tt * 16 + 4 * p + j;
+          if (pos < c.end) a.outbuf[pos * a.N + t * 16 + n] = acc[b][tt][j];
+        }
+      }
+    }
+  }
+}
+
 bool gemm_regime(int64_t T, int k, int E) {
   const int64_t slots = T * k;
   const int64_t seg_max = slots < E ? slots : E;
   return slots >= kGemmMinSlotsPerExpert * seg_max;
+}
+
+// PHANTOM_MOE_GEMM_KERNEL=v1 selects the register-staged tile pipeline
+// (gemm_tile, 4 waves) instead of the LDS ring (gemm_tile2, 8 waves).
+static bool gemm_v1() {
+  const char* v = getenv("PHANTOM_MOE_GEMM_KERNEL");
+  return v && strcmp(v, "v1") == 0;
 }
 
 static int64_t gemm_max_items(const ExpertArgs& x, int BM, int64_t n_nb) {
@@ -502,9 +797,15 @@ hipError_t launch_gemm_gate_up(const ExpertArgs& x, const Workspace& ws, hipStre
   g.hq16 = ws.hq;
   g.KqI = ceil_div(x.I, kQuad);
   g.h_zero_row = x.T * x.k + (x.has_shared ? x.T : 0);
-  const int64_t max_items = gemm_max_items(x, kGemmBMGateUp, ceil_div(x.I, kGemmRowsGU));
-  hipLaunchKernelGGL(gemm_gate_up_kernel, dim3(resident_grid(gemm_gate_up_kernel, kGemmWaves * kWave, max_items)),
-                     dim3(kGemmWaves * kWave), 0, stream, g);
+  if (gemm_v1()) {
+    const int64_t max_items = gemm_max_items(x, kGemmBMGateUp, ceil_div(x.I, kGemmRowsGU));
+    hipLaunchKernelGGL(gemm_gate_up_kernel, dim3(resident_grid(gemm_gate_up_kernel, kGemmWaves * kWave, max_items)),
+                       dim3(kGemmWaves * kWave), 0, stream, g);
+  } else {
+    const int64_t max_items = gemm_max_items(x, kGemmBMGateUp, ceil_div(x.I, kG2Waves * 16));
+    hipLaunchKernelGGL(gemm_gate_up_kernel2, dim3(resident_grid(gemm_gate_up_kernel2, kG2Waves * kWave, max_items)),
+                       dim3(kG2Waves * kWave), 0, stream, g);
+  }
   return hipGetLastError();
 }
 
@@ -522,9 +823,15 @@ hipError_t launch_gemm_down(const ExpertArgs& x, const Workspace& ws, hipStream_
   g.sh_nib1 = x.sh_down_nib;
   g.sh_sc1 = x.sh_down_scale;
   g.outbuf = ws.outbuf;
-  const int64_t max_items = gemm_max_items(x, kGemmBMDown, ceil_div(x.H, kGemmRowsDown));
-  hipLaunchKernelGGL(gemm_down_kernel, dim3(resident_grid(gemm_down_kernel, kGemmWaves * kWave, max_items)),
-                     dim3(kGemmWaves * kWave), 0, stream, g);
+  if (gemm_v1()) {
+    const int64_t max_items = gemm_max_items(x, kGemmBMDown, ceil_div(x.H, kGemmRowsDown));
+    hipLaunchKernelGGL(gemm_down_kernel, dim3(resident_grid(gemm_down_kernel, kGemmWaves * kWave, max_items)),
+                       dim3(kGemmWaves * kWave), 0, stream, g);
+  } else {
+    const int64_t max_items = gemm_max_items(x, kGemmBMDown, ceil_div(x.H, kG2Waves * 16 * kGemmNBDown));
+    hipLaunchKernelGGL(gemm_down_kernel2, dim3(resident_grid(gemm_down_kernel2, kG2Waves * kWave, max_items)),
+                       dim3(kG2Waves * kWave), 0, stream, g);
+  }
   return hipGetLastError();
 }
 

@@ -183,4 +183,60 @@ __device__ inline float buf_load_f32(BufRsrc r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
 }
 
+
+// Direct-to-LDS buffer loads: each lane's 16 (or 4) bytes land at
+// lds + lane * 16 (or 4); lds must be wave-uniform.  They count in vmcnt like
+// other loads and are not tracked by the compiler's waits for LDS reads, so
+// the reader waits explicitly (wait_vmcnt) before a barrier.
+__device__ inline void dma_b128(BufRsrc r, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, (int)voff,
+                                           (int)soff, 0, 0);
+}
+
+__device__ inline void dma_b32(BufRsrc r, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, (int)voff,
+                                           (int)soff, 0, 0);
+}
+
+// The same 16-byte direct-to-LDS load issued from inline assembly, so the
+// compiler does not see an LDS write: a kernel that refills one stage of an
+// LDS ring while it reads another then gets no conservative vmcnt(0) before
+// its reads (the compiler cannot tell the stages apart).  The caller owns
+// the ordering: it waits with wait_vmcnt / s_waitcnt before a barrier.  M0
+// is written right before the load (a reserved register the compiler only
+// sets immediately before its own uses); the resource is raw SGPR words.
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ inline i32x4 buf_rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const i32x4 r = {(int32_t)(uint32_t)b, (int32_t)((b >> 32) & 0xFFFFu), (int32_t)bytes, 0x00020000};
+  return r;
+}
+
+__device__ inline uint32_t lds_addr(const void* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p);
+}
+
+__device__ inline void dma_b128_unseen(const i32x4& r, uint32_t lds_byte, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds_byte), "v"(voff), "s"(r), "s"(soff) : "memory");
+}
+
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima), gfx9 encoding.
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier for LDS data only: waits for this wave's LDS accesses,
+// not for its outstanding global stores (which no wave of the workgroup reads
+// back), as a __syncthreads() fence would.
+__device__ inline void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt not waited for
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 }  // namespace pmoe

@@ -96,16 +96,6 @@ __device__ inline void load_x4<float>(const float* x, int64_t off, float v[4]) {
   v[3] = r.w;
 }
 
-// Workgroup barrier for LDS data only: waits for this wave's LDS accesses,
-// not for its outstanding global stores (which no wave of the workgroup reads
-// back), as a __syncthreads() fence would.
-__device__ inline void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt not waited for
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // Block-wide exclusive scan of three values at once (256 threads or more,
 // one pair of barriers); s_tmp holds 3 ints per wave.  Returns the exclusive
 // prefixes and writes the block totals to *total.
