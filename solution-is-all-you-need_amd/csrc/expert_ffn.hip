@@ -829,12 +829,17 @@ __global__ __launch_bounds__(kTileWaves * kWave) __attribute__((amdgpu_waves_per
 
 
 // y[t] = sum_j w[t,j] * out[slot_pos[t*k+j]] (+ out[T*k + t] for the shared
-// expert), j in slot order, fp32.
+// expert), j in slot order, fp32.  Slots are taken KB at a time: the KB
+// positions and weights are loaded together, then the KB output rows, so a
+// token costs two memory round trips per KB slots instead of two per slot.
+constexpr int kCombineSlots = 8;
+
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ outbuf,
                                                       const int32_t* __restrict__ slot_pos,
                                                       const float* __restrict__ topk_w, int64_t T,
                                                       int k, int64_t H, int has_shared,
                                                       float* __restrict__ y) {
+  constexpr int KB = kCombineSlots;
   const int64_t H4 = H / 4;
   const int64_t total = T * H4;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
@@ -842,14 +847,27 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     const int64_t t = i / H4;
     const int64_t c = (i % H4) * 4;
     float4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < k; ++j) {
-      const int64_t pos = slot_pos[t * k + j];
-      const float wt = topk_w[t * k + j];
-      const float4 o = *reinterpret_cast<const float4*>(outbuf + pos * H + c);
-      acc.x += wt * o.x;
-      acc.y += wt * o.y;
-      acc.z += wt * o.z;
-      acc.w += wt * o.w;
+    for (int j0 = 0; j0 < k; j0 += KB) {
+      int64_t pos[KB];
+      float wt[KB];
+#pragma unroll
+      for (int jj = 0; jj < KB; ++jj) {
+        const int j = j0 + jj < k ? j0 + jj : k - 1;  // clamped: every load unconditional
+        pos[jj] = slot_pos[t * k + j];
+        wt[jj] = topk_w[t * k + j];
+      }
+      float4 o[KB];
+#pragma unroll
+      for (int jj = 0; jj < KB; ++jj) o[jj] = *reinterpret_cast<const float4*>(outbuf + pos[jj] * H + c);
+#pragma unroll
+      for (int jj = 0; jj < KB; ++jj) {
+        if (j0 + jj < k) {
+          acc.x += wt[jj] * o[jj].x;
+          acc.y += wt[jj] * o[jj].y;
+          acc.z += wt[jj] * o[jj].z;
+          acc.w += wt[jj] * o[jj].w;
+        }
+      }
     }
     if (has_shared) {
       const float4 o = *reinterpret_cast<const float4*>(outbuf + (T * k + t) * H + c);

@@ -353,3 +353,29 @@ def test_expert_kernels_agree(dev, cfg, monkeypatch):
     np.testing.assert_array_equal(idx_cls.cpu().numpy(), ridx)
     check_y(y_tile.cpu().numpy(), ry, cfg.name + " token-tile")
     check_y(y_cls.cpu().numpy(), ry, cfg.name + " K-split")
+
+
+GEMM_CASES = [c for c in SMALL_CASES if c.name in ("gemm_ragged_k_and_rows", "gemm_sigmoid_shared", "gemm_multi_block")]
+
+
+@pytest.mark.parametrize("cfg", GEMM_CASES, ids=lambda c: c.name)
+def test_gemm_pipelines_agree(dev, cfg, monkeypatch):
+    """The prefill GEMM has two tile pipelines: the LDS ring (default: both
+    operands copied two K quads ahead by direct-to-LDS loads, 8 waves) and the
+    register-staged one (PHANTOM_MOE_GEMM_KERNEL=v1).  Both must meet the
+    layer tolerance against the oracle, ragged K and rows and the shared
+    expert included."""
+    L = synth.host_layer(cfg)
+    xb = synth.activations(cfg.T, cfg.H, seed=11)
+    ex = dev_weights(L, dev)
+    b = None if L.router_bias is None else torch.from_numpy(L.router_bias).to(dev)
+    W = torch.from_numpy(L.router_w).to(dev)
+    x = to_bf16_tensor(xb, dev)
+    ry, ridx, _ = oracle.moe_forward(xb, L.router_w, L.gate, L.up, L.down, cfg.k, cfg.score_mode,
+                                     L.router_bias, shared=L.shared)
+    y_ring = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b)
+    monkeypatch.setenv("PHANTOM_MOE_GEMM_KERNEL", "v1")
+    y_v1 = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b)
+    monkeypatch.delenv("PHANTOM_MOE_GEMM_KERNEL")
+    check_y(y_ring.cpu().numpy(), ry, cfg.name + " LDS ring")
+    check_y(y_v1.cpu().numpy(), ry, cfg.name + " register-staged")
