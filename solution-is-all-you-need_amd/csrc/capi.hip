@@ -144,8 +144,9 @@ const char* phantom_moe_expert_kernels(int64_t T, int64_t H, int64_t I, int E, i
   static thread_local char buf[96];
   const char *gu, *dn;
   if (pmoe::gemm_regime(T, top_k, E)) {
-    gu = "gemm_gate_up_kernel";
-    dn = "gemm_down_kernel";
+    const bool ring = pmoe::gemm_uses_ring();
+    gu = ring ? "gemm_gate_up_kernel2" : "gemm_gate_up_kernel";
+    dn = ring ? "gemm_down_kernel2" : "gemm_down_kernel";
   } else {
     gu = pmoe::gate_up_tile_regime(T, H, I, E, top_k, has_shared) ? "gate_up_tile_kernel" : "gate_up_kernel";
     dn = pmoe::down_tile_regime(T, H, I, E, top_k, has_shared) ? "down_tile_kernel" : "down_kernel";

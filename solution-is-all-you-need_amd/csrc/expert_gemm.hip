@@ -772,6 +772,8 @@ static bool gemm_v1() {
   return v && strcmp(v, "v1") == 0;
 }
 
+bool gemm_uses_ring() { return !gemm_v1(); }
+
 static int64_t gemm_max_items(const ExpertArgs& x, int BM, int64_t n_nb) {
   const int64_t rows = x.T * x.k + (x.has_shared ? x.T : 0);
   return (ceil_div(rows, BM) + max_active_experts(x)) * n_nb;

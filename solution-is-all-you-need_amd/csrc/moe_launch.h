@@ -111,6 +111,7 @@ struct ExpertArgs {
 // operands; below it, as the grouped GEMV (expert_ffn.hip).
 constexpr int kGemmMinSlotsPerExpert = 64;
 bool gemm_regime(int64_t T, int k, int E);
+bool gemm_uses_ring();  // the LDS-ring tile pipeline (default) rather than the register-staged one
 hipError_t launch_gemm_gate_up(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);
 hipError_t launch_gemm_down(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);
 
