@@ -110,6 +110,13 @@ def gate_up_bytes(cfg, U: int) -> int:
     return (U + (1 if cfg.shared else 0)) * per_expert + cfg.T * cfg.H * 2
 
 
+def ffn_bytes(cfg, U: int) -> int:
+    """Algorithmic HBM bytes of the fused gate/up + down launch: the gate, up
+    and down matrices of the U active experts (plus the shared expert) and the
+    bf16 activations."""
+    return gate_up_bytes(cfg, U) + (U + (1 if cfg.shared else 0)) * cfg.H * cfg.I * 18 // 32
+
+
 def layer_bytes(cfg, U: int) -> int:
     """Algorithmic HBM bytes of one layer: expert weights of the U active
     experts (+ shared), the fp32 router weight, bf16 x in and fp32 y out."""
@@ -393,20 +400,23 @@ def main():
         out["eager"] = {"tokens_per_s": round(cfg.T * args.steps / eager_elapsed, 2),
                         "ms_per_step": round(eager_elapsed * 1e3 / args.steps, 5)}
     if use_events:
-        gu_ms = float(np.sum(stages["gate_up"]))
-        gu_bytes = float(sum(gate_up_bytes(cfg, u) for u in steps_U))
-        achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
-        # the kernel the gate/up stage launches at this shape
+        # the kernel the gate/up stage launches at this shape; one kernel for
+        # both stages means the fused launch, which the gate/up stage's events
+        # bracket (the down stage is then empty)
         names = dict(kv.split("=") for kv in _lib.load().phantom_moe_expert_kernels(
             cfg.T, cfg.H, cfg.I, cfg.E, cfg.k, int(cfg.shared)).decode().split(";"))
         gu_kernel = names["gate_up"]
+        fused = names["gate_up"] == names["down"]
+        gu_ms = float(np.sum(stages["gate_up"]))
+        gu_bytes = float(sum((ffn_bytes if fused else gate_up_bytes)(cfg, u) for u in steps_U))
+        achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
         traffic = None
         if os.path.exists(pmc_summary(gu_kernel, cfg.name)):
             with open(pmc_summary(gu_kernel, cfg.name)) as f:
                 pmc = json.load(f)
             if pmc.get("workload") == cfg.name and pmc.get("kernel") == gu_kernel:
                 traffic = pmc.get("hbm_bytes_per_launch")
-        if cfg.T >= PREFILL_T:
+        if cfg.T >= PREFILL_T and not fused:
             tf = gate_up_flops(cfg) * args.steps / (gu_ms * 1e-3) / 1e12
             out["roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
                                "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": traffic,

@@ -103,7 +103,8 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
   const size_t o_desc = take(sizeof(int4) * (size_t)(E + 1));
   const size_t o_tok = take(sizeof(int32_t) * (size_t)rows);
   const size_t o_tiles = take(sizeof(int32_t) * (size_t)(max_token_tiles(T, k, E, has_shared) * kTileWords));
-  const size_t o_ntiles = take(sizeof(int32_t));
+  const size_t o_ntiles = take(sizeof(int32_t) * 3 * kCtlStride);
+  const size_t o_tdone = take(sizeof(int32_t) * (size_t)(max_token_tiles(T, k, E, has_shared) * kCtlStride));
   const int64_t KpadI = I > 0 ? round_up(I, kQuad) : 0;
   // down operand rows plus an all-zero row
   const size_t o_hq = take(sizeof(uint16_t) * (size_t)((rows + 1) * KpadI * 2));
@@ -124,6 +125,7 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
     ws->seg_tok = reinterpret_cast<int32_t*>(b + o_tok);
     ws->tiles = reinterpret_cast<int32_t*>(b + o_tiles);
     ws->n_tiles = reinterpret_cast<int32_t*>(b + o_ntiles);
+    ws->tile_done = reinterpret_cast<int32_t*>(b + o_tdone);
     ws->hq = reinterpret_cast<uint16_t*>(b + o_hq);
     ws->hs = reinterpret_cast<float*>(b + o_hs);
     ws->outbuf = reinterpret_cast<float*>(b + o_out);
@@ -147,6 +149,8 @@ const char* phantom_moe_expert_kernels(int64_t T, int64_t H, int64_t I, int E, i
     const bool ring = pmoe::gemm_uses_ring();
     gu = ring ? "gemm_gate_up_kernel2" : "gemm_gate_up_kernel";
     dn = ring ? "gemm_down_kernel2" : "gemm_down_kernel";
+  } else if (pmoe::ffn_fused_regime(T, H, I, E, top_k, has_shared)) {
+    gu = dn = "ffn_tile_kernel";  // one launch for both stages
   } else {
     gu = pmoe::gate_up_tile_regime(T, H, I, E, top_k, has_shared) ? "gate_up_tile_kernel" : "gate_up_kernel";
     dn = pmoe::down_tile_regime(T, H, I, E, top_k, has_shared) ? "down_tile_kernel" : "down_kernel";

@@ -381,7 +381,8 @@ __device__ __attribute__((always_inline)) inline void wchunk_math(const WChunk& 
 
 // SwiGLU of one row tile rt of the token tile [m0, end) from the wave's own
 // accumulators (lane (n, p) holds positions m0 + 4p + j of row n), stored as
-// the down kernel's operand.
+// the down kernel's operand with cache policy AUX.
+template <int AUX>
 __device__ inline void tile_epilogue(const GateUpK& a, BufRsrc hqr, BufRsrc hsr, int64_t m0, int64_t end, uint32_t rt,
                                      const f32x4& ag, const f32x4& au, const f32x4& cg, const f32x4& cu) {
   const int lane = threadIdx.x % kWave;
@@ -409,8 +410,8 @@ __device__ inline void tile_epilogue(const GateUpK& a, BufRsrc hqr, BufRsrc hsr,
     const bool ok = pos < end;
     const uint32_t o = (uint32_t)pos * pos_bytes + o_row;
     if (ok) {
-      __builtin_amdgcn_raw_buffer_store_b16((unsigned short)hb, hqr, (int)o, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b16((unsigned short)lb, hqr, (int)(o + 16u), 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16((unsigned short)hb, hqr, (int)o, 0, AUX);
+      __builtin_amdgcn_raw_buffer_store_b16((unsigned short)lb, hqr, (int)(o + 16u), 0, AUX);
     }
     // the 16 rows of the tile are one half of one group: sum hi + lo over
     // them (16 consecutive lanes, fixed butterfly order)
@@ -421,7 +422,7 @@ __device__ inline void tile_epilogue(const GateUpK& a, BufRsrc hqr, BufRsrc hsr,
     sum += __shfl_xor(sum, 1, kWave);
     if (n == 0 && ok)
       __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum), hsr,
-                                            (int)((((uint32_t)pos * (uint32_t)a.KqI * 4u + g32) * 2u + half) * 4u), 0, 0);
+                                            (int)((((uint32_t)pos * (uint32_t)a.KqI * 4u + g32) * 2u + half) * 4u), 0, AUX);
   }
 }
 
@@ -429,28 +430,38 @@ __device__ inline void tile_epilogue(const GateUpK& a, BufRsrc hqr, BufRsrc hsr,
 // [Kq][64 lanes] floats.
 inline size_t tile_lds_bytes(int64_t Kq) { return (size_t)Kq * (256 * 16 + 64 * 4); }
 
-template <int D>
-__global__ __launch_bounds__(kTileWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void gate_up_tile_kernel(GateUpK a) {
-  extern __shared__ u32x4 s_x[];
+// Job geometry of a token-tile launch: row tiles per wave (M), per job
+// (kTileWaves * M) and jobs per token tile, chosen so that the jobs about
+// fill `slots` workgroups.
+struct TileJobs {
+  uint32_t M, per_job, jpt, n_jobs;
+};
+
+__device__ inline TileJobs tile_jobs(uint32_t n_tiles, uint32_t n_rt, uint32_t slots) {
+  TileJobs j;
+  const uint32_t M = (n_tiles * n_rt + kTileWaves * slots - 1) / (kTileWaves * slots);
+  j.M = M < 1 ? 1 : M;
+  j.per_job = kTileWaves * j.M;
+  j.jpt = (n_rt + j.per_job - 1) / j.per_job;
+  j.n_jobs = n_tiles * j.jpt;
+  return j;
+}
+
+// One gate/up job: token tile gt, row tiles part * per_job + w + kTileWaves * i
+// (i < M) for wave w.  Ends with the waves' last stores issued and LDS still
+// in use; the caller synchronises before the next job.
+// With a ticket counter, thread 0 draws the next ticket into nxt once the
+// tile header has arrived (a draw issued before it would hold up the
+// header's wait).  H_AUX is the cache policy of the h stores.
+template <int D, int H_AUX>
+__device__ __attribute__((always_inline)) inline void gate_up_tile_job(const GateUpK& a, u32x4* s_x, float* s_sx, uint32_t gt,
+                                                                       uint32_t part, const TileJobs& jb, int32_t* ticket,
+                                                                       uint32_t& nxt) {
   const int lane = threadIdx.x % kWave;
   const int p = lane / 16;
   const uint32_t w = (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t Kq = (uint32_t)a.Kq;
-  float* s_sx = reinterpret_cast<float*>(s_x + Kq * 256);
-  if (blockIdx.x == 0) {
-    // the all-zero down-operand row read for positions past a segment
-    for (int64_t i = threadIdx.x; i < a.KqI * 256; i += blockDim.x) a.hq[a.zero_row * a.KqI * 256 + i] = 0;
-    for (int64_t i = threadIdx.x; i < a.KqI * 8; i += blockDim.x) a.hs[a.zero_row * a.KqI * 8 + i] = 0.0f;
-  }
-  const uint32_t n_tiles = (uint32_t)__builtin_amdgcn_readfirstlane(*a.n_tiles);
   const uint32_t n_rt = (uint32_t)(a.I / kRowTile);
-  // row tiles per wave and job: enough that the jobs about fill the grid
-  uint32_t M = (n_tiles * n_rt + kTileWaves * gridDim.x - 1) / (kTileWaves * gridDim.x);
-  M = M < 1 ? 1 : M;
-  const uint32_t per_job = kTileWaves * M;
-  const uint32_t jpt = (n_rt + per_job - 1) / per_job;  // jobs per token tile
-  const uint32_t n_jobs = n_tiles * jpt;
-
   const BufRsrc xr = buf_rsrc(a.xq, (uint32_t)((a.T + 1) * a.Kq * 256));
   const BufRsrc xsr = buf_rsrc(a.xs, (uint32_t)((a.T + 1) * a.Kq * 16));
   const BufRsrc hqr = buf_rsrc(a.hq, (uint32_t)((a.zero_row + 1) * a.KqI * 512));
@@ -458,102 +469,116 @@ __global__ __launch_bounds__(kTileWaves * kWave) __attribute__((amdgpu_waves_per
   const uint32_t nib_bytes = (uint32_t)(a.I * a.Kq * 64);
   const uint32_t sc_bytes = (uint32_t)(a.I * a.Kq * 8);
 
-  for (uint32_t job = blockIdx.x; job < n_jobs; job += gridDim.x) {
-    const uint32_t gt = job / jpt;
-    const uint32_t part = job - gt * jpt;
-    const int32_t* tw = a.tiles + (int64_t)gt * kTileWords;
-    const int tok_w = tw[4 + lane % 16];
-    const int e = __builtin_amdgcn_readfirstlane(tw[0]);
-    const int64_t m0 = __builtin_amdgcn_readfirstlane(tw[1]);
-    const int64_t end = __builtin_amdgcn_readfirstlane(tw[2]);
-    // token of the lane's A-operand row; positions past the segment read the
-    // all-zero row T
-    const int tok = m0 + lane % 16 < end ? tok_w : (int)a.T;
-    const bool routed = e < a.seg.E;
-    WSrc ws;
-    ws.g = buf_rsrc(routed ? a.gate_nib + (int64_t)e * nib_bytes : a.sh_gate_nib, nib_bytes);
-    ws.u = buf_rsrc(routed ? a.up_nib + (int64_t)e * nib_bytes : a.sh_up_nib, nib_bytes);
-    ws.gs = buf_rsrc(routed ? reinterpret_cast<const uint8_t*>(a.gate_sc) + (int64_t)e * sc_bytes
-                            : reinterpret_cast<const uint8_t*>(a.sh_gate_sc), sc_bytes);
-    ws.us = buf_rsrc(routed ? reinterpret_cast<const uint8_t*>(a.up_sc) + (int64_t)e * sc_bytes
-                            : reinterpret_cast<const uint8_t*>(a.sh_up_sc), sc_bytes);
-    // this wave's row tiles: rt0 + kTileWaves * i, i < n_mine
-    const uint32_t rt0 = part * per_job + w;
-    const uint32_t left = rt0 < n_rt ? (n_rt - rt0 + kTileWaves - 1) / kTileWaves : 0;
-    const uint32_t n_mine = left < M ? left : M;
-    const int64_t total = (int64_t)n_mine * Kq;  // chunks of this wave in this job
+  const int32_t* tw = a.tiles + (int64_t)gt * kTileWords;
+  const int tok_w = tw[4 + lane % 16];
+  const int e = __builtin_amdgcn_readfirstlane(tw[0]);
+  const int64_t m0 = __builtin_amdgcn_readfirstlane(tw[1]);
+  const int64_t end = __builtin_amdgcn_readfirstlane(tw[2]);
+  // token of the lane's A-operand row; positions past the segment read the
+  // all-zero row T
+  const int tok = m0 + lane % 16 < end ? tok_w : (int)a.T;
+  if (ticket && threadIdx.x == 0) nxt = (uint32_t)atomicAdd(ticket, 1);
+  const bool routed = e < a.seg.E;
+  WSrc ws;
+  ws.g = buf_rsrc(routed ? a.gate_nib + (int64_t)e * nib_bytes : a.sh_gate_nib, nib_bytes);
+  ws.u = buf_rsrc(routed ? a.up_nib + (int64_t)e * nib_bytes : a.sh_up_nib, nib_bytes);
+  ws.gs = buf_rsrc(routed ? reinterpret_cast<const uint8_t*>(a.gate_sc) + (int64_t)e * sc_bytes
+                          : reinterpret_cast<const uint8_t*>(a.sh_gate_sc), sc_bytes);
+  ws.us = buf_rsrc(routed ? reinterpret_cast<const uint8_t*>(a.up_sc) + (int64_t)e * sc_bytes
+                          : reinterpret_cast<const uint8_t*>(a.sh_up_sc), sc_bytes);
+  // this wave's row tiles: rt0 + kTileWaves * i, i < n_mine
+  const uint32_t rt0 = part * jb.per_job + w;
+  const uint32_t left = rt0 < n_rt ? (n_rt - rt0 + kTileWaves - 1) / kTileWaves : 0;
+  const uint32_t n_mine = left < jb.M ? left : jb.M;
+  const int64_t total = (int64_t)n_mine * Kq;  // chunks of this wave in this job
 
-    // the tile's activation operand -> LDS (every wave takes a share)
-    {
-      const uint32_t row = (uint32_t)tok * Kq;
-      const uint32_t xv = row * 256u + (uint32_t)p * 64u;
-      const uint32_t sv = row * 16u + (uint32_t)p * 4u;
-      for (uint32_t b = w; b < Kq * 4; b += kTileWaves)
-        dma_b128(xr, s_x + b * kWave, xv, (b / 4) * 256u + (b % 4) * 16u);
-      for (uint32_t q = w; q < Kq; q += kTileWaves) dma_b32(xsr, s_sx + q * kWave, sv, q * 16u);
-    }
-    asm volatile("" ::: "memory");  // the operand loads stay older than the weight loads below
+  // the tile's activation operand -> LDS (every wave takes a share)
+  {
+    const uint32_t row = (uint32_t)tok * Kq;
+    const uint32_t xv = row * 256u + (uint32_t)p * 64u;
+    const uint32_t sv = row * 16u + (uint32_t)p * 4u;
+    for (uint32_t b = w; b < Kq * 4; b += kTileWaves)
+      dma_b128(xr, s_x + b * kWave, xv, (b / 4) * 256u + (b % 4) * 16u);
+    for (uint32_t q = w; q < Kq; q += kTileWaves) dma_b32(xsr, s_sx + q * kWave, sv, q * 16u);
+  }
+  asm volatile("" ::: "memory");  // the operand loads stay older than the weight loads below
 
-    // ring prologue (the load cursor stops at the last chunk; refills past
-    // the end reload it and are never used)
-    uint32_t li = 0, lq = 0;
-    int64_t loaded = 0;
-    auto advance = [&]() {
-      if (loaded + 1 < total) {
-        ++loaded;
-        if (++lq == Kq) {
-          lq = 0;
-          ++li;
-        }
+  // ring prologue (the load cursor stops at the last chunk; refills past
+  // the end reload it and are never used)
+  uint32_t li = 0, lq = 0;
+  int64_t loaded = 0;
+  auto advance = [&]() {
+    if (loaded + 1 < total) {
+      ++loaded;
+      if (++lq == Kq) {
+        lq = 0;
+        ++li;
       }
-    };
-    WChunk buf[D];
-    if (total > 0) {
-#pragma unroll
-      for (int d = 0; d < D; ++d) {
-        wchunk_load(ws, (rt0 + kTileWaves * li) * Kq + lq, buf[d]);
-        advance();
-      }
-      // the DMA is older than the D chunks just issued
-      wait_vmcnt<4 * D>();
-    } else {
-      wait_vmcnt<0>();
     }
-    // every wave's share of the operand is in LDS; no LDS access may move
-    // across the barrier
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
+  };
+  WChunk buf[D];
+  if (total > 0) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      wchunk_load(ws, (rt0 + kTileWaves * li) * Kq + lq, buf[d]);
+      advance();
+    }
+    // the DMA is older than the D chunks just issued
+    wait_vmcnt<4 * D>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  // every wave's share of the operand is in LDS; no LDS access may move
+  // across the barrier
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 
-    uint32_t ci = 0, cq = 0;
-    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    f32x4 ag = z, au = z, cg = z, cu = z;
-    auto consume = [&](WChunk& c, bool refill) {
-      wchunk_math(c, s_x + cq * 256, s_sx + cq * kWave, ag, au, cg, cu);
-      if (refill) {
-        wchunk_load(ws, (rt0 + kTileWaves * li) * Kq + lq, c);
-        advance();
-      }
-      if (++cq == Kq) {
-        tile_epilogue(a, hqr, hsr, m0, end, rt0 + kTileWaves * ci, ag, au, cg, cu);
-        ag = au = cg = cu = z;
-        cq = 0;
-        ++ci;
-      }
-    };
-    const int64_t n_full = total / D;
-    for (int64_t j = 0; j < n_full; ++j) {
-#pragma unroll
-      for (int d = 0; d < D; ++d) consume(buf[d], true);
+  uint32_t ci = 0, cq = 0;
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  f32x4 ag = z, au = z, cg = z, cu = z;
+  auto consume = [&](WChunk& c, bool refill) {
+    wchunk_math(c, s_x + cq * 256, s_sx + cq * kWave, ag, au, cg, cu);
+    if (refill) {
+      wchunk_load(ws, (rt0 + kTileWaves * li) * Kq + lq, c);
+      advance();
     }
-    const int rem = (int)(total - n_full * D);
+    if (++cq == Kq) {
+      tile_epilogue<H_AUX>(a, hqr, hsr, m0, end, rt0 + kTileWaves * ci, ag, au, cg, cu);
+      ag = au = cg = cu = z;
+      cq = 0;
+      ++ci;
+    }
+  };
+  const int64_t n_full = total / D;
+  for (int64_t j = 0; j < n_full; ++j) {
 #pragma unroll
-    for (int d = 0; d < D - 1; ++d)
-      if (d < rem) consume(buf[d], false);
+    for (int d = 0; d < D; ++d) consume(buf[d], true);
+  }
+  const int rem = (int)(total - n_full * D);
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d)
+    if (d < rem) consume(buf[d], false);
+}
+
+template <int D>
+__global__ __launch_bounds__(kTileWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void gate_up_tile_kernel(GateUpK a) {
+  extern __shared__ u32x4 s_x[];
+  float* s_sx = reinterpret_cast<float*>(s_x + (uint32_t)a.Kq * 256);
+  if (blockIdx.x == 0) {
+    // the all-zero down-operand row read for positions past a segment
+    for (int64_t i = threadIdx.x; i < a.KqI * 256; i += blockDim.x) a.hq[a.zero_row * a.KqI * 256 + i] = 0;
+    for (int64_t i = threadIdx.x; i < a.KqI * 8; i += blockDim.x) a.hs[a.zero_row * a.KqI * 8 + i] = 0.0f;
+  }
+  const uint32_t n_tiles = (uint32_t)__builtin_amdgcn_readfirstlane(*a.n_tiles);
+  const TileJobs jb = tile_jobs(n_tiles, (uint32_t)(a.I / kRowTile), gridDim.x);
+  for (uint32_t job = blockIdx.x; job < jb.n_jobs; job += gridDim.x) {
+    const uint32_t gt = job / jb.jpt;
+    uint32_t unused;
+    gate_up_tile_job<D, 0>(a, s_x, s_sx, gt, job - gt * jb.jpt, jb, nullptr, unused);
     __syncthreads();  // the operand is read by every wave before the next job overwrites it
   }
 }
-
 
 // ------------------------------------------------------------------ down
 
@@ -692,24 +717,31 @@ struct DChunk {  // one quad of one row tile of W_down
 // half-group sums [KqI][2 halves][64 lanes] floats.
 inline size_t down_tile_lds_bytes(int64_t KqI) { return (size_t)KqI * (8 * 64 * 16 + 2 * 64 * 4); }
 
-template <int D>
-__global__ __launch_bounds__(kTileWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void down_tile_kernel(DownK a) {
-  extern __shared__ u32x4 s_h[];
+// Spin bound of a fused down job waiting for its token tile's gate/up jobs
+// (each poll is one memory round trip plus a short sleep, about 1 us): far
+// beyond any real wait, it only guarantees that every wave exits.
+constexpr uint32_t kTileWaitPolls = 1u << 18;
+
+// One down job: token tile gt, row tiles of H part * per_job + w + kTileWaves * i.
+// FUSED (the gate/up + down kernel): the weight ring is loaded first, then
+// thread 0 waits until the tile's gate/up jobs have all counted in at
+// `ready` (>= target), and only then is the operand copied, by device-scope
+// loads (the h rows were stored device-scope and had completed before their
+// count was sent; the copies are issued after the count was seen).  Positions past the segment then read the segment's last row
+// instead of the zero row: their output rows are never stored, and an MFMA
+// output row depends on its own A row only.
+template <int D, bool FUSED>
+__device__ __attribute__((always_inline)) inline void down_tile_job(const DownK& a, u32x4* s_h, float* s_hs, uint32_t gt,
+                                                                    uint32_t part, const TileJobs& jb, int32_t* ready,
+                                                                    int32_t target, int32_t* err, int32_t* ticket,
+                                                                    uint32_t& nxt) {
   const int lane = threadIdx.x % kWave;
   const int n = lane % 16;
   const int p = lane / 16;
   const uint32_t w = (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t Kq = (uint32_t)a.Kq;  // quads of I
   const int64_t Kg = a.I / kGroup;
-  float* s_hs = reinterpret_cast<float*>(s_h + Kq * 512);
-  const uint32_t n_tiles = (uint32_t)__builtin_amdgcn_readfirstlane(*a.n_tiles);
   const uint32_t n_rt = (uint32_t)(a.H / kRowTile);
-  uint32_t M = (n_tiles * n_rt + kTileWaves * gridDim.x - 1) / (kTileWaves * gridDim.x);
-  M = M < 1 ? 1 : M;
-  const uint32_t per_job = kTileWaves * M;
-  const uint32_t jpt = (n_rt + per_job - 1) / per_job;
-  const uint32_t n_jobs = n_tiles * jpt;
-
   const BufRsrc hqr = buf_rsrc(a.hq, (uint32_t)((a.zero_row + 1) * a.Kq * 512));
   const BufRsrc hsr = buf_rsrc(a.hs, (uint32_t)((a.zero_row + 1) * a.Kq * 32));
   const uint32_t nib_bytes = (uint32_t)(a.H * a.Kq * 64);
@@ -717,116 +749,207 @@ __global__ __launch_bounds__(kTileWaves * kWave) __attribute__((amdgpu_waves_per
   const uint32_t mask = vgpr_const(0x03C003C0u);
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
-  for (uint32_t job = blockIdx.x; job < n_jobs; job += gridDim.x) {
-    const uint32_t gt = job / jpt;
-    const uint32_t part = job - gt * jpt;
-    const int32_t* tw = a.tiles + (int64_t)gt * kTileWords;
-    const int e = __builtin_amdgcn_readfirstlane(tw[0]);
-    const int64_t m0 = __builtin_amdgcn_readfirstlane(tw[1]);
-    const int64_t end = __builtin_amdgcn_readfirstlane(tw[2]);
-    const bool routed = e < a.seg.E;
-    const BufRsrc wr = buf_rsrc(routed ? a.down_nib + (int64_t)e * nib_bytes : a.sh_down_nib, nib_bytes);
-    const BufRsrc sr = buf_rsrc(routed ? reinterpret_cast<const uint8_t*>(a.down_sc) + (int64_t)e * sc_bytes
-                                       : reinterpret_cast<const uint8_t*>(a.sh_down_sc), sc_bytes);
-    const uint32_t rt0 = part * per_job + w;
-    const uint32_t left = rt0 < n_rt ? (n_rt - rt0 + kTileWaves - 1) / kTileWaves : 0;
-    const uint32_t n_mine = left < M ? left : M;
-    const int64_t total = (int64_t)n_mine * Kq;
+  const int32_t* tw = a.tiles + (int64_t)gt * kTileWords;
+  const int e = __builtin_amdgcn_readfirstlane(tw[0]);
+  const int64_t m0 = __builtin_amdgcn_readfirstlane(tw[1]);
+  const int64_t end = __builtin_amdgcn_readfirstlane(tw[2]);
+  if (ticket && threadIdx.x == 0) nxt = (uint32_t)atomicAdd(ticket, 1);
+  const bool routed = e < a.seg.E;
+  const BufRsrc wr = buf_rsrc(routed ? a.down_nib + (int64_t)e * nib_bytes : a.sh_down_nib, nib_bytes);
+  const BufRsrc sr = buf_rsrc(routed ? reinterpret_cast<const uint8_t*>(a.down_sc) + (int64_t)e * sc_bytes
+                                     : reinterpret_cast<const uint8_t*>(a.sh_down_sc), sc_bytes);
+  const uint32_t rt0 = part * jb.per_job + w;
+  const uint32_t left = rt0 < n_rt ? (n_rt - rt0 + kTileWaves - 1) / kTileWaves : 0;
+  const uint32_t n_mine = left < jb.M ? left : jb.M;
+  const int64_t total = (int64_t)n_mine * Kq;
 
-    // the tile's operand -> LDS: block b = (q, gi, h) is one 16-byte piece per lane
-    {
-      const int64_t pos = m0 + n < end ? m0 + n : a.zero_row;
-      const uint32_t hv = (uint32_t)pos * Kq * 512u + (uint32_t)p * 128u;
-      const uint32_t sv = (uint32_t)pos * Kq * 32u + (uint32_t)p * 8u;
-      for (uint32_t b = w; b < Kq * 8; b += kTileWaves)
-        dma_b128(hqr, s_h + b * kWave, hv, (b / 8) * 512u + ((b / 2) % 4) * 32u + (b % 2) * 16u);
-      for (uint32_t b = w; b < Kq * 2; b += kTileWaves) dma_b32(hsr, s_hs + b * kWave, sv, (b / 2) * 32u + (b % 2) * 4u);
-    }
+  // the tile's operand -> LDS: block b = (q, gi, h) is one 16-byte piece per lane
+  auto copy_operand = [&]() {
+    const int64_t pos = m0 + n < end ? m0 + n : (FUSED ? end - 1 : a.zero_row);
+    const uint32_t hv = (uint32_t)pos * Kq * 512u + (uint32_t)p * 128u;
+    const uint32_t sv = (uint32_t)pos * Kq * 32u + (uint32_t)p * 8u;
+    constexpr int aux = FUSED ? kDeviceScope : 0;
+    for (uint32_t b = w; b < Kq * 8; b += kTileWaves)
+      dma_b128<aux>(hqr, s_h + b * kWave, hv, (b / 8) * 512u + ((b / 2) % 4) * 32u + (b % 2) * 16u);
+    for (uint32_t b = w; b < Kq * 2; b += kTileWaves)
+      dma_b32<aux>(hsr, s_hs + b * kWave, sv, (b / 2) * 32u + (b % 2) * 4u);
+  };
+  if constexpr (!FUSED) {
+    copy_operand();
     asm volatile("" ::: "memory");  // the operand loads stay older than the weight loads below
+  }
 
-    uint32_t li = 0, lq = 0;
-    int64_t loaded = 0;
-    auto advance = [&]() {
-      if (loaded + 1 < total) {
-        ++loaded;
-        if (++lq == Kq) {
-          lq = 0;
-          ++li;
-        }
+  uint32_t li = 0, lq = 0;
+  int64_t loaded = 0;
+  auto advance = [&]() {
+    if (loaded + 1 < total) {
+      ++loaded;
+      if (++lq == Kq) {
+        lq = 0;
+        ++li;
       }
-    };
-    auto load = [&](DChunk& c) {
-      const uint32_t tq = (uint32_t)__builtin_amdgcn_readfirstlane((int)((rt0 + kTileWaves * li) * Kq + lq));
-      c.w = buf_load_b128(wr, (uint32_t)lane * 16u, tq * kQuadNibBytes);
-      c.s = buf_load_b64(sr, (uint32_t)n * 8u, tq * (kQuadScales * 2));
-    };
-    DChunk buf[D];
-    if (total > 0) {
-#pragma unroll
-      for (int d = 0; d < D; ++d) {
-        load(buf[d]);
-        advance();
-      }
-      wait_vmcnt<2 * D>();  // the operand copies are older than the D chunks
-    } else {
-      wait_vmcnt<0>();
     }
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
+  };
+  auto load = [&](DChunk& c) {
+    const uint32_t tq = (uint32_t)__builtin_amdgcn_readfirstlane((int)((rt0 + kTileWaves * li) * Kq + lq));
+    c.w = buf_load_b128(wr, (uint32_t)lane * 16u, tq * kQuadNibBytes);
+    c.s = buf_load_b64(sr, (uint32_t)n * 8u, tq * (kQuadScales * 2));
+  };
+  DChunk buf[D];
+  if (total > 0) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      load(buf[d]);
+      advance();
+    }
+  }
+  if constexpr (FUSED) {
+    if (threadIdx.x == 0) {
+      for (uint32_t it = 0;; ++it) {
+        if (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) break;
+        if (it >= kTileWaitPolls) {
+          __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(8);
+      }
+    }
+    __syncthreads();
+    copy_operand();
+    wait_vmcnt<0>();  // the operand copies are the youngest loads
+  } else {
+    if (total > 0) wait_vmcnt<2 * D>();  // the operand copies are older than the D chunks
+    else wait_vmcnt<0>();
+  }
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 
-    uint32_t ci = 0, cq = 0;
-    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    f32x4 acc = z, corr = z;
-    auto consume = [&](DChunk& c, bool refill) {
-      float dv[4];
-      unpack_scales(c.s, dv);
-      const uint32_t bwv[4] = {c.w.x, c.w.y, c.w.z, c.w.w};
-      const u32x4* hq_q = s_h + cq * 512;
-      f32x4 part_acc = z;
+  uint32_t ci = 0, cq = 0;
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc = z, corr = z;
+  auto consume = [&](DChunk& c, bool refill) {
+    float dv[4];
+    unpack_scales(c.s, dv);
+    const uint32_t bwv[4] = {c.w.x, c.w.y, c.w.z, c.w.w};
+    const u32x4* hq_q = s_h + cq * 512;
+    f32x4 part_acc = z;
 #pragma unroll
-      for (int gi = 0; gi < 4; ++gi) {
-        const bool real = 4 * (int64_t)cq + gi < Kg;  // padded groups hold no h
-        const u32x4 ah = real ? hq_q[(gi * 2) * kWave + lane] : zero4;
-        const u32x4 al = real ? hq_q[(gi * 2 + 1) * kWave + lane] : zero4;
-        const u32x4 bb = dequant_unit_f16(bwv[gi], mask);
-        f32x4 pp = mfma_f16_16x16x32(ah, bb, z);
-        pp = mfma_f16_16x16x32(al, bb, pp);
-        part_acc += dv[gi] * pp;
-      }
-      const float sp = (4 * (int64_t)cq + p < Kg) ? s_hs[(cq * 2) * kWave + lane] + s_hs[(cq * 2 + 1) * kWave + lane] : 0.0f;
-      corr = mfma_f32_16x16x4(sp, dv[p], corr);
-      acc += part_acc;
-      if (refill) {
-        load(c);
-        advance();
-      }
-      if (++cq == Kq) {
-        const f32x4 res = kUnitScale * acc - kUnitBias * corr;
-        const uint32_t rt = rt0 + kTileWaves * ci;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int64_t pos = m0 + 4 * p + j;
-          if (pos < end) a.outbuf[pos * a.H + rt * 16 + n] = res[j];
-        }
-        acc = corr = z;
-        cq = 0;
-        ++ci;
-      }
-    };
-    const int64_t n_full = total / D;
-    for (int64_t j = 0; j < n_full; ++j) {
-#pragma unroll
-      for (int d = 0; d < D; ++d) consume(buf[d], true);
+    for (int gi = 0; gi < 4; ++gi) {
+      const bool real = 4 * (int64_t)cq + gi < Kg;  // padded groups hold no h
+      const u32x4 ah = real ? hq_q[(gi * 2) * kWave + lane] : zero4;
+      const u32x4 al = real ? hq_q[(gi * 2 + 1) * kWave + lane] : zero4;
+      const u32x4 bb = dequant_unit_f16(bwv[gi], mask);
+      f32x4 pp = mfma_f16_16x16x32(ah, bb, z);
+      pp = mfma_f16_16x16x32(al, bb, pp);
+      part_acc += dv[gi] * pp;
     }
-    const int rem = (int)(total - n_full * D);
+    const float sp = (4 * (int64_t)cq + p < Kg) ? s_hs[(cq * 2) * kWave + lane] + s_hs[(cq * 2 + 1) * kWave + lane] : 0.0f;
+    corr = mfma_f32_16x16x4(sp, dv[p], corr);
+    acc += part_acc;
+    if (refill) {
+      load(c);
+      advance();
+    }
+    if (++cq == Kq) {
+      const f32x4 res = kUnitScale * acc - kUnitBias * corr;
+      const uint32_t rt = rt0 + kTileWaves * ci;
 #pragma unroll
-    for (int d = 0; d < D - 1; ++d)
-      if (d < rem) consume(buf[d], false);
+      for (int j = 0; j < 4; ++j) {
+        const int64_t pos = m0 + 4 * p + j;
+        if (pos < end) a.outbuf[pos * a.H + rt * 16 + n] = res[j];
+      }
+      acc = corr = z;
+      cq = 0;
+      ++ci;
+    }
+  };
+  const int64_t n_full = total / D;
+  for (int64_t j = 0; j < n_full; ++j) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) consume(buf[d], true);
+  }
+  const int rem = (int)(total - n_full * D);
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d)
+    if (d < rem) consume(buf[d], false);
+}
+
+template <int D>
+__global__ __launch_bounds__(kTileWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void down_tile_kernel(DownK a) {
+  extern __shared__ u32x4 s_h[];
+  float* s_hs = reinterpret_cast<float*>(s_h + (uint32_t)a.Kq * 512);
+  const uint32_t n_tiles = (uint32_t)__builtin_amdgcn_readfirstlane(*a.n_tiles);
+  const TileJobs jb = tile_jobs(n_tiles, (uint32_t)(a.H / kRowTile), gridDim.x);
+  for (uint32_t job = blockIdx.x; job < jb.n_jobs; job += gridDim.x) {
+    const uint32_t gt = job / jb.jpt;
+    uint32_t unused;
+    down_tile_job<D, false>(a, s_h, s_hs, gt, job - gt * jb.jpt, jb, nullptr, 0, nullptr, nullptr, unused);
     __syncthreads();  // the operand is read by every wave before the next job overwrites it
   }
 }
 
+// ------------------------------------------------ gate/up + down, one launch
+//
+// The two token-tile stages as one persistent launch.  Workgroups draw jobs
+// from a ticket counter (zeroed by the permute): every gate/up job comes
+// before every down job.  A gate/up job stores its h rows device-scope, waits
+// for those stores to complete, and adds one count on its token tile (one
+// 128-byte line per tile, zeroed by the permute); a down job loads its first
+// weight chunks, then waits for its tile's count to reach the gate/up jobs
+// per tile and copies the rows device-scope.  (Agent-scope fences instead,
+// an L2 write-back per gate/up job and an L2 invalidation per down job, made
+// the launch twice as slow as two separate launches.)  While
+// the last gate/up jobs finish, the down weight stream is already running on
+// the other CUs, instead of the chip idling between two launches.
+// No wait can deadlock, whatever the residency: a ticket is only ever held by
+// a running workgroup, the next ticket is drawn at the start of a job and is
+// larger than the current one (so a workgroup holding a gate/up ticket is
+// running a gate/up job, which never waits), and all gate/up tickets precede
+// every down ticket.  The spin is still bounded (kTileWaitPolls).
+struct FfnTileK {
+  GateUpK g;
+  DownK d;
+  int32_t* tile_done;  // finished gate/up jobs of token tile g at [g * kCtlStride] (zeroed by the permute)
+  int32_t* ctl;        // [0] token tiles, [kCtlStride] job ticket, [2 * kCtlStride] set if a wait hit its bound
+  uint32_t job_lds;  // byte offset of the job word in the dynamic LDS (after the larger operand)
+};
+
+template <int DG, int DD>
+__global__ __launch_bounds__(kTileWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void ffn_tile_kernel(FfnTileK a) {
+  extern __shared__ u32x4 s_op[];  // all LDS is dynamic: a static part would eat into the 160 KB maximum
+  uint32_t& s_job = *reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(s_op) + a.job_lds);
+  float* s_sx = reinterpret_cast<float*>(s_op + (uint32_t)a.g.Kq * 256);
+  float* s_hs = reinterpret_cast<float*>(s_op + (uint32_t)a.d.Kq * 512);
+  if (threadIdx.x == 0) s_job = (uint32_t)atomicAdd(&a.ctl[kCtlStride], 1);
+  const uint32_t n_tiles = (uint32_t)__builtin_amdgcn_readfirstlane(a.ctl[0]);
+  const TileJobs ja = tile_jobs(n_tiles, (uint32_t)(a.g.I / kRowTile), gridDim.x);
+  const TileJobs jd = tile_jobs(n_tiles, (uint32_t)(a.d.H / kRowTile), gridDim.x);
+  const uint32_t n_jobs = ja.n_jobs + jd.n_jobs;
+  __syncthreads();
+  for (;;) {
+    const uint32_t job = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_job);
+    if (job >= n_jobs) break;
+    uint32_t nxt = 0;  // the next ticket (thread 0), drawn inside the job
+    if (job < ja.n_jobs) {
+      const uint32_t gt = job / ja.jpt;
+      gate_up_tile_job<DG, kDeviceScope>(a.g, s_op, s_sx, gt, job - gt * ja.jpt, ja, &a.ctl[kCtlStride], nxt);
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's device-scope h stores have completed
+      if (threadIdx.x == 0) s_job = nxt;
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        atomicAdd(&a.tile_done[(int64_t)gt * kCtlStride], 1);
+      }
+    } else {
+      const uint32_t dj = job - ja.n_jobs;
+      const uint32_t gt = dj / jd.jpt;
+      down_tile_job<DD, true>(a.d, s_op, s_hs, gt, dj - gt * jd.jpt, jd, &a.tile_done[(int64_t)gt * kCtlStride],
+                              (int32_t)ja.jpt, &a.ctl[2 * kCtlStride], &a.ctl[kCtlStride], nxt);
+      if (threadIdx.x == 0) s_job = nxt;
+      __syncthreads();
+    }
+  }
+}
 
 // y[t] = sum_j w[t,j] * out[slot_pos[t*k+j]] (+ out[T*k + t] for the shared
 // expert), j in slot order, fp32.  Slots are taken KB at a time: the KB
@@ -965,7 +1088,89 @@ static hipError_t launch_gate_up_tile(const ExpertArgs& x, const GateUpK& g, hip
   return hipGetLastError();
 }
 
-hipError_t launch_gate_up(const ExpertArgs& x, const Workspace& ws, hipStream_t stream) {
+static DownK make_down_k(const ExpertArgs& x, const Workspace& ws) {
+  DownK d;
+  d.seg = segments_of(x, ws);
+  d.hq = ws.hq;
+  d.hs = ws.hs;
+  d.down_nib = x.down_nib;
+  d.down_sc = x.down_scale;
+  d.sh_down_nib = x.sh_down_nib;
+  d.sh_down_sc = x.sh_down_scale;
+  d.H = x.H;
+  d.I = x.I;
+  d.Kq = ceil_div(x.I, kQuad);
+  d.zero_row = x.T * x.k + (x.has_shared ? x.T : 0);
+  d.outbuf = ws.outbuf;
+  d.tiles = ws.tiles;
+  d.n_tiles = ws.n_tiles;
+  return d;
+}
+
+static size_t ffn_lds_bytes(int64_t Kq, int64_t KqI) {
+  const size_t a = tile_lds_bytes(Kq), b = down_tile_lds_bytes(KqI);
+  return a > b ? a : b;
+}
+
+// The fused gate/up + down launch (launch_gate_up runs it; launch_down then
+// has nothing to do) runs when PHANTOM_MOE_FFN_KERNEL=fused and both stages
+// are in the token-tile regime with two workgroups per CU (the larger operand
+// plus the 16-byte job word).  It is not the default: at Qwen3 shape, 32
+// tokens, it measured 60 us against 43 us for the two launches (its first
+// jobs start 5 us late, the ticket draws of all workgroups colliding, and a
+// down job is as long as the whole separate down launch, so the workgroups
+// whose gate/up job ended last finish last).
+bool ffn_fused_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared) {
+  const char* v = getenv("PHANTOM_MOE_FFN_KERNEL");
+  if (!v || strcmp(v, "fused") != 0) return false;
+  return gate_up_tile_regime(T, H, I, E, k, has_shared) && down_tile_regime(T, H, I, E, k, has_shared) &&
+         ffn_lds_bytes(ceil_div(H, kQuad), ceil_div(I, kQuad)) + 16 <= 80 * 1024;
+}
+
+// Ring depths: gate/up 3, down 2 (PHANTOM_MOE_DOWN_DEPTH=4 or 6 overrides).
+static hipError_t launch_ffn_tile(const ExpertArgs& x, const GateUpK& g, const DownK& d, const Workspace& ws,
+                                  hipStream_t stream) {
+  int depth = 2;
+  if (const char* v = getenv("PHANTOM_MOE_DOWN_DEPTH")) {
+    const int dd = atoi(v);
+    if (dd == 2 || dd == 4 || dd == 6) depth = dd;
+  }
+  FfnTileK f;
+  f.g = g;
+  f.d = d;
+  f.tile_done = ws.tile_done;
+  f.ctl = ws.n_tiles;
+  f.job_lds = (uint32_t)ffn_lds_bytes(g.Kq, d.Kq);
+  const size_t lds = f.job_lds + 16;
+  const int block = kTileWaves * kWave;
+  const int64_t max_jobs = max_token_tiles(x.T, x.k, x.E, x.has_shared) *
+                           (ceil_div(x.I / kRowTile, kTileWaves) + ceil_div(x.H / kRowTile, kTileWaves));
+#define PMOE_FFN(DD_)                                                                                    \
+  do {                                                                                                   \
+    static bool attr_set = false;                                                                        \
+    if (!attr_set) {                                                                                     \
+      hipError_t e_ = hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_tile_kernel<3, DD_>),       \
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);       \
+      if (e_ != hipSuccess) return e_;                                                                   \
+      attr_set = true;                                                                                   \
+    }                                                                                                    \
+    int per_cu = 0;                                                                                      \
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ffn_tile_kernel<3, DD_>, block, lds) !=    \
+            hipSuccess || per_cu < 1)                                                                    \
+      per_cu = 1;                                                                                        \
+    int64_t grid = (int64_t)device_cus() * per_cu;                                                       \
+    if (grid > max_jobs) grid = max_jobs;                                                                \
+    hipLaunchKernelGGL((ffn_tile_kernel<3, DD_>), dim3((unsigned)(grid < 1 ? 1 : grid)), dim3(block), lds, \
+                       stream, f);                                                                       \
+  } while (0)
+  if (depth == 2) PMOE_FFN(2);
+  else if (depth == 4) PMOE_FFN(4);
+  else PMOE_FFN(6);
+#undef PMOE_FFN
+  return hipGetLastError();
+}
+
+static GateUpK make_gate_up_k(const ExpertArgs& x, const Workspace& ws) {
   GateUpK g;
   g.seg = segments_of(x, ws);
   g.T = x.T;
@@ -987,6 +1192,12 @@ hipError_t launch_gate_up(const ExpertArgs& x, const Workspace& ws, hipStream_t 
   g.zero_row = x.T * x.k + (x.has_shared ? x.T : 0);
   g.tiles = ws.tiles;
   g.n_tiles = ws.n_tiles;
+  return g;
+}
+
+hipError_t launch_gate_up(const ExpertArgs& x, const Workspace& ws, hipStream_t stream) {
+  const GateUpK g = make_gate_up_k(x, ws);
+  if (ffn_fused_regime(x.T, x.H, x.I, x.E, x.k, x.has_shared)) return launch_ffn_tile(x, g, make_down_k(x, ws), ws, stream);
   if (tile_fits(x, g)) return launch_gate_up_tile(x, g, stream);
   // K split: about four quads per wave (fewer waves per item keep more items
   // in flight per CU), one quad of loads outstanding per wave at a time.
@@ -1057,21 +1268,9 @@ static hipError_t launch_down_tile(const ExpertArgs& x, const DownK& d, hipStrea
 }
 
 hipError_t launch_down(const ExpertArgs& x, const Workspace& ws, hipStream_t stream) {
-  DownK d;
-  d.seg = segments_of(x, ws);
-  d.hq = ws.hq;
-  d.hs = ws.hs;
-  d.down_nib = x.down_nib;
-  d.down_sc = x.down_scale;
-  d.sh_down_nib = x.sh_down_nib;
-  d.sh_down_sc = x.sh_down_scale;
-  d.H = x.H;
-  d.I = x.I;
-  d.Kq = ceil_div(x.I, kQuad);
-  d.zero_row = x.T * x.k + (x.has_shared ? x.T : 0);
-  d.outbuf = ws.outbuf;
-  d.tiles = ws.tiles;
-  d.n_tiles = ws.n_tiles;
+  // the fused launch of launch_gate_up has run the down stage too
+  if (ffn_fused_regime(x.T, x.H, x.I, x.E, x.k, x.has_shared)) return hipSuccess;
+  const DownK d = make_down_k(x, ws);
   if (d.tiles && down_tile_regime(x.T, x.H, x.I, x.E, x.k, x.has_shared)) return launch_down_tile(x, d, stream);
   Split sp = choose_split(d.Kq, kDownWaves);
   int rt = 2;  // H is a multiple of 32: an even number of 16-row tiles

@@ -184,18 +184,28 @@ __device__ inline float buf_load_f32(BufRsrc r, uint32_t voff, uint32_t soff) {
 }
 
 
+// Cache policy of a buffer access (the `aux` operand): SC1 alone makes it a
+// device-scope access, the form the compiler gives agent-scope atomic loads
+// and stores.  A device-scope store is written through to where every XCD
+// reads it, and a device-scope load is served from there, never from a
+// possibly stale line of this CU's L1 or this XCD's L2.  Data handed between
+// workgroups of one launch this way needs no L2 write-back or invalidation.
+constexpr int kDeviceScope = 16;
+
 // Direct-to-LDS buffer loads: each lane's 16 (or 4) bytes land at
 // lds + lane * 16 (or 4); lds must be wave-uniform.  They count in vmcnt like
 // other loads and are not tracked by the compiler's waits for LDS reads, so
 // the reader waits explicitly (wait_vmcnt) before a barrier.
+template <int AUX = 0>
 __device__ inline void dma_b128(BufRsrc r, void* lds, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, (int)voff,
-                                           (int)soff, 0, 0);
+                                           (int)soff, 0, AUX);
 }
 
+template <int AUX = 0>
 __device__ inline void dma_b32(BufRsrc r, void* lds, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, (int)voff,
-                                           (int)soff, 0, 0);
+                                           (int)soff, 0, AUX);
 }
 
 // The same 16-byte direct-to-LDS load issued from inline assembly, so the

@@ -17,6 +17,7 @@ constexpr int kMaxTopK = 32;
 // token of each of the 16 positions (T, the all-zero activation row, past the
 // segment end).  Routed segments come in expert order, the shared one last.
 constexpr int kTileWords = 20;
+constexpr int kCtlStride = 32;  // ints per 128-byte line: counters that atomics hit get a line each
 inline int64_t max_token_tiles(int64_t T, int k, int E, int has_shared) {
   const int64_t nslots = T * k;
   return (nslots + 15) / 16 + (nslots < E ? nslots : E) + (has_shared ? (T + 15) / 16 : 0);
@@ -35,7 +36,11 @@ struct Workspace {
   int4* desc = nullptr;             // [E + 1] {expert, begin, end, 0} per active segment
   int32_t* seg_tok = nullptr;       // [T * k + T] token of each segment position
   int32_t* tiles = nullptr;         // [max_token_tiles][kTileWords] 16-position tiles of the segments
-  int32_t* n_tiles = nullptr;       // [1]
+  // [3 * kCtlStride]: word 0 the token tile count; word kCtlStride the
+  // fused expert launch's job ticket; word 2 * kCtlStride its wait-bound flag
+  // (each in its own 128-byte line: a line that atomics hit is slow to read)
+  int32_t* n_tiles = nullptr;
+  int32_t* tile_done = nullptr;     // [max_token_tiles * kCtlStride] finished gate/up jobs per token tile
   uint16_t* hq = nullptr;          // [rows, Kpad_I * 2] fp16 hi/lo of h, MFMA operand order
   float* hs = nullptr;             // [rows, Kpad_I / 32, 2] half-group sums of h
   float* outbuf = nullptr;          // [T*k + T*shared, H] expert outputs, segment order
@@ -120,6 +125,9 @@ hipError_t launch_gemm_down(const ExpertArgs& a, const Workspace& ws, hipStream_
 bool gate_up_tile_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
 // The same for the down stage.
 bool down_tile_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
+// Both stages as one persistent token-tile launch (run by launch_gate_up;
+// launch_down is then a no-op).
+bool ffn_fused_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
 
 // The three expert stages; launch_experts runs them back to back.
 hipError_t launch_gate_up(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);

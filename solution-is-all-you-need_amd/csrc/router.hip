@@ -65,6 +65,7 @@ struct RouteK {
   int32_t* seg_tok;  // [T*k + T] token of each segment position, or null
   int32_t* tiles;    // token tiles (see kTileWords), or null
   int32_t* n_tiles;
+  int32_t* tile_done;  // per-tile gate/up job counts of the fused expert launch (zeroed here), or null
   int32_t* counter;  // select workgroups finished (fused permute); zeroed by the logits launch
   int fuse_permute;
 };
@@ -159,7 +160,7 @@ __device__ __attribute__((always_inline)) inline void block_permute(const int32_
                               int has_shared, int32_t* offsets, int32_t* offsets_user,
                               int32_t* active, int32_t* n_active, int32_t* sorted_slots,
                               int32_t* slot_pos, int4* desc, int32_t* seg_tok, int32_t* tiles,
-                              int32_t* n_tiles) {
+                              int32_t* n_tiles, int32_t* tile_done) {
   constexpr int kMaxWaves = 16;
   __shared__ int s_cnt[kMaxWaves][kMaxExperts];
   __shared__ int s_tmp[3 * kMaxWaves];
@@ -249,8 +250,10 @@ __device__ __attribute__((always_inline)) inline void block_permute(const int32_
       if (tiles) {
         // headers (pass 2 writes the tokens; words past the segment end are
         // left as they are and never read)
-        for (int j = 0; j < (tot[i] + 15) / 16; ++j)
+        for (int j = 0; j < (tot[i] + 15) / 16; ++j) {
           *reinterpret_cast<int4*>(tiles + (int64_t)(trun + j) * kTileWords) = make_int4(e, run + 16 * j, run + tot[i], 0);
+          if (tile_done) tile_done[(int64_t)(trun + j) * kCtlStride] = 0;
+        }
       }
       trun += (tot[i] + 15) / 16;
       int b = run;
@@ -281,9 +284,14 @@ __device__ __attribute__((always_inline)) inline void block_permute(const int32_
     for (int64_t j = tid; j < n_sh; j += blockDim.x) {
       int32_t* tw = tiles + (total_tiles + j) * kTileWords;
       *reinterpret_cast<int4*>(tw) = make_int4(E, total + (int)(16 * j), total + (int)T, 0);
+      if (tile_done) tile_done[(total_tiles + j) * kCtlStride] = 0;
       for (int jj = 0; jj < 16 && 16 * j + jj < T; ++jj) tw[4 + jj] = (int32_t)(16 * j + jj);
     }
-    if (tid == 0) *n_tiles = total_tiles + (int)n_sh;
+    if (tid == 0) {
+      n_tiles[0] = total_tiles + (int)n_sh;
+      n_tiles[kCtlStride] = 0;      // job ticket of the fused expert launch
+      n_tiles[2 * kCtlStride] = 0;  // its wait-bound flag
+    }
   }
   if (desc) {
     // unused slots up to the launch bound min(E, n) + shared carry expert -1
@@ -625,7 +633,10 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteK a) {
 
 // Top-k and weights, one wave per token (grid-stride).  With do_permute, a
 // launch of one workgroup continues with the permute, and a fused launch hands
-// the permute to the last workgroup to finish.
+// the permute to the last workgroup to finish.  (One workgroup of up to 16
+// waves for up to 64 tokens, its selection handed to the permute in LDS,
+// measured slower than the hand-off: route 24.4 vs 19.2 us at 32 tokens,
+// 57 vs 39 us at 64 tokens of H 7168.)
 constexpr int kSelectWaves = 4;
 constexpr int kFusedSelectBlocks = 16;
 
@@ -649,7 +660,7 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteK a) {
     // the selection reaches the permute through LDS, not a global round trip
     lds_barrier();
     block_permute(s_sel, a.T * a.k, a.k, a.E, a.T, a.has_shared, a.offsets, a.offsets_user, a.active,
-                  a.n_active, a.sorted_slots, a.slot_pos, a.desc, a.seg_tok, a.tiles, a.n_tiles);
+                  a.n_active, a.sorted_slots, a.slot_pos, a.desc, a.seg_tok, a.tiles, a.n_tiles, a.tile_done);
     return;
   }
   if (gridDim.x > 1) {
@@ -668,7 +679,7 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteK a) {
   }
   __syncthreads();
   block_permute(a.topk_idx, a.T * a.k, a.k, a.E, a.T, a.has_shared, a.offsets, a.offsets_user, a.active,
-                a.n_active, a.sorted_slots, a.slot_pos, a.desc, a.seg_tok, a.tiles, a.n_tiles);
+                a.n_active, a.sorted_slots, a.slot_pos, a.desc, a.seg_tok, a.tiles, a.n_tiles, a.tile_done);
 }
 
 __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* idx, int64_t T, int k, int E,
@@ -676,9 +687,10 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* idx, int64
                                                        int32_t* offsets_user, int32_t* active,
                                                        int32_t* n_active, int32_t* sorted_slots,
                                                        int32_t* slot_pos, int4* desc,
-                                                       int32_t* seg_tok, int32_t* tiles, int32_t* n_tiles) {
+                                                       int32_t* seg_tok, int32_t* tiles, int32_t* n_tiles,
+                                                       int32_t* tile_done) {
   block_permute(idx, T * k, k, E, T, has_shared, offsets, offsets_user, active, n_active,
-                sorted_slots, slot_pos, desc, seg_tok, tiles, n_tiles);
+                sorted_slots, slot_pos, desc, seg_tok, tiles, n_tiles, tile_done);
 }
 
 // Logits for many tokens (prefill): the same per-lane partials and tree as
@@ -853,6 +865,7 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
   const bool want_tiles = r.do_permute && r.want_tiles;
   k.tiles = want_tiles ? ws.tiles : nullptr;
   k.n_tiles = want_tiles ? ws.n_tiles : nullptr;
+  k.tile_done = want_tiles ? ws.tile_done : nullptr;
   const unsigned sel_blocks = (unsigned)ceil_div(r.T, kSelectWaves);
   k.fuse_permute = (r.do_permute && sel_blocks > 1 && sel_blocks <= kFusedSelectBlocks) ? 1 : 0;
   k.counter = k.fuse_permute ? ws.counter : nullptr;
@@ -871,7 +884,7 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
   if (err != hipSuccess || !r.do_permute || sel_blocks == 1 || k.fuse_permute) return err;
   hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, k.topk_idx, r.T, r.k,
               r.E, r.has_shared, ws.offsets, r.offsets_out, ws.active, ws.n_active, k.sorted_slots, k.slot_pos,
-              k.desc, k.seg_tok, k.tiles, k.n_tiles);
+              k.desc, k.seg_tok, k.tiles, k.n_tiles, k.tile_done);
   return hipGetLastError();
 }
 
@@ -881,7 +894,7 @@ hipError_t launch_permute(const int32_t* topk_idx, int64_t T, int k, int E, int 
   hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, topk_idx, T, k, E, has_shared,
                      ws.offsets, offsets, ws.active, ws.n_active, sorted_slots, slot_pos,
                      static_cast<int4*>(nullptr), static_cast<int32_t*>(nullptr), static_cast<int32_t*>(nullptr),
-                     static_cast<int32_t*>(nullptr));
+                     static_cast<int32_t*>(nullptr), static_cast<int32_t*>(nullptr));
   return hipGetLastError();
 }
 

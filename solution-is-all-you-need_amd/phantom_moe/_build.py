@@ -26,6 +26,10 @@ HIPCC_FLAGS = [
     "-fvisibility=hidden",
     # No packed fp32 VALU instructions anywhere in device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Atomics stay plain instructions: the wave-aggregating rewrite waits for
+    # an atomic's result right after issuing it, which would put the job
+    # ticket of the fused expert kernel on its critical path.
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wall",
 ]
 

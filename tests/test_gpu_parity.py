@@ -325,11 +325,17 @@ def test_expert_kernels_agree(dev, cfg, monkeypatch):
     """Each decode expert stage has two kernels: the token-tile kernel (the
     operand of a 16-position tile copied into LDS once, one wave per row tile)
     where the row tiles of all token tiles give at least four waves per CU
-    (eight for down), else the K-split kernel.  These shapes are in the
-    token-tile regime of both stages; both kernel pairs (the K-split ones forced by
-    PHANTOM_MOE_GATE_UP_KERNEL / PHANTOM_MOE_DOWN_KERNEL=classic) must meet the
-    layer tolerance against the oracle, shared expert and ragged last quads of
-    H and of I included."""
+    (eight for down), else the K-split kernel.  With both stages token-tile,
+    they can also run as one persistent launch (ffn_tile_kernel, selected by
+    PHANTOM_MOE_FFN_KERNEL=fused: down jobs wait on per-tile counts of
+    finished gate/up jobs).  These shapes are in the token-tile regime of both
+    stages.  The token-tile and K-split pairs (the latter forced by
+    PHANTOM_MOE_GATE_UP_KERNEL / PHANTOM_MOE_DOWN_KERNEL=classic) must meet
+    the layer tolerance against the oracle, shared expert and ragged last
+    quads of H and of I included.  The fused launch does the token-tile
+    launches' arithmetic, so its output must equal theirs bit for bit, on
+    every one of several calls (a read of h before its producers finished
+    would differ)."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     n_slots = cfg.T * cfg.k
     max_tiles = -(-n_slots // 16) + min(n_slots, cfg.E) + (-(-cfg.T // 16) if cfg.shared else 0)
@@ -343,7 +349,18 @@ def test_expert_kernels_agree(dev, cfg, monkeypatch):
     x = to_bf16_tensor(xb, dev)
     ry, ridx, _ = oracle.moe_forward(xb, L.router_w, L.gate, L.up, L.down, cfg.k, cfg.score_mode,
                                      L.router_bias, shared=L.shared)
+    lib = phantom_moe._lib.load()
+    names = lib.phantom_moe_expert_kernels(cfg.T, cfg.H, cfg.I, cfg.E, cfg.k, int(cfg.shared)).decode()
+    assert names == "gate_up=gate_up_tile_kernel;down=down_tile_kernel"
     y_tile, _, idx_tile = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b, return_routing=True)
+    y_tile = y_tile.cpu().numpy()
+    monkeypatch.setenv("PHANTOM_MOE_FFN_KERNEL", "fused")
+    names = lib.phantom_moe_expert_kernels(cfg.T, cfg.H, cfg.I, cfg.E, cfg.k, int(cfg.shared)).decode()
+    assert names == "gate_up=ffn_tile_kernel;down=ffn_tile_kernel"
+    for rep in range(4):
+        y_fus = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b).cpu().numpy()
+        assert np.array_equal(y_fus.view(np.uint32), y_tile.view(np.uint32)), f"fused call {rep + 1} differs"
+    monkeypatch.delenv("PHANTOM_MOE_FFN_KERNEL")
     monkeypatch.setenv("PHANTOM_MOE_GATE_UP_KERNEL", "classic")
     monkeypatch.setenv("PHANTOM_MOE_DOWN_KERNEL", "classic")
     y_cls, _, idx_cls = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b, return_routing=True)
@@ -351,7 +368,7 @@ def test_expert_kernels_agree(dev, cfg, monkeypatch):
     monkeypatch.delenv("PHANTOM_MOE_DOWN_KERNEL")
     np.testing.assert_array_equal(idx_tile.cpu().numpy(), ridx)
     np.testing.assert_array_equal(idx_cls.cpu().numpy(), ridx)
-    check_y(y_tile.cpu().numpy(), ry, cfg.name + " token-tile")
+    check_y(y_tile, ry, cfg.name + " token-tile")
     check_y(y_cls.cpu().numpy(), ry, cfg.name + " K-split")
 
 
