@@ -761,16 +761,22 @@ __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK&
   const uint32_t rt0 = part * jb.per_job + w;
   const uint32_t left = rt0 < n_rt ? (n_rt - rt0 + kTileWaves - 1) / kTileWaves : 0;
   const uint32_t n_mine = left < jb.M ? left : jb.M;
-  const int64_t total = (int64_t)n_mine * Kq;
+  const uint32_t total = n_mine * Kq;
 
-  // the tile's operand -> LDS: block b = (q, gi, h) is one 16-byte piece per lane
+  // the tile's operand -> LDS: block b = (q, gi, h) is one 16-byte piece per
+  // lane; the blocks of padded groups (4q + gi >= Kg, only in a ragged last
+  // quad of I) are zeroed instead, so the chunk math needs no test
   auto copy_operand = [&]() {
     const int64_t pos = m0 + n < end ? m0 + n : (FUSED ? end - 1 : a.zero_row);
     const uint32_t hv = (uint32_t)pos * Kq * 512u + (uint32_t)p * 128u;
     const uint32_t sv = (uint32_t)pos * Kq * 32u + (uint32_t)p * 8u;
     constexpr int aux = FUSED ? kDeviceScope : 0;
-    for (uint32_t b = w; b < Kq * 8; b += kTileWaves)
-      dma_b128<aux>(hqr, s_h + b * kWave, hv, (b / 8) * 512u + ((b / 2) % 4) * 32u + (b % 2) * 16u);
+    for (uint32_t b = w; b < Kq * 8; b += kTileWaves) {
+      if (4 * (b / 8) + (b / 2) % 4 < (uint32_t)Kg)
+        dma_b128<aux>(hqr, s_h + b * kWave, hv, (b / 8) * 512u + ((b / 2) % 4) * 32u + (b % 2) * 16u);
+      else
+        s_h[b * kWave + lane] = zero4;
+    }
     for (uint32_t b = w; b < Kq * 2; b += kTileWaves)
       dma_b32<aux>(hsr, s_hs + b * kWave, sv, (b / 2) * 32u + (b % 2) * 4u);
   };
@@ -779,8 +785,7 @@ __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK&
     asm volatile("" ::: "memory");  // the operand loads stay older than the weight loads below
   }
 
-  uint32_t li = 0, lq = 0;
-  int64_t loaded = 0;
+  uint32_t li = 0, lq = 0, loaded = 0;
   auto advance = [&]() {
     if (loaded + 1 < total) {
       ++loaded;
@@ -821,9 +826,7 @@ __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK&
     if (total > 0) wait_vmcnt<2 * D>();  // the operand copies are older than the D chunks
     else wait_vmcnt<0>();
   }
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
+  lds_barrier();  // this wave's copies and zero stores have landed; so have every other wave's
 
   uint32_t ci = 0, cq = 0;
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
@@ -833,20 +836,16 @@ __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK&
     unpack_scales(c.s, dv);
     const uint32_t bwv[4] = {c.w.x, c.w.y, c.w.z, c.w.w};
     const u32x4* hq_q = s_h + cq * 512;
-    f32x4 part_acc = z;
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi) {
-      const bool real = 4 * (int64_t)cq + gi < Kg;  // padded groups hold no h
-      const u32x4 ah = real ? hq_q[(gi * 2) * kWave + lane] : zero4;
-      const u32x4 al = real ? hq_q[(gi * 2 + 1) * kWave + lane] : zero4;
       const u32x4 bb = dequant_unit_f16(bwv[gi], mask);
-      f32x4 pp = mfma_f16_16x16x32(ah, bb, z);
-      pp = mfma_f16_16x16x32(al, bb, pp);
-      part_acc += dv[gi] * pp;
+      f32x4 pp = mfma_f16_16x16x32(hq_q[(gi * 2) * kWave + lane], bb, z);
+      pp = mfma_f16_16x16x32(hq_q[(gi * 2 + 1) * kWave + lane], bb, pp);
+      acc += dv[gi] * pp;
     }
-    const float sp = (4 * (int64_t)cq + p < Kg) ? s_hs[(cq * 2) * kWave + lane] + s_hs[(cq * 2 + 1) * kWave + lane] : 0.0f;
+    // padded groups' sums (not copied for them) count as zero
+    const float sp = 4 * cq + (uint32_t)p < (uint32_t)Kg ? s_hs[(cq * 2) * kWave + lane] + s_hs[(cq * 2 + 1) * kWave + lane] : 0.0f;
     corr = mfma_f32_16x16x4(sp, dv[p], corr);
-    acc += part_acc;
     if (refill) {
       load(c);
       advance();
@@ -864,15 +863,15 @@ __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK&
       ++ci;
     }
   };
-  const int64_t n_full = total / D;
-  for (int64_t j = 0; j < n_full; ++j) {
+  const uint32_t n_full = total / D;
+  for (uint32_t j = 0; j < n_full; ++j) {
 #pragma unroll
     for (int d = 0; d < D; ++d) consume(buf[d], true);
   }
-  const int rem = (int)(total - n_full * D);
+  const uint32_t rem = total - n_full * D;
 #pragma unroll
   for (int d = 0; d < D - 1; ++d)
-    if (d < rem) consume(buf[d], false);
+    if ((uint32_t)d < rem) consume(buf[d], false);
 }
 
 template <int D>
