@@ -524,7 +524,10 @@ __device__ inline int count_active(const SegSrc& seg, int* s_nact) {
   return *s_nact;
 }
 
-template <int BM, int AW>
+// SPLIT: the split-scale operands (2 MFMAs per group and position tile for
+// gate/up, 3 for down); else one MFMA per A operand against the integers
+// n - 8 (exact group sums), scaled into the accumulators with fp32 FMAs.
+template <int BM, int AW, bool SPLIT>
 __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* lds, const i32x4& ar,
                                   const i32x4 (&nr)[kG2NB], const i32x4 (&sr)[kG2NB], const int64_t (&rt)[kG2NB],
                                   f32x4 acc[kG2NB][BM / 16]) {
@@ -590,33 +593,71 @@ __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* l
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi) {
       if (4 * q + gi >= a.Kg) continue;  // padded group (uniform)
-      u32x4 bh[NB], bl[NB];
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const uint32_t s2 = gi < 2 ? bs[b].x : bs[b].y;
-        dequant_split_f16(bw[b][gi], (gi % 2) ? (s2 >> 16) : (s2 & 0xffffu), mask, bh[b], bl[b]);
-      }
-#pragma unroll
-      for (int tt = 0; tt < TT; ++tt) {
-        const u32x4* row = la + (tt * 16 + n) * UPR;
-        const int unit = (p * 4 + gi) * AW;
-        const u32x4 ah = row[unit ^ n];
+      if constexpr (SPLIT) {
+        u32x4 bh[NB], bl[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-          acc[b][tt] = mfma_f16_16x16x32(ah, bh[b], acc[b][tt]);
-          acc[b][tt] = mfma_f16_16x16x32(ah, bl[b], acc[b][tt]);
+          const uint32_t s2 = gi < 2 ? bs[b].x : bs[b].y;
+          dequant_split_f16(bw[b][gi], (gi % 2) ? (s2 >> 16) : (s2 & 0xffffu), mask, bh[b], bl[b]);
         }
-        if constexpr (AW == 2) {
-          const u32x4 al = row[(unit + 1) ^ n];
 #pragma unroll
-          for (int b = 0; b < NB; ++b) acc[b][tt] = mfma_f16_16x16x32(al, bh[b], acc[b][tt]);
+        for (int tt = 0; tt < TT; ++tt) {
+          const u32x4* row = la + (tt * 16 + n) * UPR;
+          const int unit = (p * 4 + gi) * AW;
+          const u32x4 ah = row[unit ^ n];
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            acc[b][tt] = mfma_f16_16x16x32(ah, bh[b], acc[b][tt]);
+            acc[b][tt] = mfma_f16_16x16x32(ah, bl[b], acc[b][tt]);
+          }
+          if constexpr (AW == 2) {
+            const u32x4 al = row[(unit + 1) ^ n];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) acc[b][tt] = mfma_f16_16x16x32(al, bh[b], acc[b][tt]);
+          }
         }
+      } else {
+        u32x4 bq[NB];
+        float d[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const uint32_t s2 = gi < 2 ? bs[b].x : bs[b].y;
+          d[b] = half_bits_to_float((uint16_t)((gi % 2) ? (s2 >> 16) : (s2 & 0xffffu)));
+          bq[b] = dequant_int_f16(bw[b][gi], mask);
+        }
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        // Software-pipelined by one position tile: the fp32 scaling of tile
+        // tt - 1 is issued after the MFMAs of tile tt, so it runs while they
+        // execute instead of stalling on the result it reads.
+        f32x4 pv[2][NB];
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+          const u32x4* row = la + (tt * 16 + n) * UPR;
+          const int unit = (p * 4 + gi) * AW;
+          const u32x4 ah = row[unit ^ n];
+          u32x4 al = ah;
+          if constexpr (AW == 2) al = row[(unit + 1) ^ n];
+          // the lo MFMAs follow all the hi ones, so no MFMA waits on the one before it
+#pragma unroll
+          for (int b = 0; b < NB; ++b) pv[tt & 1][b] = mfma_f16_16x16x32(ah, bq[b], z);
+          if constexpr (AW == 2) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) pv[tt & 1][b] = mfma_f16_16x16x32(al, bq[b], pv[tt & 1][b]);
+          }
+          if (tt > 0) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) acc[b][tt - 1] += d[b] * pv[(tt - 1) & 1][b];
+          }
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[b][TT - 1] += d[b] * pv[(TT - 1) & 1][b];
       }
     }
   }
   lds_barrier();  // every wave has left the ring before it is reused
 }
 
+template <bool SPLIT>
 __global__ __launch_bounds__(kG2Waves * kWave) void gemm_gate_up_kernel2(GemmK a) {
   constexpr int BM = kGemmBMGateUp;
   constexpr int TT = BM / 16;
@@ -658,7 +699,7 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_gate_up_kernel2(GemmK a
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) acc[b][tt] = z;
-    gemm_tile3<BM, 1>(a, s_row, lds_a, ar, nr, sr, rt, acc);
+    gemm_tile3<BM, 1, SPLIT>(a, s_row, lds_a, ar, nr, sr, rt, acc);
 
     // SwiGLU, h as fp16 hi + lo into LDS in down-operand chunk order, as in
     // gemm_gate_up_kernel (kG2Waves / 2 groups of I per workgroup)
@@ -702,6 +743,7 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_gate_up_kernel2(GemmK a
   }
 }
 
+template <bool SPLIT>
 __global__ __launch_bounds__(kG2Waves * kWave) void gemm_down_kernel2(GemmK a) {
   constexpr int BM = kGemmBMDown;
   constexpr int TT = BM / 16;
@@ -742,7 +784,7 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_down_kernel2(GemmK a) {
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) acc[b][tt] = z;
-    gemm_tile3<BM, 2>(a, s_row, lds_a, ar, nr, sr, rt, acc);
+    gemm_tile3<BM, 2, SPLIT>(a, s_row, lds_a, ar, nr, sr, rt, acc);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const int64_t t = (c.nb * kG2Waves + w) * NB + b;
@@ -773,6 +815,15 @@ static bool gemm_v1() {
 }
 
 bool gemm_uses_ring() { return !gemm_v1(); }
+
+// The ring kernels scale exact integer group sums in fp32 (one MFMA per A
+// operand and group; 10% faster than the split-scale operands at Qwen3 shape,
+// 4096 tokens: gate/up 479 -> 433 us, down 372 -> 333 us);
+// PHANTOM_MOE_GEMM_SCALE=split selects the split-scale operands.
+static bool gemm_split() {
+  const char* v = getenv("PHANTOM_MOE_GEMM_SCALE");
+  return v && strcmp(v, "split") == 0;
+}
 
 static int64_t gemm_max_items(const ExpertArgs& x, int BM, int64_t n_nb) {
   const int64_t rows = x.T * x.k + (x.has_shared ? x.T : 0);
@@ -805,8 +856,14 @@ hipError_t launch_gemm_gate_up(const ExpertArgs& x, const Workspace& ws, hipStre
                        dim3(kGemmWaves * kWave), 0, stream, g);
   } else {
     const int64_t max_items = gemm_max_items(x, kGemmBMGateUp, ceil_div(x.I, kG2Waves * 16));
-    hipLaunchKernelGGL(gemm_gate_up_kernel2, dim3(resident_grid(gemm_gate_up_kernel2, kG2Waves * kWave, max_items)),
-                       dim3(kG2Waves * kWave), 0, stream, g);
+    if (gemm_split())
+      hipLaunchKernelGGL(gemm_gate_up_kernel2<true>,
+                         dim3(resident_grid(gemm_gate_up_kernel2<true>, kG2Waves * kWave, max_items)),
+                         dim3(kG2Waves * kWave), 0, stream, g);
+    else
+      hipLaunchKernelGGL(gemm_gate_up_kernel2<false>,
+                         dim3(resident_grid(gemm_gate_up_kernel2<false>, kG2Waves * kWave, max_items)),
+                         dim3(kG2Waves * kWave), 0, stream, g);
   }
   return hipGetLastError();
 }
@@ -831,8 +888,13 @@ hipError_t launch_gemm_down(const ExpertArgs& x, const Workspace& ws, hipStream_
                        dim3(kGemmWaves * kWave), 0, stream, g);
   } else {
     const int64_t max_items = gemm_max_items(x, kGemmBMDown, ceil_div(x.H, kG2Waves * 16 * kGemmNBDown));
-    hipLaunchKernelGGL(gemm_down_kernel2, dim3(resident_grid(gemm_down_kernel2, kG2Waves * kWave, max_items)),
-                       dim3(kG2Waves * kWave), 0, stream, g);
+    if (gemm_split())
+      hipLaunchKernelGGL(gemm_down_kernel2<true>, dim3(resident_grid(gemm_down_kernel2<true>, kG2Waves * kWave, max_items)),
+                         dim3(kG2Waves * kWave), 0, stream, g);
+    else
+      hipLaunchKernelGGL(gemm_down_kernel2<false>,
+                         dim3(resident_grid(gemm_down_kernel2<false>, kG2Waves * kWave, max_items)),
+                         dim3(kG2Waves * kWave), 0, stream, g);
   }
   return hipGetLastError();
 }

@@ -379,9 +379,12 @@ GEMM_CASES = [c for c in SMALL_CASES if c.name in ("gemm_ragged_k_and_rows", "ge
 def test_gemm_pipelines_agree(dev, cfg, monkeypatch):
     """The prefill GEMM has two tile pipelines: the LDS ring (default: both
     operands copied two K quads ahead by direct-to-LDS loads, 8 waves) and the
-    register-staged one (PHANTOM_MOE_GEMM_KERNEL=v1).  Both must meet the
-    layer tolerance against the oracle, ragged K and rows and the shared
-    expert included."""
+    register-staged one (PHANTOM_MOE_GEMM_KERNEL=v1).  The ring has two exact
+    forms of the arithmetic: integer group sums scaled in fp32 (default) and
+    split-scale operands (PHANTOM_MOE_GEMM_SCALE=split).  All three must meet
+    the layer tolerance against the oracle, ragged K and rows and the shared
+    expert included, and the two ring forms, both exact up to fp32 rounding,
+    must agree to 1e-5 relative."""
     L = synth.host_layer(cfg)
     xb = synth.activations(cfg.T, cfg.H, seed=11)
     ex = dev_weights(L, dev)
@@ -390,9 +393,15 @@ def test_gemm_pipelines_agree(dev, cfg, monkeypatch):
     x = to_bf16_tensor(xb, dev)
     ry, ridx, _ = oracle.moe_forward(xb, L.router_w, L.gate, L.up, L.down, cfg.k, cfg.score_mode,
                                      L.router_bias, shared=L.shared)
-    y_ring = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b)
+    y_ring = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b).cpu().numpy()
+    monkeypatch.setenv("PHANTOM_MOE_GEMM_SCALE", "split")
+    y_split = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b).cpu().numpy()
+    monkeypatch.delenv("PHANTOM_MOE_GEMM_SCALE")
     monkeypatch.setenv("PHANTOM_MOE_GEMM_KERNEL", "v1")
     y_v1 = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b)
     monkeypatch.delenv("PHANTOM_MOE_GEMM_KERNEL")
-    check_y(y_ring.cpu().numpy(), ry, cfg.name + " LDS ring")
+    check_y(y_ring, ry, cfg.name + " LDS ring, fp32-scaled")
+    check_y(y_split, ry, cfg.name + " LDS ring, split-scale")
     check_y(y_v1.cpu().numpy(), ry, cfg.name + " register-staged")
+    rel = np.linalg.norm(y_ring.astype(np.float64) - y_split) / np.linalg.norm(y_split.astype(np.float64))
+    assert rel <= 1e-5, f"{cfg.name}: ring forms differ by {rel:.2e} relative"
