@@ -366,13 +366,19 @@ __device__ __attribute__((always_inline)) inline void wchunk_math(const WChunk& 
   unpack_scales(c.us, du);
   const uint32_t gwv[4] = {c.gw.x, c.gw.y, c.gw.z, c.gw.w};
   const uint32_t uwv[4] = {c.uw.x, c.uw.y, c.uw.z, c.uw.w};
+  // all eight MFMAs first, then their scaling: an FMA right behind the MFMA
+  // whose result it reads would stall the wave for the MFMA's latency
+  f32x4 pg[4], pu[4];
 #pragma unroll
   for (int gi = 0; gi < 4; ++gi) {
     const u32x4 xa = s_xq[gi * kWave + lane];
-    const u32x4 bg = dequant_unit_bf16(gwv[gi], mask);
-    const u32x4 bu = dequant_unit_bf16(uwv[gi], mask);
-    ag += dg[gi] * mfma_bf16_16x16x32(xa, bg, z);
-    au += du[gi] * mfma_bf16_16x16x32(xa, bu, z);
+    pg[gi] = mfma_bf16_16x16x32(xa, dequant_unit_bf16(gwv[gi], mask), z);
+    pu[gi] = mfma_bf16_16x16x32(xa, dequant_unit_bf16(uwv[gi], mask), z);
+  }
+#pragma unroll
+  for (int gi = 0; gi < 4; ++gi) {
+    ag += dg[gi] * pg[gi];
+    au += du[gi] * pu[gi];
   }
   const float sx = s_sxq[lane];
   cg = mfma_f32_16x16x4(sx, dg[p], cg);
@@ -836,13 +842,20 @@ __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK&
     unpack_scales(c.s, dv);
     const uint32_t bwv[4] = {c.w.x, c.w.y, c.w.z, c.w.w};
     const u32x4* hq_q = s_h + cq * 512;
+    // the four hi MFMAs, then the four lo ones (each four behind the MFMA it
+    // accumulates onto), then the scaling: no instruction waits on the one
+    // just issued
+    u32x4 bb[4];
+    f32x4 pp[4];
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi) {
-      const u32x4 bb = dequant_unit_f16(bwv[gi], mask);
-      f32x4 pp = mfma_f16_16x16x32(hq_q[(gi * 2) * kWave + lane], bb, z);
-      pp = mfma_f16_16x16x32(hq_q[(gi * 2 + 1) * kWave + lane], bb, pp);
-      acc += dv[gi] * pp;
+      bb[gi] = dequant_unit_f16(bwv[gi], mask);
+      pp[gi] = mfma_f16_16x16x32(hq_q[(gi * 2) * kWave + lane], bb[gi], z);
     }
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) pp[gi] = mfma_f16_16x16x32(hq_q[(gi * 2 + 1) * kWave + lane], bb[gi], pp[gi]);
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) acc += dv[gi] * pp[gi];
     // padded groups' sums (not copied for them) count as zero
     const float sp = 4 * cq + (uint32_t)p < (uint32_t)Kg ? s_hs[(cq * 2) * kWave + lane] + s_hs[(cq * 2 + 1) * kWave + lane] : 0.0f;
     corr = mfma_f32_16x16x4(sp, dv[p], corr);
