@@ -527,10 +527,17 @@ __device__ inline int count_active(const SegSrc& seg, int* s_nact) {
 // SPLIT: the split-scale operands (2 MFMAs per group and position tile for
 // gate/up, 3 for down); else one MFMA per A operand against the integers
 // n - 8 (exact group sums), scaled into the accumulators with fp32 FMAs.
-template <int BM, int AW, bool SPLIT>
+// VT: the leading 16-position tiles of the block that are multiplied (the
+// caller rounds the tiles holding a segment position up to 2, 4 or 8); the
+// rest lie past the segment end, so their MFMAs, A reads and scaling are
+// skipped, and their accumulators stay zero and are never stored.  A
+// compile-time count keeps the loop branch-free: a run-time test per tile
+// broke the software pipelining and cost 30%.
+template <int BM, int AW, bool SPLIT, int VT>
 __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* lds, const i32x4& ar,
                                   const i32x4 (&nr)[kG2NB], const i32x4 (&sr)[kG2NB], const int64_t (&rt)[kG2NB],
                                   f32x4 acc[kG2NB][BM / 16]) {
+  static_assert(VT >= 1 && VT <= BM / 16, "tiles to multiply");
   constexpr int NB = kG2NB;
   constexpr int TT = BM / 16;
   constexpr int UPR = 16 * AW;                // 16-byte units per A row
@@ -601,7 +608,7 @@ __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* l
           dequant_split_f16(bw[b][gi], (gi % 2) ? (s2 >> 16) : (s2 & 0xffffu), mask, bh[b], bl[b]);
         }
 #pragma unroll
-        for (int tt = 0; tt < TT; ++tt) {
+        for (int tt = 0; tt < VT; ++tt) {
           const u32x4* row = la + (tt * 16 + n) * UPR;
           const int unit = (p * 4 + gi) * AW;
           const u32x4 ah = row[unit ^ n];
@@ -631,7 +638,7 @@ __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* l
         // execute instead of stalling on the result it reads.
         f32x4 pv[2][NB];
 #pragma unroll
-        for (int tt = 0; tt < TT; ++tt) {
+        for (int tt = 0; tt < VT; ++tt) {
           const u32x4* row = la + (tt * 16 + n) * UPR;
           const int unit = (p * 4 + gi) * AW;
           const u32x4 ah = row[unit ^ n];
@@ -650,7 +657,7 @@ __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* l
           }
         }
 #pragma unroll
-        for (int b = 0; b < NB; ++b) acc[b][TT - 1] += d[b] * pv[(TT - 1) & 1][b];
+        for (int b = 0; b < NB; ++b) acc[b][VT - 1] += d[b] * pv[(VT - 1) & 1][b];
       }
     }
   }
@@ -699,7 +706,10 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_gate_up_kernel2(GemmK a
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) acc[b][tt] = z;
-    gemm_tile3<BM, 1, SPLIT>(a, s_row, lds_a, ar, nr, sr, rt, acc);
+    const int vt = __builtin_amdgcn_readfirstlane((int)ceil_div(c.end - c.m0, (int64_t)16));
+    if (vt > 4) gemm_tile3<BM, 1, SPLIT, 8>(a, s_row, lds_a, ar, nr, sr, rt, acc);
+    else if (vt > 2) gemm_tile3<BM, 1, SPLIT, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc);
+    else gemm_tile3<BM, 1, SPLIT, 2>(a, s_row, lds_a, ar, nr, sr, rt, acc);
 
     // SwiGLU, h as fp16 hi + lo into LDS in down-operand chunk order, as in
     // gemm_gate_up_kernel (kG2Waves / 2 groups of I per workgroup)
@@ -784,7 +794,9 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_down_kernel2(GemmK a) {
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) acc[b][tt] = z;
-    gemm_tile3<BM, 2, SPLIT>(a, s_row, lds_a, ar, nr, sr, rt, acc);
+    const int vt = __builtin_amdgcn_readfirstlane((int)ceil_div(c.end - c.m0, (int64_t)16));
+    if (vt > 2) gemm_tile3<BM, 2, SPLIT, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc);
+    else gemm_tile3<BM, 2, SPLIT, 2>(a, s_row, lds_a, ar, nr, sr, rt, acc);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const int64_t t = (c.nb * kG2Waves + w) * NB + b;
