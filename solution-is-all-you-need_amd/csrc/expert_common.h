@@ -27,15 +27,30 @@ __device__ inline void unpack_scales(uint2 s, float d[4]) {
   d[3] = half_bits_to_float((uint16_t)(s.y >> 16));
 }
 
-// Copies the launch slots' segment descriptors into LDS; returns how many
-// slots are in use (they come first; unused slots carry expert -1).
-__device__ inline int load_descriptors(const SegSrc& seg, int4* s_desc, int* s_nact) {
-  if (threadIdx.x == 0) *s_nact = 0;
-  __syncthreads();
-  for (int u = threadIdx.x; u < seg.max_slots; u += blockDim.x) {
-    const int4 d = seg.desc[u];
-    s_desc[u] = d;
-    if (d.x >= 0 && (u + 1 == seg.max_slots || seg.desc[u + 1].x < 0)) *s_nact = u + 1;
+// Copies the launch slots' segment descriptors into LDS, and with s_tok the
+// token of each of the first n_tok segment positions too; returns how many
+// slots are in use (they come first; unused slots carry expert -1; at least
+// one is in use, so exactly one thread finds the boundary and writes the
+// count).  All loads of an iteration are issued before its stores, so the
+// copies cost one memory round trip and one barrier.
+__device__ inline int load_descriptors(const SegSrc& seg, int4* s_desc, int* s_nact, int* s_tok = nullptr,
+                                       int64_t n_tok = 0) {
+  const int64_t n = (s_tok && n_tok > seg.max_slots) ? n_tok : seg.max_slots;
+  for (int64_t u = threadIdx.x; u < n; u += blockDim.x) {
+    const bool ds = u < seg.max_slots;
+    const bool ts = s_tok && u < n_tok;
+    int4 d = make_int4(-1, 0, 0, 0);
+    int nx = -1, tk = 0;
+    if (ds) {
+      d = seg.desc[u];
+      if (u + 1 < seg.max_slots) nx = seg.desc[u + 1].x;
+    }
+    if (ts) tk = seg.seg_tok[u];
+    if (ds) {
+      s_desc[u] = d;
+      if (d.x >= 0 && nx < 0) *s_nact = (int)u + 1;
+    }
+    if (ts) s_tok[u] = tk;
   }
   __syncthreads();
   return *s_nact;

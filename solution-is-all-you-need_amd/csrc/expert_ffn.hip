@@ -257,15 +257,13 @@ __global__ __launch_bounds__(kGateUpWaves * kWave, 4) void gate_up_kernel(GateUp
   const int ksplit = blockDim.x / kWave;
   const int n = lane % 16;
   const int p = lane / 16;
-  if constexpr (TOK_LDS) {
-    for (int64_t i = threadIdx.x; i < a.zero_row; i += blockDim.x) s_tok[i] = a.seg.seg_tok[i];
-  }
   if (blockIdx.x == 0) {
     // the all-zero down-operand row read for positions past a segment
     for (int64_t i = threadIdx.x; i < a.KqI * 256; i += blockDim.x) a.hq[a.zero_row * a.KqI * 256 + i] = 0;
     for (int64_t i = threadIdx.x; i < a.KqI * 8; i += blockDim.x) a.hs[a.zero_row * a.KqI * 8 + i] = 0.0f;
   }
-  const int n_act = load_descriptors(a.seg, s_desc, &s_nact);
+  // descriptors and (when they fit) the positions' tokens, in one round trip
+  const int n_act = load_descriptors(a.seg, s_desc, &s_nact, TOK_LDS ? s_tok : nullptr, TOK_LDS ? a.zero_row : 0);
   const int64_t n_blk = a.I / (kRowTile * RT);  // RT-tile blocks of I per expert
   const int64_t n_items = (int64_t)n_act * n_blk;
   int64_t item = blockIdx.x;
