@@ -416,14 +416,23 @@ def main():
                 pmc = json.load(f)
             if pmc.get("workload") == cfg.name and pmc.get("kernel") == gu_kernel:
                 traffic = pmc.get("hbm_bytes_per_launch")
-        if cfg.T >= PREFILL_T and not fused:
-            tf = gate_up_flops(cfg) * args.steps / (gu_ms * 1e-3) / 1e12
+        # a prefill launch is priced against the MFMA roofline when its arithmetic
+        # intensity (flops per algorithmic byte) is above the ridge point, else
+        # against HBM (DeepSeek-V3 at 2048 tokens: about 64 positions per
+        # expert, 227 flop/B, below the 312 of bf16 peak / HBM peak)
+        ridge = BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+        intensity = gate_up_flops(cfg) * args.steps / gu_bytes
+        tf = gate_up_flops(cfg) * args.steps / (gu_ms * 1e-3) / 1e12
+        if cfg.T >= PREFILL_T and not fused and intensity >= ridge:
             out["roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
                                "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
                                "algorithmic_flops_per_launch": gate_up_flops(cfg)}
         else:
             out["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
+        if cfg.T >= PREFILL_T and not fused:
+            out["roofline"].update({"intensity_flop_per_byte": round(intensity, 1), "ridge_flop_per_byte": round(ridge, 1),
+                                    "achieved_tflops": round(tf, 2), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)})
         out["roofline"].update({
             "kernel": gu_kernel,
             "down_kernel": names["down"],
