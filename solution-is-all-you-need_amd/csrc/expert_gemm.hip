@@ -637,13 +637,20 @@ __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* l
         // tt - 1 is issued after the MFMAs of tile tt, so it runs while they
         // execute instead of stalling on the result it reads.
         f32x4 pv[2][NB];
+        // the group's A operands, all read from LDS before its first MFMA
+        u32x4 ahv[VT], alv[VT];
 #pragma unroll
         for (int tt = 0; tt < VT; ++tt) {
           const u32x4* row = la + (tt * 16 + n) * UPR;
           const int unit = (p * 4 + gi) * AW;
-          const u32x4 ah = row[unit ^ n];
-          u32x4 al = ah;
-          if constexpr (AW == 2) al = row[(unit + 1) ^ n];
+          ahv[tt] = row[unit ^ n];
+          alv[tt] = ahv[tt];
+          if constexpr (AW == 2) alv[tt] = row[(unit + 1) ^ n];
+        }
+#pragma unroll
+        for (int tt = 0; tt < VT; ++tt) {
+          const u32x4 ah = ahv[tt];
+          const u32x4 al = alv[tt];
           // the lo MFMAs follow all the hi ones, so no MFMA waits on the one before it
 #pragma unroll
           for (int b = 0; b < NB; ++b) pv[tt & 1][b] = mfma_f16_16x16x32(ah, bq[b], z);
