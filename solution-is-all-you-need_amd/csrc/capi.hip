@@ -111,6 +111,8 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
   const size_t o_hs = take(sizeof(float) * (size_t)((rows + 1) * (KpadI / kGroup) * 2));
   const size_t o_out = take(sizeof(float) * (size_t)(rows * (I > 0 ? H : 0)));
   const size_t o_cnt = take(sizeof(int32_t));
+  const size_t o_pcnt = take(sizeof(int32_t) * (size_t)E * (size_t)perm_blocks(T * k));
+  const size_t o_ptb = take(sizeof(int32_t) * (size_t)E);
   if (ws && base) {
     char* b = static_cast<char*>(base);
     ws->logits = reinterpret_cast<double*>(b + o_log);
@@ -130,6 +132,8 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
     ws->hs = reinterpret_cast<float*>(b + o_hs);
     ws->outbuf = reinterpret_cast<float*>(b + o_out);
     ws->counter = reinterpret_cast<int32_t*>(b + o_cnt);
+    ws->perm_cnt = reinterpret_cast<int32_t*>(b + o_pcnt);
+    ws->perm_tb = reinterpret_cast<int32_t*>(b + o_ptb);
   }
   return off;
 }

@@ -45,7 +45,16 @@ struct Workspace {
   float* hs = nullptr;             // [rows, Kpad_I / 32, 2] half-group sums of h
   float* outbuf = nullptr;          // [T*k + T*shared, H] expert outputs, segment order
   int32_t* counter = nullptr;       // [1] router hand-off counter (reset by every route launch)
+  int32_t* perm_cnt = nullptr;      // [E][perm_blocks(T * k)] per-chunk expert counts, then bases (large batches)
+  int32_t* perm_tb = nullptr;       // [E] first token tile of each expert (large batches)
 };
+
+// Batches of at least this many slots use the many-workgroup permute.
+constexpr int64_t kPermMultiSlots = 8192;
+inline int64_t perm_blocks(int64_t n) {
+  const int64_t b = (n + 1023) / 1024;
+  return b < 4096 ? (b < 1 ? 1 : b) : 4096;
+}
 
 // The thread-local message behind phantom_moe_last_error(): set_error
 // formats it and returns `code`; clear_error empties it.

@@ -192,21 +192,38 @@ __device__ __attribute__((always_inline)) inline void block_permute(const int32_
     cached[i] = sl < end ? v : -1;
   }
 
-  // Pass 1: per-wave counts.
-  for (int64_t r0 = beg, i = 0; r0 < end; r0 += kWave, ++i) {
-    int e;
-    if (i < kCached) {
-      e = cached[0];
+  // Expert ids of rounds past the cached ones are loaded kBatch rounds at a
+  // time (from clamped indices, all issued before any is used), so a long
+  // chunk costs one memory round trip per kBatch rounds instead of one per
+  // round; the rounds are still processed in order.
+  constexpr int kBatch = 8;
+  auto load_batch = [&](int64_t r0, int (&ev)[kBatch]) {
 #pragma unroll
-      for (int j = 1; j < kCached; ++j) e = (i == j) ? cached[j] : e;
-    } else {
-      const int64_t sl = r0 + lane;
-      const int v = idx[sl < end ? sl : end - 1];
-      e = sl < end ? v : -1;
+    for (int j = 0; j < kBatch; ++j) {
+      const int64_t sl = r0 + (int64_t)j * kWave + lane;
+      const int v = idx[sl < end ? sl : (end > 0 ? end - 1 : 0)];
+      ev[j] = sl < end ? v : -1;
     }
+  };
+
+  // Pass 1: per-wave counts.
+  auto count_round = [&](int e) {
     const bool valid = (e >= 0 && e < E);
     const uint64_t m = match_expert(e, valid, nbits);
     if (valid && (m & lt_mask) == 0) s_cnt[w][e] += __popcll(m);
+  };
+  {
+    int64_t r0 = beg;
+#pragma unroll
+    for (int i = 0; i < kCached; ++i, r0 += kWave)
+      if (r0 < end) count_round(cached[i]);
+    for (; r0 < end; r0 += (int64_t)kBatch * kWave) {
+      int ev[kBatch];
+      load_batch(r0, ev);
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+        if (r0 + (int64_t)j * kWave < end) count_round(ev[j]);
+    }
   }
   lds_barrier();
 
@@ -302,17 +319,8 @@ __device__ __attribute__((always_inline)) inline void block_permute(const int32_
   lds_barrier();
 
   // Pass 2: placement.
-  for (int64_t r0 = beg, i = 0; r0 < end; r0 += kWave, ++i) {
+  auto place_round = [&](int64_t r0, int e) {
     const int64_t sl = r0 + lane;
-    int e;
-    if (i < kCached) {
-      e = cached[0];
-#pragma unroll
-      for (int j = 1; j < kCached; ++j) e = (i == j) ? cached[j] : e;
-    } else {
-      const int v = idx[sl < end ? sl : end - 1];
-      e = sl < end ? v : -1;
-    }
     const bool valid = (e >= 0 && e < E);
     const uint64_t m = match_expert(e, valid, nbits);
     if (valid) {
@@ -331,6 +339,19 @@ __device__ __attribute__((always_inline)) inline void block_permute(const int32_
       if (below == 0) s_cnt[w][e] = s_cnt[w][e] + __popcll(m);
     } else if (sl < end) {
       slot_pos[sl] = -1;
+    }
+  };
+  {
+    int64_t r0 = beg;
+#pragma unroll
+    for (int i = 0; i < kCached; ++i, r0 += kWave)
+      if (r0 < end) place_round(r0, cached[i]);
+    for (; r0 < end; r0 += (int64_t)kBatch * kWave) {
+      int ev[kBatch];
+      load_batch(r0, ev);
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+        if (r0 + (int64_t)j * kWave < end) place_round(r0 + (int64_t)j * kWave, ev[j]);
     }
   }
 }
@@ -810,6 +831,234 @@ __global__ __launch_bounds__(256) void route_logits_big_kernel(RouteK a) {
   }
 }
 
+// ------------------------------------------------- permute, many workgroups
+//
+// For large batches the one-workgroup permute is bound by one CU's issue
+// rate (65 us for 32768 slots).  The same stable counting sort then runs as
+// three launches:
+//   permute_count_kernel: workgroup b counts, per expert, the slots of its
+//     contiguous chunk into cnt[e][b];
+//   permute_scan_kernel (one workgroup): expert totals, the offsets, active
+//     list, descriptors, token-tile headers and shared segment exactly as the
+//     one-workgroup permute writes them, and cnt[e][b] replaced by the
+//     position where chunk b's first slot of expert e goes;
+//   permute_place_kernel: workgroup b re-counts its chunk per wave and places
+//     every slot at its chunk base + the counts of earlier waves + its rank
+//     within the round.
+// Chunks, waves, rounds and lanes follow slot order, so every expert's slots
+// land in increasing slot order: the same permutation as block_permute.
+// (from kPermMultiSlots slots on; chunks of about 1024 slots, perm_blocks)
+constexpr int kPermWaves = 4;
+
+// The slots [lo, hi) of this wave, counted per expert into cnt_w (LDS), or
+// (place) placed at cnt_w[e] + rank, cnt_w then advancing.  Expert ids are
+// loaded kPermBatch rounds at a time and the rounds processed in order.
+template <bool PLACE>
+__device__ __attribute__((always_inline)) inline void perm_wave_rounds(
+    const int32_t* __restrict__ idx, int64_t lo, int64_t hi, int k, int E, int nbits, int* cnt_w,
+    int32_t* sorted_slots, int32_t* slot_pos, int32_t* seg_tok, int32_t* tiles, const int* s_beg, const int* s_tb) {
+  constexpr int kPermBatch = 8;
+  const int lane = threadIdx.x % kWave;
+  const uint64_t lt_mask = (1ull << lane) - 1ull;
+  for (int64_t r0 = lo; r0 < hi; r0 += (int64_t)kPermBatch * kWave) {
+    int ev[kPermBatch];
+#pragma unroll
+    for (int j = 0; j < kPermBatch; ++j) {
+      const int64_t sl = r0 + (int64_t)j * kWave + lane;
+      const int v = idx[sl < hi ? sl : hi - 1];
+      ev[j] = sl < hi ? v : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kPermBatch; ++j) {
+      if (r0 + (int64_t)j * kWave >= hi) break;  // uniform
+      const int64_t sl = r0 + (int64_t)j * kWave + lane;
+      const int e = ev[j];
+      const bool valid = (e >= 0 && e < E);
+      const uint64_t m = match_expert(e, valid, nbits);
+      const uint64_t below = m & lt_mask;
+      if constexpr (PLACE) {
+        if (valid) {
+          const int pos = cnt_w[e] + __popcll(below);
+          sorted_slots[pos] = (int32_t)sl;
+          slot_pos[sl] = pos;
+          if (seg_tok) seg_tok[pos] = (int32_t)(sl / k);
+          if (tiles) {
+            const int rel = pos - s_beg[e];
+            tiles[(int64_t)(s_tb[e] + rel / 16) * kTileWords + 4 + rel % 16] = (int32_t)(sl / k);
+          }
+          // every lane of the group read the base before the leader bumps it
+          if (below == 0) cnt_w[e] = cnt_w[e] + __popcll(m);
+        } else if (sl < hi) {
+          slot_pos[sl] = -1;
+        }
+      } else {
+        if (valid && below == 0) cnt_w[e] += __popcll(m);
+      }
+    }
+  }
+}
+
+__device__ inline int perm_nbits(int E) {
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  return nbits;
+}
+
+__global__ __launch_bounds__(kPermWaves * kWave) void permute_count_kernel(const int32_t* idx, int64_t n, int E,
+                                                                           int64_t chunk, int32_t* cnt) {
+  __shared__ int s_cnt[kPermWaves][kMaxExperts];
+  const int w = threadIdx.x / kWave;
+  const int nb = gridDim.x;
+  for (int i = threadIdx.x; i < kPermWaves * kMaxExperts; i += blockDim.x) s_cnt[i / kMaxExperts][i % kMaxExperts] = 0;
+  lds_barrier();
+  const int64_t lo = (int64_t)blockIdx.x * chunk;
+  const int64_t hi = lo + chunk < n ? lo + chunk : n;
+  const int64_t wc = round_up(ceil_div(hi > lo ? hi - lo : 0, kPermWaves), kWave);
+  const int64_t wlo = lo + w * wc;
+  const int64_t whi = wlo + wc < hi ? wlo + wc : hi;
+  perm_wave_rounds<false>(idx, wlo, whi, 0, E, perm_nbits(E), s_cnt[w], nullptr, nullptr, nullptr, nullptr, nullptr,
+                          nullptr);
+  lds_barrier();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int t = 0;
+#pragma unroll
+    for (int ww = 0; ww < kPermWaves; ++ww) t += s_cnt[ww][e];
+    cnt[(int64_t)e * nb + blockIdx.x] = t;
+  }
+}
+
+// One workgroup of 1024 threads; thread e < E owns expert e.
+__global__ __launch_bounds__(1024) void permute_scan_kernel(int64_t n, int64_t T, int E, int nb, int has_shared,
+                                                            int32_t* cnt, int32_t* tb_out, int32_t* offsets,
+                                                            int32_t* offsets_user, int32_t* active, int32_t* n_active,
+                                                            int4* desc, int32_t* seg_tok, int32_t* tiles,
+                                                            int32_t* n_tiles, int32_t* tile_done) {
+  __shared__ int s_tmp[3 * 16];
+  const int e = threadIdx.x;
+  int tot = 0;
+  if (e < E) {
+    const int32_t* c = cnt + (int64_t)e * nb;
+    for (int b = 0; b < nb; ++b) tot += c[b];
+  }
+  const int act = tot > 0 ? 1 : 0;
+  const int ntl = (tot + 15) / 16;
+  int3 tot3;
+  const int3 ex = block_exclusive_scan3(make_int3(tot, act, ntl), s_tmp, &tot3);
+  const int total = tot3.x, total_act = tot3.y, total_tiles = tot3.z;
+  if (e < E) {
+    const int run = ex.x;
+    offsets[e] = run;
+    if (offsets_user) offsets_user[e] = run;
+    if (act) {
+      active[ex.y] = e;
+      if (desc) desc[ex.y] = make_int4(e, run, run + tot, 0);
+    }
+    if (tb_out) tb_out[e] = ex.z;
+    if (tiles) {
+      for (int j = 0; j < ntl; ++j) {
+        *reinterpret_cast<int4*>(tiles + (int64_t)(ex.z + j) * kTileWords) = make_int4(e, run + 16 * j, run + tot, 0);
+        if (tile_done) tile_done[(int64_t)(ex.z + j) * kCtlStride] = 0;
+      }
+    }
+    // chunk bases of expert e, in chunk order
+    int32_t* c = cnt + (int64_t)e * nb;
+    int b0 = run;
+    for (int b = 0; b < nb; ++b) {
+      const int v = c[b];
+      c[b] = b0;
+      b0 += v;
+    }
+  }
+  if (threadIdx.x == 0) {
+    offsets[E] = total;
+    if (offsets_user) offsets_user[E] = total;
+    offsets[E + 1] = total + (has_shared ? (int)T : 0);
+    if (has_shared) {
+      active[total_act] = E;
+      if (desc) desc[total_act] = make_int4(E, total, total + (int)T, 0);
+    }
+    *n_active = total_act + (has_shared ? 1 : 0);
+  }
+  if (has_shared && seg_tok) {
+    for (int64_t t = threadIdx.x; t < T; t += blockDim.x) seg_tok[n + t] = (int32_t)t;
+  }
+  if (tiles) {
+    const int64_t n_sh = has_shared ? (T + 15) / 16 : 0;
+    for (int64_t j = threadIdx.x; j < n_sh; j += blockDim.x) {
+      int32_t* tw = tiles + (total_tiles + j) * kTileWords;
+      *reinterpret_cast<int4*>(tw) = make_int4(E, total + (int)(16 * j), total + (int)T, 0);
+      if (tile_done) tile_done[(total_tiles + j) * kCtlStride] = 0;
+      for (int jj = 0; jj < 16 && 16 * j + jj < T; ++jj) tw[4 + jj] = (int32_t)(16 * j + jj);
+    }
+    if (threadIdx.x == 0) {
+      n_tiles[0] = total_tiles + (int)n_sh;
+      n_tiles[kCtlStride] = 0;
+      n_tiles[2 * kCtlStride] = 0;
+    }
+  }
+  if (desc) {
+    const int n_act = total_act + (has_shared ? 1 : 0);
+    const int max_active = (int)((n < E) ? n : E) + (has_shared ? 1 : 0);
+    for (int u = n_act + threadIdx.x; u < max_active; u += blockDim.x) desc[u] = make_int4(-1, 0, 0, 0);
+  }
+}
+
+__global__ __launch_bounds__(kPermWaves * kWave) void permute_place_kernel(const int32_t* idx, int64_t n, int k, int E,
+                                                                           int64_t chunk, const int32_t* cnt,
+                                                                           const int32_t* offsets, const int32_t* tb,
+                                                                           int32_t* sorted_slots, int32_t* slot_pos,
+                                                                           int32_t* seg_tok, int32_t* tiles) {
+  __shared__ int s_cnt[kPermWaves][kMaxExperts];
+  __shared__ int s_beg[kMaxExperts];
+  __shared__ int s_tb[kMaxExperts];
+  const int w = threadIdx.x / kWave;
+  const int nb = gridDim.x;
+  const int nbits = perm_nbits(E);
+  for (int i = threadIdx.x; i < kPermWaves * kMaxExperts; i += blockDim.x) s_cnt[i / kMaxExperts][i % kMaxExperts] = 0;
+  lds_barrier();
+  const int64_t lo = (int64_t)blockIdx.x * chunk;
+  const int64_t hi = lo + chunk < n ? lo + chunk : n;
+  const int64_t wc = round_up(ceil_div(hi > lo ? hi - lo : 0, kPermWaves), kWave);
+  const int64_t wlo = lo + w * wc;
+  const int64_t whi = wlo + wc < hi ? wlo + wc : hi;
+  perm_wave_rounds<false>(idx, wlo, whi, 0, E, nbits, s_cnt[w], nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
+  lds_barrier();
+  // per-wave bases: the chunk's base plus the counts of earlier waves
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int b = cnt[(int64_t)e * nb + blockIdx.x];
+#pragma unroll
+    for (int ww = 0; ww < kPermWaves; ++ww) {
+      const int c = s_cnt[ww][e];
+      s_cnt[ww][e] = b;
+      b += c;
+    }
+    if (tiles) {
+      s_beg[e] = offsets[e];
+      s_tb[e] = tb[e];
+    }
+  }
+  lds_barrier();
+  perm_wave_rounds<true>(idx, wlo, whi, k, E, nbits, s_cnt[w], sorted_slots, slot_pos, seg_tok, tiles, s_beg, s_tb);
+}
+
+// The three launches; cnt needs E * perm_blocks(T * k) ints, tb E ints.
+static hipError_t launch_permute_multi(const int32_t* idx, int64_t T, int k, int E, int has_shared,
+                                       int32_t* offsets, int32_t* offsets_user, int32_t* active, int32_t* n_active,
+                                       int32_t* sorted_slots, int32_t* slot_pos, int4* desc, int32_t* seg_tok,
+                                       int32_t* tiles, int32_t* n_tiles, int32_t* tile_done, int32_t* cnt,
+                                       int32_t* tb, hipStream_t stream) {
+  const int64_t n = T * k;
+  const int64_t nb = perm_blocks(n);
+  const int64_t chunk = ceil_div(n, nb);
+  hipLaunchKernelGGL(permute_count_kernel, dim3((unsigned)nb), dim3(kPermWaves * kWave), 0, stream, idx, n, E, chunk,
+                     cnt);
+  hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(1024), 0, stream, n, T, E, (int)nb, has_shared, cnt, tb,
+                     offsets, offsets_user, active, n_active, desc, seg_tok, tiles, n_tiles, tile_done);
+  hipLaunchKernelGGL(permute_place_kernel, dim3((unsigned)nb), dim3(kPermWaves * kWave), 0, stream, idx, n, k, E,
+                     chunk, cnt, offsets, tb, sorted_slots, slot_pos, seg_tok, tiles);
+  return hipGetLastError();
+}
+
 int router_token_tile(int64_t T) {
   if (T <= 1) return 1;
   if (T <= 64) return 4;
@@ -882,6 +1131,10 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
   else hipLaunchKernelGGL(route_select_kernel<8>, dim3(sel_blocks), sb, 0, stream, k);
   err = hipGetLastError();
   if (err != hipSuccess || !r.do_permute || sel_blocks == 1 || k.fuse_permute) return err;
+  if (r.T * r.k >= kPermMultiSlots)
+    return launch_permute_multi(k.topk_idx, r.T, r.k, r.E, r.has_shared, ws.offsets, r.offsets_out, ws.active,
+                                ws.n_active, k.sorted_slots, k.slot_pos, k.desc, k.seg_tok, k.tiles, k.n_tiles,
+                                k.tile_done, ws.perm_cnt, ws.perm_tb, stream);
   hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, k.topk_idx, r.T, r.k,
               r.E, r.has_shared, ws.offsets, r.offsets_out, ws.active, ws.n_active, k.sorted_slots, k.slot_pos,
               k.desc, k.seg_tok, k.tiles, k.n_tiles, k.tile_done);
@@ -891,6 +1144,10 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
 hipError_t launch_permute(const int32_t* topk_idx, int64_t T, int k, int E, int has_shared,
                           int32_t* offsets, int32_t* sorted_slots, int32_t* slot_pos,
                           const Workspace& ws, hipStream_t stream) {
+  if (T * k >= kPermMultiSlots)
+    return launch_permute_multi(topk_idx, T, k, E, has_shared, ws.offsets, offsets, ws.active, ws.n_active,
+                                sorted_slots, slot_pos, nullptr, nullptr, nullptr, nullptr, nullptr, ws.perm_cnt,
+                                ws.perm_tb, stream);
   hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, topk_idx, T, k, E, has_shared,
                      ws.offsets, offsets, ws.active, ws.n_active, sorted_slots, slot_pos,
                      static_cast<int4*>(nullptr), static_cast<int32_t*>(nullptr), static_cast<int32_t*>(nullptr),

@@ -205,6 +205,9 @@ SMALL_CASES = [
     synth.MoEConfig("sigmoid_shared", 512, 128, 32, 4, 12, score="sigmoid", shared=True),
     synth.MoEConfig("zipf", 1024, 256, 128, 8, 32, zipf=1.1),
     synth.MoEConfig("k1", 128, 32, 4, 1, 3),
+    # 8800 slots: the many-workgroup permute, feeding the token-tile table and
+    # the shared expert (decode regime: 17 positions per expert on average)
+    synth.MoEConfig("many_slots_tiles", 256, 256, 512, 8, 1100, shared=True),
     # GEMM regime (T*k >= 64 * min(E, T*k)): fp16 operands, 128-position tiles
     synth.MoEConfig("gemm_e4", 256, 128, 4, 2, 200),
     synth.MoEConfig("gemm_multi_block", 256, 256, 2, 2, 300),
