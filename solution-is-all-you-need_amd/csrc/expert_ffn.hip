@@ -1286,9 +1286,12 @@ hipError_t launch_down(const ExpertArgs& x, const Workspace& ws, hipStream_t str
   int rt = 2;  // H is a multiple of 32: an even number of 16-row tiles
   // Two quads of loads in flight per wave pay off only when items are few
   // (one token: 7.7 vs 8.4 us at Qwen3 shape, 28.6 vs 29.8 at H 7168, I 2048);
-  // with many items the occupancy NQ = 1 allows wins (158 vs 162 us at 8 tokens).
+  // with many items the occupancy NQ = 1 allows wins (158 vs 162 us at 8 tokens),
+  // and from 8192 items on two waves per item beat four (H 7168, I 2048: 150
+  // vs 161 us at 8 tokens, 572 vs 609 us at 64; with few items they lose).
   const int64_t items = (int64_t)max_active_experts(x) * (x.H / (kRowTile * rt));
   sp.nq = items <= 4096 ? 2 : 1;
+  if (items >= 8192) sp.ksplit = sp.ksplit < 2 ? sp.ksplit : 2;
   tiling_override("PHANTOM_MOE_DOWN_TILING", kDownWaves, &sp.ksplit, &rt, &sp.nq);
   if (rt == 4 && (x.H / kRowTile) % 4) rt = 2;
   const int block = kWave * sp.ksplit;
