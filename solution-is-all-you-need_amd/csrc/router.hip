@@ -21,9 +21,11 @@
 // descent over the 64-bit order keys finds the k-th largest key, the k
 // winners are ranked among themselves, then the weights.  For up to
 // kFusedSelectBlocks select workgroups (decode) the last workgroup to finish
-// runs the permute; beyond that permute_kernel does.  The hand-off costs one
-// agent-scope release per select workgroup (an L2 write-back on a multi-XCD
-// part), which is why it is reserved for small grids.
+// runs the permute; beyond that permute_kernel does (one workgroup), and from
+// kPermMultiSlots slots on three many-workgroup launches do (count, scan,
+// place).  The hand-off costs one agent-scope release per select workgroup
+// (an L2 write-back on a multi-XCD part), which is why it is reserved for
+// small grids.
 // Permute: per-wave expert counts, an (expert, wave)-major exclusive scan, and
 // a second pass that places every slot at base + rank-within-round, where the
 // rank comes from ballots over the bits of the expert id.  Placement depends
