@@ -441,23 +441,23 @@ struct TileJobs {
   uint32_t M, per_job, jpt, n_jobs;
 };
 
-__device__ inline TileJobs tile_jobs(uint32_t n_tiles, uint32_t n_rt, uint32_t slots) {
+__device__ inline TileJobs tile_jobs(uint32_t n_tiles, uint32_t n_rt, uint32_t slots, uint32_t nw = kTileWaves) {
   TileJobs j;
-  const uint32_t M = (n_tiles * n_rt + kTileWaves * slots - 1) / (kTileWaves * slots);
+  const uint32_t M = (n_tiles * n_rt + nw * slots - 1) / (nw * slots);
   j.M = M < 1 ? 1 : M;
-  j.per_job = kTileWaves * j.M;
+  j.per_job = nw * j.M;
   j.jpt = (n_rt + j.per_job - 1) / j.per_job;
   j.n_jobs = n_tiles * j.jpt;
   return j;
 }
 
-// One gate/up job: token tile gt, row tiles part * per_job + w + kTileWaves * i
+// One gate/up job: token tile gt, row tiles part * per_job + w + NW * i
 // (i < M) for wave w.  Ends with the waves' last stores issued and LDS still
 // in use; the caller synchronises before the next job.
 // With a ticket counter, thread 0 draws the next ticket into nxt once the
 // tile header has arrived (a draw issued before it would hold up the
 // header's wait).  H_AUX is the cache policy of the h stores.
-template <int D, int H_AUX>
+template <int D, int H_AUX, int NW = kTileWaves>
 __device__ __attribute__((always_inline)) inline void gate_up_tile_job(const GateUpK& a, u32x4* s_x, float* s_sx, uint32_t gt,
                                                                        uint32_t part, const TileJobs& jb, int32_t* ticket,
                                                                        uint32_t& nxt) {
@@ -490,9 +490,9 @@ __device__ __attribute__((always_inline)) inline void gate_up_tile_job(const Gat
                           : reinterpret_cast<const uint8_t*>(a.sh_gate_sc), sc_bytes);
   ws.us = buf_rsrc(routed ? reinterpret_cast<const uint8_t*>(a.up_sc) + (int64_t)e * sc_bytes
                           : reinterpret_cast<const uint8_t*>(a.sh_up_sc), sc_bytes);
-  // this wave's row tiles: rt0 + kTileWaves * i, i < n_mine
+  // this wave's row tiles: rt0 + NW * i, i < n_mine
   const uint32_t rt0 = part * jb.per_job + w;
-  const uint32_t left = rt0 < n_rt ? (n_rt - rt0 + kTileWaves - 1) / kTileWaves : 0;
+  const uint32_t left = rt0 < n_rt ? (n_rt - rt0 + NW - 1) / NW : 0;
   const uint32_t n_mine = left < jb.M ? left : jb.M;
   const int64_t total = (int64_t)n_mine * Kq;  // chunks of this wave in this job
 
@@ -501,9 +501,9 @@ __device__ __attribute__((always_inline)) inline void gate_up_tile_job(const Gat
     const uint32_t row = (uint32_t)tok * Kq;
     const uint32_t xv = row * 256u + (uint32_t)p * 64u;
     const uint32_t sv = row * 16u + (uint32_t)p * 4u;
-    for (uint32_t b = w; b < Kq * 4; b += kTileWaves)
+    for (uint32_t b = w; b < Kq * 4; b += NW)
       dma_b128(xr, s_x + b * kWave, xv, (b / 4) * 256u + (b % 4) * 16u);
-    for (uint32_t q = w; q < Kq; q += kTileWaves) dma_b32(xsr, s_sx + q * kWave, sv, q * 16u);
+    for (uint32_t q = w; q < Kq; q += NW) dma_b32(xsr, s_sx + q * kWave, sv, q * 16u);
   }
   asm volatile("" ::: "memory");  // the operand loads stay older than the weight loads below
 
@@ -524,7 +524,7 @@ __device__ __attribute__((always_inline)) inline void gate_up_tile_job(const Gat
   if (total > 0) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      wchunk_load(ws, (rt0 + kTileWaves * li) * Kq + lq, buf[d]);
+      wchunk_load(ws, (rt0 + NW * li) * Kq + lq, buf[d]);
       advance();
     }
     // the DMA is older than the D chunks just issued
@@ -544,11 +544,11 @@ __device__ __attribute__((always_inline)) inline void gate_up_tile_job(const Gat
   auto consume = [&](WChunk& c, bool refill) {
     wchunk_math(c, s_x + cq * 256, s_sx + cq * kWave, ag, au, cg, cu);
     if (refill) {
-      wchunk_load(ws, (rt0 + kTileWaves * li) * Kq + lq, c);
+      wchunk_load(ws, (rt0 + NW * li) * Kq + lq, c);
       advance();
     }
     if (++cq == Kq) {
-      tile_epilogue<H_AUX>(a, hqr, hsr, m0, end, rt0 + kTileWaves * ci, ag, au, cg, cu);
+      tile_epilogue<H_AUX>(a, hqr, hsr, m0, end, rt0 + NW * ci, ag, au, cg, cu);
       ag = au = cg = cu = z;
       cq = 0;
       ++ci;
@@ -565,8 +565,8 @@ __device__ __attribute__((always_inline)) inline void gate_up_tile_job(const Gat
     if (d < rem) consume(buf[d], false);
 }
 
-template <int D>
-__global__ __launch_bounds__(kTileWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void gate_up_tile_kernel(GateUpK a) {
+template <int D, int NW>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2))) void gate_up_tile_kernel(GateUpK a) {
   extern __shared__ u32x4 s_x[];
   float* s_sx = reinterpret_cast<float*>(s_x + (uint32_t)a.Kq * 256);
   if (blockIdx.x == 0) {
@@ -575,11 +575,11 @@ __global__ __launch_bounds__(kTileWaves * kWave) __attribute__((amdgpu_waves_per
     for (int64_t i = threadIdx.x; i < a.KqI * 8; i += blockDim.x) a.hs[a.zero_row * a.KqI * 8 + i] = 0.0f;
   }
   const uint32_t n_tiles = (uint32_t)__builtin_amdgcn_readfirstlane(*a.n_tiles);
-  const TileJobs jb = tile_jobs(n_tiles, (uint32_t)(a.I / kRowTile), gridDim.x);
+  const TileJobs jb = tile_jobs(n_tiles, (uint32_t)(a.I / kRowTile), gridDim.x, NW);
   for (uint32_t job = blockIdx.x; job < jb.n_jobs; job += gridDim.x) {
     const uint32_t gt = job / jb.jpt;
     uint32_t unused;
-    gate_up_tile_job<D, 0>(a, s_x, s_sx, gt, job - gt * jb.jpt, jb, nullptr, unused);
+    gate_up_tile_job<D, 0, NW>(a, s_x, s_sx, gt, job - gt * jb.jpt, jb, nullptr, unused);
     __syncthreads();  // the operand is read by every wave before the next job overwrites it
   }
 }
@@ -726,7 +726,7 @@ inline size_t down_tile_lds_bytes(int64_t KqI) { return (size_t)KqI * (8 * 64 * 
 // beyond any real wait, it only guarantees that every wave exits.
 constexpr uint32_t kTileWaitPolls = 1u << 18;
 
-// One down job: token tile gt, row tiles of H part * per_job + w + kTileWaves * i.
+// One down job: token tile gt, row tiles of H part * per_job + w + NW * i.
 // FUSED (the gate/up + down kernel): the weight ring is loaded first, then
 // thread 0 waits until the tile's gate/up jobs have all counted in at
 // `ready` (>= target), and only then is the operand copied, by device-scope
@@ -734,7 +734,7 @@ constexpr uint32_t kTileWaitPolls = 1u << 18;
 // count was sent; the copies are issued after the count was seen).  Positions past the segment then read the segment's last row
 // instead of the zero row: their output rows are never stored, and an MFMA
 // output row depends on its own A row only.
-template <int D, bool FUSED>
+template <int D, bool FUSED, int NW = kTileWaves>
 __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK& a, u32x4* s_h, float* s_hs, uint32_t gt,
                                                                     uint32_t part, const TileJobs& jb, int32_t* ready,
                                                                     int32_t target, int32_t* err, int32_t* ticket,
@@ -763,7 +763,7 @@ __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK&
   const BufRsrc sr = buf_rsrc(routed ? reinterpret_cast<const uint8_t*>(a.down_sc) + (int64_t)e * sc_bytes
                                      : reinterpret_cast<const uint8_t*>(a.sh_down_sc), sc_bytes);
   const uint32_t rt0 = part * jb.per_job + w;
-  const uint32_t left = rt0 < n_rt ? (n_rt - rt0 + kTileWaves - 1) / kTileWaves : 0;
+  const uint32_t left = rt0 < n_rt ? (n_rt - rt0 + NW - 1) / NW : 0;
   const uint32_t n_mine = left < jb.M ? left : jb.M;
   const uint32_t total = n_mine * Kq;
 
@@ -775,13 +775,13 @@ __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK&
     const uint32_t hv = (uint32_t)pos * Kq * 512u + (uint32_t)p * 128u;
     const uint32_t sv = (uint32_t)pos * Kq * 32u + (uint32_t)p * 8u;
     constexpr int aux = FUSED ? kDeviceScope : 0;
-    for (uint32_t b = w; b < Kq * 8; b += kTileWaves) {
+    for (uint32_t b = w; b < Kq * 8; b += NW) {
       if (4 * (b / 8) + (b / 2) % 4 < (uint32_t)Kg)
         dma_b128<aux>(hqr, s_h + b * kWave, hv, (b / 8) * 512u + ((b / 2) % 4) * 32u + (b % 2) * 16u);
       else
         s_h[b * kWave + lane] = zero4;
     }
-    for (uint32_t b = w; b < Kq * 2; b += kTileWaves)
+    for (uint32_t b = w; b < Kq * 2; b += NW)
       dma_b32<aux>(hsr, s_hs + b * kWave, sv, (b / 2) * 32u + (b % 2) * 4u);
   };
   if constexpr (!FUSED) {
@@ -800,7 +800,7 @@ __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK&
     }
   };
   auto load = [&](DChunk& c) {
-    const uint32_t tq = (uint32_t)__builtin_amdgcn_readfirstlane((int)((rt0 + kTileWaves * li) * Kq + lq));
+    const uint32_t tq = (uint32_t)__builtin_amdgcn_readfirstlane((int)((rt0 + NW * li) * Kq + lq));
     c.w = buf_load_b128(wr, (uint32_t)lane * 16u, tq * kQuadNibBytes);
     c.s = buf_load_b64(sr, (uint32_t)n * 8u, tq * (kQuadScales * 2));
   };
@@ -863,7 +863,7 @@ __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK&
     }
     if (++cq == Kq) {
       const f32x4 res = kUnitScale * acc - kUnitBias * corr;
-      const uint32_t rt = rt0 + kTileWaves * ci;
+      const uint32_t rt = rt0 + NW * ci;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int64_t pos = m0 + 4 * p + j;
@@ -885,16 +885,16 @@ __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK&
     if ((uint32_t)d < rem) consume(buf[d], false);
 }
 
-template <int D>
-__global__ __launch_bounds__(kTileWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void down_tile_kernel(DownK a) {
+template <int D, int NW>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2))) void down_tile_kernel(DownK a) {
   extern __shared__ u32x4 s_h[];
   float* s_hs = reinterpret_cast<float*>(s_h + (uint32_t)a.Kq * 512);
   const uint32_t n_tiles = (uint32_t)__builtin_amdgcn_readfirstlane(*a.n_tiles);
-  const TileJobs jb = tile_jobs(n_tiles, (uint32_t)(a.H / kRowTile), gridDim.x);
+  const TileJobs jb = tile_jobs(n_tiles, (uint32_t)(a.H / kRowTile), gridDim.x, NW);
   for (uint32_t job = blockIdx.x; job < jb.n_jobs; job += gridDim.x) {
     const uint32_t gt = job / jb.jpt;
     uint32_t unused;
-    down_tile_job<D, false>(a, s_h, s_hs, gt, job - gt * jb.jpt, jb, nullptr, 0, nullptr, nullptr, unused);
+    down_tile_job<D, false, NW>(a, s_h, s_hs, gt, job - gt * jb.jpt, jb, nullptr, 0, nullptr, nullptr, unused);
     __syncthreads();  // the operand is read by every wave before the next job overwrites it
   }
 }
@@ -1070,30 +1070,45 @@ static hipError_t launch_gate_up_tile(const ExpertArgs& x, const GateUpK& g, hip
     const int d = atoi(v);
     if (d >= 2 && d <= 4) depth = d;
   }
+  // Eight waves per workgroup, one workgroup per CU (two waves per SIMD, as
+  // with two 4-wave workgroups): each CU copies a tile's operand to LDS once
+  // rather than twice (Qwen3 shapes, 32 tokens: 24.5 -> 23.7 us).
+  // PHANTOM_MOE_GATE_UP_WAVES=4 selects 4-wave workgroups.
+  int nw = 8;
+  if (const char* v = getenv("PHANTOM_MOE_GATE_UP_WAVES")) {
+    const int n = atoi(v);
+    if (n == 4 || n == 8) nw = n;
+  }
   const size_t lds = tile_lds_bytes(g.Kq);
-  const int block = kTileWaves * kWave;
-  const int64_t max_jobs = max_token_tiles(x.T, x.k, x.E, x.has_shared) * ceil_div(x.I / kRowTile, kTileWaves);
-#define PMOE_TILE(D_)                                                                                    \
+  const int block = nw * kWave;
+  const int64_t max_jobs = max_token_tiles(x.T, x.k, x.E, x.has_shared) * ceil_div(x.I / kRowTile, nw);
+#define PMOE_TILE(D_, NW_)                                                                               \
   do {                                                                                                   \
     static bool attr_set = false;                                                                        \
     if (!attr_set) {                                                                                     \
-      hipError_t e_ = hipFuncSetAttribute(reinterpret_cast<const void*>(&gate_up_tile_kernel<D_>),       \
+      hipError_t e_ = hipFuncSetAttribute(reinterpret_cast<const void*>(&gate_up_tile_kernel<D_, NW_>),  \
                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);       \
       if (e_ != hipSuccess) return e_;                                                                   \
       attr_set = true;                                                                                   \
     }                                                                                                    \
     int per_cu = 0;                                                                                      \
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gate_up_tile_kernel<D_>, block, lds) !=    \
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gate_up_tile_kernel<D_, NW_>, block, lds) != \
             hipSuccess || per_cu < 1)                                                                    \
       per_cu = 1;                                                                                        \
     int64_t grid = (int64_t)device_cus() * per_cu;                                                       \
     if (grid > max_jobs) grid = max_jobs;                                                                \
-    hipLaunchKernelGGL((gate_up_tile_kernel<D_>), dim3((unsigned)(grid < 1 ? 1 : grid)), dim3(block), lds, \
-                       stream, g);                                                                       \
+    hipLaunchKernelGGL((gate_up_tile_kernel<D_, NW_>), dim3((unsigned)(grid < 1 ? 1 : grid)), dim3(block), \
+                       lds, stream, g);                                                                  \
   } while (0)
-  if (depth == 2) PMOE_TILE(2);
-  else if (depth == 3) PMOE_TILE(3);
-  else PMOE_TILE(4);
+  if (nw == 8) {
+    if (depth == 2) PMOE_TILE(2, 8);
+    else if (depth == 3) PMOE_TILE(3, 8);
+    else PMOE_TILE(4, 8);
+  } else {
+    if (depth == 2) PMOE_TILE(2, 4);
+    else if (depth == 3) PMOE_TILE(3, 4);
+    else PMOE_TILE(4, 4);
+  }
 #undef PMOE_TILE
   return hipGetLastError();
 }
@@ -1256,19 +1271,19 @@ static hipError_t launch_down_tile(const ExpertArgs& x, const DownK& d, hipStrea
   do {                                                                                                   \
     static bool attr_set = false;                                                                        \
     if (!attr_set) {                                                                                     \
-      hipError_t e_ = hipFuncSetAttribute(reinterpret_cast<const void*>(&down_tile_kernel<D_>),          \
+      hipError_t e_ = hipFuncSetAttribute(reinterpret_cast<const void*>(&down_tile_kernel<D_, kTileWaves>), \
                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);       \
       if (e_ != hipSuccess) return e_;                                                                   \
       attr_set = true;                                                                                   \
     }                                                                                                    \
     int per_cu = 0;                                                                                      \
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, down_tile_kernel<D_>, block, lds) !=       \
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, down_tile_kernel<D_, kTileWaves>, block, lds) != \
             hipSuccess || per_cu < 1)                                                                    \
       per_cu = 1;                                                                                        \
     int64_t grid = (int64_t)device_cus() * per_cu;                                                       \
     if (grid > max_jobs) grid = max_jobs;                                                                \
-    hipLaunchKernelGGL((down_tile_kernel<D_>), dim3((unsigned)(grid < 1 ? 1 : grid)), dim3(block), lds,  \
-                       stream, d);                                                                       \
+    hipLaunchKernelGGL((down_tile_kernel<D_, kTileWaves>), dim3((unsigned)(grid < 1 ? 1 : grid)), dim3(block), \
+                       lds, stream, d);                                                                  \
   } while (0)
   if (depth == 2) PMOE_DTILE(2);
   else if (depth == 4) PMOE_DTILE(4);

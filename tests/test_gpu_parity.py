@@ -338,7 +338,9 @@ def test_expert_kernels_agree(dev, cfg, monkeypatch):
     quads of H and of I included.  The fused launch does the token-tile
     launches' arithmetic, so its output must equal theirs bit for bit, on
     every one of several calls (a read of h before its producers finished
-    would differ)."""
+    would differ).  So must the gate/up token-tile kernel in 4-wave
+    workgroups (PHANTOM_MOE_GATE_UP_WAVES=4; 8 is the default): the waves of a
+    workgroup share the operand, each row tile's sums are the same."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     n_slots = cfg.T * cfg.k
     max_tiles = -(-n_slots // 16) + min(n_slots, cfg.E) + (-(-cfg.T // 16) if cfg.shared else 0)
@@ -364,6 +366,10 @@ def test_expert_kernels_agree(dev, cfg, monkeypatch):
         y_fus = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b).cpu().numpy()
         assert np.array_equal(y_fus.view(np.uint32), y_tile.view(np.uint32)), f"fused call {rep + 1} differs"
     monkeypatch.delenv("PHANTOM_MOE_FFN_KERNEL")
+    monkeypatch.setenv("PHANTOM_MOE_GATE_UP_WAVES", "4")
+    y_w4 = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b).cpu().numpy()
+    monkeypatch.delenv("PHANTOM_MOE_GATE_UP_WAVES")
+    assert np.array_equal(y_w4.view(np.uint32), y_tile.view(np.uint32)), "4-wave gate/up workgroups differ"
     monkeypatch.setenv("PHANTOM_MOE_GATE_UP_KERNEL", "classic")
     monkeypatch.setenv("PHANTOM_MOE_DOWN_KERNEL", "classic")
     y_cls, _, idx_cls = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b, return_routing=True)
