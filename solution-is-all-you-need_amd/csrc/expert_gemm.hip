@@ -122,6 +122,14 @@ __device__ inline void dequant_split_f16(uint32_t w, uint32_t d, uint32_t mask, 
   }
 }
 
+// SwiGLU of one output, silu(g) * u, from the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32; about 1 ulp each, against some 35 instructions for
+// expf and an IEEE division): the relative difference is ~1e-7.
+__device__ inline float swiglu_fast(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);
+  return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+}
+
 // Item space: for each active segment u, ceil(len_u / BM) position blocks
 // times n_nb row blocks.  s_mb[u] = first position block of segment u (an
 // exclusive prefix over segments, computed by wave 0).
@@ -395,7 +403,7 @@ __global__ __launch_bounds__(kGemmWaves * kWave) void gemm_gate_up_kernel(GemmK 
         const int m = tt * 16 + 4 * p + j;
         const float gv = acc[0][tt][j];
         const float uv = acc[1][tt][j];
-        const float hv = gv * (1.0f / (1.0f + expf(-gv))) * uv;
+        const float hv = swiglu_fast(gv, uv);
         const uint32_t hb = float_to_half_bits(hv);
         const uint32_t lb = float_to_half_bits(hv - half_bits_to_float32(hb));
         uint16_t* chunk = hs + ((gl * BM + m) * 4 + pp) * 16;
@@ -726,14 +734,16 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_gate_up_kernel2(GemmK a
     const int pp = n / 4;
     const int rr = n % 4;
     const int jj = half == 0 ? ((rr & 1) ? 4 : 0) + (rr >> 1) : ((rr & 1) ? 6 : 2) + (rr >> 1);
+    // tiles past the segment (tt >= vt) hold no position that is stored
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
+      if (tt >= vt) break;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int m = tt * 16 + 4 * p + j;
         const float gv = acc[0][tt][j];
         const float uv = acc[1][tt][j];
-        const float hv = gv * (1.0f / (1.0f + expf(-gv))) * uv;
+        const float hv = swiglu_fast(gv, uv);
         const uint32_t hb = float_to_half_bits(hv);
         const uint32_t lb = float_to_half_bits(hv - half_bits_to_float32(hb));
         uint16_t* chunk = hs + ((gl * BM + m) * 4 + pp) * 16;
