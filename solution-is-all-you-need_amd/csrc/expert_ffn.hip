@@ -1306,17 +1306,19 @@ hipError_t launch_down(const ExpertArgs& x, const Workspace& ws, hipStream_t str
   // vs 161 us at 8 tokens, 572 vs 609 us at 64; with few items they lose).
   // Below 512 items (two experts of H 4096, one token) single row tiles
   // double the items and one quad in flight per wave beats two (Mixtral shape:
-  // 31.2 vs 34.7 us).  With long rows of I (16+ quads) and up to 4096 items,
-  // four row tiles per item share each quad's activation operand (Mixtral at
-  // 16 tokens: 80.1 vs 91.9 us; H 7168, I 2048 at one token: 28.6 vs 29.1).
+  // 31.2 vs 34.7 us).  With long rows of I (16+ quads), four row tiles per
+  // item share each quad's activation operand, with two quads in flight
+  // (Mixtral at 16 tokens: 80.1 vs 91.9 us; H 7168, I 2048: 28.6 vs 29.1 us
+  // at one token, 138.8 vs 148.4 at 8, 538 vs 571 at 64).
   const int64_t items = (int64_t)max_active_experts(x) * (x.H / (kRowTile * rt));
   sp.nq = items <= 4096 ? 2 : 1;
   if (items >= 8192) sp.ksplit = sp.ksplit < 2 ? sp.ksplit : 2;
   if (items < 512) {
     rt = 1;
     sp.nq = 1;
-  } else if (d.Kq >= 16 && items <= 4096) {
+  } else if (d.Kq >= 16) {
     rt = 4;
+    sp.nq = 2;
   }
   tiling_override("PHANTOM_MOE_DOWN_TILING", kDownWaves, &sp.ksplit, &rt, &sp.nq);
   if (rt == 4 && (x.H / kRowTile) % 4) rt = 2;
