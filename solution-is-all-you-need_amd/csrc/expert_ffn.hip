@@ -247,7 +247,7 @@ __device__ __attribute__((always_inline)) inline void gu_epilogue(const GateUpK&
 constexpr int kTokLds = 2048;
 
 template <int RT, bool TOK_LDS>
-__global__ __launch_bounds__(kGateUpWaves * kWave, 4) void gate_up_kernel(GateUpK a) {
+__global__ __launch_bounds__(kGateUpWaves * kWave, RT == 1 ? 4 : 2) void gate_up_kernel(GateUpK a) {
   __shared__ float red[kGateUpWaves][RT][2][16][16];  // [wave][row tile][gate/up]
   __shared__ int4 s_desc[kMaxExperts + 1];
   __shared__ int s_tok[TOK_LDS ? kTokLds : 1];
@@ -1229,16 +1229,33 @@ hipError_t launch_gate_up(const ExpertArgs& x, const Workspace& ws, hipStream_t 
   const int64_t q4 = ceil_div(g.Kq, 4);
   int ksplit = (int)(q4 < kGateUpWaves ? q4 : kGateUpWaves);
   int rt = 1, nq = 1;
+  // With 4096+ single-tile items (H 7168, I 2048 from 8 tokens on), items of
+  // two row tiles (each quad's activation operand loaded once for both) on
+  // four waves: 196 vs 229 us at 8 tokens, 751 vs 891 us at 64; with fewer
+  // items (one token) the halved item count loses (46 vs 43 us).
+  if ((int64_t)max_active_experts(x) * (x.I / kRowTile) >= 4096) {
+    rt = 2;
+    ksplit = ksplit < 4 ? ksplit : 4;
+  }
   tiling_override("PHANTOM_MOE_GATE_UP_TILING", kGateUpWaves, &ksplit, &rt, &nq);
+  if (rt != 2 || (x.I / kRowTile) % 2) rt = 1;  // RT 4 would spill
   const int block = kWave * ksplit;
-  const int64_t max_items = (int64_t)max_active_experts(x) * (x.I / kRowTile);
+  const int64_t max_items = (int64_t)max_active_experts(x) * (x.I / (kRowTile * rt));
   // segment positions (T*k + shared T) = g.zero_row; their token ids go to LDS when they fit
-  if (g.zero_row <= kTokLds)
-    hipLaunchKernelGGL((gate_up_kernel<1, true>), dim3(resident_grid(gate_up_kernel<1, true>, block, max_items)),
-                       dim3(block), 0, stream, g);
-  else
-    hipLaunchKernelGGL((gate_up_kernel<1, false>), dim3(resident_grid(gate_up_kernel<1, false>, block, max_items)),
-                       dim3(block), 0, stream, g);
+#define PMOE_GU(RT_)                                                                                     \
+  do {                                                                                                   \
+    if (g.zero_row <= kTokLds)                                                                           \
+      hipLaunchKernelGGL((gate_up_kernel<RT_, true>),                                                    \
+                         dim3(resident_grid(gate_up_kernel<RT_, true>, block, max_items)), dim3(block), 0, \
+                         stream, g);                                                                     \
+    else                                                                                                 \
+      hipLaunchKernelGGL((gate_up_kernel<RT_, false>),                                                   \
+                         dim3(resident_grid(gate_up_kernel<RT_, false>, block, max_items)), dim3(block), 0, \
+                         stream, g);                                                                     \
+  } while (0)
+  if (rt == 2) PMOE_GU(2);
+  else PMOE_GU(1);
+#undef PMOE_GU
   return hipGetLastError();
 }
 
