@@ -2,23 +2,27 @@
 """MoE-layer throughput on one MI355X.
 
 A step is one forward of one sparse-MoE layer (router -> permute -> Q4_0
-SwiGLU experts -> weighted combine) over one batch of synthetic tokens.  The
-default workload is the Qwen3-30B-A3B-shaped layer (H=2048, I=768, E=128,
-top-8, softmax) at decode batch 32 with a fixed Zipf(1.1) router bias.  Steps
+SwiGLU experts -> weighted combine) over one batch of synthetic tokens.  Steps
 rotate over --layers distinct layer instances (distinct weights and inputs,
-about 5.4 GB at 16 instances) so weight traffic comes from HBM, not from the
-256 MB last-level cache.  Everything the timed region touches is resident in
-HBM before it starts.
+about 5.4 GB at 16 Qwen3-shaped instances) so weight traffic comes from HBM,
+not from the 256 MB last-level cache.  Everything the timed region touches is
+resident in HBM before it starts.
+
+Default run (no --workload): the headline is the batch-1 Qwen3-30B-A3B-shaped
+decode layer (H=2048, I=768, E=128, top-8 softmax, T=1), which runs as one
+kernel; sub-records carry the 4096-token Qwen3 prefill (MFMA roofline), the
+32-token Zipf-skewed Qwen3 decode batch, and the router alone at the
+reference's own benchmark shape (H=4096, E=16, top-2, one fp32 token).  Each
+record is timed from its own HIP graph replay of the K steps, after an eager
+pass with per-stage events (stage times, the roofline of the dominant kernel).
+--workload W runs one workload alone.
 
 Output: one JSON line with the whole-job tokens/s, the roofline of the
-dominant kernel (gate/up grouped GEMV, one launch between two HIP events on
-its stream), and the CPU baseline (the reference's CPU MoE
-path, restated in oracle/ref_cpu_path.py, timed on this host on a bounded
-sample).  The K timed steps run twice: eagerly with per-stage events (the
-stage and roofline figures), then as one HIP graph replay of the same K
-launches (value and ms_per_step; --no-graph keeps the eager timing).
+dominant kernel (bracketed by two HIP events on its stream), and the CPU
+baseline (the reference's CPU MoE path, restated in oracle/ref_cpu_path.py,
+timed on this host on a bounded sample).
 
-    python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--workload W]
 """
 from __future__ import annotations
 
@@ -39,6 +43,16 @@ STAGES = ("route", "gate_up", "down", "combine")
 HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000  # a record needs no system-scope release
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PREFILL_T = 1024  # from this batch on, a workload is priced against the MFMA roofline
+# The metric of the benchmark this line reports.
+METRIC = "MoE-layer decode tok/s + % of HBM peak; prefill grouped-GEMM % of MFMA peak"
+HEADLINE = "qwen3_decode_t1"
+SUB_WORKLOADS = ("qwen3_prefill_t4096", "qwen3_decode_t32_zipf")
+# The reference's router benchmark: PhantomTopKRouter at hidden 4096, 16
+# experts, top-2, one fp32 token (tests/test_moe_routing.py:199-203); its
+# published latency is 54.51 us on an RTX 4050 laptop GPU
+# (docs/testing/test_03_qwen3_30b_a3b.md:50).
+ROUTER_REF = dict(H=4096, E=16, k=2, T=1)
+ROUTER_REF_PUBLISHED_US = 54.51
 
 
 def pmc_summary(kernel: str, workload: str) -> str:
@@ -59,7 +73,9 @@ def parse_args():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--layers", type=int, default=16, help="distinct layer instances to rotate over")
-    p.add_argument("--workload", default="qwen3_decode_t32_zipf")
+    p.add_argument("--workload", default=None,
+                   help="one workload alone (default: the batch-1 Qwen3 headline plus the sub-records)")
+    p.add_argument("--no-subs", action="store_true", help="the headline alone, without the sub-records")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-stage-events", action="store_true", help="time without the per-stage events")
@@ -124,6 +140,15 @@ def layer_bytes(cfg, U: int) -> int:
     return experts + cfg.E * cfg.H * 4 + cfg.T * cfg.H * 2 + cfg.T * cfg.H * 4
 
 
+def expert_bytes(cfg, U: int) -> int:
+    """Q4_0 weight bytes of the U active experts (+ shared) of one layer."""
+    return (U + (1 if cfg.shared else 0)) * 3 * cfg.H * cfg.I * 18 // 32
+
+
+def down_flops(cfg) -> int:
+    return 2 * cfg.T * (cfg.k + (1 if cfg.shared else 0)) * cfg.H * cfg.I
+
+
 def gate_up_flops(cfg) -> int:
     return 2 * cfg.T * (cfg.k + (1 if cfg.shared else 0)) * 2 * cfg.H * cfg.I
 
@@ -132,40 +157,81 @@ def layer_flops(cfg) -> int:
     return 2 * cfg.T * (cfg.k + (1 if cfg.shared else 0)) * 3 * cfg.H * cfg.I + 2 * cfg.T * cfg.H * cfg.E
 
 
+def cpu_info():
+    """CPU model and SIMD feature flags of this host (/proc/cpuinfo)."""
+    model, flags = "unknown", []
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags"):
+                    flags = line.split(":", 1)[1].split()
+                    break
+    except OSError:
+        pass
+    simd = sorted(f for f in flags if f.startswith(("avx", "amx", "fma", "f16c", "sse4", "vnni")))
+    return model, simd
+
+
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: the cores this process may run on,
+    within the OMP_NUM_THREADS share when that is set."""
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and 0 < int(omp) < n:
+        n = int(omp)
+    return max(1, n)
+
+
 def cpu_baseline(cfg, host_layer, budget_s: float):
-    """The reference CPU path on layer instance 0, timed on a bounded sample."""
+    """The reference CPU path on layer instance 0, timed on a bounded sample:
+    all threads with weights kept packed (the reference's runtime, dequantised
+    on every call), one thread, and all threads on weights dequantised once up
+    front."""
     import numpy as np
     import torch
 
     sys.path.insert(0, ROOT)
     from oracle.ref_cpu_path import RefCPUMoE
 
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    torch.set_num_threads(threads)
     router_w, bias, gate, up, down, shared, xb = host_layer
-    layer = RefCPUMoE(router_w, gate, up, down, cfg.H, cfg.I, cfg.k, cfg.score, bias, shared)
     x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16)
-    layer(x)  # warm-up (allocator, oneDNN kernels)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        layer(x)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or n >= 50:
-            break
-    try:
-        cpu_model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
-    except (OSError, StopIteration):
-        cpu_model = "unknown"
+
+    def timed(layer, threads, budget, max_n=50):
+        torch.set_num_threads(threads)
+        layer(x)  # warm-up (allocator, oneDNN kernels)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            layer(x)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget or n >= max_n:
+                return n, el
+
+    threads = cpu_threads()
+    packed = RefCPUMoE(router_w, gate, up, down, cfg.H, cfg.I, cfg.k, cfg.score, bias, shared)
+    share = budget_s / 3.0
+    n_all, el_all = timed(packed, threads, share)
+    n_one, el_one = timed(packed, 1, share)
+    pre = RefCPUMoE(router_w, gate, up, down, cfg.H, cfg.I, cfg.k, cfg.score, bias, shared, predequant=True)
+    n_pre, el_pre = timed(pre, threads, share)
+    del pre
+    model, simd = cpu_info()
     return {
-        "value": round(cfg.T * n / el, 3),
+        "value": round(cfg.T * n_all / el_all, 3),
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{n} forwards of one {cfg.T}-token layer instance ({cfg.T * n} tokens, {el:.1f} s): torch fp32 "
-                  f"router, numpy Q4_0 dequant of every active expert on every call, torch bf16 SwiGLU, index_add_ "
-                  f"combine (oracle/ref_cpu_path.py)",
-        "cpu": cpu_model,
+        "sample": f"{n_all} forwards of one {cfg.T}-token layer instance ({cfg.T * n_all} tokens, {el_all:.1f} s) on "
+                  f"{threads} threads: torch fp32 router, numpy Q4_0 dequant of every active expert on every call, "
+                  f"torch bf16 SwiGLU, index_add_ combine (oracle/ref_cpu_path.py)",
+        "one_thread": {"value": round(cfg.T * n_one / el_one, 3), "unit": "tokens/s", "cores": 1,
+                       "sample": f"{n_one} forwards ({el_one:.1f} s)"},
+        "predequantized": {"value": round(cfg.T * n_pre / el_pre, 3), "unit": "tokens/s", "cores": threads,
+                           "sample": f"{n_pre} forwards ({el_pre:.1f} s) on bf16 weights dequantised once up front"},
+        "cpu": model,
+        "simd_flags": simd,
     }
 
 
@@ -266,27 +332,16 @@ def bench_legacy(args):
     print(json.dumps(out), flush=True)
 
 
-def main():
-    args = parse_args()
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}, "
-              f"WORLD_SIZE={world}); the sharding design is described in DESIGN.md.", file=sys.stderr)
-        sys.exit(2)
-    if args.workload in LEGACY_WORKLOADS:
-        return bench_legacy(args)
-
+def bench_moe(args, cfg, with_cpu: bool) -> dict:
+    """Time K steps of one MoE workload (eager with stage events, then one
+    HIP graph replay); returns its record."""
     import numpy as np
     import torch
 
     import phantom_moe
     from phantom_moe import _lib, synth
 
-    if not torch.cuda.is_available():
-        print("bench.py needs a GPU", file=sys.stderr)
-        sys.exit(1)
     dev = torch.device("cuda:0")
-    cfg = synth.CONFIGS[args.workload]
     L = max(1, args.layers)
 
     # ---- resident inputs: L distinct layer instances --------------------
@@ -297,7 +352,7 @@ def main():
         ex = phantom_moe.MoEWeights.from_q4_0(dl.gate, dl.up, dl.down, cfg.H, cfg.I, cfg.E, shared=dl.shared)
         xb = synth.activations(cfg.T, cfg.H, seed=42 + l)
         x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).to(dev)
-        if l == 0 and not args.no_cpu_baseline:
+        if l == 0 and with_cpu:
             host0 = (dl.router_w.cpu().numpy(), None if dl.router_bias is None else dl.router_bias.cpu().numpy(),
                      dl.gate.cpu().numpy(), dl.up.cpu().numpy(), dl.down.cpu().numpy(),
                      None if dl.shared is None else tuple(t.cpu().numpy() for t in dl.shared), xb)
@@ -357,6 +412,11 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    # every call of the single-launch path completed its hand-offs
+    status = 0
+    for lay in layers:
+        status |= _lib.workspace_status(lay.workspace)
+
     # ---- per-kernel and per-layer times, U per instance --------------------
     U = [int(torch.unique(layers[l].topk_idx).numel()) for l in range(L)]
     stages = {name: [] for name in STAGES}
@@ -369,6 +429,10 @@ def main():
                 stages[name].append(ev.elapsed_ms(e[j], e[j + 1]))
         ev.destroy(events)
     steps_U = [U[i % L] for i in range(args.steps)]
+    resident_gb = round(sum(x.experts.nbytes() for x in layers) / 1e9, 3)
+    del layers
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
 
     eager_elapsed = elapsed
     if graph_elapsed is not None:
@@ -391,24 +455,37 @@ def main():
             "workload": cfg.name,
             "H": cfg.H, "I": cfg.I, "E": cfg.E, "top_k": cfg.k, "tokens_per_step": cfg.T,
             "score": cfg.score, "zipf_bias_s": cfg.zipf, "shared_expert": cfg.shared,
-            "layer_instances": L, "weights_resident_gb": round(sum(x.experts.nbytes() for x in layers) / 1e9, 3),
+            "layer_instances": L, "weights_resident_gb": resident_gb,
             "active_experts_per_step_mean": round(float(np.mean(steps_U)), 2),
             "timing": "one HIP graph replay of the K steps" if graph_elapsed is not None else "eager launches",
         },
+        "workspace_status": status,
     }
     if graph_elapsed is not None:
         out["eager"] = {"tokens_per_s": round(cfg.T * args.steps / eager_elapsed, 2),
                         "ms_per_step": round(eager_elapsed * 1e3 / args.steps, 5)}
+    # whole-layer HBM rate on the graph clock, on both bases: all algorithmic
+    # bytes, and the active experts' weights alone
+    lay_bytes = float(sum(layer_bytes(cfg, u) for u in steps_U))
+    exp_bytes = float(sum(expert_bytes(cfg, u) for u in steps_U))
+    out["layer_hbm"] = {
+        "full_bytes_gbs": round(lay_bytes / elapsed / 1e9, 1),
+        "full_bytes_frac": round(lay_bytes / elapsed / 1e9 / HBM_PEAK_GBS, 4),
+        "expert_bytes_gbs": round(exp_bytes / elapsed / 1e9, 1),
+        "expert_bytes_frac": round(exp_bytes / elapsed / 1e9 / HBM_PEAK_GBS, 4),
+        "bytes_per_step": round(lay_bytes / args.steps),
+        "clock": "graph replay, launch gaps included",
+    }
     if use_events:
         # the kernel the gate/up stage launches at this shape; one kernel for
-        # both stages means the fused launch, which the gate/up stage's events
-        # bracket (the down stage is then empty)
+        # both stages means the single-launch layer, which the gate/up stage's
+        # events bracket (the other stages are then empty)
         names = dict(kv.split("=") for kv in _lib.load().phantom_moe_expert_kernels(
             cfg.T, cfg.H, cfg.I, cfg.E, cfg.k, int(cfg.shared)).decode().split(";"))
         gu_kernel = names["gate_up"]
         fused = names["gate_up"] == names["down"]
         gu_ms = float(np.sum(stages["gate_up"]))
-        gu_bytes = float(sum((ffn_bytes if fused else gate_up_bytes)(cfg, u) for u in steps_U))
+        gu_bytes = float(sum((layer_bytes if fused else gate_up_bytes)(cfg, u) for u in steps_U))
         achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
         traffic = None
         if os.path.exists(pmc_summary(gu_kernel, cfg.name)):
@@ -431,8 +508,11 @@ def main():
             out["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
         if cfg.T >= PREFILL_T and not fused:
+            dn_ms = float(np.sum(stages["down"]))
+            dn_tf = down_flops(cfg) * args.steps / (dn_ms * 1e-3) / 1e12
             out["roofline"].update({"intensity_flop_per_byte": round(intensity, 1), "ridge_flop_per_byte": round(ridge, 1),
-                                    "achieved_tflops": round(tf, 2), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)})
+                                    "achieved_tflops": round(tf, 2), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                                    "down_tflops": round(dn_tf, 2), "down_mfma_frac": round(dn_tf / BF16_PEAK_TFLOPS, 4)})
         out["roofline"].update({
             "kernel": gu_kernel,
             "down_kernel": names["down"],
@@ -440,17 +520,132 @@ def main():
             "avg_launch_us": round(gu_ms * 1e3 / args.steps, 3),
         })
         lay_ms = float(np.sum(layer_ms))
-        lay_bytes = float(sum(layer_bytes(cfg, u) for u in steps_U))
         out["layer"] = {
             "gpu_us_per_step": round(lay_ms * 1e3 / args.steps, 3),
             "stage_us": {k: round(float(np.mean(v)) * 1e3, 3) for k, v in stages.items()},
             "hbm_achieved_gbs": round(lay_bytes / (lay_ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(lay_bytes / (lay_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "tflops": round(layer_flops(cfg) * args.steps / (lay_ms * 1e-3) / 1e12, 3),
+            "mfma_frac": round(layer_flops(cfg) * args.steps / (lay_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "clock": "eager, events around each step",
         }
+        if fused:
+            out["layer"]["single_launch"] = True
     out["cpu_baseline"] = None
     if host0 is not None:
         out["cpu_baseline"] = cpu_baseline(cfg, host0, args.cpu_seconds)
+    return out
+
+
+def bench_router_ref(args) -> dict:
+    """phantom_moe_route alone at the reference's router benchmark shape
+    (hidden 4096, 16 experts, top-2, one fp32 token): K calls timed eagerly
+    with events around each, then as one HIP graph replay."""
+    import numpy as np
+    import torch
+
+    from phantom_moe import _lib
+
+    dev = torch.device("cuda:0")
+    H, E, k, T = ROUTER_REF["H"], ROUTER_REF["E"], ROUTER_REF["k"], ROUTER_REF["T"]
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    W = torch.randn((E, H), generator=g, device=dev) * 0.02
+    xs = [torch.randn((T, H), generator=g, device=dev) for _ in range(16)]
+    idx = torch.empty((T, k), dtype=torch.int32, device=dev)
+    w = torch.empty((T, k), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    nbytes = lib.phantom_moe_workspace_bytes(T, H, 0, E, k, 0)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    stream = _lib.stream_handle(dev)
+
+    def call(i, s):
+        rc = lib.phantom_moe_route(xs[i % 16].data_ptr(), 1, W.data_ptr(), None, T, H, E, k, 0, idx.data_ptr(),
+                                   w.data_ptr(), ws.data_ptr(), nbytes, s)
+        if rc:
+            _lib.check(rc, "phantom_moe_route")
+
+    for i in range(args.warmup):
+        call(i, stream)
+    ev = HipEvents()
+    evs = ev.create(2 * args.steps)
+    hip = ev.hip
+    hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        hip.hipEventRecord(ctypes.c_void_p(evs[2 * i]), ctypes.c_void_p(stream))
+        call(i, stream)
+        hip.hipEventRecord(ctypes.c_void_p(evs[2 * i + 1]), ctypes.c_void_p(stream))
+    torch.cuda.synchronize()
+    per = [ev.elapsed_ms(evs[2 * i], evs[2 * i + 1]) * 1e3 for i in range(args.steps)]
+    ev.destroy(evs)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gs = _lib.stream_handle(dev)
+        for i in range(args.steps):
+            call(i, gs)
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    graph.replay()
+    torch.cuda.synchronize()
+    g_us = (time.perf_counter() - t0) * 1e6 / args.steps
+    del graph
+    return {
+        "metric": "router latency (PhantomTopKRouter.forward: logits, top-k, softmax)",
+        "config": {"workload": "router_ref_h4096_e16_k2_t1", "H": H, "E": E, "top_k": k, "tokens": T,
+                   "x_dtype": "fp32"},
+        "us_per_call_graph": round(g_us, 3),
+        "us_per_call_eager_median": round(float(np.median(per)), 3),
+        "launches_per_call": 2,
+        "reference_published_us": ROUTER_REF_PUBLISHED_US,
+        "reference_hardware": "RTX 4050 Laptop GPU (a different GPU; context, not a like-for-like comparison)",
+        "reference_source": "docs/testing/test_03_qwen3_30b_a3b.md:50; config tests/test_moe_routing.py:199-203",
+    }
+
+
+def sub_record(rec: dict) -> dict:
+    keep = ("metric", "value", "unit", "ms_per_step", "config", "eager", "layer_hbm", "roofline", "layer",
+            "workspace_status")
+    return {k: rec[k] for k in keep if k in rec}
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); the sharding design is described in DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+    if args.workload in LEGACY_WORKLOADS:
+        return bench_legacy(args)
+
+    import torch
+
+    from phantom_moe import synth
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    if args.workload:
+        if args.workload not in synth.CONFIGS:
+            print(f"unknown workload {args.workload!r}; one of {sorted(synth.CONFIGS)} or "
+                  f"{sorted(LEGACY_WORKLOADS)}", file=sys.stderr)
+            sys.exit(2)
+        print(json.dumps(bench_moe(args, synth.CONFIGS[args.workload], not args.no_cpu_baseline)), flush=True)
+        return
+    cfg = synth.CONFIGS[HEADLINE]
+    out = bench_moe(args, cfg, not args.no_cpu_baseline)
+    out["metric_detail"] = out["metric"]
+    out["metric"] = METRIC
+    if not args.no_subs:
+        subs = {}
+        for name in SUB_WORKLOADS:
+            print(f"[bench] {name}", file=sys.stderr, flush=True)
+            subs[name] = sub_record(bench_moe(args, synth.CONFIGS[name], False))
+        print("[bench] router_ref", file=sys.stderr, flush=True)
+        subs["router_ref_h4096_e16_k2_t1"] = bench_router_ref(args)
+        out["sub"] = subs
     print(json.dumps(out), flush=True)
 
 

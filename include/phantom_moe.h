@@ -115,10 +115,38 @@ PHANTOM_MOE_API int phantom_q4_0_dequant_f32(const uint8_t* q4_0, int64_t rows, 
 /* ---------------------------------------------------------------- */
 
 /* Workspace bytes needed by phantom_moe_route / _permute / _forward for
- * these sizes.  The workspace holds only per-call intermediates (no state
- * carries between calls and no initial contents are required); one workspace
- * must not be used by calls that may run concurrently. */
+ * these sizes.  The workspace must be 256-byte aligned and must not be used
+ * by calls that may run concurrently.  Zero-fill it once before its first
+ * use (hipMemset, torch.zeros) and leave it to the library afterwards: its
+ * first 256 bytes keep a call counter that the single-launch decode path
+ * (below) derives its hand-off tags from, so no later call needs a memset;
+ * everything else is per-call scratch.  (A workspace that was never zeroed
+ * still works; only a 2^-32-per-word chance remains that stale bytes pass
+ * for a tag on its first call.) */
 PHANTOM_MOE_API size_t phantom_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int E, int top_k, int has_shared);
+
+/* Status bits that the single-launch decode path left in this workspace
+ * (0: every call since the last query completed normally; bit 0: a
+ * workgroup gave up waiting for the router logits, bit 1 for the gate/up
+ * results, bit 2 for every workgroup to start).  A call that sets a bit
+ * also writes NaN to the outputs it could not compute.  Waits for the
+ * stream, clears the bits, and must not be captured into a graph.  No
+ * counterpart in the reference, whose errors exit the process
+ * (kernels/common/cuda_utils.h:31-52). */
+PHANTOM_MOE_API int phantom_moe_workspace_status(void* workspace, size_t workspace_bytes, uint32_t* status,
+                                                 hipStream_t stream);
+
+/* Library options (process-wide; initialised from the environment on first
+ * use: PHANTOM_MOE_DECODE=staged).  A/B and test switches with no
+ * counterpart in the reference. */
+#define PHANTOM_MOE_OPT_DECODE_FUSED 1 /* 1: decode batches that fit take the single-launch path (default) */
+#define PHANTOM_MOE_OPT_FUSED_WAIT_POLLS 3 /* bound of each wait of the single-launch path (default 2^18 polls) */
+/* Failure injection for tests of the error path: bit 0 makes the logit wait,
+ * bit 1 the gate/up wait, expect a tag nobody writes, so it gives up after
+ * FUSED_WAIT_POLLS polls (every wave still exits; outputs NaN, status set). */
+#define PHANTOM_MOE_OPT_FUSED_FAULT 4
+PHANTOM_MOE_API int phantom_moe_set_option(int option, int value);
+PHANTOM_MOE_API int phantom_moe_get_option(int option, int* value);
 
 /* Router: logits = x W^T (+ bias) under the fixed-order fp64 contract,
  * top-k descending with ties to the lower expert index, weights by
@@ -146,7 +174,15 @@ PHANTOM_MOE_API int phantom_moe_permute(const int32_t* topk_idx, int64_t T, int 
  * The sh_* pointers describe one always-on shared expert of the same shapes
  * (weight 1.0), or are all NULL.  Outputs: y [T, H] fp32, topk_idx, topk_w.
  * The FFN operator semantics follow kernels/sparse_moe/sparse_matmul.cu:120-215
- * (SwiGLU, fp32 math) with 4-bit weights. */
+ * (SwiGLU, fp32 math) with 4-bit weights.
+ * Decode batches of a few tokens whose experts fit its register and LDS
+ * budgets (the batch-1 Qwen3-shaped layer among them) run as ONE kernel:
+ * router, top-k, permute, gate/up, down and combine without returning to the
+ * host, replacing the launch-per-stage structure of sparse_matmul.cu:256-363;
+ * other shapes run router, gate/up, down and combine as separate launches.
+ * Both give the same routing (bit for bit) and outputs within the layer
+ * tolerance.  Alignment: nibble buffers 16 bytes, scale buffers 8, x 8,
+ * router_w 16, workspace 256. */
 PHANTOM_MOE_API int phantom_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int E, int top_k,
                         int score_mode, const float* router_w, const float* router_bias,
                         const uint8_t* gate_nib, const uint16_t* gate_scale, const uint8_t* up_nib,

@@ -6,7 +6,11 @@
 // and its host API blocks on a timer event (cuda_utils.h:253-257); here every
 // failure is a return code plus a thread-local message.
 #include <stdarg.h>
+
+#include <atomic>
+#include <mutex>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "moe_common.h"
@@ -70,6 +74,51 @@ int check_route_shapes(const void* x, int x_dtype, const float* router_w, int64_
 
 namespace pmoe {
 
+namespace {
+
+LibConfig config_from_env() {
+  LibConfig c;
+  const char* d = getenv("PHANTOM_MOE_DECODE");
+  c.decode_fused = !(d && strcmp(d, "staged") == 0);
+  c.fused_wait_polls = kFusedWaitPollsDefault;
+  c.fused_fault = 0;
+  return c;
+}
+
+// Options live in atomics so a change from another thread is never torn;
+// they are read once per call.
+std::atomic<int> g_opt_fused{1};
+std::atomic<uint32_t> g_opt_polls{kFusedWaitPollsDefault};
+std::atomic<uint32_t> g_opt_fault{0};
+std::once_flag g_opt_once;
+
+void init_options() {
+  std::call_once(g_opt_once, [] {
+    const LibConfig c = config_from_env();
+    g_opt_fused.store(c.decode_fused ? 1 : 0);
+    g_opt_polls.store(c.fused_wait_polls);
+    g_opt_fault.store(c.fused_fault);
+  });
+}
+
+}  // namespace
+
+LibConfig lib_config() {
+  init_options();
+  LibConfig c;
+  c.decode_fused = g_opt_fused.load(std::memory_order_relaxed) != 0;
+  c.fused_wait_polls = g_opt_polls.load(std::memory_order_relaxed);
+  c.fused_fault = g_opt_fault.load(std::memory_order_relaxed);
+  return c;
+}
+
+void set_lib_config(const LibConfig& c) {
+  init_options();
+  g_opt_fused.store(c.decode_fused ? 1 : 0);
+  g_opt_polls.store(c.fused_wait_polls);
+  g_opt_fault.store(c.fused_fault);
+}
+
 int set_error(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -91,6 +140,20 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
     off = align256(off + bytes);
     return o;
   };
+  // Every plan starts with the same control words, which only the
+  // single-launch path writes; its own regions follow when the shape takes it.
+  const size_t o_ctl = take(kCtlBytes);
+  const bool fused = I > 0 && fused_shape_ok(T, H, I, E, k, has_shared);
+  size_t o_pres = 0, o_slots = 0, o_flags = 0, o_fhq = 0, o_fhs = 0;
+  if (fused) {
+    const int64_t S_max = (T * k < E ? T * k : E) + (has_shared ? 1 : 0);
+    const int64_t KqI_f = round_up(I, kQuad) / kQuad;
+    o_pres = take(sizeof(uint64_t) * (size_t)kFusedMaxGrid);
+    o_slots = take((size_t)16 * (size_t)(T * E));
+    o_flags = take(sizeof(uint64_t) * (size_t)(S_max * (I / kRowTile)));
+    o_fhq = take((size_t)512 * (size_t)((T * k + T) * KqI_f));
+    o_fhs = take((size_t)32 * (size_t)((T * k + T) * KqI_f));
+  }
   const size_t o_log = take(sizeof(double) * (size_t)(T * E));
   // x operand rows 0..T-1 plus an all-zero row T
   const size_t o_xq = take(sizeof(uint16_t) * (size_t)((T + 1) * Kpad));
@@ -115,6 +178,16 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
   const size_t o_ptb = take(sizeof(int32_t) * (size_t)E);
   if (ws && base) {
     char* b = static_cast<char*>(base);
+    ws->ctl = reinterpret_cast<uint32_t*>(b + o_ctl);
+    ws->fused = FusedWs();
+    if (fused) {
+      ws->fused.ctl = ws->ctl;
+      ws->fused.presence = reinterpret_cast<uint64_t*>(b + o_pres);
+      ws->fused.slots = reinterpret_cast<uint32_t*>(b + o_slots);
+      ws->fused.flags = reinterpret_cast<uint64_t*>(b + o_flags);
+      ws->fused.hq = reinterpret_cast<uint16_t*>(b + o_fhq);
+      ws->fused.hs = reinterpret_cast<float*>(b + o_fhs);
+    }
     ws->logits = reinterpret_cast<double*>(b + o_log);
     ws->xq = reinterpret_cast<uint16_t*>(b + o_xq);
     ws->xs = reinterpret_cast<float*>(b + o_xs);
@@ -149,7 +222,9 @@ const char* phantom_moe_version(void) { return "phantom_moe 0.1.0 gfx950"; }
 const char* phantom_moe_expert_kernels(int64_t T, int64_t H, int64_t I, int E, int top_k, int has_shared) {
   static thread_local char buf[96];
   const char *gu, *dn;
-  if (pmoe::gemm_regime(T, top_k, E)) {
+  if (pmoe::fused_plan(T, H, I, E, top_k, has_shared ? 1 : 0).ok) {
+    gu = dn = "moe_decode_fused_kernel";  // the whole layer is one launch
+  } else if (pmoe::gemm_regime(T, top_k, E)) {
     const bool ring = pmoe::gemm_uses_ring();
     gu = ring ? "gemm_gate_up_kernel2" : "gemm_gate_up_kernel";
     dn = ring ? "gemm_down_kernel2" : "gemm_down_kernel";
@@ -220,6 +295,57 @@ size_t phantom_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int E, int t
   return pmoe::plan_workspace(T, H, I, E, top_k, has_shared ? 1 : 0, nullptr, nullptr);
 }
 
+int phantom_moe_set_option(int option, int value) {
+  pmoe::LibConfig c = pmoe::lib_config();
+  switch (option) {
+    case PHANTOM_MOE_OPT_DECODE_FUSED:
+      if (value != 0 && value != 1) return fail(PHANTOM_MOE_EINVAL, "DECODE_FUSED takes 0 or 1, got %d", value);
+      c.decode_fused = value != 0;
+      break;
+    case PHANTOM_MOE_OPT_FUSED_WAIT_POLLS:
+      if (value < 1) return fail(PHANTOM_MOE_EINVAL, "FUSED_WAIT_POLLS takes a positive bound, got %d", value);
+      c.fused_wait_polls = (uint32_t)value;
+      break;
+    case PHANTOM_MOE_OPT_FUSED_FAULT:
+      if (value < 0 || value > 3) return fail(PHANTOM_MOE_EINVAL, "FUSED_FAULT takes 0..3, got %d", value);
+      c.fused_fault = (uint32_t)value;
+      break;
+    default:
+      return fail(PHANTOM_MOE_EINVAL, "unknown option %d", option);
+  }
+  pmoe::set_lib_config(c);
+  return ok();
+}
+
+int phantom_moe_get_option(int option, int* value) {
+  if (!value) return fail(PHANTOM_MOE_EINVAL, "get_option: null value");
+  const pmoe::LibConfig c = pmoe::lib_config();
+  switch (option) {
+    case PHANTOM_MOE_OPT_DECODE_FUSED: *value = c.decode_fused ? 1 : 0; break;
+    case PHANTOM_MOE_OPT_FUSED_WAIT_POLLS: *value = (int)c.fused_wait_polls; break;
+    case PHANTOM_MOE_OPT_FUSED_FAULT: *value = (int)c.fused_fault; break;
+    default: return fail(PHANTOM_MOE_EINVAL, "unknown option %d", option);
+  }
+  return ok();
+}
+
+int phantom_moe_workspace_status(void* workspace, size_t workspace_bytes, uint32_t* status, hipStream_t stream) {
+  if (!workspace || !status) return fail(PHANTOM_MOE_EINVAL, "workspace_status: null pointer");
+  if (workspace_bytes < pmoe::kCtlBytes) return fail(PHANTOM_MOE_EWORKSPACE, "workspace_status: workspace too small");
+  uint32_t* word = static_cast<uint32_t*>(workspace) + 1;
+  uint32_t v = 0;
+  hipError_t e = hipMemcpyAsync(&v, word, sizeof(v), hipMemcpyDeviceToHost, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  if (e == hipSuccess && v != 0) {
+    static const uint32_t zero = 0;
+    e = hipMemcpyAsync(word, &zero, sizeof(zero), hipMemcpyHostToDevice, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  }
+  if (e != hipSuccess) return launch_status(e, "workspace_status");
+  *status = v;
+  return ok();
+}
+
 int phantom_moe_route(const void* x, int x_dtype, const float* router_w, const float* router_bias,
                       int64_t T, int64_t H, int E, int top_k, int score_mode, int32_t* topk_idx,
                       float* topk_w, void* workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -288,6 +414,17 @@ int phantom_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_
   if (n_sh != 0 && n_sh != 6)
     return fail(PHANTOM_MOE_EINVAL, "shared expert pointers must be all null or all non-null");
   const int has_shared = n_sh == 6 ? 1 : 0;
+  // the kernels read nibbles with 16-byte and scales with 8-byte loads
+  auto misaligned = [](const void* p, uintptr_t a) { return p && reinterpret_cast<uintptr_t>(p) % a != 0; };
+  if (misaligned(gate_nib, 16) || misaligned(up_nib, 16) || misaligned(down_nib, 16) ||
+      misaligned(sh_gate_nib, 16) || misaligned(sh_up_nib, 16) || misaligned(sh_down_nib, 16))
+    return fail(PHANTOM_MOE_EINVAL, "repacked nibble buffers must be 16-byte aligned");
+  if (misaligned(gate_scale, 8) || misaligned(up_scale, 8) || misaligned(down_scale, 8) ||
+      misaligned(sh_gate_scale, 8) || misaligned(sh_up_scale, 8) || misaligned(sh_down_scale, 8))
+    return fail(PHANTOM_MOE_EINVAL, "repacked scale buffers must be 8-byte aligned");
+  if (misaligned(x, 8) || misaligned(router_w, 16))
+    return fail(PHANTOM_MOE_EINVAL, "x must be 8-byte and router_w 16-byte aligned");
+  if (misaligned(workspace, 256)) return fail(PHANTOM_MOE_EINVAL, "workspace must be 256-byte aligned");
   const size_t need = pmoe::plan_workspace(T, H, I, E, top_k, has_shared, nullptr, nullptr);
   if (!workspace || workspace_bytes < need)
     return fail(PHANTOM_MOE_EWORKSPACE, "workspace of %zu bytes required, %zu given", need,
@@ -307,16 +444,6 @@ int phantom_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_
   r.score_mode = score_mode;
   r.topk_idx = topk_idx;
   r.topk_w = topk_w;
-  const bool gemm = pmoe::gemm_regime(T, top_k, E);
-  r.prep_x = true;
-  r.prep_fp16 = gemm;
-  r.do_permute = true;
-  r.has_shared = has_shared;
-  r.want_tiles = !gemm && (pmoe::gate_up_tile_regime(T, H, I, E, top_k, has_shared) ||
-                           pmoe::down_tile_regime(T, H, I, E, top_k, has_shared));
-  if (int rc = launch_status(record_stage(0, stream), "profile event")) return rc;
-  if (int rc = launch_status(pmoe::launch_route(r, ws, stream), "route")) return rc;
-
   pmoe::ExpertArgs a = {};
   a.T = T;
   a.H = H;
@@ -338,6 +465,32 @@ int phantom_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_
   a.sh_down_scale = sh_down_scale;
   a.topk_w = topk_w;
   a.y = y;
+
+  // Decode batches of a few tokens: the whole layer in one launch.  Its
+  // profile events bracket that launch as the gate/up stage (the router,
+  // down and combine stages are then empty).
+  if (ws.fused.ctl) {
+    const pmoe::FusedPlan pl = pmoe::fused_plan(T, H, I, E, top_k, has_shared);
+    if (pl.ok) {
+      if (int rc = launch_status(record_stage(0, stream), "profile event")) return rc;
+      if (int rc = launch_status(record_stage(1, stream), "profile event")) return rc;
+      if (int rc = launch_status(pmoe::launch_decode_fused(pl, r, a, ws.fused, stream), "decode_fused")) return rc;
+      for (int i = 2; i < PHANTOM_MOE_PROFILE_EVENTS; ++i)
+        if (int rc = launch_status(record_stage(i, stream), "profile event")) return rc;
+      return ok();
+    }
+  }
+
+  const bool gemm = pmoe::gemm_regime(T, top_k, E);
+  r.prep_x = true;
+  r.prep_fp16 = gemm;
+  r.do_permute = true;
+  r.has_shared = has_shared;
+  r.want_tiles = !gemm && (pmoe::gate_up_tile_regime(T, H, I, E, top_k, has_shared) ||
+                           pmoe::down_tile_regime(T, H, I, E, top_k, has_shared));
+  if (int rc = launch_status(record_stage(0, stream), "profile event")) return rc;
+  if (int rc = launch_status(pmoe::launch_route(r, ws, stream), "route")) return rc;
+
   if (int rc = launch_status(record_stage(1, stream), "profile event")) return rc;
   if (int rc = launch_status(gemm ? pmoe::launch_gemm_gate_up(a, ws, stream) : pmoe::launch_gate_up(a, ws, stream),
                              "gate_up"))

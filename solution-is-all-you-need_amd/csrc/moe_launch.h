@@ -23,8 +23,70 @@ inline int64_t max_token_tiles(int64_t T, int k, int E, int has_shared) {
   return (nslots + 15) / 16 + (nslots < E ? nslots : E) + (has_shared ? (T + 15) / 16 : 0);
 }
 
+// ---- the single-launch decode layer (decode_fused.hip) ----------------------
+// Limits of the shapes it takes (the others run the staged launches).
+constexpr int kFusedMaxT = 8;
+constexpr int kFusedMaxLogits = 2048;  // T * E
+constexpr int kFusedMaxSlots = 256;    // T * k
+// Dynamic LDS of one workgroup (the static part is about 8 KB of routing
+// results; a CU has 160 KB).
+constexpr size_t kFusedDynLdsMax = 148 * 1024;
+constexpr int kFusedMaxGrid = 1024;  // workgroups (presence words)
+// Status bits of workspace word 1 (phantom_moe_workspace_status).
+constexpr uint32_t kStatusRouteWait = 1u;     // a workgroup gave up waiting for the logits
+constexpr uint32_t kStatusExpertWait = 2u;    // a down workgroup gave up waiting for gate/up
+constexpr uint32_t kStatusPresenceWait = 4u;  // workgroup 0 gave up waiting for every workgroup's start
+// Bytes at the start of every workspace: word 0 the generation counter of the
+// single-launch path, word 1 the status bits.
+constexpr size_t kCtlBytes = 256;
+
+// Byte offsets of the dynamic LDS regions (decode_fused.hip).
+struct FusedLds {
+  uint32_t x, wgu, wdn;  // x operand, gate/up and down weight staging
+  uint32_t route;        // routing scratch (over the staging, dead before the copies start)
+  uint32_t h, dred;      // h operand and down partials (after the workgroup's gate/up work)
+  uint32_t bytes;        // total
+};
+struct FusedPlan {
+  bool ok;
+  int G;  // workgroups (one per CU)
+  FusedLds lds;
+};
+struct FusedWs {
+  uint32_t* ctl = nullptr;       // workspace words 0 (generation) and 1 (status)
+  uint64_t* presence = nullptr;  // [kFusedMaxGrid]
+  uint32_t* slots = nullptr;     // [T * E][4] tagged logits
+  uint64_t* flags = nullptr;     // [gate/up items] tagged completion flags
+  uint16_t* hq = nullptr;        // [T*k + T][KqI * 256] fp16 hi/lo of h
+  float* hs = nullptr;           // [T*k + T][KqI * 8]
+};
+// Device-independent shape limits (the workspace plan reserves the fused
+// regions for these shapes).
+bool fused_shape_ok(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
+// The launch plan on the current device; .ok false means the staged launches.
+FusedPlan fused_plan(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
+// The dynamic LDS layout for ng gate/up and nd down items per workgroup.
+FusedLds fused_lds_layout(int T, int k, int E, int has_shared, int H, int I, int ng, int nd, int S_max);
+
+// Library options: initialised once from the environment on first use,
+// changed afterwards only by phantom_moe_set_option:
+//   PHANTOM_MOE_DECODE=staged    never take the single-launch decode path
+struct LibConfig {
+  bool decode_fused;
+  uint32_t fused_wait_polls;  // bound of each wait of the single-launch path
+  uint32_t fused_fault;       // failure injection for tests: bit 0 the logit wait, bit 1 the gate/up wait
+};
+// Each poll is one device-scope round trip plus a short sleep (about 1-2 us),
+// so the default bound is far beyond any real wait; it only guarantees that
+// every wave exits.
+constexpr uint32_t kFusedWaitPollsDefault = 1u << 18;
+LibConfig lib_config();
+void set_lib_config(const LibConfig& c);
+
 // Workspace carve-up.  Every region is 256-byte aligned.
 struct Workspace {
+  uint32_t* ctl = nullptr;  // [kCtlBytes / 4]: generation, status
+  FusedWs fused;            // regions of the single-launch path (null when the shape is not fused)
   double* logits = nullptr;         // [T, E]
   uint16_t* xq = nullptr;           // [T, Kpad_h] bf16 bits, MFMA operand order
   float* xs = nullptr;              // [T, Kpad_h / 32] group sums of x
@@ -137,6 +199,10 @@ bool down_tile_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
 // Both stages as one persistent token-tile launch (run by launch_gate_up;
 // launch_down is then a no-op).
 bool ffn_fused_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
+
+// The whole layer in one launch (decode_fused.hip); plan from fused_plan.
+hipError_t launch_decode_fused(const FusedPlan& pl, const RouteArgs& r, const ExpertArgs& x, const FusedWs& ws,
+                               hipStream_t stream);
 
 // The three expert stages; launch_experts runs them back to back.
 hipError_t launch_gate_up(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);

@@ -36,6 +36,7 @@
 
 #include "moe_common.h"
 #include "moe_launch.h"
+#include "topk_common.h"
 
 namespace pmoe {
 
@@ -71,12 +72,6 @@ struct RouteK {
   int32_t* counter;  // select workgroups finished (fused permute); zeroed by the logits launch
   int fuse_permute;
 };
-
-__device__ inline bool ranks_before(double va, int ia, double vb, int ib) {
-  const bool na = isnan(va), nb = isnan(vb);
-  if (na || nb) return (na && nb) ? (ia < ib) : nb;
-  return (va > vb) || (va == vb && ia < ib);
-}
 
 template <typename XT>
 __device__ inline void load_x4(const XT* x, int64_t off, float v[4]);
@@ -358,108 +353,13 @@ __device__ __attribute__((always_inline)) inline void block_permute(const int32_
   }
 }
 
-// Order-preserving integer key of a logit: a > b (as numbers) iff
-// key(a) > key(b), -0.0 and +0.0 share a key, and NaN maps to 1, below every
-// number (-inf has key 0x000F...F), so equal keys are exactly the ties the
-// oracle breaks by index.  Key 0 is left for padding lanes.
-__device__ inline uint64_t logit_key(double v) {
-  if (isnan(v)) return 1ull;
-  if (v == 0.0) v = 0.0;  // -0.0 -> +0.0
-  const uint64_t b = __builtin_bit_cast(uint64_t, v);
-  return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
-}
-
-// Top-k of one token (called by all 64 lanes of one wave); lane l holds
-// experts l, l + 64, ... in registers.
-//  1. Radix descent over the key bits towards the largest x with
-//     #{key >= x} >= k, the k-th largest key (one ballot + popcount per bit
-//     and per register), stopping early at any x with exactly k keys >= x.
-//  2. Winners: every key > x, then keys == x in increasing expert index until
-//     k are taken -- the (value desc, index asc) order's first k.
-//  3. The k winners are compacted to LDS in index order and lane i < k ranks
-//     winner i among them; rank r goes to slot r.
+// Top-k and weights of token t (topk_common.h), from the logits in the
+// workspace to the caller's topk_idx / topk_w (and s_out when non-null).
 template <int NV>
 __device__ void wave_topk(const RouteK& a, int64_t t, uint64_t* s_ck, double* s_cv, int* s_ci,
                           double* s_val, int* s_idx, double* s_e, int* s_out) {
-  const int lane = threadIdx.x % kWave;
-  const uint64_t lt_mask = (1ull << lane) - 1ull;
-  uint64_t key[NV];
-  double val[NV];
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int e = lane + kWave * v;
-    const double lv = a.logits[t * a.E + (e < a.E ? e : a.E - 1)];  // unconditional load
-    val[v] = e < a.E ? lv : 0.0;
-    key[v] = e < a.E ? logit_key(lv) : 0ull;
-  }
-  // Invariant: #{key >= kth} >= k.  Once it is exactly k the winners are
-  // known (every other key is below kth), so the descent stops there --
-  // usually at the first bit that separates the k-th and (k+1)-th keys.
-  uint64_t kth = 0;
-  int at_kth = kWave * NV;
-  for (int bit = 63; bit >= 0 && at_kth != a.k; --bit) {
-    const uint64_t cand = kth | (1ull << bit);
-    int cnt = 0;
-#pragma unroll
-    for (int v = 0; v < NV; ++v) cnt += __popcll(__ballot(key[v] >= cand));
-    if (cnt >= a.k) {
-      kth = cand;
-      at_kth = cnt;
-    }
-  }
-  int n_gt = 0;
-#pragma unroll
-  for (int v = 0; v < NV; ++v) n_gt += __popcll(__ballot(key[v] > kth));
-  const int take_eq = a.k - n_gt;  // >= 1 by the choice of kth
-  int eq_before = 0, sel_before = 0;
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const bool eq = key[v] == kth;
-    const uint64_t meq = __ballot(eq);
-    const bool sel = key[v] > kth || (eq && eq_before + __popcll(meq & lt_mask) < take_eq);
-    const uint64_t msel = __ballot(sel);
-    if (sel) {
-      const int pos = sel_before + __popcll(msel & lt_mask);
-      s_ck[pos] = key[v];
-      s_cv[pos] = val[v];
-      s_ci[pos] = lane + kWave * v;
-    }
-    eq_before += __popcll(meq);
-    sel_before += __popcll(msel);
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  if (lane < a.k) {
-    const uint64_t mk = s_ck[lane];
-    const int me = s_ci[lane];
-    int r = 0;
-    for (int j = 0; j < a.k; ++j) {
-      const uint64_t kj = s_ck[j];
-      r += (kj > mk || (kj == mk && s_ci[j] < me)) ? 1 : 0;
-    }
-    s_idx[r] = me;
-    s_val[r] = s_cv[lane];
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  // Weights: lane i (< k) owns slot i; every lane sums the k terms in slot
-  // order, so the normaliser is the same sequential fp64 sum as the oracle's.
-  double ej = 0.0;
-  if (lane < a.k) {
-    const double v = s_val[lane];
-    ej = (a.score_mode == 0) ? exp(v - s_val[0]) : 1.0 / (1.0 + exp(-v));
-    s_e[lane] = ej;
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  if (lane < a.k) {
-    double sum = 0.0;
-    for (int i = 0; i < a.k; ++i) sum += s_e[i];
-    a.topk_idx[t * a.k + lane] = s_idx[lane];
-    if (s_out) s_out[t * a.k + lane] = s_idx[lane];
-    a.topk_w[t * a.k + lane] = (float)(ej / sum);
-  }
-  __builtin_amdgcn_wave_barrier();
+  wave_topk_row<NV>(a.logits + t * a.E, a.E, a.k, a.score_mode, s_ck, s_cv, s_ci, s_val, s_idx, s_e,
+                    a.topk_idx + t * a.k, a.topk_w + t * a.k, s_out ? s_out + t * a.k : nullptr);
 }
 
 // MFMA-ordered copy of x (bf16) and fp32 group sums for tokens [t0, t0+TT),

@@ -14,7 +14,8 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(ROOT, "csrc")
 INCLUDE = os.path.join(os.path.dirname(ROOT), "include")
-SOURCES = ["q4_repack.hip", "router.hip", "expert_ffn.hip", "expert_gemm.hip", "legacy_ffn.hip", "gate_calibrate.hip", "capi.hip"]
+SOURCES = ["q4_repack.hip", "router.hip", "expert_ffn.hip", "expert_gemm.hip", "decode_fused.hip",
+           "legacy_ffn.hip", "gate_calibrate.hip", "capi.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -41,24 +42,38 @@ def hipcc() -> str:
     return "hipcc"
 
 
+def _compile(src: str, obj: str) -> None:
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    cmd = [hipcc(), *flags, f"-I{INCLUDE}", f"-I{CSRC}", "-c", os.path.join(CSRC, src), "-o", obj]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{res.stderr}")
+
+
 def build(verbose: bool = False) -> str:
-    """Compile all HIP sources into lib/libphantom_moe.so; returns its path."""
+    """Compile all HIP sources (one hipcc per source, in parallel) and link
+    them into lib/libphantom_moe.so; returns its path."""
+    from concurrent.futures import ThreadPoolExecutor
+
     out_dir = os.path.join(PKG_DIR, "lib")
     os.makedirs(out_dir, exist_ok=True)
     out = os.path.join(out_dir, "libphantom_moe.so")
     fd, tmp = tempfile.mkstemp(prefix="libphantom_moe.", suffix=".so.tmp", dir=out_dir)
     os.close(fd)
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}"]
-    cmd += [os.path.join(CSRC, s) for s in SOURCES]
-    cmd += ["-o", tmp]
-    try:
-        res = subprocess.run(cmd, capture_output=True, text=True)
-        if res.returncode != 0:
-            raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{res.stderr}")
-        if verbose and res.stderr:
-            print(res.stderr)
-        os.replace(tmp, out)
-    finally:
-        if os.path.exists(tmp):
-            os.unlink(tmp)
+    with tempfile.TemporaryDirectory(prefix="phantom_moe_build.") as objdir:
+        objs = [os.path.join(objdir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+        jobs = max(1, min(len(SOURCES), len(os.sched_getaffinity(0)), 8))
+        try:
+            with ThreadPoolExecutor(max_workers=jobs) as pool:
+                list(pool.map(_compile, SOURCES, objs))
+            cmd = [hipcc(), *HIPCC_FLAGS, *objs, "-o", tmp]
+            res = subprocess.run(cmd, capture_output=True, text=True)
+            if res.returncode != 0:
+                raise RuntimeError(f"hipcc link failed ({res.returncode}):\n{' '.join(cmd)}\n{res.stderr}")
+            if verbose and res.stderr:
+                print(res.stderr)
+            os.replace(tmp, out)
+        finally:
+            if os.path.exists(tmp):
+                os.unlink(tmp)
     return out

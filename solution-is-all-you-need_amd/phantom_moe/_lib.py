@@ -39,6 +39,9 @@ SIGNATURES = {
     "phantom_q4_0_unrepack": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "phantom_q4_0_dequant_f32": (_int, [_vp, _i64, _i64, _vp, _vp]),
     "phantom_moe_workspace_bytes": (_sz, [_i64, _i64, _i64, _int, _int, _int]),
+    "phantom_moe_workspace_status": (_int, [_vp, _sz, _vp, _vp]),
+    "phantom_moe_set_option": (_int, [_int, _int]),
+    "phantom_moe_get_option": (_int, [_int, _vp]),
     "phantom_moe_route": (_int, [_vp, _int, _vp, _vp, _i64, _i64, _int, _int, _int, _vp, _vp, _vp, _sz, _vp]),
     "phantom_moe_permute": (_int, [_vp, _i64, _int, _int, _vp, _vp, _vp, _vp, _sz, _vp]),
     "phantom_moe_forward": (
@@ -57,6 +60,11 @@ SIGNATURES = {
 
 _lock = threading.Lock()
 _lib = None
+
+
+OPT_DECODE_FUSED = 1  # PHANTOM_MOE_OPT_DECODE_FUSED
+OPT_FUSED_WAIT_POLLS = 3  # PHANTOM_MOE_OPT_FUSED_WAIT_POLLS
+OPT_FUSED_FAULT = 4  # PHANTOM_MOE_OPT_FUSED_FAULT
 
 
 class PhantomMoEError(RuntimeError):
@@ -107,3 +115,22 @@ def check(rc: int, what: str) -> None:
 def stream_handle(device: torch.device | None = None) -> int:
     """hipStream_t of torch's current stream on ``device`` (as an int)."""
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def set_option(option: int, value: int) -> int:
+    """Set a library option (include/phantom_moe.h); returns the previous value."""
+    lib = load()
+    old = ctypes.c_int()
+    check(lib.phantom_moe_get_option(option, ctypes.byref(old)), "phantom_moe_get_option")
+    check(lib.phantom_moe_set_option(option, value), "phantom_moe_set_option")
+    return old.value
+
+
+def workspace_status(ws: torch.Tensor) -> int:
+    """Status bits the single-launch decode path left in workspace ``ws``
+    (0 = every call completed normally); waits for the stream and clears them."""
+    lib = load()
+    st = ctypes.c_uint32()
+    check(lib.phantom_moe_workspace_status(ws.data_ptr(), ws.numel() * ws.element_size(), ctypes.byref(st),
+                                           stream_handle(ws.device)), "phantom_moe_workspace_status")
+    return st.value

@@ -46,13 +46,14 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Workspace of at least nbytes for (device, current stream).
 
     Cached per (device, stream) so calls on one stream reuse it in order;
-    grows when a larger one is asked for.  It carries no state between calls."""
+    grows when a larger one is asked for.  Zero-filled when allocated (the
+    library keeps the call counter of its single-launch path in it)."""
     stream = _lib.stream_handle(device)
     key = (device.index, stream)
     with _ws_lock:
         ws = _workspaces.get(key)
         if ws is None or ws.numel() < nbytes:
-            ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+            ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
             _workspaces[key] = ws
         return ws
 
@@ -242,7 +243,7 @@ class PreparedForward:
         lib = _lib.load()
         has_sh = experts.shared is not None
         nbytes = lib.phantom_moe_workspace_bytes(T, H, I, E, top_k, int(has_sh))
-        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         sh = [t.data_ptr() for t in experts.shared] if has_sh else [None] * 6
         self._fn = lib.phantom_moe_forward
         self._args = [

@@ -1,0 +1,222 @@
+"""The single-launch decode layer (csrc/decode_fused.hip) against the oracle
+and against the staged launches, through the C ABI.
+
+Routing indices and their order must be bit-exact; outputs within the layer
+tolerance of the fp64 oracle (helpers.check_y).  The outputs must also be
+identical bit for bit across repeated calls (each call's hand-off tags come
+from the workspace call counter; a stale tag accepted would change the
+output).
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import phantom_moe  # noqa: E402
+from helpers import check_y, oracle_for_device_layer, to_bf16_tensor  # noqa: E402
+from oracle import oracle  # noqa: E402
+from phantom_moe import _lib, synth  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+FUSED = "gate_up=moe_decode_fused_kernel;down=moe_decode_fused_kernel"
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+@pytest.fixture
+def option():
+    """Set library options for one test and restore them afterwards."""
+    saved = []
+
+    def set_(opt, value):
+        saved.append((opt, _lib.set_option(opt, value)))
+
+    yield set_
+    for opt, value in reversed(saved):
+        _lib.set_option(opt, value)
+
+
+def kernels(cfg):
+    return _lib.load().phantom_moe_expert_kernels(cfg.T, cfg.H, cfg.I, cfg.E, cfg.k, int(cfg.shared)).decode()
+
+
+def dev_weights(L, dev):
+    sh = None
+    if L.shared is not None:
+        sh = tuple(torch.from_numpy(a).to(dev) for a in L.shared)
+    return phantom_moe.MoEWeights.from_q4_0(
+        torch.from_numpy(L.gate).to(dev), torch.from_numpy(L.up).to(dev), torch.from_numpy(L.down).to(dev),
+        L.cfg.H, L.cfg.I, L.cfg.E, shared=sh)
+
+
+def run(prep, stream=None):
+    prep(stream)
+    return prep.y.clone(), prep.topk_w.clone(), prep.topk_idx.clone()
+
+
+CASES = [
+    synth.MoEConfig("f_t1", 512, 256, 32, 8, 1),
+    synth.MoEConfig("f_t1_e16_k4", 256, 128, 16, 4, 1),
+    synth.MoEConfig("f_t2", 256, 128, 16, 4, 2),
+    synth.MoEConfig("f_t4_sigmoid_shared", 512, 128, 32, 4, 4, score="sigmoid", shared=True),
+    synth.MoEConfig("f_t8", 256, 128, 16, 4, 8),
+    synth.MoEConfig("f_ragged", 96, 96, 8, 2, 3),
+    synth.MoEConfig("f_ragged_i", 384, 160, 24, 3, 2),
+    synth.MoEConfig("f_k1", 128, 32, 4, 1, 3),
+    synth.MoEConfig("f_zipf", 1024, 256, 128, 8, 1, zipf=1.1),
+    synth.MoEConfig("f_e512", 256, 64, 512, 32, 1),
+    synth.MoEConfig("f_e1", 128, 64, 1, 1, 2),
+    synth.MoEConfig("f_e64_k64", 128, 64, 64, 32, 2),
+]
+
+
+@pytest.mark.parametrize("cfg", CASES, ids=lambda c: c.name)
+def test_fused_vs_oracle_and_staged(dev, cfg, option):
+    assert kernels(cfg) == FUSED, f"{cfg.name} is not in the single-launch regime"
+    L = synth.host_layer(cfg)
+    xb = synth.activations(cfg.T, cfg.H, seed=len(cfg.name) * 13)
+    ex = dev_weights(L, dev)
+    b = None if L.router_bias is None else torch.from_numpy(L.router_bias).to(dev)
+    W = torch.from_numpy(L.router_w).to(dev)
+    prep = phantom_moe.PreparedForward(ex, W, cfg.T, cfg.k, cfg.score, b, x=to_bf16_tensor(xb, dev))
+    ry, ridx, rw = oracle.moe_forward(xb, L.router_w, L.gate, L.up, L.down, cfg.k, cfg.score_mode,
+                                      L.router_bias, shared=L.shared)
+    outs = [run(prep) for _ in range(3)]
+    torch.cuda.synchronize()
+    assert _lib.workspace_status(prep.workspace) == 0
+    y, w, idx = outs[0]
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-6, atol=1e-7)
+    check_y(y.cpu().numpy(), ry, cfg.name + " fused")
+    for i, (yi, wi, ii) in enumerate(outs[1:], 2):
+        assert torch.equal(yi, y) and torch.equal(wi, w) and torch.equal(ii, idx), f"call {i} differs"
+    # the staged launches give the same routing and meet the same tolerance
+    option(_lib.OPT_DECODE_FUSED, 0)
+    assert kernels(cfg) != FUSED
+    ys, ws_, iss = run(prep)
+    np.testing.assert_array_equal(iss.cpu().numpy(), ridx)
+    assert torch.equal(ws_, w)
+    check_y(ys.cpu().numpy(), ry, cfg.name + " staged")
+
+
+def test_fused_full_size_qwen3_t1(dev):
+    """The batch-1 Qwen3-30B-A3B-shaped layer (H 2048, I 768, E 128, top-8)
+    takes the single-launch path and matches the oracle."""
+    cfg = synth.CONFIGS["qwen3_decode_t1"]
+    assert kernels(cfg) == FUSED
+    dl = synth.device_layer(cfg, dev)
+    ex = phantom_moe.MoEWeights.from_q4_0(dl.gate, dl.up, dl.down, cfg.H, cfg.I, cfg.E)
+    for seed in (42, 43, 44):
+        xb = synth.activations(cfg.T, cfg.H, seed=seed)
+        prep = phantom_moe.PreparedForward(ex, dl.router_w, cfg.T, cfg.k, cfg.score, dl.router_bias,
+                                           x=to_bf16_tensor(xb, dev))
+        y, w, idx = run(prep)
+        assert _lib.workspace_status(prep.workspace) == 0
+        ry, ridx, rw = oracle_for_device_layer(dl, xb)
+        np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+        np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-6, atol=1e-7)
+        err, rel = check_y(y.cpu().numpy(), ry, f"qwen3_decode_t1 seed {seed}")
+        print(f"[case] qwen3_decode_t1 seed {seed}: max_abs={err:.2e} rel_l2={rel:.2e}", flush=True)
+
+
+def test_fused_graph_replays(dev):
+    """Replays of a captured single-launch layer (three dependent calls) each
+    draw fresh hand-off tags from the workspace counter: every replay, with
+    eager calls on the same workspace between replays, equals the eager
+    result bit for bit."""
+    cfg = synth.MoEConfig("g_t1", 512, 256, 32, 8, 1)
+    L = synth.host_layer(cfg)
+    ex = dev_weights(L, dev)
+    W = torch.from_numpy(L.router_w).to(dev)
+    xs = [to_bf16_tensor(synth.activations(1, cfg.H, seed=s), dev) for s in (1, 2, 3)]
+    prep = phantom_moe.PreparedForward(ex, W, 1, cfg.k, x=xs[0].clone())
+    assert kernels(cfg) == FUSED
+    eager = []
+    for x in xs:
+        prep.x.copy_(x)
+        eager.append(run(prep)[0])
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    outs = [torch.empty_like(eager[0]) for _ in xs]
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        for x, o in zip(xs, outs):
+            prep.x.copy_(x)
+            prep(_lib.stream_handle(dev))
+            o.copy_(prep.y)
+    for rep in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, eager)):
+            assert torch.equal(o, e), f"replay {rep}, call {i} differs"
+        prep.x.copy_(xs[rep % 3])
+        assert torch.equal(run(prep)[0], eager[rep % 3])
+        torch.cuda.synchronize()
+    assert _lib.workspace_status(prep.workspace) == 0
+
+
+@pytest.mark.parametrize("fault", [1, 2])
+def test_fused_wait_failure_is_reported(dev, option, fault):
+    """A wait that gives up (forced from the host: the waiters expect a tag
+    nobody writes, with a short bound) ends normally, sets the workspace
+    status and leaves NaN in the outputs it could not compute; the next call
+    is correct again."""
+    cfg = synth.MoEConfig("fail_t1", 256, 128, 16, 4, 1)
+    L = synth.host_layer(cfg)
+    ex = dev_weights(L, dev)
+    W = torch.from_numpy(L.router_w).to(dev)
+    xb = synth.activations(1, cfg.H, seed=9)
+    prep = phantom_moe.PreparedForward(ex, W, 1, cfg.k, x=to_bf16_tensor(xb, dev))
+    assert kernels(cfg) == FUSED
+    y_ok, w_ok, i_ok = run(prep)
+    option(_lib.OPT_FUSED_WAIT_POLLS, 64)
+    option(_lib.OPT_FUSED_FAULT, fault)
+    y, w, idx = run(prep)
+    torch.cuda.synchronize()
+    st = _lib.workspace_status(prep.workspace)
+    assert st & fault, f"status {st:#x} lacks bit {fault:#x}"
+    assert torch.isnan(y).all()
+    if fault == 1:
+        assert (idx == -1).all() and torch.isnan(w).all()
+    else:
+        assert torch.equal(idx, i_ok) and torch.equal(w, w_ok)
+    _lib.set_option(_lib.OPT_FUSED_FAULT, 0)
+    y2, _, _ = run(prep)
+    assert _lib.workspace_status(prep.workspace) == 0
+    assert torch.equal(y2, y_ok)
+
+
+def test_fused_nonfinite_activations(dev):
+    """NaN and +-inf in x: no fault, routing as the oracle's contract gives it
+    (NaN logits rank below every number, ties to the lower index), the other
+    tokens unaffected; the staged launches route identically."""
+    cfg = synth.MoEConfig("nan_t4", 256, 128, 16, 4, 4)
+    L = synth.host_layer(cfg)
+    ex = dev_weights(L, dev)
+    W = torch.from_numpy(L.router_w).to(dev)
+    xb = synth.activations(cfg.T, cfg.H, seed=3)
+    xb[1, 17] = 0x7FC0  # NaN
+    xb[2, 5] = 0x7F80   # +inf
+    xb[2, 6] = 0xFF80   # -inf
+    prep = phantom_moe.PreparedForward(ex, W, cfg.T, cfg.k, x=to_bf16_tensor(xb, dev))
+    assert kernels(cfg) == FUSED
+    y, w, idx = run(prep)
+    torch.cuda.synchronize()
+    assert _lib.workspace_status(prep.workspace) == 0
+    ridx, _ = oracle.route(xb, L.router_w, cfg.k, 0)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    ok = [0, 3]
+    ry, _, _ = oracle.moe_forward(xb[ok], L.router_w, L.gate, L.up, L.down, cfg.k)
+    check_y(y.cpu().numpy()[ok], ry, "finite tokens")
+    old = _lib.set_option(_lib.OPT_DECODE_FUSED, 0)
+    try:
+        ys, ws_, iss = run(prep)
+    finally:
+        _lib.set_option(_lib.OPT_DECODE_FUSED, old)
+    assert torch.equal(iss, idx)
