@@ -193,6 +193,29 @@ PHANTOM_MOE_API int phantom_moe_forward(const void* x, int x_dtype, int64_t T, i
                         int32_t* topk_idx, float* topk_w, void* workspace, size_t workspace_bytes,
                         hipStream_t stream);
 
+/* phantom_moe_forward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * scratch is a 16 MiB array in the library's device memory, one per GPU,
+ * held until the process ends; the call allocates nothing.  Sizes whose
+ * workspace (phantom_moe_workspace_bytes) exceeds 16 MiB return
+ * PHANTOM_MOE_EWORKSPACE -- with H 2048, I 768, E 128, top-8 that is
+ * T <= 128 tokens.  Every call on one GPU shares that GPU's array, so calls
+ * that may overlap on one GPU (different streams without ordering between
+ * them) race and must not be issued.  The status word of the single-launch
+ * path is not readable here: a wait that gives up shows as NaN outputs (and
+ * topk_idx -1 when the routing was lost). */
+PHANTOM_MOE_API int phantom_moe_forward_static(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int E,
+                                               int top_k, int score_mode, const float* router_w,
+                                               const float* router_bias, const uint8_t* gate_nib,
+                                               const uint16_t* gate_scale, const uint8_t* up_nib,
+                                               const uint16_t* up_scale, const uint8_t* down_nib,
+                                               const uint16_t* down_scale, const uint8_t* sh_gate_nib,
+                                               const uint16_t* sh_gate_scale, const uint8_t* sh_up_nib,
+                                               const uint16_t* sh_up_scale, const uint8_t* sh_down_nib,
+                                               const uint16_t* sh_down_scale, float* y, int32_t* topk_idx,
+                                               float* topk_w, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

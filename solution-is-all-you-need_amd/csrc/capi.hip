@@ -213,6 +213,179 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
 
 }  // namespace pmoe
 
+
+// Scratch of phantom_moe_forward_static: one copy per GPU, held until the
+// process ends.  Static storage starts zeroed, which is the state a fresh
+// workspace must start in (its first 256 bytes hold the call counter of the
+// single-launch path).  In host code `scratch` only names the symbol; its
+// device address comes from hipGetSymbolAddress, per device.
+constexpr size_t kStaticScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The device address of the current device's scratch, looked up on the
+// device's first call.
+int static_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return launch_status(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(PHANTOM_MOE_EUNSUPPORTED, "device %d above %d", dev, kMaxDevices - 1);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return launch_status(e, "hipGetSymbolAddress(scratch)");
+      if (!p || reinterpret_cast<uintptr_t>(p) % 256)
+        return fail(PHANTOM_MOE_ELAUNCH, "static scratch address %p is not 256-byte aligned", p);
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return 0;
+}
+
+bool misaligned(const void* p, uintptr_t a) { return p && reinterpret_cast<uintptr_t>(p) % a != 0; }
+
+// The arguments of one layer call (both forward entry points).
+struct ForwardCall {
+  const void* x;
+  int x_dtype;
+  int64_t T, H, I;
+  int E, top_k, score_mode;
+  const float* router_w;
+  const float* router_bias;
+  const uint8_t* gate_nib;
+  const uint16_t* gate_scale;
+  const uint8_t* up_nib;
+  const uint16_t* up_scale;
+  const uint8_t* down_nib;
+  const uint16_t* down_scale;
+  const uint8_t* sh_gate_nib;
+  const uint16_t* sh_gate_scale;
+  const uint8_t* sh_up_nib;
+  const uint16_t* sh_up_scale;
+  const uint8_t* sh_down_nib;
+  const uint16_t* sh_down_scale;
+  float* y;
+  int32_t* topk_idx;
+  float* topk_w;
+  int has_shared;  // set by check_forward
+};
+
+int check_forward(ForwardCall& c) {
+  if (int rc = check_route_shapes(c.x, c.x_dtype, c.router_w, c.T, c.H, c.E, c.top_k, c.score_mode)) return rc;
+  if (c.x_dtype != PHANTOM_MOE_X_BF16)
+    return fail(PHANTOM_MOE_EUNSUPPORTED, "phantom_moe_forward takes bf16 activations (x_dtype 0)");
+  if (c.I < 32 || c.I % 32)
+    return fail(PHANTOM_MOE_EINVAL, "I must be a positive multiple of 32, got %lld", (long long)c.I);
+  if (!c.gate_nib || !c.gate_scale || !c.up_nib || !c.up_scale || !c.down_nib || !c.down_scale)
+    return fail(PHANTOM_MOE_EINVAL, "expert weight pointers must be non-null");
+  if (!c.y || !c.topk_idx || !c.topk_w) return fail(PHANTOM_MOE_EINVAL, "y, topk_idx and topk_w must be non-null");
+  const int n_sh = (c.sh_gate_nib != nullptr) + (c.sh_gate_scale != nullptr) + (c.sh_up_nib != nullptr) +
+                   (c.sh_up_scale != nullptr) + (c.sh_down_nib != nullptr) + (c.sh_down_scale != nullptr);
+  if (n_sh != 0 && n_sh != 6)
+    return fail(PHANTOM_MOE_EINVAL, "shared expert pointers must be all null or all non-null");
+  c.has_shared = n_sh == 6 ? 1 : 0;
+  // the kernels read nibbles with 16-byte and scales with 8-byte loads
+  if (misaligned(c.gate_nib, 16) || misaligned(c.up_nib, 16) || misaligned(c.down_nib, 16) ||
+      misaligned(c.sh_gate_nib, 16) || misaligned(c.sh_up_nib, 16) || misaligned(c.sh_down_nib, 16))
+    return fail(PHANTOM_MOE_EINVAL, "repacked nibble buffers must be 16-byte aligned");
+  if (misaligned(c.gate_scale, 8) || misaligned(c.up_scale, 8) || misaligned(c.down_scale, 8) ||
+      misaligned(c.sh_gate_scale, 8) || misaligned(c.sh_up_scale, 8) || misaligned(c.sh_down_scale, 8))
+    return fail(PHANTOM_MOE_EINVAL, "repacked scale buffers must be 8-byte aligned");
+  if (misaligned(c.x, 8) || misaligned(c.router_w, 16))
+    return fail(PHANTOM_MOE_EINVAL, "x must be 8-byte and router_w 16-byte aligned");
+  return 0;
+}
+
+// Launch the layer on a workspace already checked to be large enough.
+int run_forward(const ForwardCall& c, void* workspace, hipStream_t stream) {
+  const int64_t T = c.T, H = c.H, I = c.I;
+  const int E = c.E, top_k = c.top_k, has_shared = c.has_shared;
+  pmoe::Workspace ws;
+  pmoe::plan_workspace(T, H, I, E, top_k, has_shared, workspace, &ws);
+
+  pmoe::RouteArgs r = {};
+  r.x = c.x;
+  r.x_dtype = c.x_dtype;
+  r.router_w = c.router_w;
+  r.router_bias = c.router_bias;
+  r.T = T;
+  r.H = H;
+  r.E = E;
+  r.k = top_k;
+  r.score_mode = c.score_mode;
+  r.topk_idx = c.topk_idx;
+  r.topk_w = c.topk_w;
+  pmoe::ExpertArgs a = {};
+  a.T = T;
+  a.H = H;
+  a.I = I;
+  a.E = E;
+  a.k = top_k;
+  a.has_shared = has_shared;
+  a.gate_nib = c.gate_nib;
+  a.gate_scale = c.gate_scale;
+  a.up_nib = c.up_nib;
+  a.up_scale = c.up_scale;
+  a.down_nib = c.down_nib;
+  a.down_scale = c.down_scale;
+  a.sh_gate_nib = c.sh_gate_nib;
+  a.sh_gate_scale = c.sh_gate_scale;
+  a.sh_up_nib = c.sh_up_nib;
+  a.sh_up_scale = c.sh_up_scale;
+  a.sh_down_nib = c.sh_down_nib;
+  a.sh_down_scale = c.sh_down_scale;
+  a.topk_w = c.topk_w;
+  a.y = c.y;
+
+  // Decode batches of a few tokens: the whole layer in one launch.  Its
+  // profile events bracket that launch as the gate/up stage (the router,
+  // down and combine stages are then empty).
+  if (ws.fused.ctl) {
+    const pmoe::FusedPlan pl = pmoe::fused_plan(T, H, I, E, top_k, has_shared);
+    if (pl.ok) {
+      if (int rc = launch_status(record_stage(0, stream), "profile event")) return rc;
+      if (int rc = launch_status(record_stage(1, stream), "profile event")) return rc;
+      if (int rc = launch_status(pmoe::launch_decode_fused(pl, r, a, ws.fused, stream), "decode_fused")) return rc;
+      for (int i = 2; i < PHANTOM_MOE_PROFILE_EVENTS; ++i)
+        if (int rc = launch_status(record_stage(i, stream), "profile event")) return rc;
+      return ok();
+    }
+  }
+
+  const bool gemm = pmoe::gemm_regime(T, top_k, E);
+  r.prep_x = true;
+  r.prep_fp16 = gemm;
+  r.do_permute = true;
+  r.has_shared = has_shared;
+  r.want_tiles = !gemm && (pmoe::gate_up_tile_regime(T, H, I, E, top_k, has_shared) ||
+                           pmoe::down_tile_regime(T, H, I, E, top_k, has_shared));
+  if (int rc = launch_status(record_stage(0, stream), "profile event")) return rc;
+  if (int rc = launch_status(pmoe::launch_route(r, ws, stream), "route")) return rc;
+
+  if (int rc = launch_status(record_stage(1, stream), "profile event")) return rc;
+  if (int rc = launch_status(gemm ? pmoe::launch_gemm_gate_up(a, ws, stream) : pmoe::launch_gate_up(a, ws, stream),
+                             "gate_up"))
+    return rc;
+  if (int rc = launch_status(record_stage(2, stream), "profile event")) return rc;
+  if (int rc = launch_status(gemm ? pmoe::launch_gemm_down(a, ws, stream) : pmoe::launch_down(a, ws, stream),
+                             "down"))
+    return rc;
+  if (int rc = launch_status(record_stage(3, stream), "profile event")) return rc;
+  if (int rc = launch_status(pmoe::launch_combine(a, ws, stream), "combine")) return rc;
+  return launch_status(record_stage(4, stream), "profile event");
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* phantom_moe_last_error(void) { return g_err; }
@@ -402,106 +575,41 @@ int phantom_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_
                         const uint8_t* sh_down_nib, const uint16_t* sh_down_scale, float* y,
                         int32_t* topk_idx, float* topk_w, void* workspace, size_t workspace_bytes,
                         hipStream_t stream) {
-  if (int rc = check_route_shapes(x, x_dtype, router_w, T, H, E, top_k, score_mode)) return rc;
-  if (x_dtype != PHANTOM_MOE_X_BF16)
-    return fail(PHANTOM_MOE_EUNSUPPORTED, "phantom_moe_forward takes bf16 activations (x_dtype 0)");
-  if (I < 32 || I % 32) return fail(PHANTOM_MOE_EINVAL, "I must be a positive multiple of 32, got %lld", (long long)I);
-  if (!gate_nib || !gate_scale || !up_nib || !up_scale || !down_nib || !down_scale)
-    return fail(PHANTOM_MOE_EINVAL, "expert weight pointers must be non-null");
-  if (!y || !topk_idx || !topk_w) return fail(PHANTOM_MOE_EINVAL, "y, topk_idx and topk_w must be non-null");
-  const int n_sh = (sh_gate_nib != nullptr) + (sh_gate_scale != nullptr) + (sh_up_nib != nullptr) +
-                   (sh_up_scale != nullptr) + (sh_down_nib != nullptr) + (sh_down_scale != nullptr);
-  if (n_sh != 0 && n_sh != 6)
-    return fail(PHANTOM_MOE_EINVAL, "shared expert pointers must be all null or all non-null");
-  const int has_shared = n_sh == 6 ? 1 : 0;
-  // the kernels read nibbles with 16-byte and scales with 8-byte loads
-  auto misaligned = [](const void* p, uintptr_t a) { return p && reinterpret_cast<uintptr_t>(p) % a != 0; };
-  if (misaligned(gate_nib, 16) || misaligned(up_nib, 16) || misaligned(down_nib, 16) ||
-      misaligned(sh_gate_nib, 16) || misaligned(sh_up_nib, 16) || misaligned(sh_down_nib, 16))
-    return fail(PHANTOM_MOE_EINVAL, "repacked nibble buffers must be 16-byte aligned");
-  if (misaligned(gate_scale, 8) || misaligned(up_scale, 8) || misaligned(down_scale, 8) ||
-      misaligned(sh_gate_scale, 8) || misaligned(sh_up_scale, 8) || misaligned(sh_down_scale, 8))
-    return fail(PHANTOM_MOE_EINVAL, "repacked scale buffers must be 8-byte aligned");
-  if (misaligned(x, 8) || misaligned(router_w, 16))
-    return fail(PHANTOM_MOE_EINVAL, "x must be 8-byte and router_w 16-byte aligned");
+  ForwardCall c = {x, x_dtype, T, H, I, E, top_k, score_mode, router_w, router_bias,
+                   gate_nib, gate_scale, up_nib, up_scale, down_nib, down_scale,
+                   sh_gate_nib, sh_gate_scale, sh_up_nib, sh_up_scale, sh_down_nib, sh_down_scale,
+                   y, topk_idx, topk_w, 0};
+  if (int rc = check_forward(c)) return rc;
   if (misaligned(workspace, 256)) return fail(PHANTOM_MOE_EINVAL, "workspace must be 256-byte aligned");
-  const size_t need = pmoe::plan_workspace(T, H, I, E, top_k, has_shared, nullptr, nullptr);
+  const size_t need = pmoe::plan_workspace(T, H, I, E, top_k, c.has_shared, nullptr, nullptr);
   if (!workspace || workspace_bytes < need)
     return fail(PHANTOM_MOE_EWORKSPACE, "workspace of %zu bytes required, %zu given", need,
                 workspace ? workspace_bytes : (size_t)0);
-  pmoe::Workspace ws;
-  pmoe::plan_workspace(T, H, I, E, top_k, has_shared, workspace, &ws);
+  return run_forward(c, workspace, stream);
+}
 
-  pmoe::RouteArgs r = {};
-  r.x = x;
-  r.x_dtype = x_dtype;
-  r.router_w = router_w;
-  r.router_bias = router_bias;
-  r.T = T;
-  r.H = H;
-  r.E = E;
-  r.k = top_k;
-  r.score_mode = score_mode;
-  r.topk_idx = topk_idx;
-  r.topk_w = topk_w;
-  pmoe::ExpertArgs a = {};
-  a.T = T;
-  a.H = H;
-  a.I = I;
-  a.E = E;
-  a.k = top_k;
-  a.has_shared = has_shared;
-  a.gate_nib = gate_nib;
-  a.gate_scale = gate_scale;
-  a.up_nib = up_nib;
-  a.up_scale = up_scale;
-  a.down_nib = down_nib;
-  a.down_scale = down_scale;
-  a.sh_gate_nib = sh_gate_nib;
-  a.sh_gate_scale = sh_gate_scale;
-  a.sh_up_nib = sh_up_nib;
-  a.sh_up_scale = sh_up_scale;
-  a.sh_down_nib = sh_down_nib;
-  a.sh_down_scale = sh_down_scale;
-  a.topk_w = topk_w;
-  a.y = y;
-
-  // Decode batches of a few tokens: the whole layer in one launch.  Its
-  // profile events bracket that launch as the gate/up stage (the router,
-  // down and combine stages are then empty).
-  if (ws.fused.ctl) {
-    const pmoe::FusedPlan pl = pmoe::fused_plan(T, H, I, E, top_k, has_shared);
-    if (pl.ok) {
-      if (int rc = launch_status(record_stage(0, stream), "profile event")) return rc;
-      if (int rc = launch_status(record_stage(1, stream), "profile event")) return rc;
-      if (int rc = launch_status(pmoe::launch_decode_fused(pl, r, a, ws.fused, stream), "decode_fused")) return rc;
-      for (int i = 2; i < PHANTOM_MOE_PROFILE_EVENTS; ++i)
-        if (int rc = launch_status(record_stage(i, stream), "profile event")) return rc;
-      return ok();
-    }
-  }
-
-  const bool gemm = pmoe::gemm_regime(T, top_k, E);
-  r.prep_x = true;
-  r.prep_fp16 = gemm;
-  r.do_permute = true;
-  r.has_shared = has_shared;
-  r.want_tiles = !gemm && (pmoe::gate_up_tile_regime(T, H, I, E, top_k, has_shared) ||
-                           pmoe::down_tile_regime(T, H, I, E, top_k, has_shared));
-  if (int rc = launch_status(record_stage(0, stream), "profile event")) return rc;
-  if (int rc = launch_status(pmoe::launch_route(r, ws, stream), "route")) return rc;
-
-  if (int rc = launch_status(record_stage(1, stream), "profile event")) return rc;
-  if (int rc = launch_status(gemm ? pmoe::launch_gemm_gate_up(a, ws, stream) : pmoe::launch_gate_up(a, ws, stream),
-                             "gate_up"))
-    return rc;
-  if (int rc = launch_status(record_stage(2, stream), "profile event")) return rc;
-  if (int rc = launch_status(gemm ? pmoe::launch_gemm_down(a, ws, stream) : pmoe::launch_down(a, ws, stream),
-                             "down"))
-    return rc;
-  if (int rc = launch_status(record_stage(3, stream), "profile event")) return rc;
-  if (int rc = launch_status(pmoe::launch_combine(a, ws, stream), "combine")) return rc;
-  return launch_status(record_stage(4, stream), "profile event");
+int phantom_moe_forward_static(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int E, int top_k,
+                               int score_mode, const float* router_w, const float* router_bias,
+                               const uint8_t* gate_nib, const uint16_t* gate_scale, const uint8_t* up_nib,
+                               const uint16_t* up_scale, const uint8_t* down_nib, const uint16_t* down_scale,
+                               const uint8_t* sh_gate_nib, const uint16_t* sh_gate_scale,
+                               const uint8_t* sh_up_nib, const uint16_t* sh_up_scale,
+                               const uint8_t* sh_down_nib, const uint16_t* sh_down_scale, float* y,
+                               int32_t* topk_idx, float* topk_w, hipStream_t stream) {
+  ForwardCall c = {x, x_dtype, T, H, I, E, top_k, score_mode, router_w, router_bias,
+                   gate_nib, gate_scale, up_nib, up_scale, down_nib, down_scale,
+                   sh_gate_nib, sh_gate_scale, sh_up_nib, sh_up_scale, sh_down_nib, sh_down_scale,
+                   y, topk_idx, topk_w, 0};
+  if (int rc = check_forward(c)) return rc;
+  const size_t need = pmoe::plan_workspace(T, H, I, E, top_k, c.has_shared, nullptr, nullptr);
+  if (need > kStaticScratchBytes)
+    return fail(PHANTOM_MOE_EWORKSPACE,
+                "phantom_moe_forward_static: these sizes need %zu bytes of scratch, the static scratch holds %zu "
+                "(use phantom_moe_forward with a workspace)",
+                need, kStaticScratchBytes);
+  void* base = nullptr;
+  if (int rc = static_scratch(&base)) return rc;
+  return run_forward(c, base, stream);
 }
 
 }  // extern "C"

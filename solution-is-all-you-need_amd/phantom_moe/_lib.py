@@ -51,6 +51,10 @@ SIGNATURES = {
         + [_vp] * 6
         + [_vp, _vp, _vp, _vp, _sz, _vp],
     ),
+    "phantom_moe_forward_static": (
+        _int,
+        [_vp, _int, _i64, _i64, _i64, _int, _int, _int, _vp, _vp] + [_vp] * 6 + [_vp] * 6 + [_vp, _vp, _vp, _vp],
+    ),
     # include/phantom_legacy.h: the reference's own symbol names and order
     "sparse_mlp_forward": (_f32, [_vp] * 9 + [_int, _int, _int, _f32, _vp]),
     "predict_active_neurons": (_f32, [_vp] * 7 + [_int, _int, _int, _f32, _vp]),
