@@ -159,17 +159,24 @@ def layer_flops(cfg) -> int:
 
 def cpu_info():
     """CPU model and SIMD feature flags of this host (/proc/cpuinfo)."""
-    model, flags = "unknown", []
+    model, flags, ids = "unknown", [], {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name") and model == "unknown":
+                key = line.split(":", 1)[0].strip()
+                if key == "model name" and model == "unknown":
                     model = line.split(":", 1)[1].strip()
-                elif line.startswith("flags"):
+                elif key in ("cpu family", "model", "stepping") and key not in ids:
+                    ids[key] = line.split(":", 1)[1].strip()
+                elif key == "flags":
                     flags = line.split(":", 1)[1].split()
                     break
     except OSError:
         pass
+    if ids:
+        # the family/model/stepping numbers name the part where a hypervisor
+        # shortens the model string
+        model += " (family %s, model %s, stepping %s)" % (ids.get("cpu family"), ids.get("model"), ids.get("stepping"))
     simd = sorted(f for f in flags if f.startswith(("avx", "amx", "fma", "f16c", "sse4", "vnni")))
     return model, simd
 
@@ -520,9 +527,15 @@ def bench_moe(args, cfg, with_cpu: bool) -> dict:
             "avg_launch_us": round(gu_ms * 1e3 / args.steps, 3),
         })
         lay_ms = float(np.sum(layer_ms))
+        stage_us = {k: round(float(np.mean(v)) * 1e3, 3) for k, v in stages.items()}
+        if fused:
+            # one kernel: the events around it are the layer; the others
+            # bracket nothing but each other
+            lay_ms = gu_ms
+            stage_us = {"single_launch": stage_us["gate_up"]}
         out["layer"] = {
             "gpu_us_per_step": round(lay_ms * 1e3 / args.steps, 3),
-            "stage_us": {k: round(float(np.mean(v)) * 1e3, 3) for k, v in stages.items()},
+            "stage_us": stage_us,
             "hbm_achieved_gbs": round(lay_bytes / (lay_ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(lay_bytes / (lay_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "tflops": round(layer_flops(cfg) * args.steps / (lay_ms * 1e-3) / 1e12, 3),

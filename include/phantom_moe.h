@@ -137,9 +137,10 @@ PHANTOM_MOE_API int phantom_moe_workspace_status(void* workspace, size_t workspa
                                                  hipStream_t stream);
 
 /* Library options (process-wide; initialised from the environment on first
- * use: PHANTOM_MOE_DECODE=staged).  A/B and test switches with no
- * counterpart in the reference. */
+ * use: PHANTOM_MOE_DECODE=staged, PHANTOM_MOE_DECODE_KSPLIT=1).  A/B and
+ * test switches with no counterpart in the reference. */
 #define PHANTOM_MOE_OPT_DECODE_FUSED 1 /* 1: decode batches that fit take the single-launch path (default) */
+#define PHANTOM_MOE_OPT_DECODE_KSPLIT 2 /* 1: staged decode expert stages always as the K-split kernels (default 0) */
 #define PHANTOM_MOE_OPT_FUSED_WAIT_POLLS 3 /* bound of each wait of the single-launch path (default 2^18 polls) */
 /* Failure injection for tests of the error path: bit 0 makes the logit wait,
  * bit 1 the gate/up wait, expect a tag nobody writes, so it gives up after

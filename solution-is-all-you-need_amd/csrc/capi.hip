@@ -80,24 +80,57 @@ LibConfig config_from_env() {
   LibConfig c;
   const char* d = getenv("PHANTOM_MOE_DECODE");
   c.decode_fused = !(d && strcmp(d, "staged") == 0);
+  const char* k = getenv("PHANTOM_MOE_DECODE_KSPLIT");
+  c.force_ksplit = k && strcmp(k, "1") == 0;
   c.fused_wait_polls = kFusedWaitPollsDefault;
   c.fused_fault = 0;
   return c;
 }
 
+// "a,b,c" with a in [1, max_waves], b in {1, 2, 4}, c in {1, 2}; else unset.
+void parse_tiling(const char* name, int max_waves, int out[3]) {
+  const char* v = getenv(name);
+  int a = 0, b = 0, c = 0;
+  if (v && sscanf(v, "%d,%d,%d", &a, &b, &c) == 3 && a >= 1 && a <= max_waves && (b == 1 || b == 2 || b == 4) &&
+      (c == 1 || c == 2)) {
+    out[0] = a;
+    out[1] = b;
+    out[2] = c;
+  }
+}
+
+Tuning tuning_from_env() {
+  Tuning t;
+  if (const char* v = getenv("PHANTOM_MOE_GATE_UP_DEPTH")) {
+    const int d = atoi(v);
+    if (d >= 2 && d <= 4) t.gu_depth = d;
+  }
+  if (const char* v = getenv("PHANTOM_MOE_DOWN_DEPTH")) {
+    const int d = atoi(v);
+    if (d == 2 || d == 4 || d == 6) t.dn_depth = d;
+  }
+  parse_tiling("PHANTOM_MOE_GATE_UP_TILING", 8, t.gu_tiling);
+  parse_tiling("PHANTOM_MOE_DOWN_TILING", 4, t.dn_tiling);
+  return t;
+}
+
 // Options live in atomics so a change from another thread is never torn;
-// they are read once per call.
+// they are read once per call.  The environment is read once, on first use.
 std::atomic<int> g_opt_fused{1};
+std::atomic<int> g_opt_ksplit{0};
 std::atomic<uint32_t> g_opt_polls{kFusedWaitPollsDefault};
 std::atomic<uint32_t> g_opt_fault{0};
 std::once_flag g_opt_once;
+Tuning g_tuning;
 
 void init_options() {
   std::call_once(g_opt_once, [] {
     const LibConfig c = config_from_env();
     g_opt_fused.store(c.decode_fused ? 1 : 0);
+    g_opt_ksplit.store(c.force_ksplit ? 1 : 0);
     g_opt_polls.store(c.fused_wait_polls);
     g_opt_fault.store(c.fused_fault);
+    g_tuning = tuning_from_env();
   });
 }
 
@@ -107,6 +140,7 @@ LibConfig lib_config() {
   init_options();
   LibConfig c;
   c.decode_fused = g_opt_fused.load(std::memory_order_relaxed) != 0;
+  c.force_ksplit = g_opt_ksplit.load(std::memory_order_relaxed) != 0;
   c.fused_wait_polls = g_opt_polls.load(std::memory_order_relaxed);
   c.fused_fault = g_opt_fault.load(std::memory_order_relaxed);
   return c;
@@ -115,8 +149,14 @@ LibConfig lib_config() {
 void set_lib_config(const LibConfig& c) {
   init_options();
   g_opt_fused.store(c.decode_fused ? 1 : 0);
+  g_opt_ksplit.store(c.force_ksplit ? 1 : 0);
   g_opt_polls.store(c.fused_wait_polls);
   g_opt_fault.store(c.fused_fault);
+}
+
+const Tuning& tuning() {
+  init_options();
+  return g_tuning;
 }
 
 int set_error(int code, const char* fmt, ...) {
@@ -166,8 +206,7 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
   const size_t o_desc = take(sizeof(int4) * (size_t)(E + 1));
   const size_t o_tok = take(sizeof(int32_t) * (size_t)rows);
   const size_t o_tiles = take(sizeof(int32_t) * (size_t)(max_token_tiles(T, k, E, has_shared) * kTileWords));
-  const size_t o_ntiles = take(sizeof(int32_t) * 3 * kCtlStride);
-  const size_t o_tdone = take(sizeof(int32_t) * (size_t)(max_token_tiles(T, k, E, has_shared) * kCtlStride));
+  const size_t o_ntiles = take(sizeof(int32_t) * kCtlStride);
   const int64_t KpadI = I > 0 ? round_up(I, kQuad) : 0;
   // down operand rows plus an all-zero row
   const size_t o_hq = take(sizeof(uint16_t) * (size_t)((rows + 1) * KpadI * 2));
@@ -200,7 +239,6 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
     ws->seg_tok = reinterpret_cast<int32_t*>(b + o_tok);
     ws->tiles = reinterpret_cast<int32_t*>(b + o_tiles);
     ws->n_tiles = reinterpret_cast<int32_t*>(b + o_ntiles);
-    ws->tile_done = reinterpret_cast<int32_t*>(b + o_tdone);
     ws->hq = reinterpret_cast<uint16_t*>(b + o_hq);
     ws->hs = reinterpret_cast<float*>(b + o_hs);
     ws->outbuf = reinterpret_cast<float*>(b + o_out);
@@ -398,11 +436,8 @@ const char* phantom_moe_expert_kernels(int64_t T, int64_t H, int64_t I, int E, i
   if (pmoe::fused_plan(T, H, I, E, top_k, has_shared ? 1 : 0).ok) {
     gu = dn = "moe_decode_fused_kernel";  // the whole layer is one launch
   } else if (pmoe::gemm_regime(T, top_k, E)) {
-    const bool ring = pmoe::gemm_uses_ring();
-    gu = ring ? "gemm_gate_up_kernel2" : "gemm_gate_up_kernel";
-    dn = ring ? "gemm_down_kernel2" : "gemm_down_kernel";
-  } else if (pmoe::ffn_fused_regime(T, H, I, E, top_k, has_shared)) {
-    gu = dn = "ffn_tile_kernel";  // one launch for both stages
+    gu = "gemm_gate_up_kernel";
+    dn = "gemm_down_kernel";
   } else {
     gu = pmoe::gate_up_tile_regime(T, H, I, E, top_k, has_shared) ? "gate_up_tile_kernel" : "gate_up_kernel";
     dn = pmoe::down_tile_regime(T, H, I, E, top_k, has_shared) ? "down_tile_kernel" : "down_kernel";
@@ -475,6 +510,10 @@ int phantom_moe_set_option(int option, int value) {
       if (value != 0 && value != 1) return fail(PHANTOM_MOE_EINVAL, "DECODE_FUSED takes 0 or 1, got %d", value);
       c.decode_fused = value != 0;
       break;
+    case PHANTOM_MOE_OPT_DECODE_KSPLIT:
+      if (value != 0 && value != 1) return fail(PHANTOM_MOE_EINVAL, "DECODE_KSPLIT takes 0 or 1, got %d", value);
+      c.force_ksplit = value != 0;
+      break;
     case PHANTOM_MOE_OPT_FUSED_WAIT_POLLS:
       if (value < 1) return fail(PHANTOM_MOE_EINVAL, "FUSED_WAIT_POLLS takes a positive bound, got %d", value);
       c.fused_wait_polls = (uint32_t)value;
@@ -495,6 +534,7 @@ int phantom_moe_get_option(int option, int* value) {
   const pmoe::LibConfig c = pmoe::lib_config();
   switch (option) {
     case PHANTOM_MOE_OPT_DECODE_FUSED: *value = c.decode_fused ? 1 : 0; break;
+    case PHANTOM_MOE_OPT_DECODE_KSPLIT: *value = c.force_ksplit ? 1 : 0; break;
     case PHANTOM_MOE_OPT_FUSED_WAIT_POLLS: *value = (int)c.fused_wait_polls; break;
     case PHANTOM_MOE_OPT_FUSED_FAULT: *value = (int)c.fused_fault; break;
     default: return fail(PHANTOM_MOE_EINVAL, "unknown option %d", option);

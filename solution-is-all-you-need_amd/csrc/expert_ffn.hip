@@ -385,8 +385,7 @@ __device__ __attribute__((always_inline)) inline void wchunk_math(const WChunk& 
 
 // SwiGLU of one row tile rt of the token tile [m0, end) from the wave's own
 // accumulators (lane (n, p) holds positions m0 + 4p + j of row n), stored as
-// the down kernel's operand with cache policy AUX.
-template <int AUX>
+// the down kernel's operand.
 __device__ inline void tile_epilogue(const GateUpK& a, BufRsrc hqr, BufRsrc hsr, int64_t m0, int64_t end, uint32_t rt,
                                      const f32x4& ag, const f32x4& au, const f32x4& cg, const f32x4& cu) {
   const int lane = threadIdx.x % kWave;
@@ -414,8 +413,8 @@ __device__ inline void tile_epilogue(const GateUpK& a, BufRsrc hqr, BufRsrc hsr,
     const bool ok = pos < end;
     const uint32_t o = (uint32_t)pos * pos_bytes + o_row;
     if (ok) {
-      __builtin_amdgcn_raw_buffer_store_b16((unsigned short)hb, hqr, (int)o, 0, AUX);
-      __builtin_amdgcn_raw_buffer_store_b16((unsigned short)lb, hqr, (int)(o + 16u), 0, AUX);
+      __builtin_amdgcn_raw_buffer_store_b16((unsigned short)hb, hqr, (int)o, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16((unsigned short)lb, hqr, (int)(o + 16u), 0, 0);
     }
     // the 16 rows of the tile are one half of one group: sum hi + lo over
     // them (16 consecutive lanes, fixed butterfly order)
@@ -426,7 +425,7 @@ __device__ inline void tile_epilogue(const GateUpK& a, BufRsrc hqr, BufRsrc hsr,
     sum += __shfl_xor(sum, 1, kWave);
     if (n == 0 && ok)
       __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum), hsr,
-                                            (int)((((uint32_t)pos * (uint32_t)a.KqI * 4u + g32) * 2u + half) * 4u), 0, AUX);
+                                            (int)((((uint32_t)pos * (uint32_t)a.KqI * 4u + g32) * 2u + half) * 4u), 0, 0);
   }
 }
 
@@ -471,15 +470,12 @@ __device__ inline TileJobs tile_jobs(uint32_t n_tiles, uint32_t n_rt, uint32_t s
 }
 
 // One gate/up job: token tile gt, row tiles part * per_job + w + NW * i for
-// wave w, up to the job's end (part + 1) * per_job or the last row tile.  Ends with the waves' last stores issued and LDS still
-// in use; the caller synchronises before the next job.
-// With a ticket counter, thread 0 draws the next ticket into nxt once the
-// tile header has arrived (a draw issued before it would hold up the
-// header's wait).  H_AUX is the cache policy of the h stores.
-template <int D, int H_AUX, int NW = kTileWaves>
+// wave w, up to the job's end (part + 1) * per_job or the last row tile.
+// Ends with the waves' last stores issued and LDS still in use; the caller
+// synchronises before the next job.
+template <int D, int NW = kTileWaves>
 __device__ __attribute__((always_inline)) inline void gate_up_tile_job(const GateUpK& a, u32x4* s_x, float* s_sx, uint32_t gt,
-                                                                       uint32_t part, const TileJobs& jb, int32_t* ticket,
-                                                                       uint32_t& nxt) {
+                                                                       uint32_t part, const TileJobs& jb) {
   const int lane = threadIdx.x % kWave;
   const int p = lane / 16;
   const uint32_t w = (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -500,7 +496,6 @@ __device__ __attribute__((always_inline)) inline void gate_up_tile_job(const Gat
   // token of the lane's A-operand row; positions past the segment read the
   // all-zero row T
   const int tok = m0 + lane % 16 < end ? tok_w : (int)a.T;
-  if (ticket && threadIdx.x == 0) nxt = (uint32_t)atomicAdd(ticket, 1);
   const bool routed = e < a.seg.E;
   WSrc ws;
   ws.g = buf_rsrc(routed ? a.gate_nib + (int64_t)e * nib_bytes : a.sh_gate_nib, nib_bytes);
@@ -567,7 +562,7 @@ __device__ __attribute__((always_inline)) inline void gate_up_tile_job(const Gat
       advance();
     }
     if (++cq == Kq) {
-      tile_epilogue<H_AUX>(a, hqr, hsr, m0, end, rt0 + NW * ci, ag, au, cg, cu);
+      tile_epilogue(a, hqr, hsr, m0, end, rt0 + NW * ci, ag, au, cg, cu);
       ag = au = cg = cu = z;
       cq = 0;
       ++ci;
@@ -597,8 +592,7 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
   const TileJobs jb = tile_jobs(n_tiles, (uint32_t)(a.I / kRowTile), gridDim.x, NW);
   for (uint32_t job = blockIdx.x; job < jb.n_jobs; job += gridDim.x) {
     const uint32_t gt = job / jb.jpt;
-    uint32_t unused;
-    gate_up_tile_job<D, 0, NW>(a, s_x, s_sx, gt, job - gt * jb.jpt, jb, nullptr, unused);
+    gate_up_tile_job<D, NW>(a, s_x, s_sx, gt, job - gt * jb.jpt, jb);
     __syncthreads();  // the operand is read by every wave before the next job overwrites it
   }
 }
@@ -740,25 +734,11 @@ struct DChunk {  // one quad of one row tile of W_down
 // half-group sums [KqI][2 halves][64 lanes] floats.
 inline size_t down_tile_lds_bytes(int64_t KqI) { return (size_t)KqI * (8 * 64 * 16 + 2 * 64 * 4); }
 
-// Spin bound of a fused down job waiting for its token tile's gate/up jobs
-// (each poll is one memory round trip plus a short sleep, about 1 us): far
-// beyond any real wait, it only guarantees that every wave exits.
-constexpr uint32_t kTileWaitPolls = 1u << 18;
-
 // One down job: token tile gt, row tiles of H part * per_job + w + NW * i, up
 // to the job's end or the last row tile.
-// FUSED (the gate/up + down kernel): the weight ring is loaded first, then
-// thread 0 waits until the tile's gate/up jobs have all counted in at
-// `ready` (>= target), and only then is the operand copied, by device-scope
-// loads (the h rows were stored device-scope and had completed before their
-// count was sent; the copies are issued after the count was seen).  Positions past the segment then read the segment's last row
-// instead of the zero row: their output rows are never stored, and an MFMA
-// output row depends on its own A row only.
-template <int D, bool FUSED, int NW = kTileWaves>
+template <int D, int NW = kTileWaves>
 __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK& a, u32x4* s_h, float* s_hs, uint32_t gt,
-                                                                    uint32_t part, const TileJobs& jb, int32_t* ready,
-                                                                    int32_t target, int32_t* err, int32_t* ticket,
-                                                                    uint32_t& nxt) {
+                                                                    uint32_t part, const TileJobs& jb) {
   const int lane = threadIdx.x % kWave;
   const int n = lane % 16;
   const int p = lane / 16;
@@ -777,7 +757,6 @@ __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK&
   const int e = __builtin_amdgcn_readfirstlane(tw[0]);
   const int64_t m0 = __builtin_amdgcn_readfirstlane(tw[1]);
   const int64_t end = __builtin_amdgcn_readfirstlane(tw[2]);
-  if (ticket && threadIdx.x == 0) nxt = (uint32_t)atomicAdd(ticket, 1);
   const bool routed = e < a.seg.E;
   const BufRsrc wr = buf_rsrc(routed ? a.down_nib + (int64_t)e * nib_bytes : a.sh_down_nib, nib_bytes);
   const BufRsrc sr = buf_rsrc(routed ? reinterpret_cast<const uint8_t*>(a.down_sc) + (int64_t)e * sc_bytes
@@ -791,23 +770,19 @@ __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK&
   // lane; the blocks of padded groups (4q + gi >= Kg, only in a ragged last
   // quad of I) are zeroed instead, so the chunk math needs no test
   auto copy_operand = [&]() {
-    const int64_t pos = m0 + n < end ? m0 + n : (FUSED ? end - 1 : a.zero_row);
+    const int64_t pos = m0 + n < end ? m0 + n : a.zero_row;
     const uint32_t hv = (uint32_t)pos * Kq * 512u + (uint32_t)p * 128u;
     const uint32_t sv = (uint32_t)pos * Kq * 32u + (uint32_t)p * 8u;
-    constexpr int aux = FUSED ? kDeviceScope : 0;
     for (uint32_t b = w; b < Kq * 8; b += NW) {
       if (4 * (b / 8) + (b / 2) % 4 < (uint32_t)Kg)
-        dma_b128<aux>(hqr, s_h + b * kWave, hv, (b / 8) * 512u + ((b / 2) % 4) * 32u + (b % 2) * 16u);
+        dma_b128(hqr, s_h + b * kWave, hv, (b / 8) * 512u + ((b / 2) % 4) * 32u + (b % 2) * 16u);
       else
         s_h[b * kWave + lane] = zero4;
     }
-    for (uint32_t b = w; b < Kq * 2; b += NW)
-      dma_b32<aux>(hsr, s_hs + b * kWave, sv, (b / 2) * 32u + (b % 2) * 4u);
+    for (uint32_t b = w; b < Kq * 2; b += NW) dma_b32(hsr, s_hs + b * kWave, sv, (b / 2) * 32u + (b % 2) * 4u);
   };
-  if constexpr (!FUSED) {
-    copy_operand();
-    asm volatile("" ::: "memory");  // the operand loads stay older than the weight loads below
-  }
+  copy_operand();
+  asm volatile("" ::: "memory");  // the operand loads stay older than the weight loads below
 
   uint32_t li = 0, lq = 0, loaded = 0;
   auto advance = [&]() {
@@ -832,24 +807,8 @@ __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK&
       advance();
     }
   }
-  if constexpr (FUSED) {
-    if (threadIdx.x == 0) {
-      for (uint32_t it = 0;; ++it) {
-        if (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) break;
-        if (it >= kTileWaitPolls) {
-          __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(8);
-      }
-    }
-    __syncthreads();
-    copy_operand();
-    wait_vmcnt<0>();  // the operand copies are the youngest loads
-  } else {
-    if (total > 0) wait_vmcnt<2 * D>();  // the operand copies are older than the D chunks
-    else wait_vmcnt<0>();
-  }
+  if (total > 0) wait_vmcnt<2 * D>();  // the operand copies are older than the D chunks
+  else wait_vmcnt<0>();
   lds_barrier();  // this wave's copies and zero stores have landed; so have every other wave's
 
   uint32_t ci = 0, cq = 0;
@@ -913,71 +872,8 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
   const TileJobs jb = tile_jobs(n_tiles, (uint32_t)(a.H / kRowTile), gridDim.x, NW, false);
   for (uint32_t job = blockIdx.x; job < jb.n_jobs; job += gridDim.x) {
     const uint32_t gt = job / jb.jpt;
-    uint32_t unused;
-    down_tile_job<D, false, NW>(a, s_h, s_hs, gt, job - gt * jb.jpt, jb, nullptr, 0, nullptr, nullptr, unused);
+    down_tile_job<D, NW>(a, s_h, s_hs, gt, job - gt * jb.jpt, jb);
     __syncthreads();  // the operand is read by every wave before the next job overwrites it
-  }
-}
-
-// ------------------------------------------------ gate/up + down, one launch
-//
-// The two token-tile stages as one persistent launch.  Workgroups draw jobs
-// from a ticket counter (zeroed by the permute): every gate/up job comes
-// before every down job.  A gate/up job stores its h rows device-scope, waits
-// for those stores to complete, and adds one count on its token tile (one
-// 128-byte line per tile, zeroed by the permute); a down job loads its first
-// weight chunks, then waits for its tile's count to reach the gate/up jobs
-// per tile and copies the rows device-scope.  (Agent-scope fences instead,
-// an L2 write-back per gate/up job and an L2 invalidation per down job, made
-// the launch twice as slow as two separate launches.)  While
-// the last gate/up jobs finish, the down weight stream is already running on
-// the other CUs, instead of the chip idling between two launches.
-// No wait can deadlock, whatever the residency: a ticket is only ever held by
-// a running workgroup, the next ticket is drawn at the start of a job and is
-// larger than the current one (so a workgroup holding a gate/up ticket is
-// running a gate/up job, which never waits), and all gate/up tickets precede
-// every down ticket.  The spin is still bounded (kTileWaitPolls).
-struct FfnTileK {
-  GateUpK g;
-  DownK d;
-  int32_t* tile_done;  // finished gate/up jobs of token tile g at [g * kCtlStride] (zeroed by the permute)
-  int32_t* ctl;        // [0] token tiles, [kCtlStride] job ticket, [2 * kCtlStride] set if a wait hit its bound
-  uint32_t job_lds;  // byte offset of the job word in the dynamic LDS (after the larger operand)
-};
-
-template <int DG, int DD>
-__global__ __launch_bounds__(kTileWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void ffn_tile_kernel(FfnTileK a) {
-  extern __shared__ u32x4 s_op[];  // all LDS is dynamic: a static part would eat into the 160 KB maximum
-  uint32_t& s_job = *reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(s_op) + a.job_lds);
-  float* s_sx = reinterpret_cast<float*>(s_op + (uint32_t)a.g.Kq * 256);
-  float* s_hs = reinterpret_cast<float*>(s_op + (uint32_t)a.d.Kq * 512);
-  if (threadIdx.x == 0) s_job = (uint32_t)atomicAdd(&a.ctl[kCtlStride], 1);
-  const uint32_t n_tiles = (uint32_t)__builtin_amdgcn_readfirstlane(a.ctl[0]);
-  const TileJobs ja = tile_jobs(n_tiles, (uint32_t)(a.g.I / kRowTile), gridDim.x);
-  const TileJobs jd = tile_jobs(n_tiles, (uint32_t)(a.d.H / kRowTile), gridDim.x, kTileWaves, false);
-  const uint32_t n_jobs = ja.n_jobs + jd.n_jobs;
-  __syncthreads();
-  for (;;) {
-    const uint32_t job = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_job);
-    if (job >= n_jobs) break;
-    uint32_t nxt = 0;  // the next ticket (thread 0), drawn inside the job
-    if (job < ja.n_jobs) {
-      const uint32_t gt = job / ja.jpt;
-      gate_up_tile_job<DG, kDeviceScope>(a.g, s_op, s_sx, gt, job - gt * ja.jpt, ja, &a.ctl[kCtlStride], nxt);
-      __builtin_amdgcn_s_waitcnt(0);  // this wave's device-scope h stores have completed
-      if (threadIdx.x == 0) s_job = nxt;
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        atomicAdd(&a.tile_done[(int64_t)gt * kCtlStride], 1);
-      }
-    } else {
-      const uint32_t dj = job - ja.n_jobs;
-      const uint32_t gt = dj / jd.jpt;
-      down_tile_job<DD, true>(a.d, s_op, s_hs, gt, dj - gt * jd.jpt, jd, &a.tile_done[(int64_t)gt * kCtlStride],
-                              (int32_t)ja.jpt, &a.ctl[2 * kCtlStride], &a.ctl[kCtlStride], nxt);
-      if (threadIdx.x == 0) s_job = nxt;
-      __syncthreads();
-    }
   }
 }
 
@@ -1048,27 +944,21 @@ static Split choose_split(int64_t Kq, int max_waves) {
   return s;
 }
 
-// Optional override "ksplit,rt,nq" for tuning sweeps (PHANTOM_MOE_GATE_UP_TILING /
-// PHANTOM_MOE_DOWN_TILING); values outside the supported set are ignored.
-static void tiling_override(const char* name, int max_waves, int* ksplit, int* rt, int* nq) {
-  const char* v = getenv(name);
-  if (!v) return;
-  int a = 0, b = 0, c = 0;
-  if (sscanf(v, "%d,%d,%d", &a, &b, &c) == 3 && a >= 1 && a <= max_waves && (b == 1 || b == 2 || b == 4) &&
-      (c == 1 || c == 2)) {
-    *ksplit = a;
-    *rt = b;
-    *nq = c;
-  }
+// Optional override "ksplit,rt,nq" for tuning sweeps (read once from the
+// environment, see Tuning); unset leaves the shape-chosen tiling.
+static void tiling_override(const int t[3], int* ksplit, int* rt, int* nq) {
+  if (t[0] == 0) return;
+  *ksplit = t[0];
+  *rt = t[1];
+  *nq = t[2];
 }
 
 // The token-tile kernel needs the tile table (written by the permute in the
 // decode regime), the tile's operand in LDS, and every buffer it reads or
 // writes addressable with 32-bit offsets.
-// PHANTOM_MOE_GATE_UP_KERNEL=classic selects the K-split kernel instead.
+// The K-split kernel can be forced (option PHANTOM_MOE_OPT_DECODE_KSPLIT).
 bool gate_up_tile_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared) {
-  const char* v = getenv("PHANTOM_MOE_GATE_UP_KERNEL");
-  if (v && strcmp(v, "classic") == 0) return false;
+  if (lib_config().force_ksplit) return false;
   const int64_t lim = (int64_t)1 << 31;
   const int64_t Kq = ceil_div(H, kQuad), KqI = ceil_div(I, kQuad);
   const int64_t rows = T * k + (has_shared ? T : 0);
@@ -1083,22 +973,13 @@ static bool tile_fits(const ExpertArgs& x, const GateUpK& g) {
   return g.tiles != nullptr && gate_up_tile_regime(x.T, x.H, x.I, x.E, x.k, x.has_shared);
 }
 
-// PHANTOM_MOE_GATE_UP_DEPTH=2..4 overrides the ring depth for tuning sweeps.
+// Ring depth 3 (a tuning override may set 2..4).
 static hipError_t launch_gate_up_tile(const ExpertArgs& x, const GateUpK& g, hipStream_t stream) {
-  int depth = 3;
-  if (const char* v = getenv("PHANTOM_MOE_GATE_UP_DEPTH")) {
-    const int d = atoi(v);
-    if (d >= 2 && d <= 4) depth = d;
-  }
+  const int depth = tuning().gu_depth ? tuning().gu_depth : 3;
   // Eight waves per workgroup, one workgroup per CU (two waves per SIMD, as
   // with two 4-wave workgroups): each CU copies a tile's operand to LDS once
   // rather than twice (Qwen3 shapes, 32 tokens: 24.5 -> 23.7 us).
-  // PHANTOM_MOE_GATE_UP_WAVES=4 selects 4-wave workgroups.
-  int nw = 8;
-  if (const char* v = getenv("PHANTOM_MOE_GATE_UP_WAVES")) {
-    const int n = atoi(v);
-    if (n == 4 || n == 8) nw = n;
-  }
+  constexpr int nw = 8;
   const size_t lds = tile_lds_bytes(g.Kq);
   const int block = nw * kWave;
   const int64_t max_jobs = max_token_tiles(x.T, x.k, x.E, x.has_shared) * ceil_div(x.I / kRowTile, nw);
@@ -1120,15 +1001,9 @@ static hipError_t launch_gate_up_tile(const ExpertArgs& x, const GateUpK& g, hip
     hipLaunchKernelGGL((gate_up_tile_kernel<D_, NW_>), dim3((unsigned)(grid < 1 ? 1 : grid)), dim3(block), \
                        lds, stream, g);                                                                  \
   } while (0)
-  if (nw == 8) {
-    if (depth == 2) PMOE_TILE(2, 8);
-    else if (depth == 3) PMOE_TILE(3, 8);
-    else PMOE_TILE(4, 8);
-  } else {
-    if (depth == 2) PMOE_TILE(2, 4);
-    else if (depth == 3) PMOE_TILE(3, 4);
-    else PMOE_TILE(4, 4);
-  }
+  if (depth == 2) PMOE_TILE(2, nw);
+  else if (depth == 3) PMOE_TILE(3, nw);
+  else PMOE_TILE(4, nw);
 #undef PMOE_TILE
   return hipGetLastError();
 }
@@ -1150,69 +1025,6 @@ static DownK make_down_k(const ExpertArgs& x, const Workspace& ws) {
   d.tiles = ws.tiles;
   d.n_tiles = ws.n_tiles;
   return d;
-}
-
-static size_t ffn_lds_bytes(int64_t Kq, int64_t KqI) {
-  const size_t a = tile_lds_bytes(Kq), b = down_tile_lds_bytes(KqI);
-  return a > b ? a : b;
-}
-
-// The fused gate/up + down launch (launch_gate_up runs it; launch_down then
-// has nothing to do) runs when PHANTOM_MOE_FFN_KERNEL=fused and both stages
-// are in the token-tile regime with two workgroups per CU (the larger operand
-// plus the 16-byte job word).  It is not the default: at Qwen3 shape, 32
-// tokens, it measured 60 us against 43 us for the two launches (its first
-// jobs start 5 us late, the ticket draws of all workgroups colliding, and a
-// down job is as long as the whole separate down launch, so the workgroups
-// whose gate/up job ended last finish last).
-bool ffn_fused_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared) {
-  const char* v = getenv("PHANTOM_MOE_FFN_KERNEL");
-  if (!v || strcmp(v, "fused") != 0) return false;
-  return gate_up_tile_regime(T, H, I, E, k, has_shared) && down_tile_regime(T, H, I, E, k, has_shared) &&
-         ffn_lds_bytes(ceil_div(H, kQuad), ceil_div(I, kQuad)) + 16 <= 80 * 1024;
-}
-
-// Ring depths: gate/up 3, down 2 (PHANTOM_MOE_DOWN_DEPTH=4 or 6 overrides).
-static hipError_t launch_ffn_tile(const ExpertArgs& x, const GateUpK& g, const DownK& d, const Workspace& ws,
-                                  hipStream_t stream) {
-  int depth = 2;
-  if (const char* v = getenv("PHANTOM_MOE_DOWN_DEPTH")) {
-    const int dd = atoi(v);
-    if (dd == 2 || dd == 4 || dd == 6) depth = dd;
-  }
-  FfnTileK f;
-  f.g = g;
-  f.d = d;
-  f.tile_done = ws.tile_done;
-  f.ctl = ws.n_tiles;
-  f.job_lds = (uint32_t)ffn_lds_bytes(g.Kq, d.Kq);
-  const size_t lds = f.job_lds + 16;
-  const int block = kTileWaves * kWave;
-  const int64_t max_jobs = max_token_tiles(x.T, x.k, x.E, x.has_shared) *
-                           (ceil_div(x.I / kRowTile, kTileWaves) + ceil_div(x.H / kRowTile, kTileWaves));
-#define PMOE_FFN(DD_)                                                                                    \
-  do {                                                                                                   \
-    static bool attr_set = false;                                                                        \
-    if (!attr_set) {                                                                                     \
-      hipError_t e_ = hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_tile_kernel<3, DD_>),       \
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);       \
-      if (e_ != hipSuccess) return e_;                                                                   \
-      attr_set = true;                                                                                   \
-    }                                                                                                    \
-    int per_cu = 0;                                                                                      \
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ffn_tile_kernel<3, DD_>, block, lds) !=    \
-            hipSuccess || per_cu < 1)                                                                    \
-      per_cu = 1;                                                                                        \
-    int64_t grid = (int64_t)device_cus() * per_cu;                                                       \
-    if (grid > max_jobs) grid = max_jobs;                                                                \
-    hipLaunchKernelGGL((ffn_tile_kernel<3, DD_>), dim3((unsigned)(grid < 1 ? 1 : grid)), dim3(block), lds, \
-                       stream, f);                                                                       \
-  } while (0)
-  if (depth == 2) PMOE_FFN(2);
-  else if (depth == 4) PMOE_FFN(4);
-  else PMOE_FFN(6);
-#undef PMOE_FFN
-  return hipGetLastError();
 }
 
 static GateUpK make_gate_up_k(const ExpertArgs& x, const Workspace& ws) {
@@ -1242,7 +1054,6 @@ static GateUpK make_gate_up_k(const ExpertArgs& x, const Workspace& ws) {
 
 hipError_t launch_gate_up(const ExpertArgs& x, const Workspace& ws, hipStream_t stream) {
   const GateUpK g = make_gate_up_k(x, ws);
-  if (ffn_fused_regime(x.T, x.H, x.I, x.E, x.k, x.has_shared)) return launch_ffn_tile(x, g, make_down_k(x, ws), ws, stream);
   if (tile_fits(x, g)) return launch_gate_up_tile(x, g, stream);
   // K split: about four quads per wave (fewer waves per item keep more items
   // in flight per CU), one quad of loads outstanding per wave at a time.
@@ -1257,7 +1068,7 @@ hipError_t launch_gate_up(const ExpertArgs& x, const Workspace& ws, hipStream_t 
     rt = 2;
     ksplit = ksplit < 4 ? ksplit : 4;
   }
-  tiling_override("PHANTOM_MOE_GATE_UP_TILING", kGateUpWaves, &ksplit, &rt, &nq);
+  tiling_override(tuning().gu_tiling, &ksplit, &rt, &nq);
   if (rt != 2 || (x.I / kRowTile) % 2) rt = 1;  // RT 4 would spill
   const int block = kWave * ksplit;
   const int64_t max_items = (int64_t)max_active_experts(x) * (x.I / (kRowTile * rt));
@@ -1280,8 +1091,7 @@ hipError_t launch_gate_up(const ExpertArgs& x, const Workspace& ws, hipStream_t 
 }
 
 bool down_tile_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared) {
-  const char* v = getenv("PHANTOM_MOE_DOWN_KERNEL");
-  if (v && strcmp(v, "classic") == 0) return false;
+  if (lib_config().force_ksplit) return false;
   const int64_t lim = (int64_t)1 << 31;
   const int64_t KqI = ceil_div(I, kQuad);
   const int64_t rows = T * k + (has_shared ? T : 0);
@@ -1294,13 +1104,9 @@ bool down_tile_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
          H * KqI * 64 < lim && (rows + 1) * KqI * 512 < lim;
 }
 
-// PHANTOM_MOE_DOWN_DEPTH=2, 4 or 6 overrides the ring depth for tuning sweeps.
+// Ring depth 2 (a tuning override may set 4 or 6).
 static hipError_t launch_down_tile(const ExpertArgs& x, const DownK& d, hipStream_t stream) {
-  int depth = 2;
-  if (const char* v = getenv("PHANTOM_MOE_DOWN_DEPTH")) {
-    const int dd = atoi(v);
-    if (dd == 2 || dd == 4 || dd == 6) depth = dd;
-  }
+  const int depth = tuning().dn_depth ? tuning().dn_depth : 2;
   const size_t lds = down_tile_lds_bytes(d.Kq);
   const int block = kTileWaves * kWave;
   const int64_t max_jobs = max_token_tiles(x.T, x.k, x.E, x.has_shared) * ceil_div(x.H / kRowTile, kTileWaves);
@@ -1330,8 +1136,6 @@ static hipError_t launch_down_tile(const ExpertArgs& x, const DownK& d, hipStrea
 }
 
 hipError_t launch_down(const ExpertArgs& x, const Workspace& ws, hipStream_t stream) {
-  // the fused launch of launch_gate_up has run the down stage too
-  if (ffn_fused_regime(x.T, x.H, x.I, x.E, x.k, x.has_shared)) return hipSuccess;
   const DownK d = make_down_k(x, ws);
   if (d.tiles && down_tile_regime(x.T, x.H, x.I, x.E, x.k, x.has_shared)) return launch_down_tile(x, d, stream);
   Split sp = choose_split(d.Kq, kDownWaves);
@@ -1357,7 +1161,7 @@ hipError_t launch_down(const ExpertArgs& x, const Workspace& ws, hipStream_t str
     rt = 4;
     sp.nq = 2;
   }
-  tiling_override("PHANTOM_MOE_DOWN_TILING", kDownWaves, &sp.ksplit, &rt, &sp.nq);
+  tiling_override(tuning().dn_tiling, &sp.ksplit, &rt, &sp.nq);
   if (rt == 4 && (x.H / kRowTile) % 4) rt = 2;
   const int block = kWave * sp.ksplit;
   const int64_t max_items = (int64_t)max_active_experts(x) * (x.H / (kRowTile * rt));

@@ -213,8 +213,8 @@ __device__ inline void dma_b32(BufRsrc r, void* lds, uint32_t voff, uint32_t sof
 // LDS ring while it reads another then gets no conservative vmcnt(0) before
 // its reads (the compiler cannot tell the stages apart).  The caller owns
 // the ordering: it waits with wait_vmcnt / s_waitcnt before a barrier.  M0
-// is written right before the load (a reserved register the compiler only
-// sets immediately before its own uses); the resource is raw SGPR words.
+// is written right before the load and declared clobbered, so the compiler
+// reloads it before any later use of its own; the resource is raw SGPR words.
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 __device__ inline i32x4 buf_rsrc_words(const void* base, uint32_t bytes) {
@@ -229,7 +229,7 @@ __device__ inline uint32_t lds_addr(const void* p) {
 
 __device__ inline void dma_b128_unseen(const i32x4& r, uint32_t lds_byte, uint32_t voff, uint32_t soff) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :: "s"(lds_byte), "v"(voff), "s"(r), "s"(soff) : "memory");
+               :: "s"(lds_byte), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
 }
 
 // s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima), gfx9 encoding.

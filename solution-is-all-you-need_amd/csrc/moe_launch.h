@@ -70,12 +70,25 @@ FusedLds fused_lds_layout(int T, int k, int E, int has_shared, int H, int I, int
 
 // Library options: initialised once from the environment on first use,
 // changed afterwards only by phantom_moe_set_option:
-//   PHANTOM_MOE_DECODE=staged    never take the single-launch decode path
+//   PHANTOM_MOE_DECODE=staged       never take the single-launch decode path
+//   PHANTOM_MOE_DECODE_KSPLIT=1     decode expert stages always as the K-split
+//                                   kernels (not the token-tile ones)
 struct LibConfig {
   bool decode_fused;
+  bool force_ksplit;
   uint32_t fused_wait_polls;  // bound of each wait of the single-launch path
   uint32_t fused_fault;       // failure injection for tests: bit 0 the logit wait, bit 1 the gate/up wait
 };
+// Tuning overrides for sweeps, read from the environment once, on first use
+// (0 = the shape-chosen value):
+//   PHANTOM_MOE_GATE_UP_DEPTH=2..4, PHANTOM_MOE_DOWN_DEPTH=2|4|6   token-tile weight-ring depths
+//   PHANTOM_MOE_GATE_UP_TILING / PHANTOM_MOE_DOWN_TILING = "waves,row_tiles,quads"   K-split tiling
+struct Tuning {
+  int gu_depth = 0, dn_depth = 0;
+  int gu_tiling[3] = {0, 0, 0};
+  int dn_tiling[3] = {0, 0, 0};
+};
+const Tuning& tuning();
 // Each poll is one device-scope round trip plus a short sleep (about 1-2 us),
 // so the default bound is far beyond any real wait; it only guarantees that
 // every wave exits.
@@ -98,11 +111,7 @@ struct Workspace {
   int4* desc = nullptr;             // [E + 1] {expert, begin, end, 0} per active segment
   int32_t* seg_tok = nullptr;       // [T * k + T] token of each segment position
   int32_t* tiles = nullptr;         // [max_token_tiles][kTileWords] 16-position tiles of the segments
-  // [3 * kCtlStride]: word 0 the token tile count; word kCtlStride the
-  // fused expert launch's job ticket; word 2 * kCtlStride its wait-bound flag
-  // (each in its own 128-byte line: a line that atomics hit is slow to read)
-  int32_t* n_tiles = nullptr;
-  int32_t* tile_done = nullptr;     // [max_token_tiles * kCtlStride] finished gate/up jobs per token tile
+  int32_t* n_tiles = nullptr;       // [kCtlStride]: word 0 the token tile count
   uint16_t* hq = nullptr;          // [rows, Kpad_I * 2] fp16 hi/lo of h, MFMA operand order
   float* hs = nullptr;             // [rows, Kpad_I / 32, 2] half-group sums of h
   float* outbuf = nullptr;          // [T*k + T*shared, H] expert outputs, segment order
@@ -187,7 +196,6 @@ struct ExpertArgs {
 // operands; below it, as the grouped GEMV (expert_ffn.hip).
 constexpr int kGemmMinSlotsPerExpert = 64;
 bool gemm_regime(int64_t T, int k, int E);
-bool gemm_uses_ring();  // the LDS-ring tile pipeline (default) rather than the register-staged one
 hipError_t launch_gemm_gate_up(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);
 hipError_t launch_gemm_down(const ExpertArgs& a, const Workspace& ws, hipStream_t stream);
 
@@ -196,9 +204,6 @@ hipError_t launch_gemm_down(const ExpertArgs& a, const Workspace& ws, hipStream_
 bool gate_up_tile_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
 // The same for the down stage.
 bool down_tile_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
-// Both stages as one persistent token-tile launch (run by launch_gate_up;
-// launch_down is then a no-op).
-bool ffn_fused_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
 
 // The whole layer in one launch (decode_fused.hip); plan from fused_plan.
 hipError_t launch_decode_fused(const FusedPlan& pl, const RouteArgs& r, const ExpertArgs& x, const FusedWs& ws,

@@ -68,7 +68,6 @@ struct RouteK {
   int32_t* seg_tok;  // [T*k + T] token of each segment position, or null
   int32_t* tiles;    // token tiles (see kTileWords), or null
   int32_t* n_tiles;
-  int32_t* tile_done;  // per-tile gate/up job counts of the fused expert launch (zeroed here), or null
   int32_t* counter;  // select workgroups finished (fused permute); zeroed by the logits launch
   int fuse_permute;
 };
@@ -157,7 +156,7 @@ __device__ __attribute__((always_inline)) inline void block_permute(const int32_
                               int has_shared, int32_t* offsets, int32_t* offsets_user,
                               int32_t* active, int32_t* n_active, int32_t* sorted_slots,
                               int32_t* slot_pos, int4* desc, int32_t* seg_tok, int32_t* tiles,
-                              int32_t* n_tiles, int32_t* tile_done) {
+                              int32_t* n_tiles) {
   constexpr int kMaxWaves = 16;
   __shared__ int s_cnt[kMaxWaves][kMaxExperts];
   __shared__ int s_tmp[3 * kMaxWaves];
@@ -266,7 +265,6 @@ __device__ __attribute__((always_inline)) inline void block_permute(const int32_
         // left as they are and never read)
         for (int j = 0; j < (tot[i] + 15) / 16; ++j) {
           *reinterpret_cast<int4*>(tiles + (int64_t)(trun + j) * kTileWords) = make_int4(e, run + 16 * j, run + tot[i], 0);
-          if (tile_done) tile_done[(int64_t)(trun + j) * kCtlStride] = 0;
         }
       }
       trun += (tot[i] + 15) / 16;
@@ -298,13 +296,10 @@ __device__ __attribute__((always_inline)) inline void block_permute(const int32_
     for (int64_t j = tid; j < n_sh; j += blockDim.x) {
       int32_t* tw = tiles + (total_tiles + j) * kTileWords;
       *reinterpret_cast<int4*>(tw) = make_int4(E, total + (int)(16 * j), total + (int)T, 0);
-      if (tile_done) tile_done[(total_tiles + j) * kCtlStride] = 0;
       for (int jj = 0; jj < 16 && 16 * j + jj < T; ++jj) tw[4 + jj] = (int32_t)(16 * j + jj);
     }
     if (tid == 0) {
       n_tiles[0] = total_tiles + (int)n_sh;
-      n_tiles[kCtlStride] = 0;      // job ticket of the fused expert launch
-      n_tiles[2 * kCtlStride] = 0;  // its wait-bound flag
     }
   }
   if (desc) {
@@ -583,7 +578,7 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteK a) {
     // the selection reaches the permute through LDS, not a global round trip
     lds_barrier();
     block_permute(s_sel, a.T * a.k, a.k, a.E, a.T, a.has_shared, a.offsets, a.offsets_user, a.active,
-                  a.n_active, a.sorted_slots, a.slot_pos, a.desc, a.seg_tok, a.tiles, a.n_tiles, a.tile_done);
+                  a.n_active, a.sorted_slots, a.slot_pos, a.desc, a.seg_tok, a.tiles, a.n_tiles);
     return;
   }
   if (gridDim.x > 1) {
@@ -602,7 +597,7 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteK a) {
   }
   __syncthreads();
   block_permute(a.topk_idx, a.T * a.k, a.k, a.E, a.T, a.has_shared, a.offsets, a.offsets_user, a.active,
-                a.n_active, a.sorted_slots, a.slot_pos, a.desc, a.seg_tok, a.tiles, a.n_tiles, a.tile_done);
+                a.n_active, a.sorted_slots, a.slot_pos, a.desc, a.seg_tok, a.tiles, a.n_tiles);
 }
 
 __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* idx, int64_t T, int k, int E,
@@ -610,10 +605,9 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* idx, int64
                                                        int32_t* offsets_user, int32_t* active,
                                                        int32_t* n_active, int32_t* sorted_slots,
                                                        int32_t* slot_pos, int4* desc,
-                                                       int32_t* seg_tok, int32_t* tiles, int32_t* n_tiles,
-                                                       int32_t* tile_done) {
+                                                       int32_t* seg_tok, int32_t* tiles, int32_t* n_tiles) {
   block_permute(idx, T * k, k, E, T, has_shared, offsets, offsets_user, active, n_active,
-                sorted_slots, slot_pos, desc, seg_tok, tiles, n_tiles, tile_done);
+                sorted_slots, slot_pos, desc, seg_tok, tiles, n_tiles);
 }
 
 // Logits for many tokens (prefill): the same per-lane partials and tree as
@@ -834,7 +828,7 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(int64_t n, int64_t T
                                                             int32_t* cnt, int32_t* tb_out, int32_t* offsets,
                                                             int32_t* offsets_user, int32_t* active, int32_t* n_active,
                                                             int4* desc, int32_t* seg_tok, int32_t* tiles,
-                                                            int32_t* n_tiles, int32_t* tile_done) {
+                                                            int32_t* n_tiles) {
   __shared__ int s_tmp[3 * 16];
   const int e = threadIdx.x;
   int tot = 0;
@@ -859,7 +853,6 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(int64_t n, int64_t T
     if (tiles) {
       for (int j = 0; j < ntl; ++j) {
         *reinterpret_cast<int4*>(tiles + (int64_t)(ex.z + j) * kTileWords) = make_int4(e, run + 16 * j, run + tot, 0);
-        if (tile_done) tile_done[(int64_t)(ex.z + j) * kCtlStride] = 0;
       }
     }
     // chunk bases of expert e, in chunk order
@@ -889,13 +882,10 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(int64_t n, int64_t T
     for (int64_t j = threadIdx.x; j < n_sh; j += blockDim.x) {
       int32_t* tw = tiles + (total_tiles + j) * kTileWords;
       *reinterpret_cast<int4*>(tw) = make_int4(E, total + (int)(16 * j), total + (int)T, 0);
-      if (tile_done) tile_done[(total_tiles + j) * kCtlStride] = 0;
       for (int jj = 0; jj < 16 && 16 * j + jj < T; ++jj) tw[4 + jj] = (int32_t)(16 * j + jj);
     }
     if (threadIdx.x == 0) {
       n_tiles[0] = total_tiles + (int)n_sh;
-      n_tiles[kCtlStride] = 0;
-      n_tiles[2 * kCtlStride] = 0;
     }
   }
   if (desc) {
@@ -947,7 +937,7 @@ __global__ __launch_bounds__(kPermWaves * kWave) void permute_place_kernel(const
 static hipError_t launch_permute_multi(const int32_t* idx, int64_t T, int k, int E, int has_shared,
                                        int32_t* offsets, int32_t* offsets_user, int32_t* active, int32_t* n_active,
                                        int32_t* sorted_slots, int32_t* slot_pos, int4* desc, int32_t* seg_tok,
-                                       int32_t* tiles, int32_t* n_tiles, int32_t* tile_done, int32_t* cnt,
+                                       int32_t* tiles, int32_t* n_tiles, int32_t* cnt,
                                        int32_t* tb, hipStream_t stream) {
   const int64_t n = T * k;
   const int64_t nb = perm_blocks(n);
@@ -955,7 +945,7 @@ static hipError_t launch_permute_multi(const int32_t* idx, int64_t T, int k, int
   hipLaunchKernelGGL(permute_count_kernel, dim3((unsigned)nb), dim3(kPermWaves * kWave), 0, stream, idx, n, E, chunk,
                      cnt);
   hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(1024), 0, stream, n, T, E, (int)nb, has_shared, cnt, tb,
-                     offsets, offsets_user, active, n_active, desc, seg_tok, tiles, n_tiles, tile_done);
+                     offsets, offsets_user, active, n_active, desc, seg_tok, tiles, n_tiles);
   hipLaunchKernelGGL(permute_place_kernel, dim3((unsigned)nb), dim3(kPermWaves * kWave), 0, stream, idx, n, k, E,
                      chunk, cnt, offsets, tb, sorted_slots, slot_pos, seg_tok, tiles);
   return hipGetLastError();
@@ -1016,7 +1006,6 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
   const bool want_tiles = r.do_permute && r.want_tiles;
   k.tiles = want_tiles ? ws.tiles : nullptr;
   k.n_tiles = want_tiles ? ws.n_tiles : nullptr;
-  k.tile_done = want_tiles ? ws.tile_done : nullptr;
   const unsigned sel_blocks = (unsigned)ceil_div(r.T, kSelectWaves);
   k.fuse_permute = (r.do_permute && sel_blocks > 1 && sel_blocks <= kFusedSelectBlocks) ? 1 : 0;
   k.counter = k.fuse_permute ? ws.counter : nullptr;
@@ -1036,10 +1025,10 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
   if (r.T * r.k >= kPermMultiSlots)
     return launch_permute_multi(k.topk_idx, r.T, r.k, r.E, r.has_shared, ws.offsets, r.offsets_out, ws.active,
                                 ws.n_active, k.sorted_slots, k.slot_pos, k.desc, k.seg_tok, k.tiles, k.n_tiles,
-                                k.tile_done, ws.perm_cnt, ws.perm_tb, stream);
+                                ws.perm_cnt, ws.perm_tb, stream);
   hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, k.topk_idx, r.T, r.k,
               r.E, r.has_shared, ws.offsets, r.offsets_out, ws.active, ws.n_active, k.sorted_slots, k.slot_pos,
-              k.desc, k.seg_tok, k.tiles, k.n_tiles, k.tile_done);
+              k.desc, k.seg_tok, k.tiles, k.n_tiles);
   return hipGetLastError();
 }
 
@@ -1048,12 +1037,12 @@ hipError_t launch_permute(const int32_t* topk_idx, int64_t T, int k, int E, int 
                           const Workspace& ws, hipStream_t stream) {
   if (T * k >= kPermMultiSlots)
     return launch_permute_multi(topk_idx, T, k, E, has_shared, ws.offsets, offsets, ws.active, ws.n_active,
-                                sorted_slots, slot_pos, nullptr, nullptr, nullptr, nullptr, nullptr, ws.perm_cnt,
+                                sorted_slots, slot_pos, nullptr, nullptr, nullptr, nullptr, ws.perm_cnt,
                                 ws.perm_tb, stream);
   hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, topk_idx, T, k, E, has_shared,
                      ws.offsets, offsets, ws.active, ws.n_active, sorted_slots, slot_pos,
                      static_cast<int4*>(nullptr), static_cast<int32_t*>(nullptr), static_cast<int32_t*>(nullptr),
-                     static_cast<int32_t*>(nullptr), static_cast<int32_t*>(nullptr));
+                     static_cast<int32_t*>(nullptr));
   return hipGetLastError();
 }
 

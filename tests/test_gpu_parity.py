@@ -17,7 +17,7 @@ import phantom_moe  # noqa: E402
 from helpers import (bf16_tensor_bits, check_y, oracle_for_device_layer, repacked_layout,  # noqa: E402
                      to_bf16_tensor)
 from oracle import oracle  # noqa: E402
-from phantom_moe import q4_0, synth  # noqa: E402
+from phantom_moe import _lib, q4_0, synth  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
@@ -213,6 +213,9 @@ SMALL_CASES = [
     synth.MoEConfig("gemm_multi_block", 256, 256, 2, 2, 300),
     synth.MoEConfig("gemm_ragged_k_and_rows", 416, 96, 3, 1, 257),
     synth.MoEConfig("gemm_sigmoid_shared", 512, 256, 8, 2, 300, score="sigmoid", shared=True),
+    # about 130 positions per expert: a full 128-position block plus a short
+    # tail block (its 16-position tiles past the segment skipped)
+    synth.MoEConfig("gemm_tail", 256, 128, 2, 1, 262),
 ]
 
 
@@ -324,23 +327,15 @@ TILE_CASES = [
 
 
 @pytest.mark.parametrize("cfg", TILE_CASES, ids=lambda c: c.name)
-def test_expert_kernels_agree(dev, cfg, monkeypatch):
+def test_expert_kernels_agree(dev, cfg):
     """Each decode expert stage has two kernels: the token-tile kernel (the
     operand of a 16-position tile copied into LDS once, one wave per row tile)
     where the row tiles of all token tiles give at least four waves per CU
-    (eight for down), else the K-split kernel.  With both stages token-tile,
-    they can also run as one persistent launch (ffn_tile_kernel, selected by
-    PHANTOM_MOE_FFN_KERNEL=fused: down jobs wait on per-tile counts of
-    finished gate/up jobs).  These shapes are in the token-tile regime of both
-    stages.  The token-tile and K-split pairs (the latter forced by
-    PHANTOM_MOE_GATE_UP_KERNEL / PHANTOM_MOE_DOWN_KERNEL=classic) must meet
-    the layer tolerance against the oracle, shared expert and ragged last
-    quads of H and of I included.  The fused launch does the token-tile
-    launches' arithmetic, so its output must equal theirs bit for bit, on
-    every one of several calls (a read of h before its producers finished
-    would differ).  So must the gate/up token-tile kernel in 4-wave
-    workgroups (PHANTOM_MOE_GATE_UP_WAVES=4; 8 is the default): the waves of a
-    workgroup share the operand, each row tile's sums are the same."""
+    (eight for down), else the K-split kernel.  These shapes are in the
+    token-tile regime of both stages; the K-split pair is forced with the
+    option PHANTOM_MOE_OPT_DECODE_KSPLIT.  Both pairs must meet the layer
+    tolerance against the oracle, shared expert and ragged last quads of H and
+    of I included, with identical routing."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     n_slots = cfg.T * cfg.k
     max_tiles = -(-n_slots // 16) + min(n_slots, cfg.E) + (-(-cfg.T // 16) if cfg.shared else 0)
@@ -358,59 +353,16 @@ def test_expert_kernels_agree(dev, cfg, monkeypatch):
     names = lib.phantom_moe_expert_kernels(cfg.T, cfg.H, cfg.I, cfg.E, cfg.k, int(cfg.shared)).decode()
     assert names == "gate_up=gate_up_tile_kernel;down=down_tile_kernel"
     y_tile, _, idx_tile = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b, return_routing=True)
-    y_tile = y_tile.cpu().numpy()
-    monkeypatch.setenv("PHANTOM_MOE_FFN_KERNEL", "fused")
-    names = lib.phantom_moe_expert_kernels(cfg.T, cfg.H, cfg.I, cfg.E, cfg.k, int(cfg.shared)).decode()
-    assert names == "gate_up=ffn_tile_kernel;down=ffn_tile_kernel"
-    for rep in range(4):
-        y_fus = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b).cpu().numpy()
-        assert np.array_equal(y_fus.view(np.uint32), y_tile.view(np.uint32)), f"fused call {rep + 1} differs"
-    monkeypatch.delenv("PHANTOM_MOE_FFN_KERNEL")
-    monkeypatch.setenv("PHANTOM_MOE_GATE_UP_WAVES", "4")
-    y_w4 = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b).cpu().numpy()
-    monkeypatch.delenv("PHANTOM_MOE_GATE_UP_WAVES")
-    assert np.array_equal(y_w4.view(np.uint32), y_tile.view(np.uint32)), "4-wave gate/up workgroups differ"
-    monkeypatch.setenv("PHANTOM_MOE_GATE_UP_KERNEL", "classic")
-    monkeypatch.setenv("PHANTOM_MOE_DOWN_KERNEL", "classic")
-    y_cls, _, idx_cls = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b, return_routing=True)
-    monkeypatch.delenv("PHANTOM_MOE_GATE_UP_KERNEL")
-    monkeypatch.delenv("PHANTOM_MOE_DOWN_KERNEL")
+    old = _lib.set_option(_lib.OPT_DECODE_KSPLIT, 1)
+    try:
+        names = lib.phantom_moe_expert_kernels(cfg.T, cfg.H, cfg.I, cfg.E, cfg.k, int(cfg.shared)).decode()
+        assert names == "gate_up=gate_up_kernel;down=down_kernel"
+        y_cls, _, idx_cls = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b, return_routing=True)
+    finally:
+        _lib.set_option(_lib.OPT_DECODE_KSPLIT, old)
     np.testing.assert_array_equal(idx_tile.cpu().numpy(), ridx)
     np.testing.assert_array_equal(idx_cls.cpu().numpy(), ridx)
-    check_y(y_tile, ry, cfg.name + " token-tile")
+    check_y(y_tile.cpu().numpy(), ry, cfg.name + " token-tile")
     check_y(y_cls.cpu().numpy(), ry, cfg.name + " K-split")
 
 
-GEMM_CASES = [c for c in SMALL_CASES if c.name in ("gemm_ragged_k_and_rows", "gemm_sigmoid_shared", "gemm_multi_block")]
-
-
-@pytest.mark.parametrize("cfg", GEMM_CASES, ids=lambda c: c.name)
-def test_gemm_pipelines_agree(dev, cfg, monkeypatch):
-    """The prefill GEMM has two tile pipelines: the LDS ring (default: both
-    operands copied two K quads ahead by direct-to-LDS loads, 8 waves) and the
-    register-staged one (PHANTOM_MOE_GEMM_KERNEL=v1).  The ring has two exact
-    forms of the arithmetic: integer group sums scaled in fp32 (default) and
-    split-scale operands (PHANTOM_MOE_GEMM_SCALE=split).  All three must meet
-    the layer tolerance against the oracle, ragged K and rows and the shared
-    expert included, and the two ring forms, both exact up to fp32 rounding,
-    must agree to 1e-5 relative."""
-    L = synth.host_layer(cfg)
-    xb = synth.activations(cfg.T, cfg.H, seed=11)
-    ex = dev_weights(L, dev)
-    b = None if L.router_bias is None else torch.from_numpy(L.router_bias).to(dev)
-    W = torch.from_numpy(L.router_w).to(dev)
-    x = to_bf16_tensor(xb, dev)
-    ry, ridx, _ = oracle.moe_forward(xb, L.router_w, L.gate, L.up, L.down, cfg.k, cfg.score_mode,
-                                     L.router_bias, shared=L.shared)
-    y_ring = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b).cpu().numpy()
-    monkeypatch.setenv("PHANTOM_MOE_GEMM_SCALE", "split")
-    y_split = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b).cpu().numpy()
-    monkeypatch.delenv("PHANTOM_MOE_GEMM_SCALE")
-    monkeypatch.setenv("PHANTOM_MOE_GEMM_KERNEL", "v1")
-    y_v1 = phantom_moe.moe_forward(x, W, ex, cfg.k, cfg.score, b)
-    monkeypatch.delenv("PHANTOM_MOE_GEMM_KERNEL")
-    check_y(y_ring, ry, cfg.name + " LDS ring, fp32-scaled")
-    check_y(y_split, ry, cfg.name + " LDS ring, split-scale")
-    check_y(y_v1.cpu().numpy(), ry, cfg.name + " register-staged")
-    rel = np.linalg.norm(y_ring.astype(np.float64) - y_split) / np.linalg.norm(y_split.astype(np.float64))
-    assert rel <= 1e-5, f"{cfg.name}: ring forms differ by {rel:.2e} relative"
