@@ -215,6 +215,9 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
   const size_t o_cnt = take(sizeof(int32_t));
   const size_t o_pcnt = take(sizeof(int32_t) * (size_t)E * (size_t)perm_blocks(T * k));
   const size_t o_ptb = take(sizeof(int32_t) * (size_t)E);
+  const bool two_pass = two_pass_shape(T, E);
+  const size_t o_apx = two_pass ? take(sizeof(float) * (size_t)(T * E + T + E)) : 0;
+  const size_t o_cand = two_pass ? take((size_t)(T * E)) : 0;
   if (ws && base) {
     char* b = static_cast<char*>(base);
     ws->ctl = reinterpret_cast<uint32_t*>(b + o_ctl);
@@ -245,6 +248,8 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
     ws->counter = reinterpret_cast<int32_t*>(b + o_cnt);
     ws->perm_cnt = reinterpret_cast<int32_t*>(b + o_pcnt);
     ws->perm_tb = reinterpret_cast<int32_t*>(b + o_ptb);
+    ws->approx = two_pass ? reinterpret_cast<float*>(b + o_apx) : nullptr;
+    ws->cand = two_pass ? reinterpret_cast<uint8_t*>(b + o_cand) : nullptr;
   }
   return off;
 }

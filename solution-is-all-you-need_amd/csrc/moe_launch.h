@@ -118,6 +118,8 @@ struct Workspace {
   int32_t* counter = nullptr;       // [1] router hand-off counter (reset by every route launch)
   int32_t* perm_cnt = nullptr;      // [E][perm_blocks(T * k)] per-chunk expert counts, then bases (large batches)
   int32_t* perm_tb = nullptr;       // [E] first token tile of each expert (large batches)
+  float* approx = nullptr;          // [T * E + T + E] approximate logits, |x_t|, |w_e| (two-pass router)
+  uint8_t* cand = nullptr;          // [E * T] candidate flags, expert-major (two-pass router)
 };
 
 // Batches of at least this many slots use the many-workgroup permute.
@@ -137,6 +139,12 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
 
 // Router tiling: tokens per logits workgroup tile.
 int router_token_tile(int64_t T);
+// Batches routed in two passes (approximate logits with an error bound, then
+// the exact logits of the candidates): bf16 x, T >= 128, E >= 16.  The
+// workspace holds their regions (approx, cand) whenever T and E qualify.
+constexpr int64_t kTwoPassMinT = 128;
+inline bool two_pass_shape(int64_t T, int E) { return T >= kTwoPassMinT && E >= 16; }
+inline bool two_pass_route(int64_t T, int E, int x_dtype) { return x_dtype == 0 && two_pass_shape(T, E); }
 
 hipError_t launch_q4_repack(const uint8_t* src, int64_t rows, int64_t K, uint8_t* nib,
                             uint16_t* scale, hipStream_t stream);

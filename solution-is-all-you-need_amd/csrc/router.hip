@@ -727,6 +727,265 @@ __global__ __launch_bounds__(256) void route_logits_big_kernel(RouteK a) {
   }
 }
 
+// ------------------------------------------------- many-token router, two passes
+//
+// For prefill batches the fixed-order fp64 logits of every (token, expert)
+// pair cost 100 us at 4096 tokens of H 2048, E 128 -- while only the top k
+// of each token, and the experts near the k-th, decide anything.  So:
+//   route_approx_kernel: L~ = x . bf16(w) on the matrix cores (fp32
+//     accumulation) for every pair, plus the norms |x_t| and |w_e|;
+//   route_candidates_kernel (one wave per token): the error bound
+//     |L~ - L| <= C(H) |x_t| |w_e| gives every expert an interval; experts
+//     whose upper end reaches the k-th largest lower end are the candidates
+//     (a superset of the exact top k: any expert below that has k others
+//     strictly above it); the others' logits are set to -inf;
+//   route_exact_kernel (per expert and block of tokens): the fixed-order
+//     fp64 logits (contract above) of the candidate pairs, 16 tokens per wave
+//     so each lane's slice of the weight row is loaded once per 16 pairs;
+//   route_select_kernel: the exact selection and weights, unchanged.
+// The bound: bf16 rounding of w is at most 2^-9 |w| (round to nearest), the
+// products x * bf16(w) are exact in fp32, and H fp32 additions in any order
+// add at most H 2^-24 of sum |x bf16(w)| (taken as H 2^-22, 4x margin, for
+// whatever order and internal precision the MFMA uses); Cauchy-Schwarz bounds
+// sum |x||w| by |x| |w|.  Tokens with a non-finite approximate logit or norm
+// take every expert as a candidate (the full exact row), so NaN and inf
+// follow the contract exactly as on the one-pass path.
+constexpr int kApproxTok = 64;     // tokens per approx workgroup (4 waves x 16)
+constexpr int kApproxExp = 32;     // experts per approx workgroup (2 tiles of 16)
+constexpr int kApproxChunk = 256;  // K staged in LDS per step
+constexpr int kApproxUnits = kApproxExp * kApproxChunk / 8 / 256;  // 8-wide W units per thread per chunk
+constexpr int kExactTok = 256;     // tokens scanned per exact workgroup
+constexpr int kExactP = 16;        // token pairs per wave pass
+
+__global__ __launch_bounds__(256) void route_approx_kernel(RouteK a, float* approx, float* nx, float* nw) {
+  // W chunk as bf16 B operands: [expert tile][K step][lane] 16-byte units
+  __shared__ u32x4 s_w[(kApproxExp / 16) * (kApproxChunk / 32) * kWave];
+  __shared__ float s_nw[kApproxExp];
+  const int lane = threadIdx.x % kWave;
+  const int w = threadIdx.x / kWave;
+  const int64_t t0 = (int64_t)blockIdx.y * kApproxTok;
+  const int e0 = blockIdx.x * kApproxExp;
+  const uint16_t* x = static_cast<const uint16_t*>(a.x);
+  if (a.prep_x) prep_x_tile(a, t0, kApproxTok);
+  if (a.counter && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *a.counter = 0;
+  // A rows: token t0 + 16 w + lane % 16 (clamped), K 8 (lane / 16) .. + 8 of each step
+  const int64_t tr = t0 + 16 * w + lane % 16;
+  const uint16_t* xrow = x + (tr < a.T ? tr : a.T - 1) * a.H + 8 * (lane / 16);
+  f32x4 acc[kApproxExp / 16];
+#pragma unroll
+  for (int i = 0; i < kApproxExp / 16; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float sx = 0.0f;                // this lane's share of |x|^2
+  float sw[kApproxUnits];         // |w_e|^2 shares of the units this thread converts
+#pragma unroll
+  for (int i = 0; i < kApproxUnits; ++i) sw[i] = 0.0f;
+  // unit u = threadIdx.x + 256 i: expert u / 32, 8-wide K block u % 32 of the chunk
+  float4 wr[kApproxUnits][2];
+  u32x4 ar[kApproxChunk / 32];
+  auto load = [&](int64_t c0) {
+    const int kc = (int)(a.H - c0 < kApproxChunk ? a.H - c0 : kApproxChunk);
+#pragma unroll
+    for (int i = 0; i < kApproxUnits; ++i) {
+      const int u = threadIdx.x + 256 * i;
+      const int e = u / 32, kb = u % 32;
+      const int ec = e0 + e < a.E ? e0 + e : a.E - 1;
+      const int kbc = 8 * kb < kc ? kb : 0;  // past the end: a valid address, zeroed at the store
+      const float4* src = reinterpret_cast<const float4*>(a.W + (int64_t)ec * a.H + c0 + 8 * kbc);
+      wr[i][0] = src[0];
+      wr[i][1] = src[1];
+    }
+#pragma unroll
+    for (int s = 0; s < kApproxChunk / 32; ++s)
+      ar[s] = 32 * s < kc ? *reinterpret_cast<const u32x4*>(xrow + c0 + 32 * s) : u32x4{0u, 0u, 0u, 0u};
+  };
+  load(0);
+  for (int64_t c0 = 0; c0 < a.H; c0 += kApproxChunk) {
+    const int kc = (int)(a.H - c0 < kApproxChunk ? a.H - c0 : kApproxChunk);  // multiple of 32
+#pragma unroll
+    for (int i = 0; i < kApproxUnits; ++i) {
+      const int u = threadIdx.x + 256 * i;
+      const int e = u / 32, kb = u % 32;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (8 * kb < kc) {
+        const float f[8] = {wr[i][0].x, wr[i][0].y, wr[i][0].z, wr[i][0].w,
+                            wr[i][1].x, wr[i][1].y, wr[i][1].z, wr[i][1].w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sw[i] = __builtin_fmaf(f[j], f[j], sw[i]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = float_to_bf16_bits(f[2 * j]) | (float_to_bf16_bits(f[2 * j + 1]) << 16);
+      }
+      s_w[((e / 16) * (kApproxChunk / 32) + kb / 4) * kWave + (e % 16) + 16 * (kb % 4)] = v;
+    }
+    u32x4 av[kApproxChunk / 32];
+#pragma unroll
+    for (int s = 0; s < kApproxChunk / 32; ++s) av[s] = ar[s];
+    __syncthreads();
+    if (c0 + kApproxChunk < a.H) load(c0 + kApproxChunk);  // the next chunk flies during this one's MFMAs
+#pragma unroll
+    for (int s = 0; s < kApproxChunk / 32; ++s) {
+      if (32 * s >= kc) break;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = bf16_bits_to_float(av[s][j] & 0xffffu), hi = bf16_bits_to_float(av[s][j] >> 16);
+        sx = __builtin_fmaf(lo, lo, sx);
+        sx = __builtin_fmaf(hi, hi, sx);
+      }
+#pragma unroll
+      for (int et = 0; et < kApproxExp / 16; ++et)
+        acc[et] = mfma_bf16_16x16x32(av[s], s_w[(et * (kApproxChunk / 32) + s) * kWave + lane], acc[et]);
+    }
+    __syncthreads();  // every wave has read the B operands before the next chunk overwrites them
+  }
+  // |x_t|^2: the four lanes of a row hold disjoint shares
+  sx += __shfl_xor(sx, 16, kWave);
+  sx += __shfl_xor(sx, 32, kWave);
+  // |w_e|^2: the 32 threads of expert e (u / 32 == e, consecutive lanes)
+#pragma unroll
+  for (int i = 0; i < kApproxUnits; ++i) {
+    float v = sw[i];
+    v += __shfl_xor(v, 1, kWave);
+    v += __shfl_xor(v, 2, kWave);
+    v += __shfl_xor(v, 4, kWave);
+    v += __shfl_xor(v, 8, kWave);
+    v += __shfl_xor(v, 16, kWave);
+    if (lane % 32 == 0) s_nw[(threadIdx.x + 256 * i) / 32] = v;
+  }
+  __syncthreads();
+  // outputs: lane (n, g) of tile et holds tokens 16 w + 4 g + j, expert 16 et + n
+#pragma unroll
+  for (int et = 0; et < kApproxExp / 16; ++et) {
+    const int e = e0 + 16 * et + lane % 16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t t = t0 + 16 * w + 4 * (lane / 16) + j;
+      if (t < a.T && e < a.E) approx[t * a.E + e] = acc[et][j];
+    }
+  }
+  if (blockIdx.x == 0 && lane < 16 && tr < a.T) nx[tr] = sqrtf(sx);
+  if (blockIdx.y == 0 && threadIdx.x < kApproxExp && e0 + (int)threadIdx.x < a.E)
+    nw[e0 + threadIdx.x] = sqrtf(s_nw[threadIdx.x]);
+}
+
+// Order-preserving 32-bit key of a finite or infinite fp32 value.
+__device__ inline uint32_t f32_key(float v) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, v == 0.0f ? 0.0f : v);
+  return (b >> 31) ? ~b : (b | 0x80000000u);
+}
+
+// Candidates of each token (one wave per token): cand[e * T + t] = 1 for a
+// candidate, else 0 and logits[t][e] = -inf.
+template <int NV>
+__global__ __launch_bounds__(256) void route_candidates_kernel(RouteK a, const float* approx, const float* nx,
+                                                               const float* nw, uint8_t* cand) {
+  const int lane = threadIdx.x % kWave;
+  const int w = threadIdx.x / kWave;
+  // C(H) of the bound, with 2^-8 relative room for the rounding of the norms
+  const float cH = (1.0f / 512.0f + (float)a.H * (1.0f / 4194304.0f) * 1.002f) * (1.0f + 1.0f / 256.0f);
+  const float sqrtH = sqrtf((float)a.H) * 1.01f;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + w; t < a.T; t += (int64_t)gridDim.x * 4) {
+    const float nxt = nx[t];
+    float lo[NV], hi[NV];
+    bool all = !isfinite(nxt);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int e = lane + kWave * v;
+      const int ec = e < a.E ? e : a.E - 1;
+      const float l = approx[t * a.E + ec];
+      const float b = a.bias ? a.bias[ec] : 0.0f;
+      const float m = l + b;
+      // + fp32 rounding of m and of the interval ends, + inputs the matrix
+      // cores may flush as denormals (each |x| or |w| < 2^-126, so their
+      // products sum to at most 2^-126 sqrt(H) (|x| + |w|))
+      const float bnd = cH * nxt * nw[ec] + (fabsf(l) + fabsf(b)) * (1.0f / 4194304.0f) +
+                        sqrtH * 2.4e-38f * (nxt + nw[ec]) + 1e-30f;
+      all = all || (e < a.E && !(isfinite(m) && isfinite(bnd)));
+      lo[v] = m - bnd;
+      hi[v] = m + bnd;
+    }
+    all = __ballot(all) != 0ull;
+    // the k-th largest lower end: radix descent over 32-bit keys
+    uint32_t kth = 0;
+    if (!all) {
+      uint32_t key[NV];
+#pragma unroll
+      for (int v = 0; v < NV; ++v) key[v] = lane + kWave * v < a.E ? f32_key(lo[v]) : 0u;
+      for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t c = kth | (1u << bit);
+        int cnt = 0;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) cnt += __popcll(__ballot(key[v] >= c));
+        if (cnt >= a.k) kth = c;
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int e = lane + kWave * v;
+      if (e < a.E) {
+        const bool c = all || f32_key(hi[v]) >= kth;
+        cand[(int64_t)e * a.T + t] = c ? 1 : 0;
+        if (!c) a.logits[t * a.E + e] = -INFINITY;
+      }
+    }
+  }
+}
+
+// Exact logits of the candidate pairs of expert blockIdx.y among tokens
+// [kExactTok * blockIdx.x, + kExactTok): the tokens are compacted in LDS, then
+// each wave takes 16 at a time (the last group padded by repeating its last
+// token): lane l sums, for each token, the h with (h mod 256) / 4 == l in
+// increasing h, with its slice of the weight row loaded once for the 16.
+__global__ __launch_bounds__(256) void route_exact_kernel(RouteK a, const uint8_t* cand) {
+  __shared__ int s_tok[kExactTok];
+  __shared__ int s_cnt[4];
+  const int lane = threadIdx.x % kWave;
+  const int w = threadIdx.x / kWave;
+  const int e = blockIdx.y;
+  const int64_t t0 = (int64_t)blockIdx.x * kExactTok;
+  // compaction in token order: wave w takes tokens t0 + 64 w + lane
+  const int64_t t = t0 + 64 * w + lane;
+  const bool c = t < a.T && cand[(int64_t)e * a.T + t] != 0;
+  const uint64_t m = __ballot(c);
+  if (lane == 0) s_cnt[w] = __popcll(m);
+  __syncthreads();
+  int base = 0, n = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    base += i < w ? s_cnt[i] : 0;
+    n += s_cnt[i];
+  }
+  if (c) s_tok[base + __popcll(m & ((1ull << lane) - 1ull))] = (int)(t - t0);
+  __syncthreads();
+  const uint16_t* x = static_cast<const uint16_t*>(a.x);
+  const float* wrow = a.W + (int64_t)e * a.H;
+  const double bias = a.bias ? (double)a.bias[e] : 0.0;
+  for (int g0 = kExactP * w; g0 < n; g0 += kExactP * 4) {
+    int64_t tk[kExactP];
+#pragma unroll
+    for (int j = 0; j < kExactP; ++j) tk[j] = t0 + s_tok[g0 + j < n ? g0 + j : n - 1];
+    double acc[kExactP];
+#pragma unroll
+    for (int j = 0; j < kExactP; ++j) acc[j] = 0.0;
+    for (int64_t h0 = 4 * lane; h0 < a.H; h0 += 256) {
+      const float4 wv = *reinterpret_cast<const float4*>(wrow + h0);
+      const double wd[4] = {(double)wv.x, (double)wv.y, (double)wv.z, (double)wv.w};
+#pragma unroll
+      for (int j = 0; j < kExactP; ++j) {
+        const uint2 xv = *reinterpret_cast<const uint2*>(x + tk[j] * a.H + h0);
+        acc[j] += (double)bf16_bits_to_float(xv.x & 0xffffu) * wd[0];
+        acc[j] += (double)bf16_bits_to_float(xv.x >> 16) * wd[1];
+        acc[j] += (double)bf16_bits_to_float(xv.y & 0xffffu) * wd[2];
+        acc[j] += (double)bf16_bits_to_float(xv.y >> 16) * wd[3];
+      }
+    }
+    const double tot = tree_reduce_pairs<kExactP>(acc);
+    if ((lane & 3) == 0) {
+      const int pair = tree_pair_of_lane<kExactP>(lane);
+      double v = tot;
+      if (a.bias) v = v + bias;
+      a.logits[tk[pair] * a.E + e] = v;
+    }
+  }
+}
+
 // ------------------------------------------------- permute, many workgroups
 //
 // For large batches the one-workgroup permute is bound by one CU's issue
@@ -972,6 +1231,24 @@ static hipError_t launch_logits_t(const RouteK& k, int TT, int n_ttiles, hipStre
   return hipGetLastError();
 }
 
+// The two-pass router (approximate logits, candidates, exact candidate
+// logits, then the usual selection) from this many bf16 tokens on (E >= 16).
+static hipError_t launch_route_two_pass(const RouteK& k, const Workspace& ws, hipStream_t stream) {
+  float* approx = ws.approx;
+  float* nx = approx + k.T * k.E;
+  float* nw = nx + k.T;
+  hipLaunchKernelGGL(route_approx_kernel, dim3((unsigned)ceil_div(k.E, kApproxExp), (unsigned)ceil_div(k.T, kApproxTok)),
+                     dim3(256), 0, stream, k, approx, nx, nw);
+  const dim3 grid((unsigned)ceil_div(k.T, 4)), block(256);
+  if (k.E <= 64) hipLaunchKernelGGL(route_candidates_kernel<1>, grid, block, 0, stream, k, approx, nx, nw, ws.cand);
+  else if (k.E <= 128) hipLaunchKernelGGL(route_candidates_kernel<2>, grid, block, 0, stream, k, approx, nx, nw, ws.cand);
+  else if (k.E <= 256) hipLaunchKernelGGL(route_candidates_kernel<4>, grid, block, 0, stream, k, approx, nx, nw, ws.cand);
+  else hipLaunchKernelGGL(route_candidates_kernel<8>, grid, block, 0, stream, k, approx, nx, nw, ws.cand);
+  hipLaunchKernelGGL(route_exact_kernel, dim3((unsigned)ceil_div(k.T, kExactTok), (unsigned)k.E), dim3(256), 0, stream,
+                     k, static_cast<const uint8_t*>(ws.cand));
+  return hipGetLastError();
+}
+
 hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t stream) {
   RouteK k;
   k.x = r.x;
@@ -1009,8 +1286,10 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
   const unsigned sel_blocks = (unsigned)ceil_div(r.T, kSelectWaves);
   k.fuse_permute = (r.do_permute && sel_blocks > 1 && sel_blocks <= kFusedSelectBlocks) ? 1 : 0;
   k.counter = k.fuse_permute ? ws.counter : nullptr;
-  hipError_t err = (r.x_dtype == 0) ? launch_logits_t<uint16_t>(k, TT, n_ttiles, stream)
-                                    : launch_logits_t<float>(k, TT, n_ttiles, stream);
+  hipError_t err = two_pass_route(r.T, r.E, r.x_dtype) && ws.approx && ws.cand && !k.fuse_permute
+                       ? launch_route_two_pass(k, ws, stream)
+                       : ((r.x_dtype == 0) ? launch_logits_t<uint16_t>(k, TT, n_ttiles, stream)
+                                           : launch_logits_t<float>(k, TT, n_ttiles, stream));
   if (err != hipSuccess) return err;
   // One wave per token, four tokens per workgroup, so selection is spread
   // over many CUs.  The permute runs in the select launch up to

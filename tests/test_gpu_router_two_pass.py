@@ -1,0 +1,112 @@
+"""The many-token router (two passes: approximate logits on the matrix cores
+with an error bound, then the fixed-order fp64 logits of the candidate
+experts) against the oracle's exact routing.
+
+From 128 bf16 tokens on (E >= 16) phantom_moe_route takes this path.  Its
+result must equal the one-pass contract bit for bit: the same experts in the
+same order and the same weights.  The cases force what the bound must get
+right: logits so close that the approximate pass cannot order them (every
+expert a candidate, candidates taken 16 at a time), exact ties between
+duplicated rows (the lower index wins), a clear top k beside a cluster of
+near ties, and non-finite inputs (a token with NaN or inf falls back to the
+full exact row)."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import phantom_moe  # noqa: E402
+from helpers import to_bf16_tensor  # noqa: E402
+from oracle import oracle  # noqa: E402
+from phantom_moe import synth  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def check(dev, xb, W, k, score=0, bias=None):
+    x = to_bf16_tensor(xb, dev)
+    b = None if bias is None else torch.from_numpy(bias).to(dev)
+    w, idx = phantom_moe.route(x, torch.from_numpy(W).to(dev), k, score, b)
+    ridx, rw = oracle.route(xb, W, k, score, bias)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-6, atol=1e-7, equal_nan=True)
+    return ridx
+
+
+def base_inputs(T, H, E, seed):
+    rng = np.random.default_rng(seed)
+    xb = synth.f32_to_bf16_bits(rng.standard_normal((T, H), dtype=np.float32))
+    W = (rng.standard_normal((E, H), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    return rng, xb, W
+
+
+@pytest.mark.parametrize("kind", ["cluster", "mixed", "duplicates", "one_ulp"])
+def test_near_ties(dev, kind):
+    T, H, E, k = 256, 512, 64, 8
+    rng, xb, W = base_inputs(T, H, E, seed=hash(kind) % 1000)
+    base = W[0].copy()
+    if kind == "cluster":
+        # every logit within about 1e-6 of the others: all 64 are candidates
+        W[:] = base * (1.0 + np.float32(1e-6) * rng.standard_normal((E, H), dtype=np.float32))
+    elif kind == "mixed":
+        # a cluster of 32 near-identical experts among 32 ordinary ones
+        W[:32] = base * (1.0 + np.float32(1e-6) * rng.standard_normal((32, H), dtype=np.float32))
+    elif kind == "duplicates":
+        # exact ties: rows duplicated at distinct indices
+        W[1::4] = W[0::4]
+    else:
+        # rows one ulp apart in a single element
+        W[:] = base
+        for e in range(E):
+            W[e, e % H] = np.nextafter(base[e % H], np.float32(np.inf) if e % 2 else np.float32(-np.inf))
+    ridx = check(dev, xb, W.astype(np.float32), k)
+    assert ridx.shape == (T, k)
+
+
+@pytest.mark.parametrize("T,H,E,k,score", [
+    (128, 416, 16, 4, 0),      # the smallest two-pass batch; H not a multiple of 256
+    (333, 2048, 128, 8, 0),    # ragged token blocks
+    (200, 7168, 256, 8, 1),    # DeepSeek-V3 router shape, sigmoid scores
+    (160, 256, 512, 32, 0),    # the widest rows (8 logits per lane), top-32
+    (129, 1024, 100, 6, 1),    # E not a multiple of 16
+])
+def test_shapes_with_bias(dev, T, H, E, k, score):
+    rng, xb, W = base_inputs(T, H, E, seed=T + H + E)
+    bias = (rng.standard_normal(E).astype(np.float32) * np.float32(0.05)).astype(np.float32)
+    check(dev, xb, W, k, score, bias)
+
+
+def test_non_finite_inputs(dev):
+    """NaN and +-inf in some tokens and in the bias: those rows take the full
+    exact path and rank exactly as the contract says; other tokens are
+    unaffected."""
+    T, H, E, k = 192, 256, 64, 8
+    rng, xb, W = base_inputs(T, H, E, seed=77)
+    xb[3, 10] = 0x7FC0   # NaN
+    xb[50, 0] = 0x7F80   # +inf
+    xb[51, 7] = 0xFF80   # -inf
+    xb[52, 0] = 0x7F80
+    xb[52, 1] = 0xFF80   # inf - inf
+    check(dev, xb, W, k)
+    bias = np.zeros(E, np.float32)
+    bias[5] = np.nan
+    bias[9] = -np.inf
+    bias[12] = np.inf
+    check(dev, xb, W, k, 0, bias)
+
+
+def test_wide_logit_range(dev):
+    """Logits from tiny to large magnitudes (scaled rows and tokens): the
+    bound scales with |x| |w|, so the selection stays exact."""
+    T, H, E, k = 256, 512, 128, 8
+    rng, xb, W = base_inputs(T, H, E, seed=5)
+    W *= (10.0 ** rng.uniform(-6, 3, size=(E, 1))).astype(np.float32)
+    xf = synth.bf16_bits_to_f32(xb) * (10.0 ** rng.uniform(-4, 4, size=(T, 1))).astype(np.float32)
+    check(dev, synth.f32_to_bf16_bits(xf.astype(np.float32)), W.astype(np.float32), k)
