@@ -270,6 +270,11 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
   __shared__ int s_seg_beg[kFusedMaxSlots + 1];
   __shared__ int s_seg_cnt[kFusedMaxSlots + 1];
   __shared__ short s_e2u[kMaxExperts];
+  // combine: per slot (then per token of the shared expert) the down
+  // partials' first index, the step between parts, and the number of parts
+  __shared__ int s_cb_base[kFusedMaxSlots + kFusedMaxT];
+  __shared__ int s_cb_step[kFusedMaxSlots + kFusedMaxT];
+  __shared__ int s_cb_np[kFusedMaxSlots + kFusedMaxT];
   __shared__ uint32_t s_epoch;
   __shared__ int s_nseg;
   __shared__ int s_fail;
@@ -346,7 +351,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
     s_epoch = tg;
     __hip_atomic_store(&a.presence[b], tag64(tg), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __syncthreads();
+  lds_barrier();
   const uint32_t tag = (uint32_t)uni((int)s_epoch);
 
   // ---- 1. publish the logit ---------------------------------------------
@@ -362,23 +367,23 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
   }
 
   // ---- 2. wait for every logit; top-k; segments ----------------------------
-  // Two polls per lane are in flight at a time: the next load is issued
-  // before the previous one is checked, so a slot is seen within about one
-  // poll interval of its arrival rather than a full round trip later.
+  // One poll per lane in flight: a load left in flight at the exit would
+  // make the first later instruction that reuses its registers wait for it
+  // (a memory round trip).
   {
     const uint32_t want = tag + a.skew_route;
     for (int i0 = w * kWave; i0 < T * E; i0 += kFThreads) {
       const int i = i0 + lane;
-      const uint32_t off = i < T * E ? (uint32_t)i * 16u : 0xFFFFF000u;
       bool done = i >= T * E;
-      u32x4 prev = __builtin_amdgcn_raw_buffer_load_b128(slot_r, (int)off, 0, kDeviceScope);
       for (uint32_t it = 0;; ++it) {
-        const u32x4 next = __builtin_amdgcn_raw_buffer_load_b128(slot_r, (int)off, 0, kDeviceScope);
-        if (!done && prev.y == want && prev.w == ~want) {
-          const double lv = __builtin_bit_cast(double, ((uint64_t)prev.z << 32) | prev.x);
-          s_lv[i] = lv;
-          s_key[i] = logit_key(lv);
-          done = true;
+        if (!done) {
+          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(slot_r, (int)((uint32_t)i * 16u), 0, kDeviceScope);
+          if (v.y == want && v.w == ~want) {
+            const double lv = __builtin_bit_cast(double, ((uint64_t)v.z << 32) | v.x);
+            s_lv[i] = lv;
+            s_key[i] = logit_key(lv);
+            done = true;
+          }
         }
         if (__all(done)) break;
         if (it >= a.wait_polls) {
@@ -388,13 +393,11 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
           }
           break;
         }
-        __builtin_amdgcn_s_sleep(1);
-        prev = next;
       }
     }
   }
   for (int i = threadIdx.x; i < T * E; i += kFThreads) s_rank[i] = 0;
-  __syncthreads();
+  lds_barrier();
   const bool route_failed = uni(s_fail) != 0;
   if (!route_failed) {
     // Top-k of every token by rank counting over the whole workgroup: the
@@ -430,7 +433,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
       if (P == 1) s_rank[el] = cnt;
       else atomicAdd(&s_rank[el], cnt);
     }
-    __syncthreads();
+    lds_barrier();
     // one wave per token: its k winners to their slots, then the weights,
     // softmax exp(l_j - l_0) or sigmoid(l_j) normalised by their sum over the
     // k slots in slot order, in fp64, stored as fp32
@@ -462,7 +465,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (route_failed) {
     // no routing: this workgroup's outputs cannot be computed
     if (b == 0)
@@ -536,11 +539,11 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
       }
     } else {
       for (int e = threadIdx.x; e < E; e += kFThreads) s_emask[e] = 0;
-      __syncthreads();
+      lds_barrier();
       for (int s = threadIdx.x; s < T * k; s += kFThreads)
         __hip_atomic_fetch_or(&s_emask[s_sel_idx[s]], 1ull << (s / k), __ATOMIC_RELAXED,
                               __HIP_MEMORY_SCOPE_WORKGROUP);
-      __syncthreads();
+      lds_barrier();
       if (w == 0) {
         // active experts in increasing id, their segment sizes and offsets
         const uint64_t lt = (1ull << lane) - 1ull;
@@ -581,7 +584,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
           s_nseg = nu + (a.has_shared ? 1 : 0);
         }
       }
-      __syncthreads();
+      lds_barrier();
       // every slot's segment position (tokens in increasing order within a
       // segment: the stable permute) and every position's token
       for (int s = threadIdx.x; s < T * k; s += kFThreads) {
@@ -595,7 +598,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
         for (int t = threadIdx.x; t < T; t += kFThreads) s_seg_tok[T * k + t] = t;
     }
   }
-  __syncthreads();  // the routing scratch is dead from here on
+  lds_barrier();  // the routing scratch is dead from here on
 
   // ---- 3. work lists; every weight chunk of the workgroup -> LDS ------------
   const int S = route_failed ? 0 : uni(s_nseg);
@@ -614,6 +617,22 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
   // this wave's pairs per down item, and its down copies (nibbles + scales)
   const int cnt_w = (n_c - w * per) < per ? ((n_c - w * per) > 0 ? n_c - w * per : 0) : per;
   const int dn_copies = nd * cnt_w * 2;
+
+  // the combine's tables, while the routing results are at hand: slot s at
+  // position pos of segment u reads part pt of output row nn at
+  // (beg * KqI + pt * cnt + pos - beg) * 16 + nn, u's parts being the waves
+  // its (segment, quad) pairs fall to
+  if (S > 0 && nd > 0) {
+    for (int s = threadIdx.x; s < T * k + (a.has_shared ? T : 0); s += kFThreads) {
+      const bool sh = s >= T * k;
+      const int u = sh ? S - 1 : s_e2u[s_sel_idx[s]];
+      const int pos = sh ? T * k + (s - T * k) : s_slot_pos[s];
+      const int beg = s_seg_beg[u], cnt = s_seg_cnt[u];
+      s_cb_base[s] = (beg * KqI + pos - beg) * 16;
+      s_cb_step[s] = cnt * 16;
+      s_cb_np[s] = ((u + 1) * KqI - 1) / per - (u * KqI) / per + 1;
+    }
+  }
 
   const uint32_t gnib_bytes = (uint32_t)I * (uint32_t)Kq * 64u;  // one expert's gate (or up) nibbles
   const uint32_t gsc_bytes = (uint32_t)I * (uint32_t)Kq * 8u;
@@ -745,7 +764,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     for (int o = threadIdx.x; o < ng * 256; o += kFThreads) {
       const int ii = o / 256;
       const int mm = (o % 256) / 16;
@@ -799,7 +818,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
     }
     // every h store of the workgroup has completed before any flag is set
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    lds_barrier();
     if (threadIdx.x < ng) store_tag(flag_r, (uint32_t)(b + (int)threadIdx.x * G) * 8u, tag);
   }
 
@@ -827,22 +846,13 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
         }
       }
     }
-    // wait for every gate/up item of the layer (two polls in flight per lane)
+    // wait for every gate/up item of the layer (one poll per lane in flight)
     const uint32_t want = tag + a.skew_flags;
-    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     for (int i0 = w * kWave; i0 < n_gu; i0 += kFThreads) {
       const int i = i0 + lane;
-      const uint32_t off = i < n_gu ? (uint32_t)i * 8u : 0xFFFFF000u;
       bool done = i >= n_gu;
-      auto ld = [&]() {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(flag_r, (int)off, 0, kDeviceScope);
-        u32x2 r = {(uint32_t)v[0], (uint32_t)v[1]};
-        return r;
-      };
-      u32x2 prev = ld();
       for (uint32_t it = 0;; ++it) {
-        const u32x2 next = ld();
-        done = done || (prev.x == want && prev.y == ~want);
+        if (!done) done = tag_is(flag_r, (uint32_t)i * 8u, want);
         if (__all(done)) break;
         if (it >= a.wait_polls) {
           if (lane == 0) {
@@ -851,11 +861,9 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
           }
           break;
         }
-        __builtin_amdgcn_s_sleep(1);
-        prev = next;
       }
     }
-    __syncthreads();
+    lds_barrier();
     const bool h_failed = uni(s_fail) != 0;
     // h of every segment position -> LDS (device-scope loads, issued after the
     // flags arrived), plus an all-zero row; groups past I are zero
@@ -899,7 +907,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
       }
     }
     wait_vmcnt<0>();  // the h copies
-    __syncthreads();
+    lds_barrier();
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     for (int dd = 0; dd < nd; ++dd) {
       // The wave's pairs [w * per, w * per + per) in (segment, quad) order:
@@ -954,32 +962,38 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
           chunk(cc, bb, dv);
         }
       }
-      __syncthreads();
+      lds_barrier();
       const int rH = dn_first + dd * G;
       if (threadIdx.x < T * 16) {
+        // the slots' tables and partials are independent loads, issued eight
+        // slots at a time; the sums run in slot order
         const int t = threadIdx.x / 16;
         const int nn = threadIdx.x % 16;
         float acc_y = 0.0f;
-        for (int j = 0; j < k; ++j) {
-          const int pos = s_slot_pos[t * k + j];
-          const int su = s_e2u[s_sel_idx[t * k + j]];
-          const int beg = s_seg_beg[su], cnt = s_seg_cnt[su];
-          const int nparts = ((su + 1) * KqI - 1) / per - (su * KqI) / per + 1;
-          float sq = 0.0f;
-          for (int pt = 0; pt < nparts; ++pt) sq += s_dred[((beg * KqI + pt * cnt) + (pos - beg)) * 16 + nn];
-          acc_y += s_sel_w[t * k + j] * sq;
+        for (int j0 = 0; j0 < k; j0 += 8) {
+          float sq[8], wj[8];
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) {
+            const int s = t * k + (j0 + jj < k ? j0 + jj : k - 1);
+            const int base = s_cb_base[s] + nn, step = s_cb_step[s], np = s_cb_np[s];
+            wj[jj] = s_sel_w[s];
+            sq[jj] = s_dred[base];
+            for (int pt = 1; pt < np; ++pt) sq[jj] += s_dred[base + pt * step];
+          }
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj)
+            if (j0 + jj < k) acc_y += wj[jj] * sq[jj];
         }
         if (a.has_shared) {
-          const int su = S - 1;
-          const int beg = s_seg_beg[su], cnt = s_seg_cnt[su];
-          const int nparts = ((su + 1) * KqI - 1) / per - (su * KqI) / per + 1;
-          float sq = 0.0f;
-          for (int pt = 0; pt < nparts; ++pt) sq += s_dred[((beg * KqI + pt * cnt) + t) * 16 + nn];
+          const int s = T * k + t;
+          const int base = s_cb_base[s] + nn, step = s_cb_step[s], np = s_cb_np[s];
+          float sq = s_dred[base];
+          for (int pt = 1; pt < np; ++pt) sq += s_dred[base + pt * step];
           acc_y += sq;
         }
         a.y[(int64_t)t * H + rH * 16 + nn] = h_failed ? __builtin_nanf("") : acc_y;
       }
-      __syncthreads();  // s_dred is free for the next item
+      lds_barrier();  // s_dred is free for the next item
     }
   }
   if (S == 0 && dn_first < n_dn) {
