@@ -184,15 +184,11 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
   // single-launch path writes; its own regions follow when the shape takes it.
   const size_t o_ctl = take(kCtlBytes);
   const bool fused = I > 0 && fused_shape_ok(T, H, I, E, k, has_shared);
-  size_t o_pres = 0, o_slots = 0, o_flags = 0, o_fhq = 0, o_fhs = 0;
+  size_t o_pres = 0, o_slots = 0, o_hv = 0;
   if (fused) {
-    const int64_t S_max = (T * k < E ? T * k : E) + (has_shared ? 1 : 0);
-    const int64_t KqI_f = round_up(I, kQuad) / kQuad;
     o_pres = take(sizeof(uint64_t) * (size_t)kFusedMaxGrid);
     o_slots = take((size_t)16 * (size_t)(T * E));
-    o_flags = take(sizeof(uint64_t) * (size_t)(S_max * (I / kRowTile)));
-    o_fhq = take((size_t)512 * (size_t)((T * k + T) * KqI_f));
-    o_fhs = take((size_t)32 * (size_t)((T * k + T) * KqI_f));
+    o_hv = take((size_t)16 * (size_t)((T * k + T) * (I / 2)));
   }
   const size_t o_log = take(sizeof(double) * (size_t)(T * E));
   // x operand rows 0..T-1 plus an all-zero row T
@@ -226,9 +222,7 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
       ws->fused.ctl = ws->ctl;
       ws->fused.presence = reinterpret_cast<uint64_t*>(b + o_pres);
       ws->fused.slots = reinterpret_cast<uint32_t*>(b + o_slots);
-      ws->fused.flags = reinterpret_cast<uint64_t*>(b + o_flags);
-      ws->fused.hq = reinterpret_cast<uint16_t*>(b + o_fhq);
-      ws->fused.hs = reinterpret_cast<float*>(b + o_fhs);
+      ws->fused.hv = reinterpret_cast<uint32_t*>(b + o_hv);
     }
     ws->logits = reinterpret_cast<double*>(b + o_log);
     ws->xq = reinterpret_cast<uint16_t*>(b + o_xq);

@@ -12,49 +12,52 @@
 // Why one launch.  A batch-1 Qwen3-shaped layer reads 22 MB, about 3 us at
 // HBM peak, so five dependent launches (each a dispatch plus at least one
 // memory round trip) dominate it.  Here every workgroup of one resident grid
-// (one per CU) runs the same program:
-//   1. Its waves compute logits (the router's fixed-order fp64 contract, one
-//      wave per (token, expert)) and publish each as a tagged 16-byte slot.
-//   2. It waits until all T*E slots carry this call's tag and runs the top-k
-//      and weights itself, from the same logits with the same instructions as
-//      every other workgroup, so all agree bit for bit without a second
-//      hand-off.  It then builds the expert segments (stable permute) in LDS.
-//   3. It copies ALL its weights into LDS at once with direct-to-LDS loads
-//      (the copies need no registers, so every byte of the layer is requested
-//      right after routing): those of its gate/up items (segment x 16-row
-//      tile of I, K split over the 8 waves; item i to workgroup i mod G) and
-//      of its down items (16-row tile of H: every segment x quad of I; item d
-//      to workgroup G - 1 - d mod G, so the workgroups with fewer gate/up
-//      items take them).  Every workgroup thus shares both phases.
-//   4. Gate/up items: MFMA, cross-wave sum in wave order, SwiGLU, h stored
-//      device-scope as the fp16 hi/lo down operand; then one tagged flag per
-//      item.
-//   5. Down items: expand the down weights into MFMA operands in registers
-//      while waiting for every gate/up flag, copy h of all segment positions
-//      into LDS, MFMA per (segment, quad), then per output row
+// (one per CU) runs the same program, and the program is a chain of phases
+// whose length is set by memory round trips and by how many instructions one
+// wave issues in a row (a wave issues at most one instruction every four
+// cycles), so every phase spreads its work over waves and lanes:
+//   0. Waves that own a (token, expert) logit compute it (the router's
+//      fixed-order fp64 contract) and publish it at once as a tagged 16-byte
+//      slot; the other waves build the MFMA-ordered x operand in LDS.
+//   1. Every workgroup polls all T*E slots into LDS and ranks each logit
+//      among its token's (value descending, NaN last, ties to the lower
+//      index) with all of its threads.
+//   2. Wave 0 turns the ranks into expert segments (experts ascending,
+//      tokens ascending: the stable permute) while the other waves compute
+//      each token's routing weights.  Every workgroup does this from the same
+//      logits with the same instructions, so all agree bit for bit.
+//   3. Every wave issues all of its weight copies into LDS with direct-to-LDS
+//      loads (no registers held, every byte of the layer requested right after
+//      routing): gate/up items (segment x 16-row tile of I, K split over the 8
+//      waves; item i to workgroup i mod G) and down items (16-row tile of H:
+//      every segment x quad of I, contiguous ranges per wave; item d to
+//      workgroup G - 1 - d mod G, so the workgroups with fewer gate/up items
+//      take them).  The copy list of a wave is worked out lane-parallel first.
+//   4. Slot positions and segment tokens, while the copies are in flight.
+//   5. Gate/up items as their copies land: MFMA (only the lanes of real
+//      segment positions read the x operand), cross-wave sum in wave order,
+//      SwiGLU, and h stored device-scope as tagged units {hi|lo of row i, tag,
+//      hi|lo of row i + 2, ~tag}: data and readiness in one store, no flag and
+//      no wait for the stores to complete.
+//   6. Down items: expand the down weights into MFMA operands in registers,
+//      then poll the tagged h units of every segment position straight into
+//      the down operand in LDS (one memory round trip after the last store),
+//      MFMA per (segment, quad), and per output row
 //      y[t] = sum_j w[t,j] * (sum_q part[q]) (+ shared expert), j in slot
 //      order: the combine is fused, no expert-output round trip.
-// Each wave reads back only the LDS it loaded itself, so the copies need a
-// wait for the wave's own loads and no barrier.  Loops run over the wave's
-// chunks without unrolling: the kernel stays a few thousand instructions,
-// inside the instruction cache (a first version that kept every chunk in
-// registers unrolled its epilogues per chunk to 15k instructions and spent
-// most of its time in instruction fetch).
 //
 // Hand-off protocol (no memset, no host involvement, graph-replay safe).
-// Word 0 of the workspace is a generation counter.  Every workgroup reads it
-// once at start; this call's tag is gen + 1.  Logit slots hold
+// Word 0 of the workspace is a generation counter.  Every wave reads it once
+// at start; this call's tag is gen + 1.  Logit slots and h units hold
 // {lo32, tag, hi32, ~tag} (one 16-byte store; both halves carry the tag, so a
-// torn read cannot pass), flags and presence words {tag, ~tag}.  Workgroup 0
+// torn read cannot pass); presence words hold {tag, ~tag}.  Workgroup 0
 // bumps the counter to the tag once every workgroup has published its
-// presence (so every workgroup has read the counter); the next call therefore
-// uses a fresh tag and never mistakes this call's slots for its own.  Data
-// hand-offs use device-scope (SC1) stores and loads: a device-scope store is
+// presence (so every wave has read the counter); the next call therefore
+// uses a fresh tag and never mistakes this call's data for its own.
+// Hand-offs use device-scope (SC1) stores and loads: a device-scope store is
 // written through to where every XCD reads, and a device-scope load is never
 // served from a stale line of this XCD's L2, so no cache write-back or
-// invalidation is needed; a writer waits for its data stores to complete
-// before it stores a flag, and a reader issues its data loads only after the
-// flag has arrived.
+// invalidation is needed.
 // Every wait is bounded (LibConfig::fused_wait_polls polls); a wait that gives
 // up sets a bit of the status word (workspace word 1, read by
 // phantom_moe_workspace_status) and its workgroup writes NaN to the outputs
@@ -77,7 +80,14 @@ constexpr int kFThreads = kFW * kWave;
 constexpr uint32_t kGuChunkLds = 2304;  // gate nib 1 KB, up nib 1 KB, gate scales 128 B, up scales 128 B
 constexpr uint32_t kDnChunkLds = 1152;  // down nib 1 KB, scales 128 B
 constexpr int kFusedMaxItems = 4;       // gate/up items per workgroup
-constexpr int kPreDq = 4;               // down chunks per wave expanded into registers ahead of the hand-off
+constexpr int kPreDq = 5;               // down chunks per wave expanded into registers before h arrives
+constexpr int kHUnits = 8;              // tagged h units a thread polls at once
+
+// n / d for 0 <= n < 2^16 and 1 <= d < 2^16 with m = ceil(2^32 / d): the
+// error term n * (m - 2^32/d) / 2^32 is below 2^-16 <= 1/d, so the floor is
+// exact.
+__host__ __device__ inline uint64_t div_magic(uint32_t d) { return ((1ull << 32) + d - 1) / d; }
+__device__ inline int fdiv(int n, uint64_t m) { return (int)(((uint64_t)(uint32_t)n * m) >> 32); }
 
 struct FusedK {
   const uint16_t* x;  // [T, H] bf16
@@ -85,6 +95,7 @@ struct FusedK {
   const float* bias;  // [E] or null
   int T, H, I, E, k, score_mode, has_shared;
   int Kq, KqI;  // quads of H and of I
+  uint64_t md_E, md_nrtI, md_KqI, md_Kq4, md_upos, md_G;  // div_magic of E, I/16, KqI, 4*Kq, 64*KqI, G
   const uint8_t* gate_nib;
   const uint16_t* gate_sc;
   const uint8_t* up_nib;
@@ -102,29 +113,42 @@ struct FusedK {
   float* topk_w;
   uint32_t* ctl;       // [0] generation, [1] status bits
   uint64_t* presence;  // [gridDim.x]
-  uint32_t* slots;     // [T * E][4]
-  uint64_t* flags;     // [max gate/up items]
-  uint16_t* hq;        // [positions][KqI * 256] fp16 hi/lo of h, down operand order
-  float* hs;           // [positions][KqI * 8] half-group sums
+  uint32_t* slots;     // [T * E][4] tagged logits
+  uint32_t* hv;        // [T*k + T][I / 2][4] tagged h units
   FusedLds lds;        // dynamic LDS layout
   uint32_t wait_polls;  // bound of every wait
   uint32_t skew_route;  // added to the tag the logit wait expects (non-zero only to test the failure path)
-  uint32_t skew_flags;  // the same for the gate/up flag wait
+  uint32_t skew_h;      // the same for the h wait
 };
+
+// 4 qs bytes (little endian word) -> 8 fp16 values n - 8, exactly, in the
+// nibble order of dequant_unit_f16 (kmap order): each nibble goes into the
+// low mantissa bits of 1024.0 (fp16 0x6400, whose mantissa step is 1), and
+// 1032 is subtracted.  The MFMA then sums h * q with no offset correction.
+// mask must hold 0x000F000F (in a VGPR).
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t nib_pair_f16s(uint32_t w, uint32_t mask) {
+  const f16x2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, and_or(w, mask, 0x64006400u)) + off);
+}
+__device__ inline u32x4 dequant_unit_f16s(uint32_t w, uint32_t mask) {
+  u32x4 r;
+  r.x = nib_pair_f16s(w, mask);
+  r.y = nib_pair_f16s(w >> 4, mask);
+  r.z = nib_pair_f16s(w >> 8, mask);
+  r.w = nib_pair_f16s(w >> 12, mask);
+  return r;
+}
+
+// Start of a poll retry: to the compiler, memory the kernel arguments point
+// to may have changed here, so the polled loads after it are issued again
+// each iteration (a poll loop otherwise writes no memory, and its loads
+// could be hoisted out of it).
+__device__ inline void poll_clobber() { asm volatile("" ::: "memory"); }
 
 __device__ inline uint64_t tag64(uint32_t t) { return (uint64_t)t | ((uint64_t)(~t) << 32); }
 
-// A tagged 8-byte word {tag, ~tag} through a buffer resource, device scope.
-__device__ inline void store_tag(BufRsrc r, uint32_t off, uint32_t t) {
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  const u32x2 v = {t, ~t};
-  __builtin_amdgcn_raw_buffer_store_b64(v, r, (int)off, 0, kDeviceScope);
-}
-
-__device__ inline bool tag_is(BufRsrc r, uint32_t off, uint32_t t) {
-  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kDeviceScope);
-  return (uint32_t)v[0] == t && (uint32_t)v[1] == ~t;
-}
+__device__ inline bool tag_ok(const u32x4& v, uint32_t t) { return v.y == t && v.w == ~t; }
 
 // A value every lane of the wave holds alike (LDS reads of shared
 // bookkeeping, wave indices): stated as uniform, so the compiler keeps it in
@@ -202,39 +226,41 @@ __host__ __device__ inline uint32_t h_row_bytes(int KqI) { return (uint32_t)KqI 
 
 __host__ __device__ inline uint32_t align_lds(uint32_t v) { return (v + 255u) & ~255u; }
 
-// Routing scratch: logits and their order keys [T*E], ranks [T*E], the
-// selected logits and their exponentials [T*k], expert token masks [E].
+// Routing scratch (dead before the first weight copy is issued): the
+// logits [T*E] and their order keys [T*E], each wave's top-k scratch (k
+// candidate keys, values and indices, k ranked values and indices, k
+// exponentials: 40 k bytes), the expert token masks [E] and the ranks of one
+// token's logits [E].
 struct RouteScratch {
-  uint32_t lv, key, rank, selv, ej, emask, bytes;
+  uint32_t lv, key, topk, topk_wave, emask, rank, bytes;
 };
 __host__ __device__ inline RouteScratch route_scratch(int T, int k, int E) {
   RouteScratch r;
   r.lv = 0;
-  r.key = r.lv + align_lds((uint32_t)(T * E) * 8u);
-  r.rank = r.key + align_lds((uint32_t)(T * E) * 8u);
-  r.selv = r.rank + align_lds((uint32_t)(T * E) * 4u);
-  r.ej = r.selv + align_lds((uint32_t)(T * k) * 8u);
-  r.emask = r.ej + align_lds((uint32_t)(T * k) * 8u);
-  r.bytes = r.emask + align_lds((uint32_t)E * 8u);
+  r.key = align_lds((uint32_t)(T * E) * 8u);
+  r.topk = r.key + align_lds((uint32_t)(T * E) * 8u);
+  r.topk_wave = align_lds((uint32_t)k * 40u);
+  r.emask = r.topk + kFW * r.topk_wave;
+  r.rank = r.emask + align_lds((uint32_t)E * 8u);
+  r.bytes = r.rank + align_lds((uint32_t)E * 4u);
   return r;
 }
-__host__ __device__ inline uint32_t route_scratch_bytes(int T, int k, int E) { return route_scratch(T, k, E).bytes; }
 
 }  // namespace
 
 // Dynamic LDS layout for ng gate/up and nd down items per workgroup, S_max
 // segments:
 //   [x operand][gate/up staging][down staging]
-// The routing scratch (logits, keys, ranks, selection) is dead before the
-// first weight copy is issued, so it sits over the staging regions; the h
-// operand and the down partials are written after the workgroup's gate/up
-// work is done, so they sit over the x operand and the gate/up staging when
-// those are large enough (else after the down staging).
+// The routing scratch is dead before the first weight copy is issued, so it
+// sits over the staging regions.  The h operand and the down partials are
+// written after the workgroup's gate/up work is done, so they sit over the x
+// operand and the gate/up staging when those are large enough (else after
+// the down staging).
 FusedLds fused_lds_layout(int T, int k, int E, int has_shared, int H, int I, int ng, int nd, int S_max) {
   FusedLds l = {};
   const uint32_t Kq = (uint32_t)((H + kQuad - 1) / kQuad), KqI = (uint32_t)((I + kQuad - 1) / kQuad);
   const uint32_t npos = (uint32_t)(T * k + (has_shared ? T : 0));
-  const uint32_t route = route_scratch_bytes(T, k, E);
+  const uint32_t route = route_scratch(T, k, E).bytes;
   const uint32_t x_op = align_lds((uint32_t)(T + 1) * Kq * 256u) + align_lds((uint32_t)(T + 1) * Kq * 16u);
   // staging slots are indexed (item, wave slot, wave): a wave takes quads
   // w, w + 8, ... of a gate/up item (nq slots) and (segment, quad) pairs
@@ -243,7 +269,7 @@ FusedLds fused_lds_layout(int T, int k, int E, int has_shared, int H, int I, int
   const uint32_t per = ((uint32_t)S_max * KqI + kFW - 1) / kFW;
   const uint32_t wgu = (uint32_t)ng * nq * kFW * kGuChunkLds;
   const uint32_t wdn = (uint32_t)nd * per * kFW * kDnChunkLds;
-  const uint32_t h_op = align_lds((npos + 1) * h_row_bytes((int)KqI)) + align_lds((npos + 1) * KqI * 32u);
+  const uint32_t h_op = align_lds(npos * h_row_bytes((int)KqI));
   const uint32_t dred = align_lds(npos * KqI * 16u * 4u);
   l.x = 0;
   l.wgu = x_op;
@@ -261,6 +287,139 @@ FusedLds fused_lds_layout(int T, int k, int E, int has_shared, int H, int I, int
 
 namespace {
 
+// Expert segments of up to 64 slots (T*k <= 64), built by one wave from
+// ballots: slot s (lane s) of expert e goes to position #{slots of experts
+// < e} + #{earlier slots of e} (experts ascending, tokens ascending within an
+// expert: the stable permute); its segment is #{distinct experts < e}.
+// Writes every slot's position, every position's token, the segments
+// (expert, begin, size, and the shared expert last) and their count.
+__device__ inline void ballot_segments(int T, int k, int E, int has_shared, const int* s_sel_idx, int* s_slot_pos,
+                                       int* s_seg_tok, int* s_seg_e, int* s_seg_beg, int* s_seg_cnt, short* s_e2u,
+                                       int* s_nseg) {
+  const int lane = threadIdx.x % kWave;
+  const int nsl = T * k;
+  const bool valid = lane < nsl;
+  const int e = valid ? s_sel_idx[lane] : 0;
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  const uint64_t vmask = __ballot(valid);
+  uint64_t same = vmask;
+  for (int bt = 0; bt < nbits; ++bt) {
+    const bool bit = (e >> bt) & 1;
+    const uint64_t bb = __ballot(valid && bit);
+    same &= bit ? bb : ~bb;
+  }
+  const int in_seg = __popcll(same & lt);
+  const bool first = valid && in_seg == 0;
+  const uint64_t firsts = __ballot(first);
+  uint64_t m_all = vmask, m_first = firsts;
+  int below_all = 0, below_first = 0;
+  for (int bt = nbits - 1; bt >= 0; --bt) {
+    const uint64_t bb = __ballot(valid && ((e >> bt) & 1));
+    if ((e >> bt) & 1) {
+      below_all += __popcll(m_all & ~bb);
+      below_first += __popcll(m_first & ~bb);
+      m_all &= bb;
+      m_first &= bb;
+    } else {
+      m_all &= ~bb;
+      m_first &= ~bb;
+    }
+  }
+  const int pos = below_all + in_seg;
+  if (valid) {
+    s_slot_pos[lane] = pos;
+    s_seg_tok[pos] = lane / k;
+  }
+  if (first) {
+    s_seg_e[below_first] = e;
+    s_seg_beg[below_first] = below_all;
+    s_seg_cnt[below_first] = __popcll(same);
+    s_e2u[e] = (short)below_first;
+  }
+  const int nu = __popcll(firsts);
+  if (has_shared && lane < T) s_seg_tok[T * k + lane] = lane;
+  if (lane == 0) {
+    if (has_shared) {
+      s_seg_e[nu] = E;
+      s_seg_cnt[nu] = T;
+      s_seg_beg[nu] = T * k;
+    }
+    *s_nseg = nu + (has_shared ? 1 : 0);
+  }
+}
+
+// The tagged h units [0, nun) of positions pos0, pos0 + 1, ... (upos units a
+// position, padding groups included), unit i polled by thread tid + stride * m
+// (device scope) and written into the down operand in LDS: unit (g32, half,
+// p, r) of a position holds rows cc = 16 half + 4p + r and cc + 2 of group
+// g32, which sit at operand entries jj and jj + 1 of group unit
+// (p, g32 % 4).  Units of the groups past I are zero.  A wait that gives up
+// sets *s_fail and the status bit.
+template <int I_>
+__device__ inline void poll_h_units(int pos0, int nun, int tid, int stride, BufRsrc hv_r, uint32_t want,
+                                    uint32_t wait_polls, uint32_t* ctl, int* s_fail, char* s_hb, uint32_t hrow,
+                                    int hunits, int upos, int KgI, uint64_t md_upos) {
+  const int lane = threadIdx.x % kWave;
+  for (int i0 = 0; i0 < nun; i0 += stride * kHUnits) {
+    u32x4 v[kHUnits];
+    bool ok[kHUnits];
+    uint32_t off[kHUnits];
+#pragma unroll
+    for (int j = 0; j < kHUnits; ++j) {
+      const int i = i0 + j * stride + tid;
+      const int dp = I_ ? i / (64 * ((I_ + kQuad - 1) / kQuad)) : fdiv(i, md_upos);
+      const int uu = i - dp * upos;
+      const bool real = i < nun && uu / 16 < KgI;
+      off[j] = real ? (uint32_t)(((pos0 + dp) * hunits + uu) * 16) : 0xFFFFF000u;  // past the end: reads zero
+      v[j] = __builtin_amdgcn_raw_buffer_load_b128(hv_r, (int)off[j], 0, kDevicePoll);
+      ok[j] = !real || tag_ok(v[j], want);
+    }
+    for (uint32_t it = 0;; ++it) {
+      bool all = true;
+#pragma unroll
+      for (int j = 0; j < kHUnits; ++j) all = all && ok[j];
+      if (__all(all)) break;
+      if (it >= wait_polls) {
+        if (lane == 0) {
+          *s_fail = 1;
+          set_status(ctl, kStatusExpertWait);
+        }
+        break;
+      }
+      poll_clobber();
+#pragma unroll
+      for (int j = 0; j < kHUnits; ++j) {
+        if (!ok[j]) {
+          v[j] = __builtin_amdgcn_raw_buffer_load_b128(hv_r, (int)off[j], 0, kDevicePoll);
+          ok[j] = tag_ok(v[j], want);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kHUnits; ++j) {
+      const int i = i0 + j * stride + tid;
+      const int dp = I_ ? i / (64 * ((I_ + kQuad - 1) / kQuad)) : fdiv(i, md_upos);
+      const int uu = i - dp * upos;
+      const bool real = i < nun && uu / 16 < KgI;
+      const uint32_t v0 = real ? v[j].x : 0u, v1 = real ? v[j].z : 0u;
+      const int g32 = uu / 16, hh = (uu / 8) % 2, pq = (uu / 2) % 4, r = uu % 2;
+      if (i < nun) {
+        const int jj = hh == 0 ? (r ? 4 : 0) : (r ? 6 : 2);
+        char* d = s_hb + (size_t)(pos0 + dp) * hrow + (g32 / 4) * 512 + pq * 128 + (g32 % 4) * 32 + jj * 2;
+        *reinterpret_cast<uint32_t*>(d) = (v0 & 0xffffu) | (v1 << 16);
+        *reinterpret_cast<uint32_t*>(d + 16) = (v0 >> 16) | (v1 & 0xffff0000u);
+      }
+    }
+  }
+}
+
+// Shape parameters known at compile time (0, or -1 for SH, = read at run
+// time from the arguments): the generic instantiation reads them all; the
+// batch-1 Qwen3-30B-A3B-shaped one knows them all, so every division, loop
+// bound and bookkeeping step of a phase folds to constants.
+template <int T_, int H_, int I_, int E_, int K_, int SH_>
 __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
   __shared__ int s_sel_idx[kFusedMaxSlots];
   __shared__ float s_sel_w[kFusedMaxSlots];
@@ -275,9 +434,9 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
   __shared__ int s_cb_base[kFusedMaxSlots + kFusedMaxT];
   __shared__ int s_cb_step[kFusedMaxSlots + kFusedMaxT];
   __shared__ int s_cb_np[kFusedMaxSlots + kFusedMaxT];
-  __shared__ uint32_t s_epoch;
   __shared__ int s_nseg;
   __shared__ int s_fail;
+  __shared__ int s_pfail[kFusedMaxT];
   extern __shared__ u32x4 s_dyn[];
 
   const int lane = threadIdx.x % kWave;
@@ -286,44 +445,116 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
   const int p = lane / 16;
   const int G = (int)gridDim.x;
   const int b = (int)blockIdx.x;
-  const int T = a.T, H = a.H, I = a.I, E = a.E, k = a.k;
-  const int Kq = a.Kq, KqI = a.KqI;
+  const int T = T_ ? T_ : a.T, H = H_ ? H_ : a.H, I = I_ ? I_ : a.I, E = E_ ? E_ : a.E, k = K_ ? K_ : a.k;
+  const int has_sh = SH_ >= 0 ? SH_ : a.has_shared;
+  const int Kq = H_ ? (H_ + kQuad - 1) / kQuad : a.Kq, KqI = I_ ? (I_ + kQuad - 1) / kQuad : a.KqI;
+  auto div_E = [&](int v) { return E_ ? v / E_ : fdiv(v, a.md_E); };
+  auto div_Kq4 = [&](int v) { return H_ ? v / (4 * ((H_ + kQuad - 1) / kQuad)) : fdiv(v, a.md_Kq4); };
+  auto div_nrtI = [&](int v) { return I_ ? v / (I_ / kRowTile) : fdiv(v, a.md_nrtI); };
+  auto div_KqI = [&](int v) { return I_ ? v / ((I_ + kQuad - 1) / kQuad) : fdiv(v, a.md_KqI); };
+  auto div_upos = [&](int v) { return I_ ? v / (64 * ((I_ + kQuad - 1) / kQuad)) : fdiv(v, a.md_upos); };
   const int Kg = H / kGroup, KgI = I / kGroup;
+  const int npos = T * k + (has_sh ? T : 0);
   char* lds = reinterpret_cast<char*>(s_dyn);
   char* rs = lds + a.lds.route;  // routing scratch
   const RouteScratch rl = route_scratch(T, k, E);
   double* s_lv = reinterpret_cast<double*>(rs + rl.lv);
   uint64_t* s_key = reinterpret_cast<uint64_t*>(rs + rl.key);
-  int* s_rank = reinterpret_cast<int*>(rs + rl.rank);
-  double* s_selv = reinterpret_cast<double*>(rs + rl.selv);
-  double* s_ej = reinterpret_cast<double*>(rs + rl.ej);
   uint64_t* s_emask = reinterpret_cast<uint64_t*>(rs + rl.emask);
+  int* s_rank = reinterpret_cast<int*>(rs + rl.rank);
   u32x4* s_xop = reinterpret_cast<u32x4*>(lds + a.lds.x);  // [(T+1) Kq][4 p][4 gi]
   float* s_xs = reinterpret_cast<float*>(lds + a.lds.x + align_lds((uint32_t)(T + 1) * Kq * 256u));
 
-  // ---- 0. generation (thread 0), router task, x operand ---------------
-  uint32_t gen = 0;
-  if (threadIdx.x == 0) {
-    gen = __hip_atomic_load(&a.ctl[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_fail = 0;
-  }
+  // ---- 0. generation; logits published as computed; x operand -------------
+  const uint32_t tag =
+      (uint32_t)uni((int)__hip_atomic_load(&a.ctl[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) + 1u;
+  const BufRsrc slot_r = buf_rsrc(a.slots, (uint32_t)(T * E * 16));
   // at most one (token, expert) logit per wave: the grid has >= T*E waves
   const int task = w * G + b;
-  double logit = 0.0;
   if (task < T * E) {
-    const int t = task / E, e = task % E;
-    logit = fixed_dot_bf16(a.x + (int64_t)t * H, a.W + (int64_t)e * H, H);
+    const int t = div_E(task), e = task - t * E;
+    double logit = fixed_dot_bf16(a.x + (int64_t)t * H, a.W + (int64_t)e * H, H);
     if (a.bias) logit = logit + (double)a.bias[e];
+    if (lane == 0) {
+      const uint64_t bits = __builtin_bit_cast(uint64_t, logit);
+      u32x4 v;
+      v.x = (uint32_t)bits;
+      v.y = tag;
+      v.z = (uint32_t)(bits >> 32);
+      v.w = ~tag;
+      __builtin_amdgcn_raw_buffer_store_b128(v, slot_r, task * 16, 0, kDeviceScope);
+    }
   }
-  // the MFMA-ordered x operand of every token (and an all-zero row T) and its
-  // group sums, built while the logits are in flight elsewhere: one thread per
-  // (token, quad, group), the 4 parts p in order; the group sum adds the parts
-  // as (p0 + p1) + (p2 + p3), each part ((x0 + x1) + (x2 + x3)) + ((x16 + x17)
-  // + (x18 + x19)) over its 8 elements
+  // ---- 1. top-k of every token: wave kFW - 1 - t polls token t's logits
+  // from the start (the last waves hold no logit unless T*E > 7G) and selects
+  // and weighs its experts with the staged router's own instructions
+  // (wave_topk_row), so both paths route bit for bit alike.
+  const int tpoll = kFW - 1 - w;
+  bool poll_failed = false;
+  if (tpoll < T) {
+    const int t = tpoll;
+    const uint32_t want = tag + a.skew_route;
+    // every slot of the token in flight at once, then the checks
+    constexpr int kNV = kMaxExperts / kWave;
+    bool done[kNV];
+#pragma unroll
+    for (int v = 0; v < kNV; ++v) done[v] = lane + v * kWave >= E;
+    for (uint32_t it = 0;; ++it) {
+      poll_clobber();
+      u32x4 sv[kNV];
+#pragma unroll
+      for (int v = 0; v < kNV; ++v)
+        if (!done[v]) sv[v] = __builtin_amdgcn_raw_buffer_load_b128(slot_r, (t * E + lane + v * kWave) * 16, 0, kDevicePoll);
+      bool all = true;
+#pragma unroll
+      for (int v = 0; v < kNV; ++v) {
+        if (!done[v] && tag_ok(sv[v], want)) {
+          const double lv = __builtin_bit_cast(double, ((uint64_t)sv[v].z << 32) | sv[v].x);
+          s_lv[t * E + lane + v * kWave] = lv;
+          s_key[t * E + lane + v * kWave] = logit_key(lv);
+          done[v] = true;
+        }
+        all = all && done[v];
+      }
+      if (__all(all)) break;
+      if (it >= a.wait_polls) {
+        poll_failed = true;
+        if (lane == 0) set_status(a.ctl, kStatusRouteWait);
+        break;
+      }
+    }
+    if (!poll_failed && T == 1) {
+      // one token: the whole workgroup ranks its logits (below)
+      for (int e = lane; e < E; e += kWave) s_rank[e] = 0;
+    } else if (!poll_failed) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      char* tk = rs + rl.topk + (uint32_t)w * rl.topk_wave;
+      uint64_t* s_ck = reinterpret_cast<uint64_t*>(tk);
+      double* s_cv = reinterpret_cast<double*>(tk + 8 * k);
+      double* s_val = reinterpret_cast<double*>(tk + 16 * k);
+      double* s_e = reinterpret_cast<double*>(tk + 24 * k);
+      int* s_ci = reinterpret_cast<int*>(tk + 32 * k);
+      int* s_idx = reinterpret_cast<int*>(tk + 36 * k);
+      const double* row = s_lv + t * E;
+      int* oi = s_sel_idx + t * k;
+      float* ow = s_sel_w + t * k;
+      if (E <= 64) wave_topk_row<1>(row, E, k, a.score_mode, s_ck, s_cv, s_ci, s_val, s_idx, s_e, oi, ow, nullptr);
+      else if (E <= 128) wave_topk_row<2>(row, E, k, a.score_mode, s_ck, s_cv, s_ci, s_val, s_idx, s_e, oi, ow, nullptr);
+      else if (E <= 256) wave_topk_row<4>(row, E, k, a.score_mode, s_ck, s_cv, s_ci, s_val, s_idx, s_e, oi, ow, nullptr);
+      else wave_topk_row<8>(row, E, k, a.score_mode, s_ck, s_cv, s_ci, s_val, s_idx, s_e, oi, ow, nullptr);
+    }
+  }
+  // The MFMA-ordered x operand of every token (and an all-zero row T) and its
+  // group sums, from the waves in increasing order: one
+  // thread per (token, quad, group), the 4 parts p in order; the group sum
+  // adds the parts as (p0 + p1) + (p2 + p3), each part ((x0 + x1) + (x2 + x3))
+  // + ((x16 + x17) + (x18 + x19)) over its 8 elements.
   for (int j = threadIdx.x; j < (T + 1) * Kq * 4; j += kFThreads) {
-    const int tok = j / (Kq * 4);
-    const int q = (j / 4) % Kq;
-    const int gi = j % 4;
+    const int tok = div_Kq4(j);
+    const int rem = j - tok * Kq * 4;
+    const int q = rem / 4;
+    const int gi = rem % 4;
     const int g = 4 * q + gi;
     const bool valid = tok < T && g < Kg;
     const uint16_t* xr = a.x + (int64_t)(valid ? tok : 0) * H + (int64_t)(valid ? g : 0) * kGroup;
@@ -346,75 +577,30 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
     }
     s_xs[(tok * Kq + q) * 4 + gi] = (sp[0] + sp[1]) + (sp[2] + sp[3]);
   }
-  if (threadIdx.x == 0) {
-    const uint32_t tg = gen + 1;
-    s_epoch = tg;
-    __hip_atomic_store(&a.presence[b], tag64(tg), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  lds_barrier();
-  const uint32_t tag = (uint32_t)uni((int)s_epoch);
+  if (threadIdx.x == 0) s_fail = 0;
+  if (tpoll < T && lane == 0) s_pfail[tpoll] = poll_failed ? 1 : 0;
+  lds_barrier();  // every wave of the workgroup has read the generation
+  if (threadIdx.x == 0) __hip_atomic_store(&a.presence[b], tag64(tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  // ---- 1. publish the logit ---------------------------------------------
-  const BufRsrc slot_r = buf_rsrc(a.slots, (uint32_t)(T * E * 16));
-  if (task < T * E && lane == 0) {
-    const uint64_t bits = __builtin_bit_cast(uint64_t, logit);
-    u32x4 v;
-    v.x = (uint32_t)bits;
-    v.y = tag;
-    v.z = (uint32_t)(bits >> 32);
-    v.w = ~tag;
-    __builtin_amdgcn_raw_buffer_store_b128(v, slot_r, (int)(task * 16), 0, kDeviceScope);
-  }
+  int pf = 0;
+  for (int t = 0; t < T; ++t) pf |= s_pfail[t];
+  const bool route_failed = uni(pf) != 0;
 
-  // ---- 2. wait for every logit; top-k; segments ----------------------------
-  // One poll per lane in flight: a load left in flight at the exit would
-  // make the first later instruction that reuses its registers wait for it
-  // (a memory round trip).
-  {
-    const uint32_t want = tag + a.skew_route;
-    for (int i0 = w * kWave; i0 < T * E; i0 += kFThreads) {
-      const int i = i0 + lane;
-      bool done = i >= T * E;
-      for (uint32_t it = 0;; ++it) {
-        if (!done) {
-          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(slot_r, (int)((uint32_t)i * 16u), 0, kDeviceScope);
-          if (v.y == want && v.w == ~want) {
-            const double lv = __builtin_bit_cast(double, ((uint64_t)v.z << 32) | v.x);
-            s_lv[i] = lv;
-            s_key[i] = logit_key(lv);
-            done = true;
-          }
-        }
-        if (__all(done)) break;
-        if (it >= a.wait_polls) {
-          if (lane == 0) {
-            s_fail = 1;
-            set_status(a.ctl, kStatusRouteWait);
-          }
-          break;
-        }
-      }
-    }
-  }
-  for (int i = threadIdx.x; i < T * E; i += kFThreads) s_rank[i] = 0;
-  lds_barrier();
-  const bool route_failed = uni(s_fail) != 0;
-  if (!route_failed) {
-    // Top-k of every token by rank counting over the whole workgroup: the
-    // rank of logit i is the number of logits of its token before it in the
-    // order (value descending, NaN last, ties to the lower index; the order
-    // keys of topk_common.h), split over P threads per logit, the keys read
-    // eight at a time.  Rank r < k lands in slot r: the selection and order
-    // of wave_topk_row, and its weights below, bit for bit.
-    const int n_el = T * E;
+  // One token: every logit's rank among the E (the number of logits before
+  // it in the order of wave_topk_row: value descending, NaN last, ties to the
+  // lower index), P threads per logit over E/P keys each; rank r < k is slot
+  // r.  Then wave 0 takes the winners to their slots and segments (experts
+  // ascending) while wave 1 computes the weights exactly as wave_topk_row
+  // does, so the selection, its order and the weights equal the staged
+  // router's bit for bit.
+  if (T == 1 && !route_failed) {
     int P = 1;
-    while (2 * P * n_el <= kFThreads && 2 * P <= E) P *= 2;
+    while (2 * P * E <= kFThreads) P *= 2;
     const int span = (E + P - 1) / P;
-    for (int r = threadIdx.x; r < n_el * P; r += kFThreads) {
-      const int el = r % n_el, pp = r / n_el;
-      const int t = el / E, i = el % E;
-      const uint64_t ki = s_key[el];
-      const uint64_t* row = s_key + t * E;
+    if ((int)threadIdx.x < E * P) {
+      const int pp = div_E(threadIdx.x);
+      const int e = (int)threadIdx.x - pp * E;
+      const uint64_t ke = s_key[e];
       const int j0 = pp * span;
       const int j1 = j0 + span < E ? j0 + span : E;
       int cnt = 0;
@@ -422,183 +608,136 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
       for (; j + 8 <= j1; j += 8) {
         uint64_t kk[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) kk[q] = row[j + q];
+        for (int q = 0; q < 8; ++q) kk[q] = s_key[j + q];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) cnt += (kk[q] > ki || (kk[q] == ki && j + q < i)) ? 1 : 0;
+        for (int q = 0; q < 8; ++q) cnt += (kk[q] > ke || (kk[q] == ke && j + q < e)) ? 1 : 0;
       }
       for (; j < j1; ++j) {
-        const uint64_t kj = row[j];
-        cnt += (kj > ki || (kj == ki && j < i)) ? 1 : 0;
+        const uint64_t kj = s_key[j];
+        cnt += (kj > ke || (kj == ke && j < e)) ? 1 : 0;
       }
-      if (P == 1) s_rank[el] = cnt;
-      else atomicAdd(&s_rank[el], cnt);
+      if (P == 1) s_rank[e] = cnt;
+      else atomicAdd(&s_rank[e], cnt);
     }
     lds_barrier();
-    // one wave per token: its k winners to their slots, then the weights,
-    // softmax exp(l_j - l_0) or sigmoid(l_j) normalised by their sum over the
-    // k slots in slot order, in fp64, stored as fp32
-    for (int t = w; t < T; t += kFW) {
+    if (w == 0) {
+      const uint64_t lt = (1ull << lane) - 1ull;
+      int nsel = 0;
       for (int e0 = 0; e0 < E; e0 += kWave) {
         const int e = e0 + lane;
-        if (e < E) {
-          const int rk = s_rank[t * E + e];
-          if (rk < k) {
-            s_sel_idx[t * k + rk] = e;
-            s_selv[t * k + rk] = s_lv[t * E + e];
-          }
+        const int r = e < E ? s_rank[e] : k;
+        const bool sel = r < k;
+        const uint64_t bal = __ballot(sel);
+        if (sel) {
+          const int u = nsel + __popcll(bal & lt);
+          s_seg_e[u] = e;
+          s_seg_beg[u] = u;
+          s_seg_cnt[u] = 1;
+          s_seg_tok[u] = 0;
+          s_e2u[e] = (short)u;
+          s_sel_idx[r] = e;
+          s_slot_pos[r] = u;
         }
+        nsel += __popcll(bal);
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      if (lane == 0) {
+        if (has_sh) {
+          s_seg_e[k] = E;
+          s_seg_cnt[k] = 1;
+          s_seg_beg[k] = k;
+          s_seg_tok[k] = 0;
+        }
+        s_nseg = k + (has_sh ? 1 : 0);
+      }
+    } else if (w == 1) {
+      char* tk = rs + rl.topk + (uint32_t)w * rl.topk_wave;
+      double* s_val = reinterpret_cast<double*>(tk + 16 * k);
+      double* s_e = reinterpret_cast<double*>(tk + 24 * k);
+      for (int e = lane; e < E; e += kWave) {
+        const int r = s_rank[e];
+        if (r < k) s_val[r] = s_lv[e];
+      }
       __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       double ej = 0.0;
       if (lane < k) {
-        const double v = s_selv[t * k + lane];
-        ej = (a.score_mode == 0) ? exp(v - s_selv[t * k]) : 1.0 / (1.0 + exp(-v));
-        s_ej[t * k + lane] = ej;
+        const double v = s_val[lane];
+        ej = (a.score_mode == 0) ? exp(v - s_val[0]) : 1.0 / (1.0 + exp(-v));
+        s_e[lane] = ej;
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       if (lane < k) {
         double sum = 0.0;
-        for (int i = 0; i < k; ++i) sum += s_ej[t * k + i];
-        s_sel_w[t * k + lane] = (float)(ej / sum);
+        for (int i = 0; i < k; ++i) sum += s_e[i];
+        s_sel_w[lane] = (float)(ej / sum);
       }
     }
+    lds_barrier();
   }
-  lds_barrier();
-  if (route_failed) {
-    // no routing: this workgroup's outputs cannot be computed
-    if (b == 0)
-      for (int i = threadIdx.x; i < T * k; i += kFThreads) {
-        a.topk_idx[i] = -1;
-        a.topk_w[i] = __builtin_nanf("");
-      }
-  } else {
-    if (b == 0)
-      for (int i = threadIdx.x; i < T * k; i += kFThreads) {
-        a.topk_idx[i] = s_sel_idx[i];
-        a.topk_w[i] = s_sel_w[i];
-      }
+
+  // ---- 2. expert segments (experts ascending, tokens ascending within one:
+  // the stable permute) -------------------------------------------------------
+  if (!route_failed && T > 1) {
     if (T * k <= kWave) {
-      // Up to 64 slots: one wave builds the segments from ballots.  Slot s
-      // (lane s) of expert e goes to position #{slots of experts < e} +
-      // #{earlier slots of e} (experts ascending, tokens ascending within an
-      // expert: the stable permute); its segment is #{distinct experts < e}.
-      if (w == 0) {
-        const int nsl = T * k;
-        const bool valid = lane < nsl;
-        const int e = valid ? s_sel_idx[lane] : 0;
-        int nbits = 1;
-        while ((1 << nbits) < E) ++nbits;
-        const uint64_t lt = (1ull << lane) - 1ull;
-        const uint64_t vmask = __ballot(valid);
-        uint64_t same = vmask;
-        for (int bt = 0; bt < nbits; ++bt) {
-          const bool bit = (e >> bt) & 1;
-          const uint64_t bb = __ballot(valid && bit);
-          same &= bit ? bb : ~bb;
-        }
-        const int in_seg = __popcll(same & lt);
-        const bool first = valid && in_seg == 0;
-        const uint64_t firsts = __ballot(first);
-        uint64_t m_all = vmask, m_first = firsts;
-        int below_all = 0, below_first = 0;
-        for (int bt = nbits - 1; bt >= 0; --bt) {
-          const uint64_t bb = __ballot(valid && ((e >> bt) & 1));
-          if ((e >> bt) & 1) {
-            below_all += __popcll(m_all & ~bb);
-            below_first += __popcll(m_first & ~bb);
-            m_all &= bb;
-            m_first &= bb;
-          } else {
-            m_all &= ~bb;
-            m_first &= ~bb;
-          }
-        }
-        const int pos = below_all + in_seg;
-        if (valid) {
-          s_slot_pos[lane] = pos;
-          s_seg_tok[pos] = lane / k;
-        }
-        if (first) {
-          s_seg_e[below_first] = e;
-          s_seg_beg[below_first] = below_all;
-          s_seg_cnt[below_first] = __popcll(same);
-          s_e2u[e] = (short)below_first;
-        }
-        const int nu = __popcll(firsts);
-        if (a.has_shared && lane < T) s_seg_tok[T * k + lane] = lane;
-        if (lane == 0) {
-          if (a.has_shared) {
-            s_seg_e[nu] = E;
-            s_seg_cnt[nu] = T;
-            s_seg_beg[nu] = T * k;
-          }
-          s_nseg = nu + (a.has_shared ? 1 : 0);
-        }
-      }
+      if (w == 0)
+        ballot_segments(T, k, E, has_sh, s_sel_idx, s_slot_pos, s_seg_tok, s_seg_e, s_seg_beg, s_seg_cnt,
+                        s_e2u, &s_nseg);
     } else {
       for (int e = threadIdx.x; e < E; e += kFThreads) s_emask[e] = 0;
       lds_barrier();
-      for (int s = threadIdx.x; s < T * k; s += kFThreads)
-        __hip_atomic_fetch_or(&s_emask[s_sel_idx[s]], 1ull << (s / k), __ATOMIC_RELAXED,
+      for (int s2 = threadIdx.x; s2 < T * k; s2 += kFThreads)
+        __hip_atomic_fetch_or(&s_emask[s_sel_idx[s2]], 1ull << (s2 / k), __ATOMIC_RELAXED,
                               __HIP_MEMORY_SCOPE_WORKGROUP);
       lds_barrier();
       if (w == 0) {
         // active experts in increasing id, their segment sizes and offsets
         const uint64_t lt = (1ull << lane) - 1ull;
-        int nu = 0;
+        int nu = 0, run = 0;
         for (int e0 = 0; e0 < E; e0 += kWave) {
           const int e = e0 + lane;
           const uint64_t m = e < E ? s_emask[e] : 0ull;
+          const int c = __popcll(m);
           const uint64_t bal = __ballot(m != 0ull);
-          if (m != 0ull) {
-            const int u = nu + __popcll(bal & lt);
-            s_seg_e[u] = e;
-            s_seg_cnt[u] = __popcll(m);
-            s_e2u[e] = (short)u;
-          }
-          nu += __popcll(bal);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        int run = 0;
-        for (int u0 = 0; u0 < nu; u0 += kWave) {
-          const int u = u0 + lane;
-          const int c = u < nu ? s_seg_cnt[u] : 0;
           int inc = c;
 #pragma unroll
           for (int off = 1; off < kWave; off <<= 1) {
             const int o = __shfl_up(inc, off, kWave);
             if (lane >= off) inc += o;
           }
-          if (u < nu) s_seg_beg[u] = run + inc - c;
+          if (m != 0ull) {
+            const int u = nu + __popcll(bal & lt);
+            s_seg_e[u] = e;
+            s_seg_cnt[u] = c;
+            s_seg_beg[u] = run + inc - c;
+            s_e2u[e] = (short)u;
+          }
+          nu += __popcll(bal);
           run += __shfl(inc, kWave - 1, kWave);
         }
         if (lane == 0) {
-          if (a.has_shared) {
+          if (has_sh) {
             s_seg_e[nu] = E;
             s_seg_cnt[nu] = T;
             s_seg_beg[nu] = T * k;
           }
-          s_nseg = nu + (a.has_shared ? 1 : 0);
+          s_nseg = nu + (has_sh ? 1 : 0);
         }
       }
       lds_barrier();
-      // every slot's segment position (tokens in increasing order within a
-      // segment: the stable permute) and every position's token
-      for (int s = threadIdx.x; s < T * k; s += kFThreads) {
-        const int t = s / k;
-        const int e = s_sel_idx[s];
+      // every slot's segment position and every position's token
+      for (int s2 = threadIdx.x; s2 < T * k; s2 += kFThreads) {
+        const int t = s2 / k;
+        const int e = s_sel_idx[s2];
         const int pos = s_seg_beg[s_e2u[e]] + __popcll(s_emask[e] & ((1ull << t) - 1ull));
-        s_slot_pos[s] = pos;
+        s_slot_pos[s2] = pos;
         s_seg_tok[pos] = t;
       }
-      if (a.has_shared)
+      if (has_sh)
         for (int t = threadIdx.x; t < T; t += kFThreads) s_seg_tok[T * k + t] = t;
     }
+    lds_barrier();
   }
-  lds_barrier();  // the routing scratch is dead from here on
 
   // ---- 3. work lists; every weight chunk of the workgroup -> LDS ------------
   const int S = route_failed ? 0 : uni(s_nseg);
@@ -606,32 +745,39 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
   const int n_gu = S * nrtI;
   const int n_dn = H / kRowTile;
   // gate/up items b, b + G, ...; down items G - 1 - b, G - 1 - b + G, ...
-  const int ng = b < n_gu ? (n_gu - b + G - 1) / G : 0;
+  const int ng = b < n_gu ? fdiv(n_gu - b + G - 1, a.md_G) : 0;
   const int dn_first = G - 1 - b;
-  const int nd = (S > 0 && dn_first < n_dn) ? (n_dn - dn_first + G - 1) / G : 0;
-  // gate/up: wave w takes quads w, w + 8, ... (nq slots) of each item
+  const int nd = (S > 0 && dn_first < n_dn) ? fdiv(n_dn - dn_first + G - 1, a.md_G) : 0;
+  // gate/up: wave w takes quads w, w + 8, ... (nqw of them) of each item
   const int nq = (Kq + kFW - 1) / kFW;
-  // down: wave w takes (segment, quad) pairs [w * per, w * per + per) of each item
+  const int nqw = Kq > w ? (Kq - 1 - w) / kFW + 1 : 0;
+  // down: wave w takes (segment, quad) pairs [w * per, w * per + cnt_w) of each item
   const int n_c = S * KqI;
   const int per = (n_c + kFW - 1) / kFW;
-  // this wave's pairs per down item, and its down copies (nibbles + scales)
   const int cnt_w = (n_c - w * per) < per ? ((n_c - w * per) > 0 ? n_c - w * per : 0) : per;
-  const int dn_copies = nd * cnt_w * 2;
+  const int gu_copies = ng * nqw * 4;  // vmcnt entries: gate nibbles, up nibbles, gate scales, up scales
 
-  // the combine's tables, while the routing results are at hand: slot s at
-  // position pos of segment u reads part pt of output row nn at
-  // (beg * KqI + pt * cnt + pos - beg) * 16 + nn, u's parts being the waves
-  // its (segment, quad) pairs fall to
-  if (S > 0 && nd > 0) {
-    for (int s = threadIdx.x; s < T * k + (a.has_shared ? T : 0); s += kFThreads) {
-      const bool sh = s >= T * k;
-      const int u = sh ? S - 1 : s_e2u[s_sel_idx[s]];
-      const int pos = sh ? T * k + (s - T * k) : s_slot_pos[s];
-      const int beg = s_seg_beg[u], cnt = s_seg_cnt[u];
-      s_cb_base[s] = (beg * KqI + pos - beg) * 16;
-      s_cb_step[s] = cnt * 16;
-      s_cb_np[s] = ((u + 1) * KqI - 1) / per - (u * KqI) / per + 1;
+  // each gate/up item's row tile of I and segment
+  int it_rt[kFusedMaxItems], it_e[kFusedMaxItems], it_beg[kFusedMaxItems], it_cnt[kFusedMaxItems];
+#pragma unroll
+  for (int ii = 0; ii < kFusedMaxItems; ++ii) {
+    it_rt[ii] = it_e[ii] = it_beg[ii] = it_cnt[ii] = 0;
+    if (ii < ng) {
+      const int item = b + ii * G;
+      const int u = div_nrtI(item);
+      it_rt[ii] = item - u * nrtI;
+      it_e[ii] = uni(s_seg_e[u]);
+      it_beg[ii] = uni(s_seg_beg[u]);
+      it_cnt[ii] = uni(s_seg_cnt[u]);
     }
+  }
+  // lane c < cnt_w: the expert and quad of this wave's c-th down pair
+  int my_e = 0, my_q = 0;
+  if (nd > 0 && lane < cnt_w) {
+    const int pair = w * per + lane;
+    const int u = div_KqI(pair);
+    my_q = pair - u * KqI;
+    my_e = s_seg_e[u];
   }
 
   const uint32_t gnib_bytes = (uint32_t)I * (uint32_t)Kq * 64u;  // one expert's gate (or up) nibbles
@@ -644,11 +790,10 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
   };
   char* wgu = lds + a.lds.wgu;
   char* wdn = lds + a.lds.wdn;
-  if (ng > 0) {
-    for (int ii = 0; ii < ng; ++ii) {
-      const int item = b + ii * G;
-      const int u = item / nrtI, rt = item % nrtI;
-      const int e = uni(s_seg_e[u]);
+#pragma unroll
+  for (int ii = 0; ii < kFusedMaxItems; ++ii) {
+    if (ii < ng) {
+      const int e = it_e[ii];
       const bool routed = e < E;
       const BufRsrc gn = routed ? buf_rsrc(a.gate_nib, stack(gnib_bytes)) : buf_rsrc(a.sh_gate_nib, gnib_bytes);
       const BufRsrc un = routed ? buf_rsrc(a.up_nib, stack(gnib_bytes)) : buf_rsrc(a.sh_up_nib, gnib_bytes);
@@ -656,10 +801,9 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
       const BufRsrc us = routed ? buf_rsrc(a.up_sc, stack(gsc_bytes)) : buf_rsrc(a.sh_up_sc, gsc_bytes);
       const uint32_t eo_n = routed ? (uint32_t)e * gnib_bytes : 0u;
       const uint32_t eo_s = routed ? (uint32_t)e * gsc_bytes : 0u;
-      for (int qq = 0; qq < nq; ++qq) {
+      for (int qq = 0; qq < nqw; ++qq) {
         const int q = w + kFW * qq;
-        if (q >= Kq) break;
-        const uint32_t tq = (uint32_t)(rt * Kq + q);
+        const uint32_t tq = (uint32_t)(it_rt[ii] * Kq + q);
         char* slot = wgu + ((ii * nq + qq) * kFW + w) * kGuChunkLds;
         dma_b128(gn, slot, (uint32_t)lane * 16u, eo_n + tq * kQuadNibBytes);
         dma_b128(un, slot + 1024, (uint32_t)lane * 16u, eo_n + tq * kQuadNibBytes);
@@ -669,67 +813,114 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
       }
     }
   }
-  if (nd > 0) {
-    for (int dd = 0; dd < nd; ++dd) {
-      const int rH = dn_first + dd * G;
-      for (int cc = 0; cc < per; ++cc) {
-        const int pair = w * per + cc;
-        if (pair >= n_c) break;
-        const int u = pair / KqI, q = pair % KqI;
-        const int e = uni(s_seg_e[u]);
-        const bool routed = e < E;
-        const BufRsrc dn = routed ? buf_rsrc(a.down_nib, stack(dnib_bytes)) : buf_rsrc(a.sh_down_nib, dnib_bytes);
-        const BufRsrc ds = routed ? buf_rsrc(a.down_sc, stack(dsc_bytes)) : buf_rsrc(a.sh_down_sc, dsc_bytes);
-        const uint32_t tq = (uint32_t)(rH * KqI + q);
-        char* slot = wdn + ((dd * per + cc) * kFW + w) * kDnChunkLds;
-        dma_b128(dn, slot, (uint32_t)lane * 16u, (routed ? (uint32_t)e * dnib_bytes : 0u) + tq * kQuadNibBytes);
-        if (lane < 32)
-          dma_b32(ds, slot + 1024, (uint32_t)lane * 4u, (routed ? (uint32_t)e * dsc_bytes : 0u) + tq * (kQuadScales * 2));
-      }
+  // The down copies go out once this workgroup's gate/up copies have landed
+  // (at once without gate/up items): the gate/up weights, which the h
+  // hand-off waits for, then share HBM only with each other and with the
+  // down weights of workgroups that are already done with theirs.
+  auto issue_down = [&]() {
+  for (int dd = 0; dd < nd; ++dd) {
+    const int rH = dn_first + dd * G;
+    for (int cc = 0; cc < cnt_w; ++cc) {
+      const int e = __builtin_amdgcn_readlane(my_e, cc);
+      const int q = __builtin_amdgcn_readlane(my_q, cc);
+      const bool routed = e < E;
+      const BufRsrc dn = routed ? buf_rsrc(a.down_nib, stack(dnib_bytes)) : buf_rsrc(a.sh_down_nib, dnib_bytes);
+      const BufRsrc ds = routed ? buf_rsrc(a.down_sc, stack(dsc_bytes)) : buf_rsrc(a.sh_down_sc, dsc_bytes);
+      const uint32_t tq = (uint32_t)(rH * KqI + q);
+      char* slot = wdn + ((dd * per + cc) * kFW + w) * kDnChunkLds;
+      dma_b128(dn, slot, (uint32_t)lane * 16u, (routed ? (uint32_t)e * dnib_bytes : 0u) + tq * kQuadNibBytes);
+      if (lane < 32)
+        dma_b32(ds, slot + 1024, (uint32_t)lane * 4u, (routed ? (uint32_t)e * dsc_bytes : 0u) + tq * (kQuadScales * 2));
+    }
+  }
+  };
+  if (ng == 0) issue_down();
+
+  // ---- 4. routing outputs and the combine's tables, while the copies land ----
+  if (b == 0)
+    for (int i = threadIdx.x; i < T * k; i += kFThreads) {
+      a.topk_idx[i] = route_failed ? -1 : s_sel_idx[i];
+      a.topk_w[i] = route_failed ? __builtin_nanf("") : s_sel_w[i];
+    }
+  // the combine's tables: slot s at position pos of segment u reads part pt
+  // of output row nn at (beg * KqI + pt * cnt + pos - beg) * 16 + nn, u's
+  // parts being the waves its (segment, quad) pairs fall to
+  if (S > 0 && nd > 0) {
+    for (int s = threadIdx.x; s < T * k + (has_sh ? T : 0); s += kFThreads) {
+      const bool sh = s >= T * k;
+      const int u = sh ? S - 1 : s_e2u[s_sel_idx[s]];
+      const int pos = sh ? s : s_slot_pos[s];
+      const int beg = s_seg_beg[u], cnt = s_seg_cnt[u];
+      s_cb_base[s] = (beg * KqI + pos - beg) * 16;
+      s_cb_step[s] = cnt * 16;
+      s_cb_np[s] = ((u + 1) * KqI - 1) / per - (u * KqI) / per + 1;
     }
   }
 
-  // ---- 4. gate/up items ----------------------------------------------------
-  // Every item's chunks first, its accumulators in registers (at most
-  // kFusedMaxItems items), then one reduction for all items: each wave writes
-  // its partial sums over its own first staging slot of the item (read by
-  // nobody else, and dead once the wave's MFMAs are done), one barrier, and
-  // the SwiGLU epilogue of every item spread over the workgroup.
-  const BufRsrc hq_r = buf_rsrc(a.hq, (uint32_t)((T * k + T) * KqI * 512));
-  const BufRsrc hs_r = buf_rsrc(a.hs, (uint32_t)((T * k + T) * KqI * 32));
-  const BufRsrc flag_r = buf_rsrc(a.flags, (uint32_t)(n_gu > 0 ? n_gu * 8 : 8));
-  if (ng > 0) {
-    const uint32_t mask = vgpr_const(0x00780078u);
-    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    int tok[kFusedMaxItems];
+  // ---- 5. gate/up items ----------------------------------------------------
+  // Items in copy order, each as soon as its copies have landed, the
+  // accumulators in registers; then one reduction for all items: each wave
+  // writes its partial sums over its own first staging slot of the item
+  // (read by nobody else, and dead once the wave's MFMAs are done), one
+  // barrier, and the SwiGLU epilogue of every item spread over the workgroup.
+  const int hunits = I / 2;  // tagged h units per segment position
+  const BufRsrc hv_r = buf_rsrc(a.hv, (uint32_t)(npos * hunits * 16));
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  // The down weights of a single item are expanded into MFMA operands
+  // (fp16 n - 8 and fp32 scales) while h is on its way, so that only MFMAs
+  // remain once it has arrived.
+  const uint32_t dmask = vgpr_const(0x000F000Fu);
+  const bool pre = nd == 1;  // the first kPreDq chunks of a single item
+  u32x4 pbb[kPreDq][4];
+  float pdv[kPreDq][4];
+  auto expand_down = [&]() {
+    wait_vmcnt<0>();  // this wave's down copies
+    if (pre) {
 #pragma unroll
-    for (int ii = 0; ii < kFusedMaxItems; ++ii) {
-      tok[ii] = T;
-      if (ii < ng) {
-        const int u = (b + ii * G) / nrtI;
-        const int beg = uni(s_seg_beg[u]), cnt = uni(s_seg_cnt[u]);
-        if (n < cnt) tok[ii] = s_seg_tok[beg + n];
+      for (int c = 0; c < kPreDq; ++c) {
+        if (c < cnt_w) {
+          const char* slot = wdn + (c * kFW + w) * kDnChunkLds;
+          const u32x4 wv = *reinterpret_cast<const u32x4*>(slot + lane * 16);
+          unpack_scales(*reinterpret_cast<const uint2*>(slot + 1024 + n * 8), pdv[c]);
+          pbb[c][0] = dequant_unit_f16s(wv.x, dmask);
+          pbb[c][1] = dequant_unit_f16s(wv.y, dmask);
+          pbb[c][2] = dequant_unit_f16s(wv.z, dmask);
+          pbb[c][3] = dequant_unit_f16s(wv.w, dmask);
+        }
       }
     }
-    // this wave's gate/up copies have landed (each wave reads only its own;
-    // its down copies, issued after them, may still be in flight)
-    wait_vmcnt_le(dn_copies);
+  };
+  if (ng > 0) {
+    const uint32_t mask = vgpr_const(0x00780078u);
     f32x4 ag[kFusedMaxItems], au[kFusedMaxItems], cg[kFusedMaxItems], cu[kFusedMaxItems];
+    // Only the lanes of real segment positions read the x operand; the
+    // others keep whatever they hold: an MFMA row of A feeds only the same
+    // row of the result, and those rows are never read.
+    u32x4 xa[4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    float sx = 0.0f;
 #pragma unroll
     for (int ii = 0; ii < kFusedMaxItems; ++ii) {
       ag[ii] = au[ii] = cg[ii] = cu[ii] = z;
       if (ii < ng) {
-        for (int qq = 0; qq < nq; ++qq) {
+        const bool pv = n < it_cnt[ii];
+        const int tok = pv ? s_seg_tok[it_beg[ii] + n] : 0;
+        wait_vmcnt_le(gu_copies - (ii + 1) * nqw * 4);  // this item's copies
+        if (ii == ng - 1 && nd > 0) issue_down();
+        for (int qq = 0; qq < nqw; ++qq) {
           const int q = w + kFW * qq;
-          if (q >= Kq) break;
           const char* slot = wgu + ((ii * nq + qq) * kFW + w) * kGuChunkLds;
           const u32x4 gw = *reinterpret_cast<const u32x4*>(slot + lane * 16);
           const u32x4 uw = *reinterpret_cast<const u32x4*>(slot + 1024 + lane * 16);
           const uint2 gsv = *reinterpret_cast<const uint2*>(slot + 2048 + n * 8);
           const uint2 usv = *reinterpret_cast<const uint2*>(slot + 2176 + n * 8);
-          const u32x4* xo = s_xop + ((tok[ii] * Kq + q) * 4 + p) * 4;
-          const u32x4 xa[4] = {xo[0], xo[1], xo[2], xo[3]};
-          const float sx = s_xs[(tok[ii] * Kq + q) * 4 + p];
+          if (pv) {
+            const u32x4* xo = s_xop + ((tok * Kq + q) * 4 + p) * 4;
+            xa[0] = xo[0];
+            xa[1] = xo[1];
+            xa[2] = xo[2];
+            xa[3] = xo[3];
+            sx = s_xs[(tok * Kq + q) * 4 + p];
+          }
           float dg[4], du[4];
           unpack_scales(gsv, dg);
           unpack_scales(usv, du);
@@ -757,191 +948,123 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
         float* red = reinterpret_cast<float*>(wgu + ((ii * nq) * kFW + w) * kGuChunkLds);  // [gate/up][16][16]
         const f32x4 rg = kUnitScale * ag[ii] - kUnitBias * cg[ii];
         const f32x4 ru = kUnitScale * au[ii] - kUnitBias * cu[ii];
+        // lane (n, p) holds positions 4p + j of output row n; only real
+        // positions are read back
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          red[(4 * p + j) * 16 + n] = rg[j];
-          red[256 + (4 * p + j) * 16 + n] = ru[j];
+          if (4 * p + j < it_cnt[ii]) {
+            red[(4 * p + j) * 16 + n] = rg[j];
+            red[256 + (4 * p + j) * 16 + n] = ru[j];
+          }
         }
       }
     }
     lds_barrier();
     for (int o = threadIdx.x; o < ng * 256; o += kFThreads) {
-      const int ii = o / 256;
+      const int ii = o / 256;  // wave-uniform
       const int mm = (o % 256) / 16;
       const int nn = o % 16;
       const int item = b + ii * G;
-      const int u = item / nrtI, rt = item % nrtI;
+      const int u = div_nrtI(item);
+      const int rt = item - u * nrtI;
       const int beg = s_seg_beg[u], cnt = s_seg_cnt[u];
-      const float* red0 = reinterpret_cast<const float*>(wgu + ((ii * nq) * kFW) * kGuChunkLds);
-      float gv[kFW], uv[kFW];
-#pragma unroll
-      for (int s2 = 0; s2 < kFW; ++s2) {
-        gv[s2] = red0[s2 * (kGuChunkLds / 4) + mm * 16 + nn];
-        uv[s2] = red0[s2 * (kGuChunkLds / 4) + 256 + mm * 16 + nn];
-      }
-      float g = 0.0f, uu = 0.0f;
-#pragma unroll
-      for (int s2 = 0; s2 < kFW; ++s2) {
-        g += gv[s2];
-        uu += uv[s2];
-      }
-      const float h = g * (1.0f / (1.0f + expf(-g))) * uu;
-      const uint32_t hb = float_to_half_bits(h);
-      const float hf = half_bits_to_float32(hb);
-      const uint32_t lb = float_to_half_bits(h - hf);
-      const float lf = half_bits_to_float32(lb);
       const bool ok = mm < cnt;
-      const int pos = beg + mm;
-      const int i = rt * 16 + nn;  // row of I
-      const int g32 = i / kGroup;
-      const int cc = i % kGroup;
-      const int half = cc / 16;
-      const int pp = (cc % 16) / 4;
-      const int rr = cc % 4;
-      // kmap(p, j) = 4p + {0, 2, 16, 18, 1, 3, 17, 19}[j], inverted per half
-      const int jj = half == 0 ? ((rr & 1) ? 4 : 0) + (rr >> 1) : ((rr & 1) ? 6 : 2) + (rr >> 1);
-      const uint32_t off = (uint32_t)((((pos * KqI + g32 / 4) * 16 + pp * 4 + (g32 % 4)) * 16 + jj) * 2);
+      uint32_t v = 0u;
       if (ok) {
-        __builtin_amdgcn_raw_buffer_store_b16((unsigned short)hb, hq_r, (int)off, 0, kDeviceScope);
-        __builtin_amdgcn_raw_buffer_store_b16((unsigned short)lb, hq_r, (int)(off + 16u), 0, kDeviceScope);
-      }
-      // the 16 rows of the tile are one half of one group: sum hi + lo
-      // over them (16 consecutive lanes, fixed butterfly order)
-      float sum = hf + lf;
-      sum += __shfl_xor(sum, 8, kWave);
-      sum += __shfl_xor(sum, 4, kWave);
-      sum += __shfl_xor(sum, 2, kWave);
-      sum += __shfl_xor(sum, 1, kWave);
-      if (nn == 0 && ok)
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum), hs_r,
-                                              (int)(((pos * KqI * 4 + g32) * 2 + half) * 4), 0, kDeviceScope);
-    }
-    // every h store of the workgroup has completed before any flag is set
-    __builtin_amdgcn_s_waitcnt(0);
-    lds_barrier();
-    if (threadIdx.x < ng) store_tag(flag_r, (uint32_t)(b + (int)threadIdx.x * G) * 8u, tag);
-  }
-
-  // ---- 5. down items with the combine --------------------------------------
-  if (nd > 0) {
-    // The down weights of a single item are expanded into MFMA operands now
-    // (fp16 1 + n/16 and fp32 scales), while the gate/up results are still
-    // on their way, so that only MFMAs remain after the hand-off.
-    const uint32_t dmask = vgpr_const(0x03C003C0u);
-    const bool pre = nd == 1;  // the first kPreDq chunks of a single item (more would spill)
-    u32x4 pbb[kPreDq][4];
-    float pdv[kPreDq][4];
-    wait_vmcnt<0>();  // this wave's down copies
-    if (pre) {
+        const float* red0 = reinterpret_cast<const float*>(wgu + ((ii * nq) * kFW) * kGuChunkLds);
+        float gv[kFW], uv[kFW];
 #pragma unroll
-      for (int c = 0; c < kPreDq; ++c) {
-        if (c < cnt_w) {
-          const char* slot = wdn + (c * kFW + w) * kDnChunkLds;
-          const u32x4 wv = *reinterpret_cast<const u32x4*>(slot + lane * 16);
-          unpack_scales(*reinterpret_cast<const uint2*>(slot + 1024 + n * 8), pdv[c]);
-          pbb[c][0] = dequant_unit_f16(wv.x, dmask);
-          pbb[c][1] = dequant_unit_f16(wv.y, dmask);
-          pbb[c][2] = dequant_unit_f16(wv.z, dmask);
-          pbb[c][3] = dequant_unit_f16(wv.w, dmask);
+        for (int s2 = 0; s2 < kFW; ++s2) {
+          gv[s2] = red0[s2 * (kGuChunkLds / 4) + mm * 16 + nn];
+          uv[s2] = red0[s2 * (kGuChunkLds / 4) + 256 + mm * 16 + nn];
         }
+        float g = 0.0f, uu = 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 < kFW; ++s2) {
+          g += gv[s2];
+          uu += uv[s2];
+        }
+        const float h = g * (1.0f / (1.0f + expf(-g))) * uu;
+        const uint32_t hb = float_to_half_bits(h);
+        const uint32_t lb = float_to_half_bits(h - half_bits_to_float32(hb));
+        v = hb | (lb << 16);
+      }
+      // the unit of rows cc and cc + 2 of a half-group (cc % 4 < 2) is
+      // stored by the lane of row cc with its partner's value
+      const uint32_t v2 = __shfl_down(v, 2, kWave);
+      if (ok && (nn & 2) == 0) {
+        const int i = rt * 16 + nn;  // row of I
+        const int unit = (i / kGroup) * 16 + (rt & 1) * 8 + (nn >> 2) * 2 + (nn & 1);
+        u32x4 hvv;
+        hvv.x = v;
+        hvv.y = tag;
+        hvv.z = v2;
+        hvv.w = ~tag;
+        __builtin_amdgcn_raw_buffer_store_b128(hvv, hv_r, ((beg + mm) * hunits + unit) * 16, 0, kDeviceScope);
       }
     }
-    // wait for every gate/up item of the layer (one poll per lane in flight)
-    const uint32_t want = tag + a.skew_flags;
-    for (int i0 = w * kWave; i0 < n_gu; i0 += kFThreads) {
-      const int i = i0 + lane;
-      bool done = i >= n_gu;
-      for (uint32_t it = 0;; ++it) {
-        if (!done) done = tag_is(flag_r, (uint32_t)i * 8u, want);
-        if (__all(done)) break;
-        if (it >= a.wait_polls) {
-          if (lane == 0) {
-            s_fail = 1;
-            set_status(a.ctl, kStatusExpertWait);
-          }
-          break;
-        }
-      }
-    }
-    lds_barrier();
-    const bool h_failed = uni(s_fail) != 0;
-    // h of every segment position -> LDS (device-scope loads, issued after the
-    // flags arrived), plus an all-zero row; groups past I are zero
-    const int npos = T * k + (a.has_shared ? T : 0);
+  }
+  if (nd > 0) expand_down();
+
+  // ---- 6. down items with the combine --------------------------------------
+  if (nd > 0) {
+    lds_barrier();  // every wave's gate/up epilogue has read its partials: the h region is free
+    // h of every segment position, polled into the down operand (poll_h_units)
     const uint32_t hrow = h_row_bytes(KqI);
     char* s_hb = lds + a.lds.h;
-    float* s_hs = reinterpret_cast<float*>(s_hb + align_lds((uint32_t)(npos + 1) * hrow));
     float* s_dred = reinterpret_cast<float*>(lds + a.lds.dred);
-    {
-      const int nu16 = (npos + 1) * KqI * 32;  // 16-byte units
-      constexpr int U = 4;
-      for (int i0 = threadIdx.x; i0 < nu16; i0 += kFThreads * U) {
-        u32x4 v[U];
-#pragma unroll
-        for (int r = 0; r < U; ++r) {
-          const int i = i0 + r * kFThreads;
-          const int pos = i / (KqI * 32);
-          const int rem = i % (KqI * 32);
-          const int g = 4 * (rem / 32) + ((rem % 32) / 2) % 4;  // units of a quad: [p 4][gi 4][hi, lo]
-          const bool ok = i < nu16 && pos < npos && g < KgI;
-          v[r] = __builtin_amdgcn_raw_buffer_load_b128(hq_r, ok ? (uint32_t)(pos * KqI * 512 + rem * 16) : 0xFFFFF000u,
-                                                        0, kDeviceScope);
-        }
-#pragma unroll
-        for (int r = 0; r < U; ++r) {
-          const int i = i0 + r * kFThreads;
-          if (i < nu16) {
-            const int pos = i / (KqI * 32);
-            const int rem = i % (KqI * 32);
-            *reinterpret_cast<u32x4*>(s_hb + (size_t)pos * hrow + rem * 16) = v[r];
-          }
-        }
-      }
-      const int nsum = (npos + 1) * KqI * 8;
-      for (int i = threadIdx.x; i < nsum; i += kFThreads) {
-        const int pos = i / (KqI * 8);
-        const int g = (i % (KqI * 8)) / 2;
-        const bool ok = pos < npos && g < KgI;
-        s_hs[i] = __builtin_bit_cast(
-            float, __builtin_amdgcn_raw_buffer_load_b32(hs_r, ok ? (uint32_t)(i * 4) : 0xFFFFF000u, 0, kDeviceScope));
-      }
+    const int upos = KqI * 64;  // h units per position, padding groups included
+    // When every wave's (segment, quad) pairs are exactly one segment (wave w:
+    // segment w), each wave polls the h of its own segment and goes on to its
+    // MFMAs as soon as that has arrived; otherwise the workgroup polls all of
+    // h and meets at a barrier.
+    const bool seg_wave = per == KqI;
+    if (seg_wave) {
+      if (w < S)
+        poll_h_units<I_>(uni(s_seg_beg[w]), uni(s_seg_cnt[w]) * upos, lane, kWave, hv_r, tag + a.skew_h, a.wait_polls,
+                         a.ctl, &s_fail, s_hb, hrow, hunits, upos, KgI, a.md_upos);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+    } else {
+      poll_h_units<I_>(0, npos * upos, (int)threadIdx.x, kFThreads, hv_r, tag + a.skew_h, a.wait_polls, a.ctl, &s_fail,
+                       s_hb, hrow, hunits, upos, KgI, a.md_upos);
+      lds_barrier();
     }
-    wait_vmcnt<0>();  // the h copies
-    lds_barrier();
-    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    // The h operand of position m of a segment sits in MFMA rows 2m (fp16 hi)
+    // and 2m + 1 (fp16 lo), so one MFMA per group multiplies both halves
+    // (segments hold at most 8 positions).  Only those lanes read it; the
+    // others keep whatever they hold (those result rows are never used).
+    u32x4 hh[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) hh[r] = u32x4{0u, 0u, 0u, 0u};
     for (int dd = 0; dd < nd; ++dd) {
       // The wave's pairs [w * per, w * per + per) in (segment, quad) order:
       // consecutive quads of one segment accumulate in registers; at a
       // segment's last pair in the range the partial sum goes to LDS as part
       // w - (first wave of the segment), real positions only.
-      f32x4 acc = z, corr = z;
+      f32x4 acc = z;
       auto chunk = [&](int cc, const u32x4 (&bb)[4], const float (&dv)[4]) {
         const int pair = w * per + cc;
-        const int u = pair / KqI;
-        const int q = pair % KqI;
+        const int u = div_KqI(pair);
+        const int q = pair - u * KqI;
         const int beg = uni(s_seg_beg[u]), cnt = uni(s_seg_cnt[u]);
-        const int pos = n < cnt ? beg + n : npos;  // row npos is zero
-        const u32x4* ho = reinterpret_cast<const u32x4*>(s_hb + (size_t)pos * hrow + q * 512 + p * 128);
-        const u32x4 hh[8] = {ho[0], ho[1], ho[2], ho[3], ho[4], ho[5], ho[6], ho[7]};
-        const float sp = s_hs[(pos * KqI + q) * 8 + p * 2] + s_hs[(pos * KqI + q) * 8 + p * 2 + 1];
-        f32x4 pp[4];
+        if (n < 2 * cnt) {
+          const u32x4* ho = reinterpret_cast<const u32x4*>(s_hb + (size_t)(beg + n / 2) * hrow + q * 512 + p * 128 +
+                                                            (n & 1) * 16);
 #pragma unroll
-        for (int gi = 0; gi < 4; ++gi) pp[gi] = mfma_f16_16x16x32(hh[2 * gi], bb[gi], z);
+          for (int gi = 0; gi < 4; ++gi) hh[gi] = ho[2 * gi];
+        }
 #pragma unroll
-        for (int gi = 0; gi < 4; ++gi) pp[gi] = mfma_f16_16x16x32(hh[2 * gi + 1], bb[gi], pp[gi]);
-        corr = mfma_f32_16x16x4(sp, dv[p], corr);
-#pragma unroll
-        for (int gi = 0; gi < 4; ++gi) acc += dv[gi] * pp[gi];
+        for (int gi = 0; gi < 4; ++gi) acc += dv[gi] * mfma_f16_16x16x32(hh[gi], bb[gi], z);
         if (q == KqI - 1 || cc == per - 1 || pair + 1 == n_c) {
-          const f32x4 res = kUnitScale * acc - kUnitBias * corr;
           const int part = w - (u * KqI) / per;
-          // lane (n, p) holds positions 4p + j of output row n
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int m = 4 * p + j;
-            if (m < cnt) s_dred[((beg * KqI + part * cnt) + m) * 16 + n] = res[j];
-          }
-          acc = corr = z;
+          // lane (n, p) holds rows 4p + j of output row n: positions 2p
+          // (hi + lo in rows 4p, 4p + 1) and 2p + 1
+          const float r0 = acc[0] + acc[1], r1 = acc[2] + acc[3];
+          float* dst = s_dred + (beg * KqI + part * cnt) * 16 + n;
+          if (2 * p < cnt) dst[(2 * p) * 16] = r0;
+          if (2 * p + 1 < cnt) dst[(2 * p + 1) * 16] = r1;
+          acc = z;
         }
       };
       int c0 = 0;
@@ -951,18 +1074,17 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
           if (c < cnt_w) chunk(c, pbb[c], pdv[c]);
         c0 = kPreDq;
       }
-      {
-        for (int cc = c0; cc < cnt_w; ++cc) {
-          const char* slot = wdn + ((dd * per + cc) * kFW + w) * kDnChunkLds;
-          const u32x4 wv = *reinterpret_cast<const u32x4*>(slot + lane * 16);
-          float dv[4];
-          unpack_scales(*reinterpret_cast<const uint2*>(slot + 1024 + n * 8), dv);
-          const u32x4 bb[4] = {dequant_unit_f16(wv.x, dmask), dequant_unit_f16(wv.y, dmask),
-                               dequant_unit_f16(wv.z, dmask), dequant_unit_f16(wv.w, dmask)};
-          chunk(cc, bb, dv);
-        }
+      for (int cc = c0; cc < cnt_w; ++cc) {
+        const char* slot = wdn + ((dd * per + cc) * kFW + w) * kDnChunkLds;
+        const u32x4 wv = *reinterpret_cast<const u32x4*>(slot + lane * 16);
+        float dv[4];
+        unpack_scales(*reinterpret_cast<const uint2*>(slot + 1024 + n * 8), dv);
+        const u32x4 bb[4] = {dequant_unit_f16s(wv.x, dmask), dequant_unit_f16s(wv.y, dmask),
+                             dequant_unit_f16s(wv.z, dmask), dequant_unit_f16s(wv.w, dmask)};
+        chunk(cc, bb, dv);
       }
       lds_barrier();
+      const bool h_failed = uni(s_fail) != 0;
       const int rH = dn_first + dd * G;
       if (threadIdx.x < T * 16) {
         // the slots' tables and partials are independent loads, issued eight
@@ -984,7 +1106,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
           for (int jj = 0; jj < 8; ++jj)
             if (j0 + jj < k) acc_y += wj[jj] * sq[jj];
         }
-        if (a.has_shared) {
+        if (has_sh) {
           const int s = T * k + t;
           const int base = s_cb_base[s] + nn, step = s_cb_step[s], np = s_cb_np[s];
           float sq = s_dred[base];
@@ -1002,9 +1124,9 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
       for (int i = threadIdx.x; i < T * 16; i += kFThreads) a.y[(int64_t)(i / 16) * H + dd * 16 + i % 16] = __builtin_nanf("");
   }
 
-  // ---- 6. the next call's tag --------------------------------------------------
+  // ---- 7. the next call's tag --------------------------------------------------
   if (b == 0 && w == 0) {
-    // every workgroup has read the generation once its presence is here
+    // every wave has read the generation once its workgroup's presence is here
     for (int i0 = 0; i0 < G; i0 += kWave) {
       const int i = i0 + lane;
       bool done = i >= G;
@@ -1032,9 +1154,13 @@ bool fused_shape_ok(int64_t T, int64_t H, int64_t I, int E, int k, int has_share
   // 32-bit buffer offsets over each stacked matrix and over h
   if ((uint64_t)E * (uint64_t)I * Kq * 64 >= kMaxRsrcBytes || (uint64_t)E * (uint64_t)H * KqI * 64 >= kMaxRsrcBytes)
     return false;
-  if ((T * k + T) * KqI * 512 >= ((int64_t)1 << 31)) return false;
-  // the smallest layout: one item of each kind per workgroup
+  if ((T * k + T) * (I / 2) * 16 >= ((int64_t)1 << 31)) return false;
+  // the magic divisions: every dividend and divisor below 2^16
+  if ((T + 1) * Kq * 4 >= 65536 || (T * k + T) * KqI * 64 + kFThreads * kHUnits >= 65536) return false;
+  // the smallest layout: one item of each kind per workgroup; a wave's down
+  // pairs fit one lane each
   const int S_max = (int)((T * k < E ? T * k : E) + (has_shared ? 1 : 0));
+  if (ceil_div((int64_t)S_max * KqI, kFW) > kWave) return false;
   return fused_lds_layout((int)T, k, E, has_shared, (int)H, (int)I, 1, 1, S_max).bytes <= kFusedDynLdsMax;
 }
 
@@ -1048,25 +1174,34 @@ FusedPlan fused_plan(int64_t T, int64_t H, int64_t I, int E, int k, int has_shar
   const int S_max = (int)((T * k < E ? T * k : E) + (has_shared ? 1 : 0));
   const int n_gu = S_max * (int)(I / kRowTile);
   const int n_dn = (int)(H / kRowTile);
+  if (n_gu + G >= 65536 || n_dn + G >= 65536) return pl;  // the magic divisions
   const int ng = (int)ceil_div(n_gu, G), nd = (int)ceil_div(n_dn, G);
   if (ng > kFusedMaxItems) return pl;  // the gate/up accumulators of one workgroup live in registers
   pl.lds = fused_lds_layout((int)T, k, E, has_shared, (int)H, (int)I, ng, nd, S_max);
   if (pl.lds.bytes > kFusedDynLdsMax) return pl;
   pl.G = G;
+  pl.spec = (T == 1 && H == 2048 && I == 768 && E == 128 && k == 8 && !has_shared) ? kFusedSpecQwen3T1 : 0;
   pl.ok = true;
   return pl;
 }
 
-static hipError_t launch_fused(const FusedK& a, const FusedPlan& pl, hipStream_t stream) {
+template <int T_, int H_, int I_, int E_, int K_, int SH_>
+static hipError_t launch_fused_as(const FusedK& a, const FusedPlan& pl, hipStream_t stream) {
   static bool attr_set = false;
+  auto kernel = moe_decode_fused_kernel<T_, H_, I_, E_, K_, SH_>;
   if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_decode_fused_kernel),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFusedDynLdsMax);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL(moe_decode_fused_kernel, dim3(pl.G), dim3(kFThreads), pl.lds.bytes, stream, a);
+  hipLaunchKernelGGL(kernel, dim3(pl.G), dim3(kFThreads), pl.lds.bytes, stream, a);
   return hipGetLastError();
+}
+
+static hipError_t launch_fused(const FusedK& a, const FusedPlan& pl, hipStream_t stream) {
+  if (pl.spec == kFusedSpecQwen3T1) return launch_fused_as<1, 2048, 768, 128, 8, 0>(a, pl, stream);
+  return launch_fused_as<0, 0, 0, 0, 0, -1>(a, pl, stream);
 }
 
 hipError_t launch_decode_fused(const FusedPlan& pl, const RouteArgs& r, const ExpertArgs& x, const FusedWs& ws,
@@ -1084,6 +1219,12 @@ hipError_t launch_decode_fused(const FusedPlan& pl, const RouteArgs& r, const Ex
   a.has_shared = x.has_shared;
   a.Kq = (int)ceil_div(r.H, kQuad);
   a.KqI = (int)ceil_div(x.I, kQuad);
+  a.md_E = div_magic((uint32_t)a.E);
+  a.md_nrtI = div_magic((uint32_t)(a.I / kRowTile));
+  a.md_KqI = div_magic((uint32_t)a.KqI);
+  a.md_Kq4 = div_magic((uint32_t)(4 * a.Kq));
+  a.md_upos = div_magic((uint32_t)(64 * a.KqI));
+  a.md_G = div_magic((uint32_t)pl.G);
   a.gate_nib = x.gate_nib;
   a.gate_sc = x.gate_scale;
   a.up_nib = x.up_nib;
@@ -1102,14 +1243,12 @@ hipError_t launch_decode_fused(const FusedPlan& pl, const RouteArgs& r, const Ex
   a.ctl = ws.ctl;
   a.presence = ws.presence;
   a.slots = ws.slots;
-  a.flags = ws.flags;
-  a.hq = ws.hq;
-  a.hs = ws.hs;
+  a.hv = ws.hv;
   a.lds = pl.lds;
   const LibConfig cfg = lib_config();
   a.wait_polls = cfg.fused_wait_polls;
   a.skew_route = (cfg.fused_fault & 1u) ? 1u : 0u;
-  a.skew_flags = (cfg.fused_fault & 2u) ? 1u : 0u;
+  a.skew_h = (cfg.fused_fault & 2u) ? 1u : 0u;
   return launch_fused(a, pl, stream);
 }
 

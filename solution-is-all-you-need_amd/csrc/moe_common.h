@@ -191,6 +191,11 @@ __device__ inline float buf_load_f32(BufRsrc r, uint32_t voff, uint32_t soff) {
 // possibly stale line of this CU's L1 or this XCD's L2.  Data handed between
 // workgroups of one launch this way needs no L2 write-back or invalidation.
 constexpr int kDeviceScope = 16;
+// The same for a load that polls for another workgroup's store, with the
+// intrinsic's volatile bit (bit 31, dropped when the instruction is built):
+// a plain buffer load in a loop that writes no memory may be hoisted out of
+// the loop by the compiler, which would then spin on a stale register.
+constexpr int kDevicePoll = kDeviceScope | (int)0x80000000u;
 
 // Direct-to-LDS buffer loads: each lane's 16 (or 4) bytes land at
 // lds + lane * 16 (or 4); lds must be wave-uniform.  They count in vmcnt like
@@ -240,13 +245,17 @@ __device__ inline void wait_vmcnt() {
 }
 
 // Workgroup barrier for LDS data only: waits for this wave's LDS accesses,
-// not for its outstanding global stores (which no wave of the workgroup reads
-// back), as a __syncthreads() fence would.
+// not for its outstanding global loads and stores (which no wave of the
+// workgroup reads back), as a __syncthreads() fence would.  The fences are
+// workgroup-scope release/acquire restricted to the local address space
+// (lgkmcnt(0) and nothing else), and they are real fences to the compiler:
+// an empty asm with a memory clobber is not, since alias analysis may assume
+// it cannot touch a __shared__ variable whose address never escapes, and
+// then fold another wave's store into this thread's view of the variable.
 __device__ inline void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt not waited for
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 }  // namespace pmoe

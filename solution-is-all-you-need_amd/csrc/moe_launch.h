@@ -34,7 +34,7 @@ constexpr size_t kFusedDynLdsMax = 148 * 1024;
 constexpr int kFusedMaxGrid = 1024;  // workgroups (presence words)
 // Status bits of workspace word 1 (phantom_moe_workspace_status).
 constexpr uint32_t kStatusRouteWait = 1u;     // a workgroup gave up waiting for the logits
-constexpr uint32_t kStatusExpertWait = 2u;    // a down workgroup gave up waiting for gate/up
+constexpr uint32_t kStatusExpertWait = 2u;    // a down workgroup gave up waiting for the h of gate/up
 constexpr uint32_t kStatusPresenceWait = 4u;  // workgroup 0 gave up waiting for every workgroup's start
 // Bytes at the start of every workspace: word 0 the generation counter of the
 // single-launch path, word 1 the status bits.
@@ -47,18 +47,21 @@ struct FusedLds {
   uint32_t h, dred;      // h operand and down partials (after the workgroup's gate/up work)
   uint32_t bytes;        // total
 };
+// Instantiations of the single-launch kernel: 0 reads the shape at run time;
+// kFusedSpecQwen3T1 is compiled for T 1, H 2048, I 768, E 128, top-8, no
+// shared expert (the batch-1 Qwen3-30B-A3B-shaped layer).
+constexpr int kFusedSpecQwen3T1 = 1;
 struct FusedPlan {
   bool ok;
-  int G;  // workgroups (one per CU)
+  int G;     // workgroups (one per CU)
+  int spec;  // kernel instantiation
   FusedLds lds;
 };
 struct FusedWs {
   uint32_t* ctl = nullptr;       // workspace words 0 (generation) and 1 (status)
   uint64_t* presence = nullptr;  // [kFusedMaxGrid]
   uint32_t* slots = nullptr;     // [T * E][4] tagged logits
-  uint64_t* flags = nullptr;     // [gate/up items] tagged completion flags
-  uint16_t* hq = nullptr;        // [T*k + T][KqI * 256] fp16 hi/lo of h
-  float* hs = nullptr;           // [T*k + T][KqI * 8]
+  uint32_t* hv = nullptr;        // [T*k + T][I / 2][4] tagged h units (fp16 hi/lo of two rows)
 };
 // Device-independent shape limits (the workspace plan reserves the fused
 // regions for these shapes).

@@ -32,6 +32,9 @@ HIPCC_FLAGS = [
     # ticket of the fused expert kernel on its critical path.
     "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wall",
+    # a variable read in its own initializer is undefined behaviour that the
+    # optimizer exploits (it can delete whole phases of a kernel): an error
+    "-Werror=uninitialized",
 ]
 
 
