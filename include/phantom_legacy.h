@@ -40,9 +40,16 @@
  *   - Active indices outside [0, D_ffn) are skipped; counts are clamped to
  *     [0, D_ffn].
  *   - No allocation per call: the fp16 activation vector of
- *     sparse_mlp_forward lives in a per-device buffer that grows on demand
+ *     sparse_mlp_forward lives in per-device buffers that grow on demand
  *     (allocation happens only when a larger B * D_ffn is first seen, and
- *     never under stream capture).  Calls run one at a time per process.
+ *     never under stream capture).  Eager calls and calls recorded under
+ *     stream capture use separate buffers; every eager call reserves both at
+ *     its size, and a capture at a size no eager call has reserved returns
+ *     -4 (unsupported).  A buffer a captured graph holds is never freed
+ *     while the process runs, so graphs stay valid across later, larger
+ *     eager calls.  Calls run one at a time per process; replays of graphs
+ *     that hold sparse_mlp_forward share one buffer per device, so they must
+ *     not overlap one another (they may overlap eager calls).
  *
  * Arithmetic (the reference accumulates each dot product sequentially in
  * fp32; this build uses a fixed parallel order with the same fp32 rounding

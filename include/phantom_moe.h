@@ -152,8 +152,9 @@ PHANTOM_MOE_API int phantom_moe_get_option(int option, int* value);
 /* Router: logits = x W^T (+ bias) under the fixed-order fp64 contract,
  * top-k descending with ties to the lower expert index, weights by
  * score_mode.  Replaces PhantomTopKRouter.forward
- * (tests/test_moe_routing.py:56-72).
- * Outputs topk_idx [T, top_k] int32 and topk_w [T, top_k] fp32. */
+ * (tests/test_moe_routing.py:56-72).  A NaN logit ranks below every number,
+ * -inf included (torch.topk in the reference ranks NaN above every number);
+ * -0 ties +0.  Outputs topk_idx [T, top_k] int32 and topk_w [T, top_k] fp32. */
 PHANTOM_MOE_API int phantom_moe_route(const void* x, int x_dtype, const float* router_w, const float* router_bias,
                       int64_t T, int64_t H, int E, int top_k, int score_mode, int32_t* topk_idx,
                       float* topk_w, void* workspace, size_t workspace_bytes, hipStream_t stream);

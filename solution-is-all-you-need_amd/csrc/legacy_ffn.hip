@@ -28,6 +28,7 @@
 // phantom_legacy.h), so results do not depend on timing.
 #include <math.h>
 #include <mutex>
+#include <vector>
 
 #include "moe_common.h"
 #include "moe_launch.h"
@@ -504,17 +505,51 @@ hipError_t launch_down(const uint16_t* act, const int32_t* mult, const uint16_t*
   }
 }
 
-// Per-device state of the legacy entry points: the activation buffer and the
-// timing events.  The legacy calls wait for their own work before returning
-// (as the reference's do), so one buffer per device is idle between calls; a
-// process-wide mutex keeps calls one at a time.
+// Per-device state of the legacy entry points: the activation buffers and the
+// timing events.  Eager calls wait for their own work before returning (as the
+// reference's do), so their buffer is idle between calls; a process-wide mutex
+// keeps calls one at a time.  Calls recorded under stream capture use a second
+// buffer, `cap`, so graph replays never share memory with eager calls.  Every
+// eager call makes both buffers large enough for its size.  Once a capture has
+// recorded `cap`, a graph may replay it at any later time: a larger `cap` is
+// then allocated beside it and the held one is kept, never freed, until the
+// process ends.
+struct LgBuf {
+  uint16_t* p = nullptr;
+  size_t bytes = 0;
+};
 struct LgDevice {
-  uint16_t* act = nullptr;
-  size_t act_bytes = 0;
+  LgBuf act;
+  LgBuf cap;
+  bool cap_held = false;
+  std::vector<void*> retired;
   hipEvent_t ev[2] = {nullptr, nullptr};
 };
 std::mutex g_lg_mutex;
 LgDevice g_lg_dev[64];
+
+// Makes `b` hold at least `need` bytes (rounded up to 1 MiB).  A buffer that
+// a captured graph references is retired instead of freed.
+bool lg_reserve(LgBuf* b, size_t need, bool* held, std::vector<void*>* retired) {
+  if (b->bytes >= need) return true;
+  if (b->p) {
+    if (held && *held) {
+      retired->push_back(b->p);
+      *held = false;
+    } else {
+      (void)hipFree(b->p);
+    }
+    b->p = nullptr;
+    b->bytes = 0;
+  }
+  const size_t bytes = (size_t)round_up((int64_t)need, (int64_t)1 << 20);
+  if (hipMalloc(reinterpret_cast<void**>(&b->p), bytes) != hipSuccess) {
+    b->p = nullptr;
+    return false;
+  }
+  b->bytes = bytes;
+  return true;
+}
 
 bool capturing(hipStream_t s) {
   hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
@@ -642,20 +677,19 @@ PHANTOM_LEGACY_API float sparse_mlp_forward(const phantom_half* d_input, const p
   // neuron multiplicities int32 [B, D_ffn]
   const size_t act_bytes = (size_t)round_up((int64_t)B * D_ffn, 8) * sizeof(uint16_t);
   const size_t need = act_bytes + (size_t)round_up((int64_t)B * D_ffn, 4) * sizeof(int32_t);
-  if (call.dev->act_bytes < need) {
-    if (!call.timed)
-      return (float)set_error(PHANTOM_MOE_EUNSUPPORTED, "sparse_mlp_forward: activation buffer must grow; call once outside stream capture first");
-    if (call.dev->act) {
-      (void)hipFree(call.dev->act);
-      call.dev->act = nullptr;
-      call.dev->act_bytes = 0;
-    }
-    const size_t bytes = (size_t)round_up((int64_t)need, (int64_t)1 << 20);
-    if (hipMalloc(reinterpret_cast<void**>(&call.dev->act), bytes) != hipSuccess)
-      return (float)set_error(PHANTOM_MOE_ELAUNCH, "sparse_mlp_forward: cannot allocate %zu bytes", bytes);
-    call.dev->act_bytes = bytes;
+  uint16_t* act = nullptr;
+  if (call.timed) {
+    if (!lg_reserve(&call.dev->act, need, nullptr, nullptr) ||
+        !lg_reserve(&call.dev->cap, need, &call.dev->cap_held, &call.dev->retired))
+      return (float)set_error(PHANTOM_MOE_ELAUNCH, "sparse_mlp_forward: cannot allocate %zu bytes", need);
+    act = call.dev->act.p;
+  } else {
+    if (call.dev->cap.bytes < need)
+      return (float)set_error(PHANTOM_MOE_EUNSUPPORTED, "sparse_mlp_forward: no activation buffer for B * D_ffn = %lld under stream capture; call once at this size outside capture first", (long long)B * D_ffn);
+    call.dev->cap_held = true;
+    act = call.dev->cap.p;
   }
-  int32_t* mult = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(call.dev->act) + act_bytes);
+  int32_t* mult = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(act) + act_bytes);
   LgRowsK p{};
   p.x = d_input;
   p.w1 = d_gate_weight;
@@ -669,7 +703,7 @@ PHANTOM_LEGACY_API float sparse_mlp_forward(const phantom_half* d_input, const p
   p.D_ffn = D_ffn;
   p.cover = cover;
   p.vec = D % 8 == 0 && aligned16(d_input) && aligned16(d_gate_weight) && aligned16(d_up_weight);
-  p.act = call.dev->act;
+  p.act = act;
   hipError_t e = hipSuccess;
   if (dense) {
     switch (batch_tile(B)) {

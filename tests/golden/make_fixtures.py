@@ -9,7 +9,12 @@ Nothing here runs the reference or the oracle.  Expected values come from:
     cumsum) and scipy's softmax / expit, on seeded inputs whose top-k logit
     gaps are far larger than any summation-order effect, so the expected
     selection does not depend on accumulation order;
-  - the synthetic Zipf bias definition (b_e = -s ln r_e).
+  - the synthetic Zipf bias definition (b_e = -s ln r_e);
+  - torch fp32 on the CPU for router_reference_module.npz: the reference
+    router's forward, F.linear -> torch.topk -> softmax over the top-k logits
+    (tests/test_moe_routing.py:65-71), written out here with torch's own
+    operators (the reference module is not imported), on the benchmark
+    layers' seeded activations and router weights.
 
 Run:  python tests/golden/make_fixtures.py
 """
@@ -18,10 +23,13 @@ from __future__ import annotations
 import json
 import os
 
+import sys
+
 import numpy as np
 from scipy.special import expit, softmax
 
 HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "..", "..", "solution-is-all-you-need_amd"))
 
 
 def f16_bits(v: float) -> int:
@@ -117,6 +125,57 @@ def permute_case(seed, T, k, E):
     return {"idx": idx, "offsets": offsets, "sorted_slots": sorted_slots, "slot_pos": slot_pos, "E": np.int32(E)}
 
 
+# Tokens of each benchmark layer that the reference-module fixture covers: all
+# of them up to 64 tokens, the first 1024 of a prefill batch.
+REFMOD_MAX_TOKENS = 1024
+
+
+def reference_module_routing():
+    """Per benchmark layer: the reference router's fp32 selection and weights.
+
+    The reference module (tests/test_moe_routing.py:43-71) is nn.Linear(H, E,
+    bias=False) -> torch.topk(logits, k) -> softmax(top logits), all fp32.  The
+    Zipf-skewed layer adds its fixed bias as the Linear's bias.  x is the
+    layer's bf16 activations widened to fp32 (the module needs x in the
+    weight's dtype).  The sigmoid-scored layers keep the top-k indices only
+    (the reference module has no sigmoid scoring; sigmoid is monotone, so the
+    selection is the same top-k of the logits).
+
+    A token is marked exempt when two of its k+1 largest fp64 logits are
+    closer than twice the largest |fp32 - fp64| logit difference of that
+    token: only there can fp32 and fp64 order the logits differently.
+    """
+    import torch
+    import torch.nn.functional as F
+    from phantom_moe import synth
+
+    torch.set_num_threads(8)
+    out = {}
+    for name, cfg in synth.CONFIGS.items():
+        n = min(cfg.T, REFMOD_MAX_TOKENS)
+        xb = synth.activations(cfg.T, cfg.H)[:n]
+        W = synth.router_weight(cfg.E, cfg.H)
+        b = synth.zipf_bias(cfg.E, cfg.zipf) if cfg.zipf else None
+        x = torch.from_numpy(synth.bf16_bits_to_f32(xb))
+        with torch.no_grad():
+            logits = F.linear(x, torch.from_numpy(W), None if b is None else torch.from_numpy(b))
+            top, idx = torch.topk(logits, cfg.k, dim=-1)
+            w = F.softmax(top, dim=-1)
+        l64 = synth.bf16_bits_to_f32(xb).astype(np.float64) @ W.astype(np.float64).T
+        if b is not None:
+            l64 = l64 + b.astype(np.float64)
+        err = np.abs(logits.numpy().astype(np.float64) - l64).max(axis=1)
+        srt = -np.sort(-l64, axis=1)[:, : cfg.k + 1]
+        gap = (-np.diff(srt, axis=1)).min(axis=1)
+        out[f"{name}__idx"] = idx.numpy().astype(np.int16)
+        if cfg.score == "softmax":
+            out[f"{name}__w"] = w.numpy().astype(np.float32)
+        out[f"{name}__exempt"] = (gap <= 2 * err)
+        print(f"{name}: {n} tokens, {int(out[name + '__exempt'].sum())} exempt, "
+              f"max fp32 logit error {err.max():.3g}, min gap {gap.min():.3g}")
+    return out
+
+
 def main():
     with open(os.path.join(HERE, "q4_0_kat.json"), "w") as f:
         json.dump({"source": "tests/audit_suite.py:36-41 and gguf_loader.py:369-378 (hand-derived)",
@@ -137,6 +196,7 @@ def main():
     np.savez_compressed(os.path.join(HERE, "permute_t5_k2_e8.npz"), **permute_case(22, 5, 2, 8))
     r = 1 + np.random.default_rng(3).permutation(128)
     np.save(os.path.join(HERE, "zipf_bias_e128_s1.1.npy"), (-1.1 * np.log(r.astype(np.float64))).astype(np.float32))
+    np.savez_compressed(os.path.join(HERE, "router_reference_module.npz"), **reference_module_routing())
     print("fixtures written to", HERE)
 
 

@@ -166,7 +166,10 @@ def test_python_surface_rejects_cpu_tensors():
     import phantom_moe
 
     r = phantom_moe.PhantomTopKRouter(256, 8, 2)
-    with pytest.raises(RuntimeError, match="no CPU path"):
+    with pytest.raises(RuntimeError, match="no CPU path"), torch.no_grad():
+        r(torch.randn(2, 4, 256))
+    # inference only: no silent detach of the gate weight
+    with pytest.raises(RuntimeError, match="no backward"):
         r(torch.randn(2, 4, 256))
     with pytest.raises(TypeError):
         q4_0.repack(torch.zeros(18, dtype=torch.uint8), 16, 32)

@@ -184,6 +184,55 @@ def test_activation_buffer_grows_and_is_reused(dev):
                               f"B={B} Dffn={Dffn}")
 
 
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")  # the refused capture records nothing
+def test_captured_graph_survives_buffer_growth(dev):
+    """A graph that captured sparse_mlp_forward keeps its activation buffer:
+    eager calls use a buffer of their own, and an eager call at a larger size
+    allocates a larger capture buffer without freeing the one the graph holds.
+    A capture at a size no eager call has reserved is refused."""
+    x, wg, bg, wu, bu, wd, idx, cnt = _case(80, 2, 128, 512, 0.5)
+    args = [T(a, dev) for a in (x, wg, bg, wu, bu, wd, idx, cnt)]
+    want = O.lg_sparse_mlp(x, wg, bg, wu, bu, wd, idx, cnt, 50.0)
+    legacy.sparse_mlp_forward(*args, 50.0)  # reserves both buffers at this size
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side), torch.cuda.graph(g, stream=side):
+        y_cap, ms = legacy.sparse_mlp_forward(*args, 50.0)
+    assert ms == 0.0
+    torch.cuda.current_stream(dev).wait_stream(side)
+    g.replay()
+    torch.cuda.synchronize(dev)
+    assert_f16_close_bits(y_cap.cpu().numpy(), want, "first replay")
+    # eager calls in between, the second one larger than anything before
+    y_small, _ = legacy.sparse_mlp_forward(*args, 50.0)
+    assert_f16_close_bits(y_small.cpu().numpy(), want, "eager")
+    xl, wgl, bgl, wul, bul, wdl, idxl, cntl = _case(81, 8, 128, 8192, 0.5)
+    y_big, _ = legacy.sparse_mlp_forward(*[T(a, dev) for a in (xl, wgl, bgl, wul, bul, wdl, idxl, cntl)], 50.0)
+    assert_f16_close_bits(y_big.cpu().numpy(), O.lg_sparse_mlp(xl, wgl, bgl, wul, bul, wdl, idxl, cntl, 50.0),
+                          "eager after growth")
+    y_cap.zero_()
+    g.replay()
+    torch.cuda.synchronize(dev)
+    assert_f16_close_bits(y_cap.cpu().numpy(), want, "replay after growth")
+    # refused: no buffer of this size was reserved outside capture
+    xh, wgh, bgh, wuh, buh, wdh, idxh, cnth = _case(82, 16, 64, 16384, 0.5)
+    huge = [T(a, dev) for a in (xh, wgh, bgh, wuh, buh, wdh, idxh, cnth)]
+    torch.cuda.synchronize(dev)
+    g2 = torch.cuda.CUDAGraph()
+    err = None
+    with torch.cuda.stream(side), torch.cuda.graph(g2, stream=side):
+        try:
+            legacy.sparse_mlp_forward(*huge, 50.0)
+        except RuntimeError as e:
+            err = str(e)
+    assert err is not None and "under stream capture" in err
+    del g2
+    g.replay()
+    torch.cuda.synchronize(dev)
+    assert_f16_close_bits(y_cap.cpu().numpy(), want, "replay after a refused capture")
+
+
 def test_errors_raise_not_exit(dev):
     x, wg, bg, wu, bu, wd, idx, cnt = _case(70, 1, 64, 128, 0.5)
     with pytest.raises(RuntimeError, match="no list position"):

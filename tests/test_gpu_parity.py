@@ -148,10 +148,36 @@ def test_route_full_size_configs(dev, name):
     np.testing.assert_allclose(w.sum(-1).cpu().numpy(), 1.0, atol=1e-5)
 
 
+@pytest.mark.parametrize("name", list(synth.CONFIGS))
+def test_route_matches_reference_module_fixture(dev, name):
+    """The HIP router on a whole benchmark batch against the reference router
+    module's fp32 forward (tests/test_moe_routing.py:65-71) recorded in
+    router_reference_module.npz for its first tokens (all up to 64, 1024 of a
+    prefill batch): equal indices in equal order on every token not marked as
+    within fp32 rounding of a tie, softmax weights to fp32 rounding."""
+    f = load_npz("router_reference_module.npz")
+    cfg = synth.CONFIGS[name]
+    ref_idx = f[f"{name}__idx"].astype(np.int64)
+    ok = ~f[f"{name}__exempt"]
+    n = ref_idx.shape[0]
+    xb = synth.activations(cfg.T, cfg.H)
+    W = synth.router_weight(cfg.E, cfg.H)
+    b = synth.zipf_bias(cfg.E, cfg.zipf) if cfg.zipf else None
+    w, idx = phantom_moe.route(to_bf16_tensor(xb, dev), torch.from_numpy(W).to(dev), cfg.k, cfg.score,
+                               None if b is None else torch.from_numpy(b).to(dev))
+    idx = idx.cpu().numpy()[:n]
+    np.testing.assert_array_equal(idx[ok], ref_idx[ok])
+    if cfg.score == "softmax":
+        np.testing.assert_allclose(w.cpu().numpy()[:n][ok], f[f"{name}__w"][ok], rtol=1e-5, atol=1e-6)
+
+
 def test_router_module_reference_contract(dev):
     """tests/test_moe_routing.py:139-159 on the drop-in module."""
     torch.manual_seed(0)
     router = phantom_moe.PhantomTopKRouter(256, 8, 2).to(dev)
+    with pytest.raises(RuntimeError, match="no backward"):
+        router(torch.randn(2, 4, 256, device=dev))
+    router.gate.weight.requires_grad_(False)
     for dt in (torch.float32, torch.bfloat16):
         x = torch.randn(2, 4, 256, device=dev).to(dt)
         weights, indices = router(x)

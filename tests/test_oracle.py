@@ -190,6 +190,31 @@ def test_router_against_numpy_and_reference_torch_module():
     np.testing.assert_allclose(tw.numpy()[ok], w[ok], rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("name", list(synth.CONFIGS))
+def test_router_matches_reference_module_fixture(name):
+    """The oracle's fp64 selection against the reference router module's fp32
+    forward (F.linear -> topk -> softmax, tests/test_moe_routing.py:65-71)
+    recorded in router_reference_module.npz for every benchmark layer: indices
+    and their order are equal on every token the fixture does not mark as
+    within fp32 rounding of a tie (it marks none of these seeded layers), and
+    the softmax weights agree to fp32 rounding."""
+    f = load_npz("router_reference_module.npz")
+    cfg = synth.CONFIGS[name]
+    ref_idx = f[f"{name}__idx"].astype(np.int64)
+    exempt = f[f"{name}__exempt"]
+    n = ref_idx.shape[0]
+    assert n == min(cfg.T, 1024) and ref_idx.shape[1] == cfg.k
+    xb = synth.activations(cfg.T, cfg.H)[:n]
+    W = synth.router_weight(cfg.E, cfg.H)
+    b = synth.zipf_bias(cfg.E, cfg.zipf) if cfg.zipf else None
+    idx, w = oracle.route(xb, W, cfg.k, cfg.score_mode, b)
+    ok = ~exempt
+    np.testing.assert_array_equal(idx[ok], ref_idx[ok])
+    assert (idx == ref_idx).all(axis=1).mean() == 1.0
+    if cfg.score == "softmax":
+        np.testing.assert_allclose(w[ok], f[f"{name}__w"][ok], rtol=1e-5, atol=1e-6)
+
+
 def test_router_sigmoid_and_bias_closed_form():
     rng = np.random.default_rng(4)
     T, H, E, k = 5, 256, 32, 6
