@@ -14,7 +14,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "_build", "libmoe_oracle.so")
+# PHANTOM_ORACLE_LIB selects another build of the same sources (the sanitized
+# one of `make -C oracle asan`).
+_LIB_PATH = os.environ.get("PHANTOM_ORACLE_LIB") or os.path.join(_HERE, "_build", "libmoe_oracle.so")
 _lib = None
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")

@@ -38,6 +38,20 @@ HIPCC_FLAGS = [
 ]
 
 
+# Host-side AddressSanitizer + UndefinedBehaviorSanitizer for a CPU-only test
+# build (lib/asan/libphantom_moe.so): the C-ABI validation, planning and error
+# paths run instrumented; device code is compiled as usual.  Each flag applies
+# to the host pass only.
+SANITIZE_FLAGS = [
+    "-Xarch_host", "-fsanitize=address",
+    "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-sanitize-recover=undefined",
+    "-Xarch_host", "-fno-omit-frame-pointer",
+    "-Xarch_host", "-g",
+]
+SANITIZE_LINK_FLAGS = ["-shared-libsan"]
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
         if cand and (os.path.sep not in cand or os.path.exists(cand)):
@@ -45,20 +59,22 @@ def hipcc() -> str:
     return "hipcc"
 
 
-def _compile(src: str, obj: str) -> None:
-    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+def _compile(src: str, obj: str, extra: tuple = ()) -> None:
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"] + list(extra)
     cmd = [hipcc(), *flags, f"-I{INCLUDE}", f"-I{CSRC}", "-c", os.path.join(CSRC, src), "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{res.stderr}")
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, sanitize: bool = False) -> str:
     """Compile all HIP sources (one hipcc per source, in parallel) and link
-    them into lib/libphantom_moe.so; returns its path."""
+    them into lib/libphantom_moe.so (with ``sanitize``: the host-sanitized
+    lib/asan/libphantom_moe.so); returns its path."""
     from concurrent.futures import ThreadPoolExecutor
 
-    out_dir = os.path.join(PKG_DIR, "lib")
+    out_dir = os.path.join(PKG_DIR, "lib", "asan") if sanitize else os.path.join(PKG_DIR, "lib")
+    extra = tuple(SANITIZE_FLAGS) if sanitize else ()
     os.makedirs(out_dir, exist_ok=True)
     out = os.path.join(out_dir, "libphantom_moe.so")
     fd, tmp = tempfile.mkstemp(prefix="libphantom_moe.", suffix=".so.tmp", dir=out_dir)
@@ -68,8 +84,8 @@ def build(verbose: bool = False) -> str:
         jobs = max(1, min(len(SOURCES), len(os.sched_getaffinity(0)), 8))
         try:
             with ThreadPoolExecutor(max_workers=jobs) as pool:
-                list(pool.map(_compile, SOURCES, objs))
-            cmd = [hipcc(), *HIPCC_FLAGS, *objs, "-o", tmp]
+                list(pool.map(_compile, SOURCES, objs, [extra] * len(SOURCES)))
+            cmd = [hipcc(), *HIPCC_FLAGS, *extra, *(SANITIZE_LINK_FLAGS if sanitize else []), *objs, "-o", tmp]
             res = subprocess.run(cmd, capture_output=True, text=True)
             if res.returncode != 0:
                 raise RuntimeError(f"hipcc link failed ({res.returncode}):\n{' '.join(cmd)}\n{res.stderr}")
@@ -80,3 +96,9 @@ def build(verbose: bool = False) -> str:
             if os.path.exists(tmp):
                 os.unlink(tmp)
     return out
+
+
+if __name__ == "__main__":
+    import sys
+
+    print(build(verbose=True, sanitize="--sanitize" in sys.argv[1:]))

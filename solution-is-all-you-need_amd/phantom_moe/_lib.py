@@ -19,7 +19,9 @@ import threading
 import torch  # noqa: F401  (must precede the CDLL, see module docstring)
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
-LIB_PATH = os.path.join(LIB_DIR, "libphantom_moe.so")
+# PHANTOM_MOE_LIB selects another build of the same sources (the host-sanitized
+# lib/asan/libphantom_moe.so of ``python -m phantom_moe._build --sanitize``).
+LIB_PATH = os.environ.get("PHANTOM_MOE_LIB") or os.path.join(LIB_DIR, "libphantom_moe.so")
 
 # Function name -> (restype, argtypes).  Mirrors include/phantom_moe.h and
 # include/phantom_legacy.h.
