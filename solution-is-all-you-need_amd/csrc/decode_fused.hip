@@ -423,6 +423,7 @@ template <int T_, int H_, int I_, int E_, int K_, int SH_>
 __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
   __shared__ int s_sel_idx[kFusedMaxSlots];
   __shared__ float s_sel_w[kFusedMaxSlots];
+  __shared__ double s_sel_v[kMaxTopK];  // one token: the selected logits in slot order
   __shared__ int s_slot_pos[kFusedMaxSlots];
   __shared__ int s_seg_tok[kFusedMaxSlots + kFusedMaxT];
   __shared__ int s_seg_e[kFusedMaxSlots + 1];
@@ -590,9 +591,11 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
   // it in the order of wave_topk_row: value descending, NaN last, ties to the
   // lower index), P threads per logit over E/P keys each; rank r < k is slot
   // r.  Then wave 0 takes the winners to their slots and segments (experts
-  // ascending) while wave 1 computes the weights exactly as wave_topk_row
-  // does, so the selection, its order and the weights equal the staged
-  // router's bit for bit.
+  // ascending) while wave 1 gathers the selected logits in slot order; the
+  // weights (only the combine and the routing outputs need them) are
+  // computed after the weight copies are issued, exactly as wave_topk_row
+  // computes them, so the selection, its order and the weights equal the
+  // staged router's bit for bit.
   if (T == 1 && !route_failed) {
     int P = 1;
     while (2 * P * E <= kFThreads) P *= 2;
@@ -650,27 +653,9 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
         s_nseg = k + (has_sh ? 1 : 0);
       }
     } else if (w == 1) {
-      char* tk = rs + rl.topk + (uint32_t)w * rl.topk_wave;
-      double* s_val = reinterpret_cast<double*>(tk + 16 * k);
-      double* s_e = reinterpret_cast<double*>(tk + 24 * k);
       for (int e = lane; e < E; e += kWave) {
         const int r = s_rank[e];
-        if (r < k) s_val[r] = s_lv[e];
-      }
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      double ej = 0.0;
-      if (lane < k) {
-        const double v = s_val[lane];
-        ej = (a.score_mode == 0) ? exp(v - s_val[0]) : 1.0 / (1.0 + exp(-v));
-        s_e[lane] = ej;
-      }
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      if (lane < k) {
-        double sum = 0.0;
-        for (int i = 0; i < k; ++i) sum += s_e[i];
-        s_sel_w[lane] = (float)(ej / sum);
+        if (r < k) s_sel_v[r] = s_lv[e];
       }
     }
     lds_barrier();
@@ -842,10 +827,26 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
   if (ng == 0) issue_down();
 
   // ---- 4. routing outputs and the combine's tables, while the copies land ----
+  if (T == 1 && !route_failed && w == 1) {
+    // one token's weights (softmax over the selected logits, or sigmoid
+    // renormalised), summed in slot order as wave_topk_row sums them
+    double ej = 0.0;
+    if (lane < k) {
+      const double v = s_sel_v[lane];
+      ej = (a.score_mode == 0) ? exp(v - s_sel_v[0]) : 1.0 / (1.0 + exp(-v));
+    }
+    double sum = 0.0;
+    for (int i = 0; i < k; ++i) sum += __shfl(ej, i, kWave);
+    if (lane < k) {
+      const float wt = (float)(ej / sum);
+      s_sel_w[lane] = wt;
+      if (b == 0) a.topk_w[lane] = wt;
+    }
+  }
   if (b == 0)
     for (int i = threadIdx.x; i < T * k; i += kFThreads) {
       a.topk_idx[i] = route_failed ? -1 : s_sel_idx[i];
-      a.topk_w[i] = route_failed ? __builtin_nanf("") : s_sel_w[i];
+      if (T > 1 || route_failed) a.topk_w[i] = route_failed ? __builtin_nanf("") : s_sel_w[i];
     }
   // the combine's tables: slot s at position pos of segment u reads part pt
   // of output row nn at (beg * KqI + pt * cnt + pos - beg) * 16 + nn, u's
