@@ -128,7 +128,7 @@ PHANTOM_MOE_API size_t phantom_moe_workspace_bytes(int64_t T, int64_t H, int64_t
 /* Status bits that the single-launch decode path left in this workspace
  * (0: every call since the last query completed normally; bit 0: a
  * workgroup gave up waiting for the router logits, bit 1 for the gate/up
- * results, bit 2 for every workgroup to start).  A call that sets a bit
+ * results or the down partials, bit 2 for every workgroup to start).  A call that sets a bit
  * also writes NaN to the outputs it could not compute.  Waits for the
  * stream, clears the bits, and must not be captured into a graph.  No
  * counterpart in the reference, whose errors exit the process
@@ -137,7 +137,8 @@ PHANTOM_MOE_API int phantom_moe_workspace_status(void* workspace, size_t workspa
                                                  hipStream_t stream);
 
 /* Library options (process-wide; initialised from the environment on first
- * use: PHANTOM_MOE_DECODE=staged, PHANTOM_MOE_DECODE_KSPLIT=1).  A/B and
+ * use: PHANTOM_MOE_DECODE=staged, PHANTOM_MOE_DECODE_KSPLIT=1,
+ * PHANTOM_MOE_DECODE_X8=0).  A/B and
  * test switches with no counterpart in the reference. */
 #define PHANTOM_MOE_OPT_DECODE_FUSED 1 /* 1: decode batches that fit take the single-launch path (default) */
 #define PHANTOM_MOE_OPT_DECODE_KSPLIT 2 /* 1: staged decode expert stages always as the K-split kernels (default 0) */
@@ -146,6 +147,10 @@ PHANTOM_MOE_API int phantom_moe_workspace_status(void* workspace, size_t workspa
  * bit 1 the gate/up wait, expect a tag nobody writes, so it gives up after
  * FUSED_WAIT_POLLS polls (every wave still exits; outputs NaN, status set). */
 #define PHANTOM_MOE_OPT_FUSED_FAULT 4
+/* 1: a batch-1, top-8 decode without a shared expert (compiled for H 2048,
+ * I 768, E 128) runs with expert slot j on XCD j of an 8-XCD, 256-CU part
+ * (default); 0: in the generic single-launch kernel. */
+#define PHANTOM_MOE_OPT_DECODE_X8 5
 PHANTOM_MOE_API int phantom_moe_set_option(int option, int value);
 PHANTOM_MOE_API int phantom_moe_get_option(int option, int* value);
 

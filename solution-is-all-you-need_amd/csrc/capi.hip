@@ -82,6 +82,8 @@ LibConfig config_from_env() {
   c.decode_fused = !(d && strcmp(d, "staged") == 0);
   const char* k = getenv("PHANTOM_MOE_DECODE_KSPLIT");
   c.force_ksplit = k && strcmp(k, "1") == 0;
+  const char* x8 = getenv("PHANTOM_MOE_DECODE_X8");
+  c.decode_x8 = !(x8 && strcmp(x8, "0") == 0);
   c.fused_wait_polls = kFusedWaitPollsDefault;
   c.fused_fault = 0;
   return c;
@@ -118,6 +120,7 @@ Tuning tuning_from_env() {
 // they are read once per call.  The environment is read once, on first use.
 std::atomic<int> g_opt_fused{1};
 std::atomic<int> g_opt_ksplit{0};
+std::atomic<int> g_opt_x8{1};
 std::atomic<uint32_t> g_opt_polls{kFusedWaitPollsDefault};
 std::atomic<uint32_t> g_opt_fault{0};
 std::once_flag g_opt_once;
@@ -128,6 +131,7 @@ void init_options() {
     const LibConfig c = config_from_env();
     g_opt_fused.store(c.decode_fused ? 1 : 0);
     g_opt_ksplit.store(c.force_ksplit ? 1 : 0);
+    g_opt_x8.store(c.decode_x8 ? 1 : 0);
     g_opt_polls.store(c.fused_wait_polls);
     g_opt_fault.store(c.fused_fault);
     g_tuning = tuning_from_env();
@@ -141,6 +145,7 @@ LibConfig lib_config() {
   LibConfig c;
   c.decode_fused = g_opt_fused.load(std::memory_order_relaxed) != 0;
   c.force_ksplit = g_opt_ksplit.load(std::memory_order_relaxed) != 0;
+  c.decode_x8 = g_opt_x8.load(std::memory_order_relaxed) != 0;
   c.fused_wait_polls = g_opt_polls.load(std::memory_order_relaxed);
   c.fused_fault = g_opt_fault.load(std::memory_order_relaxed);
   return c;
@@ -150,6 +155,7 @@ void set_lib_config(const LibConfig& c) {
   init_options();
   g_opt_fused.store(c.decode_fused ? 1 : 0);
   g_opt_ksplit.store(c.force_ksplit ? 1 : 0);
+  g_opt_x8.store(c.decode_x8 ? 1 : 0);
   g_opt_polls.store(c.fused_wait_polls);
   g_opt_fault.store(c.fused_fault);
 }
@@ -184,11 +190,17 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
   // single-launch path writes; its own regions follow when the shape takes it.
   const size_t o_ctl = take(kCtlBytes);
   const bool fused = I > 0 && fused_shape_ok(T, H, I, E, k, has_shared);
-  size_t o_pres = 0, o_slots = 0, o_hv = 0;
+  size_t o_pres = 0, o_slots = 0, o_hv = 0, o_xsl = 0, o_xh = 0, o_xpt = 0;
+  const bool x8 = fused && x8_shape(T, H, I, E, k, has_shared);
   if (fused) {
     o_pres = take(sizeof(uint64_t) * (size_t)kFusedMaxGrid);
     o_slots = take((size_t)16 * (size_t)(T * E));
     o_hv = take((size_t)16 * (size_t)((T * k + T) * (I / 2)));
+  }
+  if (x8) {
+    o_xsl = take((size_t)16 * 8 * (size_t)E);
+    o_xh = take((size_t)16 * 8 * (size_t)(I / 2));
+    o_xpt = take((size_t)16 * 8 * (size_t)(H / 2));
   }
   const size_t o_log = take(sizeof(double) * (size_t)(T * E));
   // x operand rows 0..T-1 plus an all-zero row T
@@ -223,6 +235,11 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
       ws->fused.presence = reinterpret_cast<uint64_t*>(b + o_pres);
       ws->fused.slots = reinterpret_cast<uint32_t*>(b + o_slots);
       ws->fused.hv = reinterpret_cast<uint32_t*>(b + o_hv);
+    }
+    if (x8) {
+      ws->fused.xslots = reinterpret_cast<uint32_t*>(b + o_xsl);
+      ws->fused.xh = reinterpret_cast<uint32_t*>(b + o_xh);
+      ws->fused.xpart = reinterpret_cast<uint32_t*>(b + o_xpt);
     }
     ws->logits = reinterpret_cast<double*>(b + o_log);
     ws->xq = reinterpret_cast<uint16_t*>(b + o_xq);
@@ -432,8 +449,10 @@ const char* phantom_moe_version(void) { return "phantom_moe 0.1.0 gfx950"; }
 const char* phantom_moe_expert_kernels(int64_t T, int64_t H, int64_t I, int E, int top_k, int has_shared) {
   static thread_local char buf[96];
   const char *gu, *dn;
-  if (pmoe::fused_plan(T, H, I, E, top_k, has_shared ? 1 : 0).ok) {
-    gu = dn = "moe_decode_fused_kernel";  // the whole layer is one launch
+  const pmoe::FusedPlan fp = pmoe::fused_plan(T, H, I, E, top_k, has_shared ? 1 : 0);
+  if (fp.ok) {
+    // the whole layer is one launch
+    gu = dn = fp.spec == pmoe::kFusedSpecX8 ? "moe_decode_x8_kernel" : "moe_decode_fused_kernel";
   } else if (pmoe::gemm_regime(T, top_k, E)) {
     gu = "gemm_gate_up_kernel";
     dn = "gemm_down_kernel";
@@ -521,6 +540,10 @@ int phantom_moe_set_option(int option, int value) {
       if (value < 0 || value > 3) return fail(PHANTOM_MOE_EINVAL, "FUSED_FAULT takes 0..3, got %d", value);
       c.fused_fault = (uint32_t)value;
       break;
+    case PHANTOM_MOE_OPT_DECODE_X8:
+      if (value != 0 && value != 1) return fail(PHANTOM_MOE_EINVAL, "DECODE_X8 takes 0 or 1, got %d", value);
+      c.decode_x8 = value != 0;
+      break;
     default:
       return fail(PHANTOM_MOE_EINVAL, "unknown option %d", option);
   }
@@ -536,6 +559,7 @@ int phantom_moe_get_option(int option, int* value) {
     case PHANTOM_MOE_OPT_DECODE_KSPLIT: *value = c.force_ksplit ? 1 : 0; break;
     case PHANTOM_MOE_OPT_FUSED_WAIT_POLLS: *value = (int)c.fused_wait_polls; break;
     case PHANTOM_MOE_OPT_FUSED_FAULT: *value = (int)c.fused_fault; break;
+    case PHANTOM_MOE_OPT_DECODE_X8: *value = c.decode_x8 ? 1 : 0; break;
     default: return fail(PHANTOM_MOE_EINVAL, "unknown option %d", option);
   }
   return ok();

@@ -1152,6 +1152,596 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
 
 }  // namespace
 
+// ---------------------------------------------- batch 1, top-8, one XCD a slot
+//
+// One token with eight routed experts and no shared expert on an 8-XCD part
+// (the batch-1 Qwen3-30B-A3B-shaped layer).  Selected expert j (slot j of
+// the top-k order) runs entirely on XCD j, on the 32 workgroups the
+// dispatcher places there.  It deals workgroups to the XCDs round-robin, so
+// b, b + 8, b + 16, ... share an XCD, but the XCD the deal starts on varies
+// between launches (graph replays start elsewhere than eager launches): each
+// workgroup reads its XCD from the hardware XCC_ID register and takes
+// b / 8 as its rank on it.  Every hand-off but the last then stays inside
+// one XCD's L2 and moves a few KB:
+//   0. Each XCD computes all E logits itself (E / 32 per workgroup, one per
+//      wave, the router's fixed-order fp64 contract) and publishes them in
+//      its own slot array with plain stores, which land in the XCD's L2; one
+//      wave per workgroup polls them with L1-bypassing loads.  (In the
+//      generic kernel 256 workgroups poll one device-scope slot array, and
+//      the last poll ends about 2 us after the last logit is stored.)
+//   1. Ranks and weights exactly as the generic kernel computes them.
+//   2. The workgroup's weight copies, every wave its own share: gate/up in
+//      half tiles (8 rows of I of gate and the same 8 rows of up make one
+//      MFMA B operand, so the 96 half tiles of an expert are 3 per
+//      workgroup) over the 16 quads of H, then 4 row tiles of H of down over
+//      all of I.
+//   3. Gate/up as the generic kernel computes it (bf16 offset operands, the
+//      offset by one fp32 MFMA), the 8 waves' K-split partials summed in wave
+//      order, SwiGLU, and h stored to the XCD's L2 as tagged units
+//      {hi(i) | hi(i+1), tag, lo(i) | lo(i+1), ~tag}.
+//   4. With its down weights already expanded into registers, every
+//      workgroup polls the I / 2 h units of its XCD into the down operand
+//      (MFMA rows 0 and 1 = fp16 hi and lo of h).
+//   5. Down rows [64 rho, 64 rho + 64) of slot j's expert (rho = b / 8); the
+//      partial outputs go out device-scope as tagged units, and workgroup
+//      (j, rho) combines rows 64 rho + 8 j .. + 8 over the 8 slots in slot
+//      order, y = sum_j w_j d_j: the only cross-XCD hand-off.
+// A workgroup that gives up a wait still publishes what the others wait for
+// (NaN values), so a failure costs one bounded wait, sets a status bit and
+// leaves NaN in the outputs it touches.
+namespace {
+
+constexpr int kX8Xcds = 8;
+constexpr int kX8Grid = 256;
+constexpr int kX8PerXcd = kX8Grid / kX8Xcds;
+constexpr uint32_t kX8Chunk = 1152;  // 1 KiB of nibbles + 128 B of scales
+// Cache policy of a poll of data another CU of this XCD stored: SC0 (not
+// served by this CU's L1; this XCD's L2 holds the latest copy), with the
+// intrinsic's volatile bit as in kDevicePoll.
+constexpr int kXcdPoll = 1 | (int)0x80000000u;
+
+struct X8K {
+  const uint16_t* x;
+  const float* W;
+  const float* bias;
+  int score_mode;
+  const uint8_t* gate_nib;
+  const uint16_t* gate_sc;
+  const uint8_t* up_nib;
+  const uint16_t* up_sc;
+  const uint8_t* down_nib;
+  const uint16_t* down_sc;
+  float* y;
+  int32_t* topk_idx;
+  float* topk_w;
+  uint32_t* ctl;
+  uint64_t* presence;
+  uint32_t* xslots;  // [8][E][4] tagged logits, one array per XCD
+  uint32_t* xh;      // [8][I / 2][4] tagged h units
+  uint32_t* xpart;   // [8][H / 2][4] tagged down partials (device scope)
+  uint32_t wait_polls;
+  uint32_t skew_route;
+  uint32_t skew_h;
+};
+
+// The nibble expansions of dequant_unit_bf16 and dequant_unit_f16s as plain
+// expressions.  Instructions written in inline assembly are invisible to the
+// compiler's hazard checks, and this kernel keeps one element of its MFMA
+// results (the token's row), so the compiler reuses the other elements'
+// registers right after an MFMA issues: an inline-assembly write there is
+// not held back, and the MFMA's own later write of that register then
+// clobbers it (seen as wrong, run-to-run varying gate/up sums).
+__device__ inline u32x4 x8_dequant_bf16(uint32_t w) {
+  u32x4 r;
+  r.x = ((w << 3) & 0x00780078u) | 0x3F803F80u;
+  r.y = ((w >> 1) & 0x00780078u) | 0x3F803F80u;
+  r.z = ((w >> 5) & 0x00780078u) | 0x3F803F80u;
+  r.w = ((w >> 9) & 0x00780078u) | 0x3F803F80u;
+  return r;
+}
+__device__ inline uint32_t x8_nib_pair_f16s(uint32_t w) {
+  const f16x2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, (w & 0x000F000Fu) | 0x64006400u) + off);
+}
+__device__ inline u32x4 x8_dequant_f16s(uint32_t w) {
+  u32x4 r;
+  r.x = x8_nib_pair_f16s(w);
+  r.y = x8_nib_pair_f16s(w >> 4);
+  r.z = x8_nib_pair_f16s(w >> 8);
+  r.w = x8_nib_pair_f16s(w >> 12);
+  return r;
+}
+
+constexpr int x8_rank_threads(int E) {
+  int P = 1;
+  while (2 * P * E <= kFThreads) P *= 2;
+  return P;
+}
+
+// Dynamic LDS layout (bytes).
+template <int H, int I, int E>
+struct X8Lds {
+  static constexpr int Kq = H / kQuad, KqI = I / kQuad;
+  static constexpr int htPer = I / 8 / kX8PerXcd;         // gate/up half tiles per workgroup
+  static constexpr int qPerW = Kq / kFW;                  // quads of H per wave and half tile
+  static constexpr int GU = htPer * qPerW;                // gate/up (half tile, quad) pairs per wave
+  static constexpr int tdPer = H / kRowTile / kX8PerXcd;  // down row tiles per workgroup
+  static constexpr int DN = KqI / 2;                      // down (tile, quad) pairs per wave
+  static constexpr uint32_t xop = 0;                      // [Kq][4 p][4 gi] x 16 B
+  static constexpr uint32_t xs = xop + Kq * 256;          // [Kq][4] fp32 group sums
+  static constexpr uint32_t gu = xs + Kq * 16;            // [8 waves][GU] chunks
+  static constexpr uint32_t dn = gu + kFW * GU * kX8Chunk;  // [8 waves][DN] chunks
+  static constexpr uint32_t hop = dn + kFW * DN * kX8Chunk; // [KqI][4 p][4 gi][hi, lo] x 16 B
+  static constexpr uint32_t gred = hop + KqI * 512;         // [8 waves][htPer][16] fp32
+  static constexpr uint32_t dred = gred + kFW * htPer * 64; // [8 waves][16] fp32
+  static constexpr uint32_t lv = dred + kFW * 64;           // [E] fp64 logits
+  static constexpr uint32_t key = lv + E * 8;               // [E] order keys
+  static constexpr uint32_t rank = key + E * 8;             // [E] ranks
+  static constexpr uint32_t bytes = rank + E * 4;
+};
+
+template <int H_, int I_, int E_>
+__global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
+  constexpr int H = H_, I = I_, E = E_, K = kX8Xcds;
+  using L = X8Lds<H, I, E>;
+  constexpr int Kq = L::Kq, KqI = L::KqI, htPer = L::htPer, qPerW = L::qPerW, GU = L::GU, tdPer = L::tdPer,
+                DN = L::DN;
+  constexpr int LPW = E / kX8PerXcd;      // logits per workgroup
+  constexpr int yRows = H / kX8Grid;      // rows of y each workgroup combines
+  constexpr int P = x8_rank_threads(E);  // threads per logit in the ranking
+  static_assert(H % (kQuad * kFW) == 0 && I % (8 * kX8PerXcd) == 0 && H % (kRowTile * kX8PerXcd) == 0 &&
+                    I % kQuad == 0,
+                "whole quads of H per wave, whole half tiles and row tiles per workgroup");
+  static_assert(tdPer * 2 == kFW && KqI % 2 == 0, "down: two waves per row tile, half of I each");
+  static_assert(tdPer * kRowTile == kWave, "one partial row per lane of wave 0");
+  static_assert(E % kX8PerXcd == 0 && LPW < kFW - 1 && E % kWave == 0 && E * P <= kFThreads, "logits");
+  static_assert(htPer * 8 <= kWave && I / 2 <= kFThreads && yRows * K / 2 <= kWave && yRows <= kWave, "lanes");
+  static_assert(GU * 4 + DN * 2 <= 47, "vmcnt");
+  static_assert(L::bytes <= kFusedDynLdsMax, "LDS");
+
+  __shared__ int s_sel_idx[K];
+  __shared__ double s_sel_v[K];
+  __shared__ float s_sel_w[K];
+  __shared__ int s_pfail, s_hfail;
+  extern __shared__ u32x4 s_dyn[];
+  char* lds = reinterpret_cast<char*>(s_dyn);
+  u32x4* s_xop = reinterpret_cast<u32x4*>(lds + L::xop);
+  float* s_xs = reinterpret_cast<float*>(lds + L::xs);
+  char* s_hop = lds + L::hop;
+  float* s_gred = reinterpret_cast<float*>(lds + L::gred);
+  float* s_dred = reinterpret_cast<float*>(lds + L::dred);
+  double* s_lv = reinterpret_cast<double*>(lds + L::lv);
+  uint64_t* s_key = reinterpret_cast<uint64_t*>(lds + L::key);
+  int* s_rank = reinterpret_cast<int*>(lds + L::rank);
+
+  const int lane = threadIdx.x % kWave;
+  const int w = uni(threadIdx.x / kWave);
+  const int n = lane % 16;
+  const int p = lane / 16;
+  const int b = (int)blockIdx.x;
+  const int xcd = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 0x7u);  // HW_REG_XCC_ID, bits 2:0
+  const int rho = b / kX8Xcds;
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+
+  // ---- 0. generation; this XCD's logits; x operand -------------------------
+  const uint32_t tag =
+      (uint32_t)uni((int)__hip_atomic_load(&a.ctl[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) + 1u;
+  if (threadIdx.x == 0) s_hfail = 0;
+  const BufRsrc sl_r = buf_rsrc(a.xslots + (size_t)xcd * E * 4, (uint32_t)(E * 16));
+  if (w < LPW) {
+    const int e = rho * LPW + w;
+    double logit = fixed_dot_bf16(a.x, a.W + (int64_t)e * H, H);
+    if (a.bias) logit = logit + (double)a.bias[e];
+    if (lane == 0) {
+      const uint64_t bits = __builtin_bit_cast(uint64_t, logit);
+      u32x4 v;
+      v.x = (uint32_t)bits;
+      v.y = tag;
+      v.z = (uint32_t)(bits >> 32);
+      v.w = ~tag;
+      __builtin_amdgcn_raw_buffer_store_b128(v, sl_r, e * 16, 0, 0);  // into this XCD's L2
+    }
+  } else if (w == LPW) {
+    // the MFMA-ordered x operand and its group sums, as the generic kernel
+    // builds them: one lane per (quad, group)
+    for (int j = lane; j < Kq * 4; j += kWave) {
+      const int q = j / 4, gi = j % 4;
+      const uint16_t* xr = a.x + (int64_t)(4 * q + gi) * kGroup;
+      float sp[4];
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        const uint2 lo = *reinterpret_cast<const uint2*>(xr + 4 * pp);
+        const uint2 hi = *reinterpret_cast<const uint2*>(xr + 16 + 4 * pp);
+        u32x4 v;
+        v.x = (lo.x & 0xffffu) | (lo.y << 16);
+        v.y = (hi.x & 0xffffu) | (hi.y << 16);
+        v.z = (lo.x >> 16) | (lo.y & 0xffff0000u);
+        v.w = (hi.x >> 16) | (hi.y & 0xffff0000u);
+        s_xop[(q * 4 + pp) * 4 + gi] = v;
+        sp[pp] = ((bf16_bits_to_float(lo.x & 0xffffu) + bf16_bits_to_float(lo.x >> 16)) +
+                  (bf16_bits_to_float(lo.y & 0xffffu) + bf16_bits_to_float(lo.y >> 16))) +
+                 ((bf16_bits_to_float(hi.x & 0xffffu) + bf16_bits_to_float(hi.x >> 16)) +
+                  (bf16_bits_to_float(hi.y & 0xffffu) + bf16_bits_to_float(hi.y >> 16)));
+      }
+      s_xs[q * 4 + gi] = (sp[0] + sp[1]) + (sp[2] + sp[3]);
+    }
+  } else if (w == kFW - 1) {
+    // ---- 1. poll this XCD's E logits into LDS
+    const uint32_t want = tag + a.skew_route;
+    constexpr int kNV = E / kWave;
+    bool done[kNV];
+#pragma unroll
+    for (int v = 0; v < kNV; ++v) done[v] = false;
+    bool failed = false;
+    for (uint32_t it = 0;; ++it) {
+      poll_clobber();
+      u32x4 sv[kNV];
+#pragma unroll
+      for (int v = 0; v < kNV; ++v)
+        if (!done[v]) sv[v] = __builtin_amdgcn_raw_buffer_load_b128(sl_r, (lane + v * kWave) * 16, 0, kXcdPoll);
+      bool all = true;
+#pragma unroll
+      for (int v = 0; v < kNV; ++v) {
+        if (!done[v] && tag_ok(sv[v], want)) {
+          const double lv = __builtin_bit_cast(double, ((uint64_t)sv[v].z << 32) | sv[v].x);
+          s_lv[lane + v * kWave] = lv;
+          s_key[lane + v * kWave] = logit_key(lv);
+          done[v] = true;
+        }
+        all = all && done[v];
+      }
+      if (__all(all)) break;
+      if (it >= a.wait_polls) {
+        failed = true;
+        if (lane == 0) set_status(a.ctl, kStatusRouteWait);
+        break;
+      }
+    }
+    for (int e = lane; e < E; e += kWave) s_rank[e] = 0;
+    if (lane == 0) s_pfail = failed ? 1 : 0;
+  }
+  lds_barrier();  // every wave has read the generation; logits, ranks zeroed, x operand in LDS
+  if (threadIdx.x == 0) __hip_atomic_store(&a.presence[b], tag64(tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const bool route_failed = uni(s_pfail) != 0;
+
+  // ranks (the number of logits before each in wave_topk_row's order: value
+  // descending, NaN last, ties to the lower index), P threads per logit;
+  // rank r < K is slot r
+  if (!route_failed) {
+    constexpr int span = (E + P - 1) / P;
+    if ((int)threadIdx.x < E * P) {
+      const int pp = (int)threadIdx.x / E;
+      const int e = (int)threadIdx.x - pp * E;
+      const uint64_t ke = s_key[e];
+      const int j0 = pp * span;
+      const int j1 = j0 + span < E ? j0 + span : E;
+      int cnt = 0;
+      int j = j0;
+      for (; j + 8 <= j1; j += 8) {
+        uint64_t kk[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) kk[q] = s_key[j + q];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) cnt += (kk[q] > ke || (kk[q] == ke && j + q < e)) ? 1 : 0;
+      }
+      for (; j < j1; ++j) {
+        const uint64_t kj = s_key[j];
+        cnt += (kj > ke || (kj == ke && j < e)) ? 1 : 0;
+      }
+      if (P == 1) s_rank[e] = cnt;
+      else atomicAdd(&s_rank[e], cnt);
+    }
+    lds_barrier();
+    if (w == 0) {
+      for (int e = lane; e < E; e += kWave) {
+        const int r = s_rank[e];
+        if (r < K) s_sel_idx[r] = e;
+      }
+    } else if (w == 1) {
+      for (int e = lane; e < E; e += kWave) {
+        const int r = s_rank[e];
+        if (r < K) s_sel_v[r] = s_lv[e];
+      }
+    }
+    lds_barrier();
+  }
+  const int ex = route_failed ? 0 : uni(s_sel_idx[xcd]);  // this XCD's expert
+
+  // ---- 2. this wave's weight copies ------------------------------------------
+  // gate/up pair c = i * qPerW + qq: half tile ht = htPer * rho + i (rows
+  // 8 ht .. 8 ht + 7 of I: row tile ht / 2, half ht % 2), quad qPerW * w + qq.
+  // A chunk holds the gate half's 32 operand units, the up half's, then
+  // their scales; lane (n, p) of the B operand reads unit 8p + n % 8 of the
+  // gate half for n < 8 and of the up half for n >= 8.  Down pair c: row
+  // tile tdPer * rho + w / 2, quad DN * (w % 2) + c.
+  const uint32_t s_gu = lds_addr(lds + L::gu) + (uint32_t)w * GU * kX8Chunk;
+  const uint32_t s_dn = lds_addr(lds + L::dn) + (uint32_t)w * DN * kX8Chunk;
+  const char* gu_w = lds + L::gu + w * GU * kX8Chunk;
+  const char* dn_w = lds + L::dn + w * DN * kX8Chunk;
+  if (!route_failed) {
+    constexpr uint32_t gnib = (uint32_t)I * Kq * 64u, gsc = (uint32_t)I * Kq * 8u;
+    constexpr uint32_t dnib = (uint32_t)H * KqI * 64u, dsc = (uint32_t)H * KqI * 8u;
+    const i32x4 gn = buf_rsrc_words(a.gate_nib + (size_t)ex * gnib, gnib);
+    const i32x4 un = buf_rsrc_words(a.up_nib + (size_t)ex * gnib, gnib);
+    const i32x4 gs = buf_rsrc_words(reinterpret_cast<const char*>(a.gate_sc) + (size_t)ex * gsc, gsc);
+    const i32x4 us = buf_rsrc_words(reinterpret_cast<const char*>(a.up_sc) + (size_t)ex * gsc, gsc);
+    const i32x4 dn = buf_rsrc_words(a.down_nib + (size_t)ex * dnib, dnib);
+    const i32x4 ds = buf_rsrc_words(reinterpret_cast<const char*>(a.down_sc) + (size_t)ex * dsc, dsc);
+#pragma unroll
+    for (int c = 0; c < GU; ++c) {
+      const int ht = htPer * rho + c / qPerW;
+      const int q = qPerW * w + c % qPerW;
+      const uint32_t tq = (uint32_t)uni((ht / 2) * Kq + q);
+      const uint32_t slot = s_gu + (uint32_t)c * kX8Chunk;
+      if (lane < 32) {
+        // unit 8p + r of the half: row 8 (ht % 2) + r, part p of the 1 KiB unit
+        const uint32_t nv = (uint32_t)(16 * (lane / 8) + 8 * (ht % 2) + lane % 8) * 16u;
+        dma_b128_unseen(gn, slot, nv, tq * kQuadNibBytes);
+        dma_b128_unseen(un, slot + 512u, nv, tq * kQuadNibBytes);
+      }
+      if (lane < 4) {
+        const uint32_t sv = (uint32_t)(64 * (ht % 2) + 16 * lane);
+        dma_b128_unseen(gs, slot + 1024u, sv, tq * 128u);
+        dma_b128_unseen(us, slot + 1088u, sv, tq * 128u);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < DN; ++c) {
+      const uint32_t tq = (uint32_t)uni((tdPer * rho + w / 2) * KqI + DN * (w % 2) + c);
+      const uint32_t slot = s_dn + (uint32_t)c * kX8Chunk;
+      dma_b128_unseen(dn, slot, (uint32_t)lane * 16u, tq * kQuadNibBytes);
+      if (lane < 8) dma_b128_unseen(ds, slot + 1024u, (uint32_t)lane * 16u, tq * 128u);
+    }
+  }
+
+  // ---- routing outputs, while the copies land --------------------------------
+  if (!route_failed && w == 1) {
+    // softmax over the selected logits (or sigmoid renormalised), summed in
+    // slot order as wave_topk_row sums them
+    double ej = 0.0;
+    if (lane < K) {
+      const double v = s_sel_v[lane];
+      ej = (a.score_mode == 0) ? exp(v - s_sel_v[0]) : 1.0 / (1.0 + exp(-v));
+    }
+    double sum = 0.0;
+    for (int i = 0; i < K; ++i) sum += __shfl(ej, i, kWave);
+    if (lane < K) {
+      const float wt = (float)(ej / sum);
+      s_sel_w[lane] = wt;
+      if (b == 0) a.topk_w[lane] = wt;
+    }
+  }
+  if (b == 0 && threadIdx.x < K) {
+    a.topk_idx[threadIdx.x] = route_failed ? -1 : s_sel_idx[threadIdx.x];
+    if (route_failed) a.topk_w[threadIdx.x] = __builtin_nanf("");
+  }
+
+  // ---- 3. gate/up ---------------------------------------------------------------
+  if (!route_failed) {
+    f32x4 ag[htPer], cg[htPer];
+#pragma unroll
+    for (int i = 0; i < htPer; ++i) ag[i] = cg[i] = z;
+    // only lane row 0 (the token) reads the x operand; the other rows stay
+    // zero (an MFMA row of A feeds only the same row of the result)
+    u32x4 xa[4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    float sx = 0.0f;
+#pragma unroll
+    for (int c = 0; c < GU; ++c) {
+      const int i = c / qPerW;
+      const int q = qPerW * w + c % qPerW;
+      wait_vmcnt_le((GU - 1 - c) * 4 + DN * 2);  // this pair's copies (the younger ones may fly)
+      poll_clobber();
+      const char* slot = gu_w + c * kX8Chunk;
+      const u32x4 gw = *reinterpret_cast<const u32x4*>(slot + (n >= 8 ? 512 : 0) + (8 * p + (n & 7)) * 16);
+      const uint2 dsv = *reinterpret_cast<const uint2*>(slot + 1024 + n * 8);
+      if (n == 0) {
+        const u32x4* xo = s_xop + (q * 4 + p) * 4;
+        xa[0] = xo[0];
+        xa[1] = xo[1];
+        xa[2] = xo[2];
+        xa[3] = xo[3];
+        sx = s_xs[q * 4 + p];
+      }
+      float d[4];
+      unpack_scales(dsv, d);
+      const uint32_t gwv[4] = {gw.x, gw.y, gw.z, gw.w};
+      f32x4 pg[4];
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) pg[gi] = mfma_bf16_16x16x32(xa[gi], x8_dequant_bf16(gwv[gi]), z);
+      cg[i] = mfma_f32_16x16x4(sx, d[p], cg[i]);
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) ag[i] += d[gi] * pg[gi];
+    }
+    // lane (n, 0) holds result row 0 (the token) of column n: gate row n of
+    // the half for n < 8, up row n - 8 for n >= 8
+    if (p == 0) {
+#pragma unroll
+      for (int i = 0; i < htPer; ++i) s_gred[(w * htPer + i) * 16 + n] = kUnitScale * ag[i][0] - kUnitBias * cg[i][0];
+    }
+  }
+  lds_barrier();
+  const BufRsrc xh_r = buf_rsrc(a.xh + (size_t)xcd * (I / 2) * 4, (uint32_t)(I / 2 * 16));
+  if (w == 0) {
+    // SwiGLU of the workgroup's 8 htPer rows of I, the wave partials summed
+    // in wave order; units of rows (i, i + 1) go to this XCD's L2
+    uint32_t hb = 0u, lb = 0u;
+    if (lane < htPer * 8) {
+      const int i = lane / 8, r = lane % 8;
+      float h = __builtin_nanf("");
+      if (!route_failed) {
+        float g = 0.0f, u = 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 < kFW; ++s2) {
+          g += s_gred[(s2 * htPer + i) * 16 + r];
+          u += s_gred[(s2 * htPer + i) * 16 + 8 + r];
+        }
+        h = g * (1.0f / (1.0f + expf(-g))) * u;
+      }
+      hb = float_to_half_bits(h);
+      lb = float_to_half_bits(h - half_bits_to_float32(hb));
+    }
+    const uint32_t hb2 = __shfl_down(hb, 1, kWave), lb2 = __shfl_down(lb, 1, kWave);
+    if (lane < htPer * 8 && (lane & 1) == 0) {
+      const int row = 8 * (htPer * rho + lane / 8) + lane % 8;  // even row of I
+      u32x4 v;
+      v.x = hb | (hb2 << 16);
+      v.y = tag;
+      v.z = lb | (lb2 << 16);
+      v.w = ~tag;
+      __builtin_amdgcn_raw_buffer_store_b128(v, xh_r, (row / 2) * 16, 0, 0);
+    }
+  }
+
+  // ---- 4. down weights into registers, then h into the down operand -----------
+  u32x4 bb[DN][4];
+  float dv[DN][4];
+  if (!route_failed) {
+    wait_vmcnt<0>();  // this wave's down copies
+    poll_clobber();
+#pragma unroll
+    for (int c = 0; c < DN; ++c) {
+      const char* slot = dn_w + c * kX8Chunk;
+      const u32x4 wv = *reinterpret_cast<const u32x4*>(slot + lane * 16);
+      unpack_scales(*reinterpret_cast<const uint2*>(slot + 1024 + n * 8), dv[c]);
+      bb[c][0] = x8_dequant_f16s(wv.x);
+      bb[c][1] = x8_dequant_f16s(wv.y);
+      bb[c][2] = x8_dequant_f16s(wv.z);
+      bb[c][3] = x8_dequant_f16s(wv.w);
+    }
+  }
+  if ((int)threadIdx.x < I / 2) {
+    // unit u holds rows i0 = 2u and i0 + 1: in group i0 / 32 they sit at K
+    // positions kmap(pp, s) and kmap(pp, s + 4) of part pp = (i0 % 16) / 4
+    const int u = (int)threadIdx.x;
+    const uint32_t want = tag + a.skew_h;
+    u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xh_r, u * 16, 0, kXcdPoll);
+    bool ok = tag_ok(v, want);
+    for (uint32_t it = 0;; ++it) {
+      if (__all(ok)) break;
+      if (it >= a.wait_polls) {
+        if (lane == 0) {
+          s_hfail = 1;
+          set_status(a.ctl, kStatusExpertWait);
+        }
+        break;
+      }
+      poll_clobber();
+      if (!ok) {
+        v = __builtin_amdgcn_raw_buffer_load_b128(xh_r, u * 16, 0, kXcdPoll);
+        ok = tag_ok(v, want);
+      }
+    }
+    if (!ok) v.x = v.z = 0x7E007E00u;  // fp16 NaN
+    const int i0 = 2 * u, g32 = i0 / kGroup, jj = i0 % kGroup;
+    const int pp = (jj % 16) / 4, off = jj - 4 * pp;  // 0, 2, 16 or 18
+    const int s = ((off & 2) ? 1 : 0) + (off >= 16 ? 2 : 0);
+    uint16_t* e16 = reinterpret_cast<uint16_t*>(s_hop + (((g32 / 4) * 4 + pp) * 4 + g32 % 4) * 32);
+    e16[s] = (uint16_t)(v.x & 0xffffu);
+    e16[s + 4] = (uint16_t)(v.x >> 16);
+    e16[8 + s] = (uint16_t)(v.z & 0xffffu);
+    e16[8 + s + 4] = (uint16_t)(v.z >> 16);
+  }
+  lds_barrier();
+  const bool h_failed = uni(s_hfail) != 0;
+
+  // ---- 5. down, then the combine over the XCDs ---------------------------------
+  if (!route_failed) {
+    f32x4 acc = z;
+    u32x4 hh[4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+#pragma unroll
+    for (int c = 0; c < DN; ++c) {
+      const int q = DN * (w % 2) + c;
+      if (n < 2) {
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi)
+          hh[gi] = *reinterpret_cast<const u32x4*>(s_hop + ((q * 4 + p) * 4 + gi) * 32 + n * 16);
+      }
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) acc += dv[c][gi] * mfma_f16_16x16x32(hh[gi], bb[c][gi], z);
+    }
+    // lane (n, 0): result rows 0 (h hi) and 1 (h lo) of output row n
+    if (p == 0) s_dred[w * 16 + n] = acc[0] + acc[1];
+  }
+  lds_barrier();
+  const BufRsrc pt_r = buf_rsrc(a.xpart, (uint32_t)(kX8Xcds * H / 2 * 16));
+  if (w == 0) {
+    // rows 64 rho + lane of slot xcd's output, the two waves of each row tile
+    // in order; units of rows (r, r + 1) go out device-scope
+    float d = __builtin_nanf("");
+    if (!route_failed && !h_failed) {
+      const int i = lane / 16, nn = lane % 16;
+      d = s_dred[(2 * i) * 16 + nn] + s_dred[(2 * i + 1) * 16 + nn];
+    }
+    const float d2 = __shfl_down(d, 1, kWave);
+    if ((lane & 1) == 0) {
+      const int row = tdPer * kRowTile * rho + lane;
+      u32x4 v;
+      v.x = __builtin_bit_cast(uint32_t, d);
+      v.y = tag;
+      v.z = __builtin_bit_cast(uint32_t, d2);
+      v.w = ~tag;
+      __builtin_amdgcn_raw_buffer_store_b128(v, pt_r, ((xcd * H + row) / 2) * 16, 0, kDeviceScope);
+    }
+  } else if (w == 1) {
+    // rows row0 .. row0 + yRows of y: lane t < K * yRows / 2 polls unit t % 4
+    // of slot t / 4 (of yRows / 2 units), then lane r < yRows sums its row
+    // over the slots in slot order
+    constexpr int UPS = yRows / 2;
+    const int row0 = tdPer * kRowTile * rho + yRows * xcd;
+    const bool mine = lane < K * UPS;
+    const int j = lane / UPS, uu = lane % UPS;
+    const uint32_t off = mine ? (uint32_t)(((j * H + row0) / 2 + uu) * 16) : 0u;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    bool ok = !mine;
+    if (mine) {
+      v = __builtin_amdgcn_raw_buffer_load_b128(pt_r, (int)off, 0, kDevicePoll);
+      ok = tag_ok(v, tag);
+    }
+    for (uint32_t it = 0;; ++it) {
+      if (__all(ok)) break;
+      if (it >= a.wait_polls) {
+        if (lane == 0) set_status(a.ctl, kStatusExpertWait);
+        break;
+      }
+      poll_clobber();
+      if (!ok) {
+        v = __builtin_amdgcn_raw_buffer_load_b128(pt_r, (int)off, 0, kDevicePoll);
+        ok = tag_ok(v, tag);
+      }
+    }
+    if (!ok) v.x = v.z = 0x7FC00000u;  // NaN
+    float yv = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < K; ++jj) {
+      const int src = jj * UPS + (lane % yRows) / 2;
+      const uint32_t lo = (uint32_t)__shfl((int)v.x, src, kWave), hi = (uint32_t)__shfl((int)v.z, src, kWave);
+      const float dj = __builtin_bit_cast(float, (lane & 1) ? hi : lo);
+      yv += (route_failed ? 0.0f : s_sel_w[jj]) * dj;
+    }
+    if (lane < yRows) a.y[row0 + lane] = route_failed ? __builtin_nanf("") : yv;
+  }
+
+  // ---- 6. the next call's tag ---------------------------------------------------
+  if (b == 0 && w == 2) {
+    for (int i0 = 0; i0 < kX8Grid; i0 += kWave) {
+      const int i = i0 + lane;
+      bool done = false;
+      for (uint32_t it = 0;; ++it) {
+        if (!done) done = __hip_atomic_load(&a.presence[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tag64(tag);
+        if (__all(done)) break;
+        if (it >= a.wait_polls) {
+          if (lane == 0) set_status(a.ctl, kStatusPresenceWait);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    if (lane == 0) __hip_atomic_store(&a.ctl[0], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+}  // namespace
+
 bool fused_shape_ok(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared) {
   if (T < 1 || T > kFusedMaxT || T * E > kFusedMaxLogits || T * k > kFusedMaxSlots) return false;
   if (E < 1 || E > kMaxExperts || k < 1 || k > kMaxTopK || k > E) return false;
@@ -1170,10 +1760,41 @@ bool fused_shape_ok(int64_t T, int64_t H, int64_t I, int E, int k, int has_share
   return fused_lds_layout((int)T, k, E, has_shared, (int)H, (int)I, 1, 1, S_max).bytes <= kFusedDynLdsMax;
 }
 
+bool x8_shape(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared) {
+  return T == 1 && H == 2048 && I == 768 && E == 128 && k == kX8Xcds && !has_shared;
+}
+
+namespace {
+
+// XCDs of the current device (0 when the runtime cannot tell).
+int device_xccs() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || n <= 0) n = -1;
+    cached[dev] = n;
+  }
+  return cached[dev] > 0 ? cached[dev] : 0;
+}
+
+}  // namespace
+
 FusedPlan fused_plan(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared) {
   FusedPlan pl = {};
   pl.ok = false;
-  if (!lib_config().decode_fused || !fused_shape_ok(T, H, I, E, k, has_shared)) return pl;
+  const LibConfig cfg = lib_config();
+  if (!cfg.decode_fused || !fused_shape_ok(T, H, I, E, k, has_shared)) return pl;
+  if (cfg.decode_x8 && x8_shape(T, H, I, E, k, has_shared) && device_cus() == kX8Grid &&
+      device_xccs() == kX8Xcds) {
+    pl.G = kX8Grid;
+    pl.spec = kFusedSpecX8;
+    pl.lds = FusedLds{};
+    pl.lds.bytes = X8Lds<2048, 768, 128>::bytes;
+    pl.ok = true;
+    return pl;
+  }
   int G = device_cus();
   if (G > kFusedMaxGrid) G = kFusedMaxGrid;
   if ((int64_t)G * kFW < T * E || G < 2) return pl;  // one logit per wave at most
@@ -1205,6 +1826,44 @@ static hipError_t launch_fused_as(const FusedK& a, const FusedPlan& pl, hipStrea
   return hipGetLastError();
 }
 
+static hipError_t launch_x8(const FusedPlan& pl, const RouteArgs& r, const ExpertArgs& x, const FusedWs& ws,
+                            hipStream_t stream) {
+  if (!ws.xslots || !ws.xh || !ws.xpart) return hipErrorInvalidValue;  // a workspace planned for another shape
+  X8K a = {};
+  a.x = static_cast<const uint16_t*>(r.x);
+  a.W = r.router_w;
+  a.bias = r.router_bias;
+  a.score_mode = r.score_mode;
+  a.gate_nib = x.gate_nib;
+  a.gate_sc = x.gate_scale;
+  a.up_nib = x.up_nib;
+  a.up_sc = x.up_scale;
+  a.down_nib = x.down_nib;
+  a.down_sc = x.down_scale;
+  a.y = x.y;
+  a.topk_idx = r.topk_idx;
+  a.topk_w = r.topk_w;
+  a.ctl = ws.ctl;
+  a.presence = ws.presence;
+  a.xslots = ws.xslots;
+  a.xh = ws.xh;
+  a.xpart = ws.xpart;
+  const LibConfig cfg = lib_config();
+  a.wait_polls = cfg.fused_wait_polls;
+  a.skew_route = (cfg.fused_fault & 1u) ? 1u : 0u;
+  a.skew_h = (cfg.fused_fault & 2u) ? 1u : 0u;
+  static bool attr_set = false;
+  auto kernel = moe_decode_x8_kernel<2048, 768, 128>;
+  if (!attr_set) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFusedDynLdsMax);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kernel, dim3(kX8Grid), dim3(kFThreads), pl.lds.bytes, stream, a);
+  return hipGetLastError();
+}
+
 static hipError_t launch_fused(const FusedK& a, const FusedPlan& pl, hipStream_t stream) {
   if (pl.spec == kFusedSpecQwen3T1) return launch_fused_as<1, 2048, 768, 128, 8, 0>(a, pl, stream);
   return launch_fused_as<0, 0, 0, 0, 0, -1>(a, pl, stream);
@@ -1212,6 +1871,7 @@ static hipError_t launch_fused(const FusedK& a, const FusedPlan& pl, hipStream_t
 
 hipError_t launch_decode_fused(const FusedPlan& pl, const RouteArgs& r, const ExpertArgs& x, const FusedWs& ws,
                                hipStream_t stream) {
+  if (pl.spec == kFusedSpecX8) return launch_x8(pl, r, x, ws, stream);
   FusedK a = {};
   a.x = static_cast<const uint16_t*>(r.x);
   a.W = r.router_w;

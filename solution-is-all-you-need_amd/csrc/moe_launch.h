@@ -51,6 +51,11 @@ struct FusedLds {
 // kFusedSpecQwen3T1 is compiled for T 1, H 2048, I 768, E 128, top-8, no
 // shared expert (the batch-1 Qwen3-30B-A3B-shaped layer).
 constexpr int kFusedSpecQwen3T1 = 1;
+// The per-XCD batch-1 kernel (moe_decode_x8_kernel): one token, top-8, no
+// shared expert, on a part with 8 XCDs of 32 CUs, expert slot j on XCD j;
+// compiled for H 2048, I 768, E 128.
+constexpr int kFusedSpecX8 = 2;
+bool x8_shape(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
 struct FusedPlan {
   bool ok;
   int G;     // workgroups (one per CU)
@@ -62,6 +67,10 @@ struct FusedWs {
   uint64_t* presence = nullptr;  // [kFusedMaxGrid]
   uint32_t* slots = nullptr;     // [T * E][4] tagged logits
   uint32_t* hv = nullptr;        // [T*k + T][I / 2][4] tagged h units (fp16 hi/lo of two rows)
+  // the per-XCD kernel's (null unless x8_shape)
+  uint32_t* xslots = nullptr;  // [8][E][4] tagged logits
+  uint32_t* xh = nullptr;      // [8][I / 2][4] tagged h units
+  uint32_t* xpart = nullptr;   // [8][H / 2][4] tagged down partials
 };
 // Device-independent shape limits (the workspace plan reserves the fused
 // regions for these shapes).
@@ -76,8 +85,11 @@ FusedLds fused_lds_layout(int T, int k, int E, int has_shared, int H, int I, int
 //   PHANTOM_MOE_DECODE=staged       never take the single-launch decode path
 //   PHANTOM_MOE_DECODE_KSPLIT=1     decode expert stages always as the K-split
 //                                   kernels (not the token-tile ones)
+//   PHANTOM_MOE_DECODE_X8=0         batch-1 top-8 decode in the generic
+//                                   single-launch kernel, not per XCD
 struct LibConfig {
   bool decode_fused;
+  bool decode_x8;  // batch-1 top-8 decode per XCD where the shape and the device allow
   bool force_ksplit;
   uint32_t fused_wait_polls;  // bound of each wait of the single-launch path
   uint32_t fused_fault;       // failure injection for tests: bit 0 the logit wait, bit 1 the gate/up wait

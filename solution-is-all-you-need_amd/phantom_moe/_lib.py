@@ -72,6 +72,7 @@ OPT_DECODE_FUSED = 1  # PHANTOM_MOE_OPT_DECODE_FUSED
 OPT_DECODE_KSPLIT = 2  # PHANTOM_MOE_OPT_DECODE_KSPLIT
 OPT_FUSED_WAIT_POLLS = 3  # PHANTOM_MOE_OPT_FUSED_WAIT_POLLS
 OPT_FUSED_FAULT = 4  # PHANTOM_MOE_OPT_FUSED_FAULT
+OPT_DECODE_X8 = 5  # PHANTOM_MOE_OPT_DECODE_X8
 
 
 class PhantomMoEError(RuntimeError):

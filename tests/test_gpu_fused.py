@@ -20,6 +20,7 @@ from phantom_moe import _lib, synth  # noqa: E402
 pytestmark = pytest.mark.gpu
 
 FUSED = "gate_up=moe_decode_fused_kernel;down=moe_decode_fused_kernel"
+X8 = "gate_up=moe_decode_x8_kernel;down=moe_decode_x8_kernel"
 
 
 @pytest.fixture(scope="module")
@@ -105,11 +106,18 @@ def test_fused_vs_oracle_and_staged(dev, cfg, option):
     check_y(ys.cpu().numpy(), ry, cfg.name + " staged")
 
 
-def test_fused_full_size_qwen3_t1(dev):
+@pytest.mark.parametrize("x8", [1, 0], ids=["per_xcd", "generic"])
+def test_fused_full_size_qwen3_t1(dev, option, x8):
     """The batch-1 Qwen3-30B-A3B-shaped layer (H 2048, I 768, E 128, top-8)
-    takes the single-launch path and matches the oracle."""
+    takes the single-launch path and matches the oracle: per XCD (expert
+    slot j on XCD j) on an 8-XCD, 256-CU part, else in the generic kernel.
+    Repeated calls are identical bit for bit."""
     cfg = synth.CONFIGS["qwen3_decode_t1"]
-    assert kernels(cfg) == FUSED
+    option(_lib.OPT_DECODE_X8, x8)
+    name = kernels(cfg)
+    if x8 and name != X8:
+        pytest.skip(f"the per-XCD kernel needs 8 XCDs of 32 CUs ({name})")
+    assert name == (X8 if x8 else FUSED)
     dl = synth.device_layer(cfg, dev)
     ex = phantom_moe.MoEWeights.from_q4_0(dl.gate, dl.up, dl.down, cfg.H, cfg.I, cfg.E)
     for seed in (42, 43, 44):
@@ -117,12 +125,119 @@ def test_fused_full_size_qwen3_t1(dev):
         prep = phantom_moe.PreparedForward(ex, dl.router_w, cfg.T, cfg.k, cfg.score, dl.router_bias,
                                            x=to_bf16_tensor(xb, dev))
         y, w, idx = run(prep)
+        y2, w2, idx2 = run(prep)
         assert _lib.workspace_status(prep.workspace) == 0
+        assert torch.equal(y2, y) and torch.equal(w2, w) and torch.equal(idx2, idx)
         ry, ridx, rw = oracle_for_device_layer(dl, xb)
         np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
         np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-6, atol=1e-7)
         err, rel = check_y(y.cpu().numpy(), ry, f"qwen3_decode_t1 seed {seed}")
-        print(f"[case] qwen3_decode_t1 seed {seed}: max_abs={err:.2e} rel_l2={rel:.2e}", flush=True)
+        print(f"[case] qwen3_decode_t1 {'per-XCD' if x8 else 'generic'} seed {seed}: "
+              f"max_abs={err:.2e} rel_l2={rel:.2e}", flush=True)
+
+
+def x8_prep(dev, seed=7, xb=None):
+    """A batch-1 Qwen3-shaped layer on the per-XCD kernel (skips the test
+    where the device does not take it)."""
+    cfg = synth.CONFIGS["qwen3_decode_t1"]
+    if kernels(cfg) != X8:
+        pytest.skip(f"the per-XCD kernel needs 8 XCDs of 32 CUs ({kernels(cfg)})")
+    dl = synth.device_layer(cfg, dev, layer=1)
+    ex = phantom_moe.MoEWeights.from_q4_0(dl.gate, dl.up, dl.down, cfg.H, cfg.I, cfg.E)
+    if xb is None:
+        xb = synth.activations(cfg.T, cfg.H, seed=seed)
+    prep = phantom_moe.PreparedForward(ex, dl.router_w, cfg.T, cfg.k, cfg.score, dl.router_bias,
+                                       x=to_bf16_tensor(xb, dev))
+    return cfg, dl, prep, xb
+
+
+def test_x8_graph_replays(dev):
+    """Captured per-XCD calls draw fresh tags on every replay: each replay,
+    with eager calls between replays, equals the eager result bit for bit."""
+    cfg, dl, prep, _ = x8_prep(dev)
+    xs = [to_bf16_tensor(synth.activations(1, cfg.H, seed=s), dev) for s in (11, 12, 13)]
+    eager = []
+    for x in xs:
+        prep.x.copy_(x)
+        eager.append(run(prep)[0])
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    outs = [torch.empty_like(eager[0]) for _ in xs]
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        for x, o in zip(xs, outs):
+            prep.x.copy_(x)
+            prep(_lib.stream_handle(dev))
+            o.copy_(prep.y)
+    for rep in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, eager)):
+            assert torch.equal(o, e), f"replay {rep}, call {i} differs"
+        prep.x.copy_(xs[rep % 3])
+        assert torch.equal(run(prep)[0], eager[rep % 3])
+        torch.cuda.synchronize()
+    assert _lib.workspace_status(prep.workspace) == 0
+
+
+@pytest.mark.parametrize("fault", [1, 2])
+def test_x8_wait_failure_is_reported(dev, option, fault):
+    """A per-XCD wait that gives up (forced from the host with a short bound:
+    the waiters expect a tag nobody writes) ends normally, sets the status
+    and leaves NaN in y (and in the routing outputs when the logit wait gave
+    up); the next call is correct again."""
+    cfg, dl, prep, xb = x8_prep(dev, seed=21)
+    y_ok, w_ok, i_ok = run(prep)
+    option(_lib.OPT_FUSED_WAIT_POLLS, 64)
+    option(_lib.OPT_FUSED_FAULT, fault)
+    y, w, idx = run(prep)
+    torch.cuda.synchronize()
+    st = _lib.workspace_status(prep.workspace)
+    assert st & fault, f"status {st:#x} lacks bit {fault:#x}"
+    assert torch.isnan(y).all()
+    if fault == 1:
+        assert (idx == -1).all() and torch.isnan(w).all()
+    else:
+        assert torch.equal(idx, i_ok) and torch.equal(w, w_ok)
+    _lib.set_option(_lib.OPT_FUSED_FAULT, 0)
+    y2, _, _ = run(prep)
+    assert _lib.workspace_status(prep.workspace) == 0
+    assert torch.equal(y2, y_ok)
+
+
+@pytest.mark.parametrize("special", ["nan", "inf", "zero"])
+def test_x8_nonfinite_and_zero_activations(dev, special):
+    """NaN, +-inf or an all-zero x: no fault, routing as the oracle's
+    contract gives it (NaN logits rank below every number; all-zero logits
+    tie, so experts 0..7 in index order), identical to the generic kernel."""
+    cfg = synth.CONFIGS["qwen3_decode_t1"]
+    xb = synth.activations(cfg.T, cfg.H, seed=5)
+    if special == "nan":
+        xb[0, 100] = 0x7FC0
+    elif special == "inf":
+        xb[0, 7] = 0x7F80
+        xb[0, 900] = 0xFF80
+    else:
+        xb[:] = 0
+    _, dl, prep, _ = x8_prep(dev, xb=xb)
+    y, w, idx = run(prep)
+    torch.cuda.synchronize()
+    assert _lib.workspace_status(prep.workspace) == 0
+    bias = None if dl.router_bias is None else dl.router_bias.cpu().numpy()
+    ridx, _ = oracle.route(xb, dl.router_w.cpu().numpy(), cfg.k, 0, bias)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    old = _lib.set_option(_lib.OPT_DECODE_X8, 0)
+    try:
+        assert kernels(cfg) == FUSED
+        yg, wg, ig = run(prep)
+    finally:
+        _lib.set_option(_lib.OPT_DECODE_X8, old)
+    assert torch.equal(ig, idx)
+    assert torch.equal(wg.isnan(), w.isnan()) and torch.equal(wg.nan_to_num(), w.nan_to_num())
+    assert torch.equal(yg.isnan(), y.isnan())
+    if special == "zero":
+        assert (idx.cpu().numpy() == np.arange(cfg.k)).all()
+        assert torch.equal(y, torch.zeros_like(y))
 
 
 def test_fused_graph_replays(dev):
