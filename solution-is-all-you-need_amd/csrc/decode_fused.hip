@@ -1195,6 +1195,9 @@ constexpr int kX8Xcds = 8;
 constexpr int kX8Grid = 256;
 constexpr int kX8PerXcd = kX8Grid / kX8Xcds;
 constexpr uint32_t kX8Chunk = 1152;  // 1 KiB of nibbles + 128 B of scales
+// Byte offset, in the logit-slot region, of the per-XCD routing records (the
+// device-scope logit slots come first; the records sit on pages of their own).
+constexpr uint32_t kX8RecOff = 8192;
 // Cache policy of a poll of data another CU of this XCD stored: SC0 (not
 // served by this CU's L1; this XCD's L2 holds the latest copy), with the
 // intrinsic's volatile bit as in kDevicePoll.
@@ -1286,7 +1289,6 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
   using L = X8Lds<H, I, E>;
   constexpr int Kq = L::Kq, KqI = L::KqI, htPer = L::htPer, qPerW = L::qPerW, GU = L::GU, tdPer = L::tdPer,
                 DN = L::DN;
-  constexpr int LPW = E / kX8PerXcd;      // logits per workgroup
   constexpr int yRows = H / kX8Grid;      // rows of y each workgroup combines
   constexpr int P = x8_rank_threads(E);  // threads per logit in the ranking
   static_assert(H % (kQuad * kFW) == 0 && I % (8 * kX8PerXcd) == 0 && H % (kRowTile * kX8PerXcd) == 0 &&
@@ -1294,9 +1296,10 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
                 "whole quads of H per wave, whole half tiles and row tiles per workgroup");
   static_assert(tdPer * 2 == kFW && KqI % 2 == 0, "down: two waves per row tile, half of I each");
   static_assert(tdPer * kRowTile == kWave, "one partial row per lane of wave 0");
-  static_assert(E % kX8PerXcd == 0 && LPW < kFW - 1 && E % kWave == 0 && E * P <= kFThreads, "logits");
+  static_assert(E <= kX8Grid && E % kWave == 0 && E * P <= kFThreads, "logits");
+  static_assert(kX8RecOff >= (uint32_t)E * 16 && kX8RecOff + kX8Xcds * 2 * K * 16 <= 16u * kX8Xcds * E,
+                "the records fit the slot region");
   static_assert(htPer * 8 <= kWave && I / 2 <= kFThreads && yRows * K / 2 <= kWave && yRows <= kWave, "lanes");
-  static_assert(GU * 4 + DN * 2 <= 47, "vmcnt");
   static_assert(L::bytes <= kFusedDynLdsMax, "LDS");
 
   __shared__ int s_sel_idx[K];
@@ -1323,15 +1326,24 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
   const int rho = b / kX8Xcds;
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 
-  // ---- 0. generation; this XCD's logits; x operand -------------------------
+  // ---- 0. generation; logits; x operand ---------------------------------------
   const uint32_t tag =
       (uint32_t)uni((int)__hip_atomic_load(&a.ctl[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) + 1u;
   if (threadIdx.x == 0) s_hfail = 0;
-  const BufRsrc sl_r = buf_rsrc(a.xslots + (size_t)xcd * E * 4, (uint32_t)(E * 16));
-  if (w < LPW) {
-    const int e = rho * LPW + w;
-    double logit = fixed_dot_bf16(a.x, a.W + (int64_t)e * H, H);
-    if (a.bias) logit = logit + (double)a.bias[e];
+  // Logit e is computed once, by wave 0 of workgroup e (the router's
+  // fixed-order contract), and published device-scope in slot e.  Only the
+  // leader of each XCD (rank 0 on it) polls the slots, so 8 waves, not 256,
+  // hit their lines; it ranks the logits and publishes the selection to its
+  // XCD's L2 as a record of 2K tagged units (unit 2r: logit of slot r, unit
+  // 2r + 1: its expert, -1 when the leader's wait gave up), which the other
+  // workgroups of the XCD poll.
+  const bool leader = rho == 0;
+  const BufRsrc lg_r = buf_rsrc(a.xslots, (uint32_t)(E * 16));
+  const BufRsrc rec_r = buf_rsrc(reinterpret_cast<const char*>(a.xslots) + kX8RecOff + xcd * (2 * K * 16),
+                                 (uint32_t)(2 * K * 16));
+  if (w == 0 && b < E) {
+    double logit = fixed_dot_bf16(a.x, a.W + (int64_t)b * H, H);
+    if (a.bias) logit = logit + (double)a.bias[b];
     if (lane == 0) {
       const uint64_t bits = __builtin_bit_cast(uint64_t, logit);
       u32x4 v;
@@ -1339,9 +1351,9 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
       v.y = tag;
       v.z = (uint32_t)(bits >> 32);
       v.w = ~tag;
-      __builtin_amdgcn_raw_buffer_store_b128(v, sl_r, e * 16, 0, 0);  // into this XCD's L2
+      __builtin_amdgcn_raw_buffer_store_b128(v, lg_r, b * 16, 0, kDeviceScope);
     }
-  } else if (w == LPW) {
+  } else if (w == 4) {
     // the MFMA-ordered x operand and its group sums, as the generic kernel
     // builds them: one lane per (quad, group)
     for (int j = lane; j < Kq * 4; j += kWave) {
@@ -1366,94 +1378,154 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
       s_xs[q * 4 + gi] = (sp[0] + sp[1]) + (sp[2] + sp[3]);
     }
   } else if (w == kFW - 1) {
-    // ---- 1. poll this XCD's E logits into LDS
-    const uint32_t want = tag + a.skew_route;
-    constexpr int kNV = E / kWave;
-    bool done[kNV];
-#pragma unroll
-    for (int v = 0; v < kNV; ++v) done[v] = false;
+    // ---- 1. the leader polls the E logits, the others this XCD's record
     bool failed = false;
-    for (uint32_t it = 0;; ++it) {
-      poll_clobber();
-      u32x4 sv[kNV];
+    if (leader) {
+      const uint32_t want = tag + a.skew_route;
+      constexpr int kNV = E / kWave;
+      bool done[kNV];
 #pragma unroll
-      for (int v = 0; v < kNV; ++v)
-        if (!done[v]) sv[v] = __builtin_amdgcn_raw_buffer_load_b128(sl_r, (lane + v * kWave) * 16, 0, kXcdPoll);
-      bool all = true;
+      for (int v = 0; v < kNV; ++v) done[v] = false;
+      for (uint32_t it = 0;; ++it) {
+        poll_clobber();
+        u32x4 sv[kNV];
 #pragma unroll
-      for (int v = 0; v < kNV; ++v) {
-        if (!done[v] && tag_ok(sv[v], want)) {
-          const double lv = __builtin_bit_cast(double, ((uint64_t)sv[v].z << 32) | sv[v].x);
-          s_lv[lane + v * kWave] = lv;
-          s_key[lane + v * kWave] = logit_key(lv);
-          done[v] = true;
+        for (int v = 0; v < kNV; ++v)
+          if (!done[v]) sv[v] = __builtin_amdgcn_raw_buffer_load_b128(lg_r, (lane + v * kWave) * 16, 0, kDevicePoll);
+        bool all = true;
+#pragma unroll
+        for (int v = 0; v < kNV; ++v) {
+          if (!done[v] && tag_ok(sv[v], want)) {
+            const double lv = __builtin_bit_cast(double, ((uint64_t)sv[v].z << 32) | sv[v].x);
+            s_lv[lane + v * kWave] = lv;
+            s_key[lane + v * kWave] = logit_key(lv);
+            done[v] = true;
+          }
+          all = all && done[v];
         }
-        all = all && done[v];
+        if (__all(all)) break;
+        if (it >= a.wait_polls) {
+          failed = true;
+          if (lane == 0) set_status(a.ctl, kStatusRouteWait);
+          break;
+        }
       }
-      if (__all(all)) break;
-      if (it >= a.wait_polls) {
-        failed = true;
-        if (lane == 0) set_status(a.ctl, kStatusRouteWait);
-        break;
+      for (int e = lane; e < E; e += kWave) s_rank[e] = 0;
+    } else {
+      const bool mine = lane < 2 * K;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      bool ok = !mine;
+      if (mine) {
+        v = __builtin_amdgcn_raw_buffer_load_b128(rec_r, lane * 16, 0, kXcdPoll);
+        ok = tag_ok(v, tag);
+      }
+      for (uint32_t it = 0;; ++it) {
+        if (__all(ok)) break;
+        if (it >= a.wait_polls) {
+          failed = true;
+          if (lane == 0) set_status(a.ctl, kStatusRouteWait);
+          break;
+        }
+        poll_clobber();
+        if (!ok) {
+          v = __builtin_amdgcn_raw_buffer_load_b128(rec_r, lane * 16, 0, kXcdPoll);
+          ok = tag_ok(v, tag);
+        }
+      }
+      if (!failed) {
+        if (mine && (lane & 1)) {
+          s_sel_idx[lane / 2] = (int)v.x;
+          if ((int)v.x < 0) failed = true;  // the leader's wait gave up
+        }
+        if (mine && !(lane & 1)) s_sel_v[lane / 2] = __builtin_bit_cast(double, ((uint64_t)v.z << 32) | v.x);
+        failed = __ballot(failed) != 0ull;
       }
     }
-    for (int e = lane; e < E; e += kWave) s_rank[e] = 0;
     if (lane == 0) s_pfail = failed ? 1 : 0;
   }
-  lds_barrier();  // every wave has read the generation; logits, ranks zeroed, x operand in LDS
+  lds_barrier();  // every wave has read the generation; logits or the selection, x operand in LDS
   if (threadIdx.x == 0) __hip_atomic_store(&a.presence[b], tag64(tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const bool route_failed = uni(s_pfail) != 0;
 
-  // ranks (the number of logits before each in wave_topk_row's order: value
-  // descending, NaN last, ties to the lower index), P threads per logit;
-  // rank r < K is slot r
-  if (!route_failed) {
-    constexpr int span = (E + P - 1) / P;
-    if ((int)threadIdx.x < E * P) {
-      const int pp = (int)threadIdx.x / E;
-      const int e = (int)threadIdx.x - pp * E;
-      const uint64_t ke = s_key[e];
-      const int j0 = pp * span;
-      const int j1 = j0 + span < E ? j0 + span : E;
-      int cnt = 0;
-      int j = j0;
-      for (; j + 8 <= j1; j += 8) {
-        uint64_t kk[8];
+  if (leader) {
+    if (!route_failed) {
+      // rank of logit e in wave_topk_row's order (value descending, NaN
+      // last, ties to the lower index): the number of larger keys, counted
+      // without branches by P threads per logit (keys j0 .. j0 + span are
+      // the same for the whole wave, so the LDS reads broadcast), plus the
+      // number of equal keys at lower indices; equal counts mean equal keys,
+      // so wave 0 finds those among the counts below K with ballots
+      constexpr int span = E / P;
+      static_assert(E % P == 0 && E == 2 * kWave && K == 8, "two logits per lane of the selecting wave");
+      if ((int)threadIdx.x < E * P) {
+        const int pp = uni((int)threadIdx.x / E);
+        const int e = (int)threadIdx.x - pp * E;
+        const uint64_t ke = s_key[e];
+        const int j0 = pp * span;
+        int cnt = 0;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) kk[q] = s_key[j + q];
+        for (int q = 0; q < span; ++q) cnt += (int)(s_key[j0 + q] > ke);
+        if (P == 1) s_rank[e] = cnt;
+        else atomicAdd(&s_rank[e], cnt);
+      }
+      lds_barrier();
+      if (w == 0) {
+        const int c0 = s_rank[lane], c1 = s_rank[lane + kWave];
+        uint64_t m00 = __ballot(c0 < K), m01 = __ballot(c1 < K);  // half 0 / half 1 lanes with a count below K
+        uint64_t m10 = m00, m11 = m01;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) cnt += (kk[q] > ke || (kk[q] == ke && j + q < e)) ? 1 : 0;
+        for (int bt = 0; bt < 3; ++bt) {
+          const uint64_t b0 = __ballot((c0 >> bt) & 1), b1 = __ballot((c1 >> bt) & 1);
+          m00 &= ((c0 >> bt) & 1) ? b0 : ~b0;
+          m01 &= ((c0 >> bt) & 1) ? b1 : ~b1;
+          m10 &= ((c1 >> bt) & 1) ? b0 : ~b0;
+          m11 &= ((c1 >> bt) & 1) ? b1 : ~b1;
+        }
+        const uint64_t lt = (1ull << lane) - 1ull;
+        const int r0 = c0 + __popcll(m00 & lt);                   // e = lane
+        const int r1 = c1 + __popcll(m10) + __popcll(m11 & lt);   // e = lane + 64
+        (void)m01;
+        if (c0 < K && r0 < K) {
+          s_sel_idx[r0] = lane;
+          s_sel_v[r0] = s_lv[lane];
+        }
+        if (c1 < K && r1 < K) {
+          s_sel_idx[r1] = lane + kWave;
+          s_sel_v[r1] = s_lv[lane + kWave];
+        }
       }
-      for (; j < j1; ++j) {
-        const uint64_t kj = s_key[j];
-        cnt += (kj > ke || (kj == ke && j < e)) ? 1 : 0;
-      }
-      if (P == 1) s_rank[e] = cnt;
-      else atomicAdd(&s_rank[e], cnt);
+      lds_barrier();
     }
-    lds_barrier();
-    if (w == 0) {
-      for (int e = lane; e < E; e += kWave) {
-        const int r = s_rank[e];
-        if (r < K) s_sel_idx[r] = e;
+    if (w == 0 && lane < 2 * K) {
+      // this XCD's record (expert -1 when the leader's wait gave up)
+      const int r = lane / 2;
+      u32x4 v;
+      if (lane & 1) {
+        v.x = v.z = route_failed ? 0xFFFFFFFFu : (uint32_t)s_sel_idx[r];
+      } else {
+        const uint64_t bits = route_failed ? 0ull : __builtin_bit_cast(uint64_t, s_sel_v[r]);
+        v.x = (uint32_t)bits;
+        v.z = (uint32_t)(bits >> 32);
       }
-    } else if (w == 1) {
-      for (int e = lane; e < E; e += kWave) {
-        const int r = s_rank[e];
-        if (r < K) s_sel_v[r] = s_lv[e];
-      }
+      v.y = tag;
+      v.w = ~tag;
+      __builtin_amdgcn_raw_buffer_store_b128(v, rec_r, lane * 16, 0, 0);
     }
-    lds_barrier();
   }
   const int ex = route_failed ? 0 : uni(s_sel_idx[xcd]);  // this XCD's expert
 
   // ---- 2. this wave's weight copies ------------------------------------------
-  // gate/up pair c = i * qPerW + qq: half tile ht = htPer * rho + i (rows
-  // 8 ht .. 8 ht + 7 of I: row tile ht / 2, half ht % 2), quad qPerW * w + qq.
-  // A chunk holds the gate half's 32 operand units, the up half's, then
-  // their scales; lane (n, p) of the B operand reads unit 8p + n % 8 of the
-  // gate half for n < 8 and of the up half for n >= 8.  Down pair c: row
-  // tile tdPer * rho + w / 2, quad DN * (w % 2) + c.
+  // Gate/up pair c = 2 i + qq: half tile ht = htPer * rho + i (rows 8 ht ..
+  // 8 ht + 7 of I: row tile ht / 2, half ht % 2) and quad 2 w + qq.  A
+  // wave's gate/up staging holds the gate scales of its pairs (64 bytes
+  // each), the up scales, then per half tile the gate units of both quads
+  // (512 bytes each: unit 8p + r = row 8 (ht % 2) + r, part p) and the up
+  // units.  Down pair c: row tile tdPer * rho + w / 2, quad DN * (w % 2) + c;
+  // its staging holds the scales of the pairs (128 bytes each), then their
+  // 1 KiB nibble units.  Every copy is one instruction: a wave issues
+  // 2 + 2 htPer gate/up copies and 1 + DN down copies, scales first.
+  constexpr uint32_t kGuSc = GU * 64;  // bytes of one kind of gate/up scales
+  static_assert(qPerW == 2 && GU * 4 <= kWave && DN * 8 <= kWave, "one copy instruction per kind");
   const uint32_t s_gu = lds_addr(lds + L::gu) + (uint32_t)w * GU * kX8Chunk;
   const uint32_t s_dn = lds_addr(lds + L::dn) + (uint32_t)w * DN * kX8Chunk;
   const char* gu_w = lds + L::gu + w * GU * kX8Chunk;
@@ -1467,31 +1539,28 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
     const i32x4 us = buf_rsrc_words(reinterpret_cast<const char*>(a.up_sc) + (size_t)ex * gsc, gsc);
     const i32x4 dn = buf_rsrc_words(a.down_nib + (size_t)ex * dnib, dnib);
     const i32x4 ds = buf_rsrc_words(reinterpret_cast<const char*>(a.down_sc) + (size_t)ex * dsc, dsc);
-#pragma unroll
-    for (int c = 0; c < GU; ++c) {
-      const int ht = htPer * rho + c / qPerW;
-      const int q = qPerW * w + c % qPerW;
-      const uint32_t tq = (uint32_t)uni((ht / 2) * Kq + q);
-      const uint32_t slot = s_gu + (uint32_t)c * kX8Chunk;
-      if (lane < 32) {
-        // unit 8p + r of the half: row 8 (ht % 2) + r, part p of the 1 KiB unit
-        const uint32_t nv = (uint32_t)(16 * (lane / 8) + 8 * (ht % 2) + lane % 8) * 16u;
-        dma_b128_unseen(gn, slot, nv, tq * kQuadNibBytes);
-        dma_b128_unseen(un, slot + 512u, nv, tq * kQuadNibBytes);
-      }
-      if (lane < 4) {
-        const uint32_t sv = (uint32_t)(64 * (ht % 2) + 16 * lane);
-        dma_b128_unseen(gs, slot + 1024u, sv, tq * 128u);
-        dma_b128_unseen(us, slot + 1088u, sv, tq * 128u);
-      }
+    // scales: lane l < 4 GU takes 16 bytes (two rows) of pair l / 4
+    if (lane < GU * 4) {
+      const int c = lane / 4, ht = htPer * rho + c / 2;
+      const uint32_t off = (uint32_t)(((ht / 2) * Kq + 2 * w + c % 2) * 128 + 64 * (ht % 2) + 16 * (lane % 4));
+      dma_b128_unseen(gs, s_gu, off, 0u);
+      dma_b128_unseen(us, s_gu + kGuSc, off, 0u);
     }
+    // nibbles of half tile i: lane l takes unit l % 32 of quad 2 w + l / 32
+    const uint32_t unit = (uint32_t)(16 * ((lane % 32) / 8) + lane % 8) * 16u + (uint32_t)(lane / 32) * kQuadNibBytes;
 #pragma unroll
-    for (int c = 0; c < DN; ++c) {
-      const uint32_t tq = (uint32_t)uni((tdPer * rho + w / 2) * KqI + DN * (w % 2) + c);
-      const uint32_t slot = s_dn + (uint32_t)c * kX8Chunk;
-      dma_b128_unseen(dn, slot, (uint32_t)lane * 16u, tq * kQuadNibBytes);
-      if (lane < 8) dma_b128_unseen(ds, slot + 1024u, (uint32_t)lane * 16u, tq * 128u);
+    for (int i = 0; i < htPer; ++i) {
+      const int ht = htPer * rho + i;
+      const uint32_t soff = (uint32_t)uni(((ht / 2) * Kq + 2 * w) * kQuadNibBytes + 128 * (ht % 2));
+      dma_b128_unseen(gn, s_gu + 2 * kGuSc + (uint32_t)i * 2048u, unit, soff);
+      dma_b128_unseen(un, s_gu + 2 * kGuSc + (uint32_t)i * 2048u + 1024u, unit, soff);
     }
+    const uint32_t tq0 = (uint32_t)uni((tdPer * rho + w / 2) * KqI + DN * (w % 2));
+    if (lane < DN * 8) dma_b128_unseen(ds, s_dn, (uint32_t)lane * 16u, tq0 * 128u);
+#pragma unroll
+    for (int c = 0; c < DN; ++c)
+      dma_b128_unseen(dn, s_dn + (uint32_t)DN * 128u + (uint32_t)c * kQuadNibBytes, (uint32_t)lane * 16u,
+                      (tq0 + (uint32_t)c) * kQuadNibBytes);
   }
 
   // ---- routing outputs, while the copies land --------------------------------
@@ -1529,11 +1598,14 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
     for (int c = 0; c < GU; ++c) {
       const int i = c / qPerW;
       const int q = qPerW * w + c % qPerW;
-      wait_vmcnt_le((GU - 1 - c) * 4 + DN * 2);  // this pair's copies (the younger ones may fly)
-      poll_clobber();
-      const char* slot = gu_w + c * kX8Chunk;
-      const u32x4 gw = *reinterpret_cast<const u32x4*>(slot + (n >= 8 ? 512 : 0) + (8 * p + (n & 7)) * 16);
-      const uint2 dsv = *reinterpret_cast<const uint2*>(slot + 1024 + n * 8);
+      // this half tile's copies (the younger ones may fly)
+      if (c % qPerW == 0) {
+        wait_vmcnt_le(2 * (htPer - 1 - i) + 1 + DN);
+        poll_clobber();
+      }
+      const u32x4 gw = *reinterpret_cast<const u32x4*>(gu_w + 2 * kGuSc + i * 2048 + (n >= 8 ? 1024 : 0) +
+                                                        (c % qPerW) * 512 + (8 * p + (n & 7)) * 16);
+      const uint2 dsv = *reinterpret_cast<const uint2*>(gu_w + (n >= 8 ? kGuSc : 0) + c * 64 + (n & 7) * 8);
       if (n == 0) {
         const u32x4* xo = s_xop + (q * 4 + p) * 4;
         xa[0] = xo[0];
@@ -1600,9 +1672,8 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
     poll_clobber();
 #pragma unroll
     for (int c = 0; c < DN; ++c) {
-      const char* slot = dn_w + c * kX8Chunk;
-      const u32x4 wv = *reinterpret_cast<const u32x4*>(slot + lane * 16);
-      unpack_scales(*reinterpret_cast<const uint2*>(slot + 1024 + n * 8), dv[c]);
+      const u32x4 wv = *reinterpret_cast<const u32x4*>(dn_w + DN * 128 + c * kQuadNibBytes + lane * 16);
+      unpack_scales(*reinterpret_cast<const uint2*>(dn_w + c * 128 + n * 8), dv[c]);
       bb[c][0] = x8_dequant_f16s(wv.x);
       bb[c][1] = x8_dequant_f16s(wv.y);
       bb[c][2] = x8_dequant_f16s(wv.z);
