@@ -1195,9 +1195,9 @@ constexpr int kX8Xcds = 8;
 constexpr int kX8Grid = 256;
 constexpr int kX8PerXcd = kX8Grid / kX8Xcds;
 constexpr uint32_t kX8Chunk = 1152;  // 1 KiB of nibbles + 128 B of scales
-// Byte offset, in the logit-slot region, of the per-XCD routing records (the
-// device-scope logit slots come first; the records sit on pages of their own).
-constexpr uint32_t kX8RecOff = 8192;
+// Logit-slot region: the device-scope slots (E x 16 bytes, padded to
+// kX8CopyOff), then one copy of them per XCD in that XCD's L2.
+constexpr uint32_t kX8CopyOff = 4096;
 // Cache policy of a poll of data another CU of this XCD stored: SC0 (not
 // served by this CU's L1; this XCD's L2 holds the latest copy), with the
 // intrinsic's volatile bit as in kDevicePoll.
@@ -1219,7 +1219,7 @@ struct X8K {
   float* topk_w;
   uint32_t* ctl;
   uint64_t* presence;
-  uint32_t* xslots;  // [8][E][4] tagged logits, one array per XCD
+  uint32_t* xslots;  // [E][4] device-scope tagged logits, then [8][E][4] per-XCD copies
   uint32_t* xh;      // [8][I / 2][4] tagged h units
   uint32_t* xpart;   // [8][H / 2][4] tagged down partials (device scope)
   uint32_t wait_polls;
@@ -1297,8 +1297,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
   static_assert(tdPer * 2 == kFW && KqI % 2 == 0, "down: two waves per row tile, half of I each");
   static_assert(tdPer * kRowTile == kWave, "one partial row per lane of wave 0");
   static_assert(E <= kX8Grid && E % kWave == 0 && E * P <= kFThreads, "logits");
-  static_assert(kX8RecOff >= (uint32_t)E * 16 && kX8RecOff + kX8Xcds * 2 * K * 16 <= 16u * kX8Xcds * E,
-                "the records fit the slot region");
+  static_assert(kX8CopyOff >= (uint32_t)E * 16 && kX8CopyOff % 256 == 0, "the copies start on lines of their own");
   static_assert(htPer * 8 <= kWave && I / 2 <= kFThreads && yRows * K / 2 <= kWave && yRows <= kWave, "lanes");
   static_assert(L::bytes <= kFusedDynLdsMax, "LDS");
 
@@ -1332,15 +1331,14 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
   if (threadIdx.x == 0) s_hfail = 0;
   // Logit e is computed once, by wave 0 of workgroup e (the router's
   // fixed-order contract), and published device-scope in slot e.  Only the
-  // leader of each XCD (rank 0 on it) polls the slots, so 8 waves, not 256,
-  // hit their lines; it ranks the logits and publishes the selection to its
-  // XCD's L2 as a record of 2K tagged units (unit 2r: logit of slot r, unit
-  // 2r + 1: its expert, -1 when the leader's wait gave up), which the other
-  // workgroups of the XCD poll.
+  // leader of each XCD (rank 0 on it) polls those slots, so 8 waves, not
+  // 256, hit their lines; it stores each logit into its XCD's copy of the
+  // slots (L2) as soon as it sees it, and every other workgroup of the XCD
+  // polls that copy.  Every workgroup then ranks the logits itself.
   const bool leader = rho == 0;
   const BufRsrc lg_r = buf_rsrc(a.xslots, (uint32_t)(E * 16));
-  const BufRsrc rec_r = buf_rsrc(reinterpret_cast<const char*>(a.xslots) + kX8RecOff + xcd * (2 * K * 16),
-                                 (uint32_t)(2 * K * 16));
+  const BufRsrc cp_r = buf_rsrc(reinterpret_cast<const char*>(a.xslots) + kX8CopyOff + xcd * (E * 16),
+                                (uint32_t)(E * 16));
   if (w == 0 && b < E) {
     double logit = fixed_dot_bf16(a.x, a.W + (int64_t)b * H, H);
     if (a.bias) logit = logit + (double)a.bias[b];
@@ -1378,83 +1376,61 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
       s_xs[q * 4 + gi] = (sp[0] + sp[1]) + (sp[2] + sp[3]);
     }
   } else if (w == kFW - 1) {
-    // ---- 1. the leader polls the E logits, the others this XCD's record
+    // ---- 1. the E logits into LDS: the leader from the device-scope slots
+    // (each copied on into this XCD's L2 at once), the others from that copy
+    const uint32_t want = tag + a.skew_route;
+    constexpr int kNV = E / kWave;
+    bool done[kNV];
+#pragma unroll
+    for (int v = 0; v < kNV; ++v) done[v] = false;
     bool failed = false;
-    if (leader) {
-      const uint32_t want = tag + a.skew_route;
-      constexpr int kNV = E / kWave;
-      bool done[kNV];
+    for (uint32_t it = 0;; ++it) {
+      poll_clobber();
+      u32x4 sv[kNV];
 #pragma unroll
-      for (int v = 0; v < kNV; ++v) done[v] = false;
-      for (uint32_t it = 0;; ++it) {
-        poll_clobber();
-        u32x4 sv[kNV];
+      for (int v = 0; v < kNV; ++v)
+        if (!done[v])
+          sv[v] = leader ? __builtin_amdgcn_raw_buffer_load_b128(lg_r, (lane + v * kWave) * 16, 0, kDevicePoll)
+                         : __builtin_amdgcn_raw_buffer_load_b128(cp_r, (lane + v * kWave) * 16, 0, kXcdPoll);
+      bool all = true;
 #pragma unroll
-        for (int v = 0; v < kNV; ++v)
-          if (!done[v]) sv[v] = __builtin_amdgcn_raw_buffer_load_b128(lg_r, (lane + v * kWave) * 16, 0, kDevicePoll);
-        bool all = true;
-#pragma unroll
-        for (int v = 0; v < kNV; ++v) {
-          if (!done[v] && tag_ok(sv[v], want)) {
-            const double lv = __builtin_bit_cast(double, ((uint64_t)sv[v].z << 32) | sv[v].x);
-            s_lv[lane + v * kWave] = lv;
-            s_key[lane + v * kWave] = logit_key(lv);
-            done[v] = true;
-          }
-          all = all && done[v];
+      for (int v = 0; v < kNV; ++v) {
+        if (!done[v] && tag_ok(sv[v], want)) {
+          if (leader) __builtin_amdgcn_raw_buffer_store_b128(sv[v], cp_r, (lane + v * kWave) * 16, 0, 0);
+          const double lv = __builtin_bit_cast(double, ((uint64_t)sv[v].z << 32) | sv[v].x);
+          s_lv[lane + v * kWave] = lv;
+          s_key[lane + v * kWave] = logit_key(lv);
+          done[v] = true;
         }
-        if (__all(all)) break;
-        if (it >= a.wait_polls) {
-          failed = true;
-          if (lane == 0) set_status(a.ctl, kStatusRouteWait);
-          break;
-        }
+        all = all && done[v];
       }
-      for (int e = lane; e < E; e += kWave) s_rank[e] = 0;
-    } else {
-      const bool mine = lane < 2 * K;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      bool ok = !mine;
-      if (mine) {
-        v = __builtin_amdgcn_raw_buffer_load_b128(rec_r, lane * 16, 0, kXcdPoll);
-        ok = tag_ok(v, tag);
-      }
-      for (uint32_t it = 0;; ++it) {
-        if (__all(ok)) break;
-        if (it >= a.wait_polls) {
-          failed = true;
-          if (lane == 0) set_status(a.ctl, kStatusRouteWait);
-          break;
-        }
-        poll_clobber();
-        if (!ok) {
-          v = __builtin_amdgcn_raw_buffer_load_b128(rec_r, lane * 16, 0, kXcdPoll);
-          ok = tag_ok(v, tag);
-        }
-      }
-      if (!failed) {
-        if (mine && (lane & 1)) {
-          s_sel_idx[lane / 2] = (int)v.x;
-          if ((int)v.x < 0) failed = true;  // the leader's wait gave up
-        }
-        if (mine && !(lane & 1)) s_sel_v[lane / 2] = __builtin_bit_cast(double, ((uint64_t)v.z << 32) | v.x);
-        failed = __ballot(failed) != 0ull;
+      if (__all(all)) break;
+      if (it >= a.wait_polls) {
+        failed = true;
+        if (lane == 0) set_status(a.ctl, kStatusRouteWait);
+        break;
       }
     }
+    for (int e = lane; e < E; e += kWave) s_rank[e] = 0;
     if (lane == 0) s_pfail = failed ? 1 : 0;
   }
-  lds_barrier();  // every wave has read the generation; logits or the selection, x operand in LDS
+  lds_barrier();  // every wave has read the generation; logits and x operand in LDS
   if (threadIdx.x == 0) __hip_atomic_store(&a.presence[b], tag64(tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const bool route_failed = uni(s_pfail) != 0;
 
-  if (leader) {
+  {
     if (!route_failed) {
       // rank of logit e in wave_topk_row's order (value descending, NaN
       // last, ties to the lower index): the number of larger keys, counted
       // without branches by P threads per logit (keys j0 .. j0 + span are
-      // the same for the whole wave, so the LDS reads broadcast), plus the
-      // number of equal keys at lower indices; equal counts mean equal keys,
-      // so wave 0 finds those among the counts below K with ballots
+      // the same for the whole wave, so the LDS reads broadcast; all are
+      // issued before the first comparison), plus the number of equal keys
+      // at lower indices.  Sorted by key, position i has a count of at most
+      // i, equal to i unless it ties with an earlier one; so when exactly K
+      // logits have a count below K and those counts add up to K (K - 1) / 2,
+      // the counts are the ranks.  Otherwise (equal keys among the top K)
+      // wave 0 orders the equal counts by index with ballots (equal counts
+      // mean equal keys).
       constexpr int span = E / P;
       static_assert(E % P == 0 && E == 2 * kWave && K == 8, "two logits per lane of the selecting wave");
       if ((int)threadIdx.x < E * P) {
@@ -1462,15 +1438,34 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
         const int e = (int)threadIdx.x - pp * E;
         const uint64_t ke = s_key[e];
         const int j0 = pp * span;
+        uint64_t kk[span];
+#pragma unroll
+        for (int q = 0; q < span; ++q) kk[q] = s_key[j0 + q];
+        __builtin_amdgcn_sched_barrier(0);
         int cnt = 0;
 #pragma unroll
-        for (int q = 0; q < span; ++q) cnt += (int)(s_key[j0 + q] > ke);
+        for (int q = 0; q < span; ++q) cnt += (int)(kk[q] > ke);
         if (P == 1) s_rank[e] = cnt;
         else atomicAdd(&s_rank[e], cnt);
       }
       lds_barrier();
       if (w == 0) {
         const int c0 = s_rank[lane], c1 = s_rank[lane + kWave];
+        const uint64_t in0 = __ballot(c0 < K), in1 = __ballot(c1 < K);
+        int csum = 0;
+#pragma unroll
+        for (int bt = 0; bt < 3; ++bt)
+          csum += (__popcll(__ballot(c0 < K && ((c0 >> bt) & 1))) + __popcll(__ballot(c1 < K && ((c1 >> bt) & 1)))) << bt;
+        if (__popcll(in0) + __popcll(in1) == K && csum == K * (K - 1) / 2) {
+          if (c0 < K) {
+            s_sel_idx[c0] = lane;
+            s_sel_v[c0] = s_lv[lane];
+          }
+          if (c1 < K) {
+            s_sel_idx[c1] = lane + kWave;
+            s_sel_v[c1] = s_lv[lane + kWave];
+          }
+        } else {
         uint64_t m00 = __ballot(c0 < K), m01 = __ballot(c1 < K);  // half 0 / half 1 lanes with a count below K
         uint64_t m10 = m00, m11 = m01;
 #pragma unroll
@@ -1493,23 +1488,9 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
           s_sel_idx[r1] = lane + kWave;
           s_sel_v[r1] = s_lv[lane + kWave];
         }
+        }
       }
       lds_barrier();
-    }
-    if (w == 0 && lane < 2 * K) {
-      // this XCD's record (expert -1 when the leader's wait gave up)
-      const int r = lane / 2;
-      u32x4 v;
-      if (lane & 1) {
-        v.x = v.z = route_failed ? 0xFFFFFFFFu : (uint32_t)s_sel_idx[r];
-      } else {
-        const uint64_t bits = route_failed ? 0ull : __builtin_bit_cast(uint64_t, s_sel_v[r]);
-        v.x = (uint32_t)bits;
-        v.z = (uint32_t)(bits >> 32);
-      }
-      v.y = tag;
-      v.w = ~tag;
-      __builtin_amdgcn_raw_buffer_store_b128(v, rec_r, lane * 16, 0, 0);
     }
   }
   const int ex = route_failed ? 0 : uni(s_sel_idx[xcd]);  // this XCD's expert
