@@ -1504,7 +1504,10 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
   // units.  Down pair c: row tile tdPer * rho + w / 2, quad DN * (w % 2) + c;
   // its staging holds the scales of the pairs (128 bytes each), then their
   // 1 KiB nibble units.  Every copy is one instruction: a wave issues
-  // 2 + 2 htPer gate/up copies and 1 + DN down copies, scales first.
+  // 2 + 2 htPer gate/up copies here, scales first, and its 1 + DN down
+  // copies once its gate/up data has landed (they are needed only after the
+  // h hand-off, and issued with the gate/up copies they delayed them:
+  // 14.03 -> 13.82 us a layer).
   constexpr uint32_t kGuSc = GU * 64;  // bytes of one kind of gate/up scales
   static_assert(qPerW == 2 && GU * 4 <= kWave && DN * 8 <= kWave, "one copy instruction per kind");
   const uint32_t s_gu = lds_addr(lds + L::gu) + (uint32_t)w * GU * kX8Chunk;
@@ -1513,13 +1516,10 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
   const char* dn_w = lds + L::dn + w * DN * kX8Chunk;
   if (!route_failed) {
     constexpr uint32_t gnib = (uint32_t)I * Kq * 64u, gsc = (uint32_t)I * Kq * 8u;
-    constexpr uint32_t dnib = (uint32_t)H * KqI * 64u, dsc = (uint32_t)H * KqI * 8u;
     const i32x4 gn = buf_rsrc_words(a.gate_nib + (size_t)ex * gnib, gnib);
     const i32x4 un = buf_rsrc_words(a.up_nib + (size_t)ex * gnib, gnib);
     const i32x4 gs = buf_rsrc_words(reinterpret_cast<const char*>(a.gate_sc) + (size_t)ex * gsc, gsc);
     const i32x4 us = buf_rsrc_words(reinterpret_cast<const char*>(a.up_sc) + (size_t)ex * gsc, gsc);
-    const i32x4 dn = buf_rsrc_words(a.down_nib + (size_t)ex * dnib, dnib);
-    const i32x4 ds = buf_rsrc_words(reinterpret_cast<const char*>(a.down_sc) + (size_t)ex * dsc, dsc);
     // scales: lane l < 4 GU takes 16 bytes (two rows) of pair l / 4
     if (lane < GU * 4) {
       const int c = lane / 4, ht = htPer * rho + c / 2;
@@ -1536,12 +1536,6 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
       dma_b128_unseen(gn, s_gu + 2 * kGuSc + (uint32_t)i * 2048u, unit, soff);
       dma_b128_unseen(un, s_gu + 2 * kGuSc + (uint32_t)i * 2048u + 1024u, unit, soff);
     }
-    const uint32_t tq0 = (uint32_t)uni((tdPer * rho + w / 2) * KqI + DN * (w % 2));
-    if (lane < DN * 8) dma_b128_unseen(ds, s_dn, (uint32_t)lane * 16u, tq0 * 128u);
-#pragma unroll
-    for (int c = 0; c < DN; ++c)
-      dma_b128_unseen(dn, s_dn + (uint32_t)DN * 128u + (uint32_t)c * kQuadNibBytes, (uint32_t)lane * 16u,
-                      (tq0 + (uint32_t)c) * kQuadNibBytes);
   }
 
   // ---- routing outputs, while the copies land --------------------------------
@@ -1581,7 +1575,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
       const int q = qPerW * w + c % qPerW;
       // this half tile's copies (the younger ones may fly)
       if (c % qPerW == 0) {
-        wait_vmcnt_le(2 * (htPer - 1 - i) + 1 + DN);
+        wait_vmcnt_le(2 * (htPer - 1 - i));
         poll_clobber();
       }
       const u32x4 gw = *reinterpret_cast<const u32x4*>(gu_w + 2 * kGuSc + i * 2048 + (n >= 8 ? 1024 : 0) +
@@ -1604,6 +1598,18 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
       cg[i] = mfma_f32_16x16x4(sx, d[p], cg[i]);
 #pragma unroll
       for (int gi = 0; gi < 4; ++gi) ag[i] += d[gi] * pg[gi];
+    }
+    {
+      // this wave's down copies (see the copy section)
+      constexpr uint32_t dnib = (uint32_t)H * KqI * 64u, dsc = (uint32_t)H * KqI * 8u;
+      const i32x4 dn = buf_rsrc_words(a.down_nib + (size_t)ex * dnib, dnib);
+      const i32x4 ds = buf_rsrc_words(reinterpret_cast<const char*>(a.down_sc) + (size_t)ex * dsc, dsc);
+    const uint32_t tq0 = (uint32_t)uni((tdPer * rho + w / 2) * KqI + DN * (w % 2));
+    if (lane < DN * 8) dma_b128_unseen(ds, s_dn, (uint32_t)lane * 16u, tq0 * 128u);
+#pragma unroll
+    for (int c = 0; c < DN; ++c)
+      dma_b128_unseen(dn, s_dn + (uint32_t)DN * 128u + (uint32_t)c * kQuadNibBytes, (uint32_t)lane * 16u,
+                      (tq0 + (uint32_t)c) * kQuadNibBytes);
     }
     // lane (n, 0) holds result row 0 (the token) of column n: gate row n of
     // the half for n < 8, up row n - 8 for n >= 8
