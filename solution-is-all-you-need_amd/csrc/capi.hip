@@ -198,7 +198,7 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
     o_hv = take((size_t)16 * (size_t)((T * k + T) * (I / 2)));
   }
   if (x8) {
-    o_xsl = take((size_t)4096 + (size_t)16 * 8 * (size_t)E);  // device-scope slots, then one copy per XCD
+    o_xsl = take((size_t)256 * (size_t)E);  // device-scope logit slots, 256 bytes apart
     o_xh = take((size_t)16 * 8 * (size_t)(I / 2));
     o_xpt = take((size_t)16 * 8 * (size_t)(H / 2));
   }

@@ -1161,20 +1161,20 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
 // b, b + 8, b + 16, ... share an XCD, but the XCD the deal starts on varies
 // between launches (graph replays start elsewhere than eager launches): each
 // workgroup reads its XCD from the hardware XCC_ID register and takes
-// b / 8 as its rank on it.  Every hand-off but the last then stays inside
-// one XCD's L2 and moves a few KB:
-//   0. Each XCD computes all E logits itself (E / 32 per workgroup, one per
-//      wave, the router's fixed-order fp64 contract) and publishes them in
-//      its own slot array with plain stores, which land in the XCD's L2; one
-//      wave per workgroup polls them with L1-bypassing loads.  (In the
-//      generic kernel 256 workgroups poll one device-scope slot array, and
-//      the last poll ends about 2 us after the last logit is stored.)
-//   1. Ranks and weights exactly as the generic kernel computes them.
+// b / 8 as its rank on it.  Every hand-off after routing but the last then
+// stays inside one XCD's L2 and moves a few KB:
+//   0. Logit e is computed once, by wave 0 of workgroup e (the router's
+//      fixed-order fp64 contract), and published device-scope as a tagged
+//      slot; the slots sit kX8SlotStride bytes apart, so the polls of all
+//      256 workgroups spread over the memory channels.
+//   1. Every workgroup polls the E slots and ranks the logits (branch-free
+//      counts of larger keys, then equal keys ordered by index) and computes
+//      the weights exactly as the generic kernel does.
 //   2. The workgroup's weight copies, every wave its own share: gate/up in
 //      half tiles (8 rows of I of gate and the same 8 rows of up make one
 //      MFMA B operand, so the 96 half tiles of an expert are 3 per
-//      workgroup) over the 16 quads of H, then 4 row tiles of H of down over
-//      all of I.
+//      workgroup) over the 16 quads of H; then, once those have landed, 4
+//      row tiles of H of down over all of I.
 //   3. Gate/up as the generic kernel computes it (bf16 offset operands, the
 //      offset by one fp32 MFMA), the 8 waves' K-split partials summed in wave
 //      order, SwiGLU, and h stored to the XCD's L2 as tagged units
@@ -1185,7 +1185,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
 //   5. Down rows [64 rho, 64 rho + 64) of slot j's expert (rho = b / 8); the
 //      partial outputs go out device-scope as tagged units, and workgroup
 //      (j, rho) combines rows 64 rho + 8 j .. + 8 over the 8 slots in slot
-//      order, y = sum_j w_j d_j: the only cross-XCD hand-off.
+//      order, y = sum_j w_j d_j: the only cross-XCD hand-off after routing.
 // A workgroup that gives up a wait still publishes what the others wait for
 // (NaN values), so a failure costs one bounded wait, sets a status bit and
 // leaves NaN in the outputs it touches.
@@ -1195,9 +1195,11 @@ constexpr int kX8Xcds = 8;
 constexpr int kX8Grid = 256;
 constexpr int kX8PerXcd = kX8Grid / kX8Xcds;
 constexpr uint32_t kX8Chunk = 1152;  // 1 KiB of nibbles + 128 B of scales
-// Logit-slot region: the device-scope slots (E x 16 bytes, padded to
-// kX8CopyOff), then one copy of them per XCD in that XCD's L2.
-constexpr uint32_t kX8CopyOff = 4096;
+// Byte stride of the device-scope logit slots.  Every workgroup polls all
+// of them; slots 16 bytes apart put all those polls on a few memory
+// channels (C1 13.95 us a layer, against 13.63 at 256 bytes and 13.82 with
+// one poller per XCD relaying the logits through its L2).
+constexpr uint32_t kX8SlotStride = 256;
 // Cache policy of a poll of data another CU of this XCD stored: SC0 (not
 // served by this CU's L1; this XCD's L2 holds the latest copy), with the
 // intrinsic's volatile bit as in kDevicePoll.
@@ -1219,7 +1221,7 @@ struct X8K {
   float* topk_w;
   uint32_t* ctl;
   uint64_t* presence;
-  uint32_t* xslots;  // [E][4] device-scope tagged logits, then [8][E][4] per-XCD copies
+  uint32_t* xslots;  // [E] device-scope tagged logits, kX8SlotStride bytes apart
   uint32_t* xh;      // [8][I / 2][4] tagged h units
   uint32_t* xpart;   // [8][H / 2][4] tagged down partials (device scope)
   uint32_t wait_polls;
@@ -1297,7 +1299,6 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
   static_assert(tdPer * 2 == kFW && KqI % 2 == 0, "down: two waves per row tile, half of I each");
   static_assert(tdPer * kRowTile == kWave, "one partial row per lane of wave 0");
   static_assert(E <= kX8Grid && E % kWave == 0 && E * P <= kFThreads, "logits");
-  static_assert(kX8CopyOff >= (uint32_t)E * 16 && kX8CopyOff % 256 == 0, "the copies start on lines of their own");
   static_assert(htPer * 8 <= kWave && I / 2 <= kFThreads && yRows * K / 2 <= kWave && yRows <= kWave, "lanes");
   static_assert(L::bytes <= kFusedDynLdsMax, "LDS");
 
@@ -1330,15 +1331,9 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
       (uint32_t)uni((int)__hip_atomic_load(&a.ctl[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) + 1u;
   if (threadIdx.x == 0) s_hfail = 0;
   // Logit e is computed once, by wave 0 of workgroup e (the router's
-  // fixed-order contract), and published device-scope in slot e.  Only the
-  // leader of each XCD (rank 0 on it) polls those slots, so 8 waves, not
-  // 256, hit their lines; it stores each logit into its XCD's copy of the
-  // slots (L2) as soon as it sees it, and every other workgroup of the XCD
-  // polls that copy.  Every workgroup then ranks the logits itself.
-  const bool leader = rho == 0;
-  const BufRsrc lg_r = buf_rsrc(a.xslots, (uint32_t)(E * 16));
-  const BufRsrc cp_r = buf_rsrc(reinterpret_cast<const char*>(a.xslots) + kX8CopyOff + xcd * (E * 16),
-                                (uint32_t)(E * 16));
+  // fixed-order contract), and published device-scope in slot e; every
+  // workgroup polls all E slots and ranks the logits itself.
+  const BufRsrc lg_r = buf_rsrc(a.xslots, (uint32_t)(E * kX8SlotStride));
   if (w == 0 && b < E) {
     double logit = fixed_dot_bf16(a.x, a.W + (int64_t)b * H, H);
     if (a.bias) logit = logit + (double)a.bias[b];
@@ -1349,7 +1344,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
       v.y = tag;
       v.z = (uint32_t)(bits >> 32);
       v.w = ~tag;
-      __builtin_amdgcn_raw_buffer_store_b128(v, lg_r, b * 16, 0, kDeviceScope);
+      __builtin_amdgcn_raw_buffer_store_b128(v, lg_r, b * kX8SlotStride, 0, kDeviceScope);
     }
   } else if (w == 4) {
     // the MFMA-ordered x operand and its group sums, as the generic kernel
@@ -1376,8 +1371,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
       s_xs[q * 4 + gi] = (sp[0] + sp[1]) + (sp[2] + sp[3]);
     }
   } else if (w == kFW - 1) {
-    // ---- 1. the E logits into LDS: the leader from the device-scope slots
-    // (each copied on into this XCD's L2 at once), the others from that copy
+    // ---- 1. the E logits into LDS
     const uint32_t want = tag + a.skew_route;
     constexpr int kNV = E / kWave;
     bool done[kNV];
@@ -1390,13 +1384,11 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
 #pragma unroll
       for (int v = 0; v < kNV; ++v)
         if (!done[v])
-          sv[v] = leader ? __builtin_amdgcn_raw_buffer_load_b128(lg_r, (lane + v * kWave) * 16, 0, kDevicePoll)
-                         : __builtin_amdgcn_raw_buffer_load_b128(cp_r, (lane + v * kWave) * 16, 0, kXcdPoll);
+          sv[v] = __builtin_amdgcn_raw_buffer_load_b128(lg_r, (lane + v * kWave) * kX8SlotStride, 0, kDevicePoll);
       bool all = true;
 #pragma unroll
       for (int v = 0; v < kNV; ++v) {
         if (!done[v] && tag_ok(sv[v], want)) {
-          if (leader) __builtin_amdgcn_raw_buffer_store_b128(sv[v], cp_r, (lane + v * kWave) * 16, 0, 0);
           const double lv = __builtin_bit_cast(double, ((uint64_t)sv[v].z << 32) | sv[v].x);
           s_lv[lane + v * kWave] = lv;
           s_key[lane + v * kWave] = logit_key(lv);

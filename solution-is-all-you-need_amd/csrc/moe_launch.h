@@ -68,7 +68,7 @@ struct FusedWs {
   uint32_t* slots = nullptr;     // [T * E][4] tagged logits
   uint32_t* hv = nullptr;        // [T*k + T][I / 2][4] tagged h units (fp16 hi/lo of two rows)
   // the per-XCD kernel's (null unless x8_shape)
-  uint32_t* xslots = nullptr;  // [E][4] tagged logits (4096 bytes), then [8][E][4] per-XCD copies
+  uint32_t* xslots = nullptr;  // [E] tagged logits, 256 bytes apart
   uint32_t* xh = nullptr;      // [8][I / 2][4] tagged h units
   uint32_t* xpart = nullptr;   // [8][H / 2][4] tagged down partials
 };
