@@ -363,36 +363,54 @@ __device__ void wave_topk(const RouteK& a, int64_t t, uint64_t* s_ck, double* s_
 // chunk (p, gi) of quad q holds elements kmap(p, 0..7) of group 4q + gi, read
 // as two 8-byte runs (4p..4p+3 and 4p+16..4p+19).  A group's sum adds its
 // four parts' 8-element sums by an xor butterfly over p (lanes 4 and 8 apart).
+// A thread's chunks come kPrepBatch at a time, all their loads issued before
+// the first store: the compiler cannot move a load of x above a store to the
+// copy (it cannot prove they do not alias), so a chunk at a time paid one
+// memory round trip per chunk (16 of them per thread for 4096 tokens).
+constexpr int kPrepBatch = 8;
 __device__ void prep_x_tile(const RouteK& a, int64_t t0, int TT) {
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
   const int Kg = (int)(a.H / kGroup);
   const int per_tok = (int)a.Kq * 16;
   const int n = TT * per_tok;
   const int lane = threadIdx.x % kWave;
+  const int stride = (int)(gridDim.x * blockDim.x);
   const int wave0 = (int)(blockIdx.x * blockDim.x) + (int)(threadIdx.x / kWave) * kWave;
-  for (int c0 = wave0; c0 < n; c0 += (int)(gridDim.x * blockDim.x)) {  // wave-uniform
-    const int c = c0 + lane;
-    const int ti = c / per_tok;
-    const int cc = c - ti * per_tok;
-    const int64_t t = t0 + ti;
-    const bool valid = c < n && t < a.T;
-    const int gi = cc & 3;
-    const int p = (cc >> 2) & 3;
-    const int g = 4 * (cc >> 4) + gi;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    float sum = 0.0f;
-    if (valid && g < Kg) {
-      const uint16_t* xr = x + t * a.H + (int64_t)g * kGroup + 4 * p;
-      const uint2 lo = *reinterpret_cast<const uint2*>(xr);
-      const uint2 hi = *reinterpret_cast<const uint2*>(xr + 16);
-      v.x = (lo.x & 0xffffu) | (lo.y << 16);
-      v.y = (hi.x & 0xffffu) | (hi.y << 16);
-      v.z = (lo.x >> 16) | (lo.y & 0xffff0000u);
-      v.w = (hi.x >> 16) | (hi.y & 0xffff0000u);
-      sum = ((bf16_bits_to_float(lo.x & 0xffffu) + bf16_bits_to_float(lo.x >> 16)) +
-             (bf16_bits_to_float(lo.y & 0xffffu) + bf16_bits_to_float(lo.y >> 16))) +
-            ((bf16_bits_to_float(hi.x & 0xffffu) + bf16_bits_to_float(hi.x >> 16)) +
-             (bf16_bits_to_float(hi.y & 0xffffu) + bf16_bits_to_float(hi.y >> 16)));
+  for (int c00 = wave0; c00 < n; c00 += kPrepBatch * stride) {  // wave-uniform
+    uint2 lo[kPrepBatch], hi[kPrepBatch];
+#pragma unroll
+    for (int u = 0; u < kPrepBatch; ++u) {
+      const int c = c00 + u * stride + lane;
+      const int ti = c / per_tok;
+      const int cc = c - ti * per_tok;
+      const int64_t t = t0 + ti;
+      const int g = 4 * (cc >> 4) + (cc & 3);
+      lo[u] = hi[u] = make_uint2(0u, 0u);
+      if (c < n && t < a.T && g < Kg) {
+        const uint16_t* xr = x + t * a.H + (int64_t)g * kGroup + 4 * ((cc >> 2) & 3);
+        lo[u] = *reinterpret_cast<const uint2*>(xr);
+        hi[u] = *reinterpret_cast<const uint2*>(xr + 16);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kPrepBatch; ++u) {
+      const int c = c00 + u * stride + lane;
+      const int ti = c / per_tok;
+      const int cc = c - ti * per_tok;
+      const int64_t t = t0 + ti;
+      const bool valid = c < n && t < a.T;
+      const int gi = cc & 3;
+      const int p = (cc >> 2) & 3;
+      const int g = 4 * (cc >> 4) + gi;
+      u32x4 v;
+      v.x = (lo[u].x & 0xffffu) | (lo[u].y << 16);
+      v.y = (hi[u].x & 0xffffu) | (hi[u].y << 16);
+      v.z = (lo[u].x >> 16) | (lo[u].y & 0xffff0000u);
+      v.w = (hi[u].x >> 16) | (hi[u].y & 0xffff0000u);
+      float sum = ((bf16_bits_to_float(lo[u].x & 0xffffu) + bf16_bits_to_float(lo[u].x >> 16)) +
+                   (bf16_bits_to_float(lo[u].y & 0xffffu) + bf16_bits_to_float(lo[u].y >> 16))) +
+                  ((bf16_bits_to_float(hi[u].x & 0xffffu) + bf16_bits_to_float(hi[u].x >> 16)) +
+                   (bf16_bits_to_float(hi[u].y & 0xffffu) + bf16_bits_to_float(hi[u].y >> 16)));
       if (a.prep_fp16) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -401,12 +419,12 @@ __device__ void prep_x_tile(const RouteK& a, int64_t t0, int TT) {
                  (float_to_half_bits(bf16_bits_to_float(b2 >> 16)) << 16);
         }
       }
-    }
-    sum += __shfl_xor(sum, 4, kWave);
-    sum += __shfl_xor(sum, 8, kWave);
-    if (valid) {
-      *reinterpret_cast<u32x4*>(a.xq + (t * per_tok + cc) * 8) = v;
-      if (p == 0) a.xs[t * a.Kq * 4 + g] = sum;
+      sum += __shfl_xor(sum, 4, kWave);
+      sum += __shfl_xor(sum, 8, kWave);
+      if (valid) {
+        *reinterpret_cast<u32x4*>(a.xq + (t * per_tok + cc) * 8) = v;
+        if (p == 0) a.xs[t * a.Kq * 4 + g] = sum;
+      }
     }
   }
 }
@@ -751,10 +769,10 @@ __global__ __launch_bounds__(256) void route_logits_big_kernel(RouteK a) {
 // take every expert as a candidate (the full exact row), so NaN and inf
 // follow the contract exactly as on the one-pass path.
 constexpr int kApproxTok = 64;     // tokens per approx workgroup (4 waves x 16)
-constexpr int kApproxExp = 32;     // experts per approx workgroup (2 tiles of 16)
+constexpr int kApproxExp = 16;     // experts per approx workgroup (one tile of 16; 512 workgroups at E 128)
 constexpr int kApproxChunk = 256;  // K staged in LDS per step
 constexpr int kApproxUnits = kApproxExp * kApproxChunk / 8 / 256;  // 8-wide W units per thread per chunk
-constexpr int kExactTok = 256;     // tokens scanned per exact workgroup
+constexpr int kExactTok = 1024;    // tokens scanned per exact workgroup (a multiple of 256)
 constexpr int kExactP = 16;        // token pairs per wave pass
 
 __global__ __launch_bounds__(256) void route_approx_kernel(RouteK a, float* approx, float* nx, float* nw) {
@@ -934,25 +952,33 @@ __global__ __launch_bounds__(256) void route_candidates_kernel(RouteK a, const f
 // token): lane l sums, for each token, the h with (h mod 256) / 4 == l in
 // increasing h, with its slice of the weight row loaded once for the 16.
 __global__ __launch_bounds__(256) void route_exact_kernel(RouteK a, const uint8_t* cand) {
+  constexpr int kSub = kExactTok / 256;  // 256-token sub-blocks, one token per thread each
   __shared__ int s_tok[kExactTok];
-  __shared__ int s_cnt[4];
+  __shared__ int s_cnt[4 * kSub];
   const int lane = threadIdx.x % kWave;
   const int w = threadIdx.x / kWave;
   const int e = blockIdx.y;
   const int64_t t0 = (int64_t)blockIdx.x * kExactTok;
-  // compaction in token order: wave w takes tokens t0 + 64 w + lane
-  const int64_t t = t0 + 64 * w + lane;
-  const bool c = t < a.T && cand[(int64_t)e * a.T + t] != 0;
-  const uint64_t m = __ballot(c);
-  if (lane == 0) s_cnt[w] = __popcll(m);
-  __syncthreads();
-  int base = 0, n = 0;
+  // compaction in token order: in sub-block sb, wave w takes tokens
+  // t0 + 256 sb + 64 w + lane
+  bool c[kSub];
+  uint64_t m[kSub];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    base += i < w ? s_cnt[i] : 0;
-    n += s_cnt[i];
+  for (int sb = 0; sb < kSub; ++sb) {
+    const int64_t t = t0 + 256 * sb + 64 * w + lane;
+    c[sb] = t < a.T && cand[(int64_t)e * a.T + t] != 0;
+    m[sb] = __ballot(c[sb]);
+    if (lane == 0) s_cnt[sb * 4 + w] = __popcll(m[sb]);
   }
-  if (c) s_tok[base + __popcll(m & ((1ull << lane) - 1ull))] = (int)(t - t0);
+  __syncthreads();
+  int n = 0;
+  for (int i = 0; i < 4 * kSub; ++i) n += s_cnt[i];
+#pragma unroll
+  for (int sb = 0; sb < kSub; ++sb) {
+    int base = 0;
+    for (int i = 0; i < sb * 4 + w; ++i) base += s_cnt[i];
+    if (c[sb]) s_tok[base + __popcll(m[sb] & ((1ull << lane) - 1ull))] = 256 * sb + 64 * w + lane;
+  }
   __syncthreads();
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
   const float* wrow = a.W + (int64_t)e * a.H;
@@ -964,16 +990,28 @@ __global__ __launch_bounds__(256) void route_exact_kernel(RouteK a, const uint8_
     double acc[kExactP];
 #pragma unroll
     for (int j = 0; j < kExactP; ++j) acc[j] = 0.0;
+    // the loads of chunk h0 + 256 are issued before chunk h0's FMAs
+    float4 wn = make_float4(0.f, 0.f, 0.f, 0.f);
+    uint2 xn[kExactP];
+    auto load = [&](int64_t h0) {
+      wn = *reinterpret_cast<const float4*>(wrow + h0);
+#pragma unroll
+      for (int j = 0; j < kExactP; ++j) xn[j] = *reinterpret_cast<const uint2*>(x + tk[j] * a.H + h0);
+    };
+    if (4 * lane < a.H) load(4 * lane);
     for (int64_t h0 = 4 * lane; h0 < a.H; h0 += 256) {
-      const float4 wv = *reinterpret_cast<const float4*>(wrow + h0);
+      const float4 wv = wn;
+      uint2 xv[kExactP];
+#pragma unroll
+      for (int j = 0; j < kExactP; ++j) xv[j] = xn[j];
+      if (h0 + 256 < a.H) load(h0 + 256);
       const double wd[4] = {(double)wv.x, (double)wv.y, (double)wv.z, (double)wv.w};
 #pragma unroll
       for (int j = 0; j < kExactP; ++j) {
-        const uint2 xv = *reinterpret_cast<const uint2*>(x + tk[j] * a.H + h0);
-        acc[j] += (double)bf16_bits_to_float(xv.x & 0xffffu) * wd[0];
-        acc[j] += (double)bf16_bits_to_float(xv.x >> 16) * wd[1];
-        acc[j] += (double)bf16_bits_to_float(xv.y & 0xffffu) * wd[2];
-        acc[j] += (double)bf16_bits_to_float(xv.y >> 16) * wd[3];
+        acc[j] += (double)bf16_bits_to_float(xv[j].x & 0xffffu) * wd[0];
+        acc[j] += (double)bf16_bits_to_float(xv[j].x >> 16) * wd[1];
+        acc[j] += (double)bf16_bits_to_float(xv[j].y & 0xffffu) * wd[2];
+        acc[j] += (double)bf16_bits_to_float(xv[j].y >> 16) * wd[3];
       }
     }
     const double tot = tree_reduce_pairs<kExactP>(acc);
