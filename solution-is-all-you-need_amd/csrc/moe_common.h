@@ -55,14 +55,13 @@ __host__ __device__ inline int kmap(int p, int j) {
   return 4 * p + off[j];
 }
 
-// (a & m) | c in one VOP3 instruction.  gfx9 VOP3 reads at most one scalar
-// or literal operand, so the mask comes in a VGPR (hoisted out of loops by
-// the caller) and the constant in an SGPR.
-__device__ inline uint32_t and_or(uint32_t a, uint32_t m_vgpr, uint32_t c_sgpr) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m_vgpr), "s"(c_sgpr));
-  return r;
-}
+// (a & m) | c, which the compiler forms as one v_and_or_b32 (gfx9 VOP3
+// reads at most one scalar or literal operand, so the caller keeps the mask
+// in a VGPR, hoisted out of loops).  Written as an expression, not inline
+// assembly: the compiler's hazard checks do not see inline assembly, and an
+// inline v_and_or_b32 placed next to in-flight MFMAs has produced wrong
+// results (NaN outputs) once a change of register allocation put it there.
+__device__ inline uint32_t and_or(uint32_t a, uint32_t m_vgpr, uint32_t c_sgpr) { return (a & m_vgpr) | c_sgpr; }
 
 // 4 qs bytes (little endian word) -> 8 bf16 values 1 + n/16, in kmap order.
 // mask must hold 0x00780078 (in a VGPR).
@@ -85,7 +84,6 @@ __device__ inline u32x4 dequant_unit_f16(uint32_t w, uint32_t mask) {
   return r;
 }
 
-// A value the compiler must keep in a VGPR (for and_or masks).
 // A pointer the compiler cannot prove wave-uniform, made uniform (it must
 // already hold the same value in every lane), so loads from it plus a 32-bit
 // lane offset use the SGPR-base form.
@@ -97,10 +95,13 @@ __device__ inline const T* uniform_ptr(const T* p) {
   return reinterpret_cast<const T*>(((uint64_t)hi << 32) | lo);
 }
 
+// A value the compiler must keep in a VGPR (for and_or masks).  The empty
+// assembly statement emits no instruction: the compiler moves the constant
+// into the VGPR itself (so its hazard checks see the write) and can no longer
+// fold it, which keeps and_or a single v_and_or_b32.
 __device__ inline uint32_t vgpr_const(uint32_t v) {
-  uint32_t r;
-  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "s"(v));
-  return r;
+  asm volatile("" : "+v"(v));
+  return v;
 }
 
 __device__ inline f32x4 mfma_bf16_16x16x32(u32x4 a, u32x4 b, f32x4 c) {
