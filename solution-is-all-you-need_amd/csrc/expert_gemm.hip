@@ -183,9 +183,11 @@ struct TileCoord {
   int64_t nb;
 };
 
+// half >= 0: only positions [BM / 2 half, BM / 2 (half + 1)) of the block.
 template <int BM>
 __device__ inline TileCoord tile_coord(const GemmK& a, const int4* s_desc, const int* s_mb, int n_act,
-                                       const XcdPlan& xp, int64_t item, int64_t n_nb, int64_t* s_row) {
+                                       const XcdPlan& xp, int64_t item, int64_t n_nb, int64_t* s_row,
+                                       int half = -1) {
   TileCoord c;
   const int64_t mb = xp.b0 + item / n_nb;
   c.nb = item % n_nb;
@@ -194,6 +196,10 @@ __device__ inline TileCoord tile_coord(const GemmK& a, const int4* s_desc, const
   c.e = __builtin_amdgcn_readfirstlane(d.x);
   c.m0 = (int64_t)d.y + (mb - s_mb[u]) * BM;
   c.end = d.z;
+  if (half >= 0) {
+    c.m0 += (int64_t)half * (BM / 2);
+    c.end = c.end < c.m0 + BM / 2 ? c.end : c.m0 + BM / 2;
+  }
   if (threadIdx.x < BM) {
     const int64_t pos = c.m0 + threadIdx.x;
     int64_t row = a.a_zero_row;
@@ -433,8 +439,19 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_gate_up_kernel(GemmK a)
   const int64_t n_nb = ceil_div(a.N, kRows);
   const XcdPlan xp = xcd_plan(n_mb, n_nb);
   const uint32_t nib_bytes = (uint32_t)(a.N * a.Kq * 64), sc_bytes = (uint32_t)(a.N * a.Kq * 8);
-  for (int64_t item = xp.l; item < xp.n_items; item += xp.nl) {
-    const TileCoord c = tile_coord<BM>(a, a.seg.desc, s_mb, n_act, xp, item, n_nb, s_row);
+  // The XCD's items end in a partial round of r = n_items % nl items, which
+  // r of its nl workgroups run while the rest idle.  When 2 r <= nl those r
+  // items run as 2 r halves of BM / 2 positions each (still the XCD's last
+  // items, so their weights are the ones in its L2): the last round then
+  // takes about half an item (at 4096 tokens 8 -> 7.5 item times).
+  const int64_t r_last = xp.n_items % xp.nl;
+  const int64_t n_split = (r_last > 0 && 2 * r_last <= xp.nl) ? r_last : 0;
+  const int64_t n_whole = xp.n_items - n_split;
+  for (int64_t ent = xp.l; ent < xp.n_items + n_split; ent += xp.nl) {
+    const int64_t item = ent < n_whole ? ent : n_whole + (ent - n_whole) / 2;
+    const int part = ent < n_whole ? -1 : (int)((ent - n_whole) % 2);
+    const TileCoord c = tile_coord<BM>(a, a.seg.desc, s_mb, n_act, xp, item, n_nb, s_row, part);
+    if (c.m0 >= c.end) continue;  // the empty second half of a block of <= BM / 2 positions
     const int64_t n_tiles = a.N / kRowTile;
     const int64_t t = c.nb * kG2Waves + w;
     const int64_t tc = t < n_tiles ? t : n_tiles - 1;  // a tile past I computes, unstored
