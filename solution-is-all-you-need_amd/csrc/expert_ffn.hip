@@ -907,7 +907,11 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
       }
       float4 o[KB];
 #pragma unroll
-      for (int jj = 0; jj < KB; ++jj) o[jj] = *reinterpret_cast<const float4*>(outbuf + pos[jj] * H + c);
+      for (int jj = 0; jj < KB; ++jj) {
+        // read once: nontemporal, so the stream does not displace cached lines
+        const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(outbuf + pos[jj] * H + c));
+        o[jj] = make_float4(v[0], v[1], v[2], v[3]);
+      }
 #pragma unroll
       for (int jj = 0; jj < KB; ++jj) {
         if (j0 + jj < k) {
@@ -925,7 +929,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
       acc.z += o.z;
       acc.w += o.w;
     }
-    *reinterpret_cast<float4*>(y + t * H + c) = acc;
+    __builtin_nontemporal_store(f32x4{acc.x, acc.y, acc.z, acc.w}, reinterpret_cast<f32x4*>(y + t * H + c));
   }
 }
 
