@@ -1516,8 +1516,8 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
     if (lane < GU * 4) {
       const int c = lane / 4, ht = htPer * rho + c / 2;
       const uint32_t off = (uint32_t)(((ht / 2) * Kq + 2 * w + c % 2) * 128 + 64 * (ht % 2) + 16 * (lane % 4));
-      dma_b128_unseen(gs, s_gu, off, 0u);
-      dma_b128_unseen(us, s_gu + kGuSc, off, 0u);
+      dma_b128_stream(gs, s_gu, off, 0u);
+      dma_b128_stream(us, s_gu + kGuSc, off, 0u);
     }
     // nibbles of half tile i: lane l takes unit l % 32 of quad 2 w + l / 32
     const uint32_t unit = (uint32_t)(16 * ((lane % 32) / 8) + lane % 8) * 16u + (uint32_t)(lane / 32) * kQuadNibBytes;
@@ -1525,8 +1525,8 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
     for (int i = 0; i < htPer; ++i) {
       const int ht = htPer * rho + i;
       const uint32_t soff = (uint32_t)uni(((ht / 2) * Kq + 2 * w) * kQuadNibBytes + 128 * (ht % 2));
-      dma_b128_unseen(gn, s_gu + 2 * kGuSc + (uint32_t)i * 2048u, unit, soff);
-      dma_b128_unseen(un, s_gu + 2 * kGuSc + (uint32_t)i * 2048u + 1024u, unit, soff);
+      dma_b128_stream(gn, s_gu + 2 * kGuSc + (uint32_t)i * 2048u, unit, soff);
+      dma_b128_stream(un, s_gu + 2 * kGuSc + (uint32_t)i * 2048u + 1024u, unit, soff);
     }
   }
 
@@ -1597,10 +1597,10 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
       const i32x4 dn = buf_rsrc_words(a.down_nib + (size_t)ex * dnib, dnib);
       const i32x4 ds = buf_rsrc_words(reinterpret_cast<const char*>(a.down_sc) + (size_t)ex * dsc, dsc);
     const uint32_t tq0 = (uint32_t)uni((tdPer * rho + w / 2) * KqI + DN * (w % 2));
-    if (lane < DN * 8) dma_b128_unseen(ds, s_dn, (uint32_t)lane * 16u, tq0 * 128u);
+    if (lane < DN * 8) dma_b128_stream(ds, s_dn, (uint32_t)lane * 16u, tq0 * 128u);
 #pragma unroll
     for (int c = 0; c < DN; ++c)
-      dma_b128_unseen(dn, s_dn + (uint32_t)DN * 128u + (uint32_t)c * kQuadNibBytes, (uint32_t)lane * 16u,
+      dma_b128_stream(dn, s_dn + (uint32_t)DN * 128u + (uint32_t)c * kQuadNibBytes, (uint32_t)lane * 16u,
                       (tq0 + (uint32_t)c) * kQuadNibBytes);
     }
     // lane (n, 0) holds result row 0 (the token) of column n: gate row n of

@@ -233,6 +233,14 @@ __device__ inline uint32_t lds_addr(const void* p) {
   return (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p);
 }
 
+// The same copy with the nontemporal hint (nt), for weights streamed once per
+// call: the batch-1 layer reads each selected expert once, and the hint keeps
+// that stream from displacing cached lines (C1 13.6 -> 13.1 us a layer).
+__device__ inline void dma_b128_stream(const i32x4& r, uint32_t lds_byte, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+               :: "s"(lds_byte), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
+}
+
 __device__ inline void dma_b128_unseen(const i32x4& r, uint32_t lds_byte, uint32_t voff, uint32_t soff) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :: "s"(lds_byte), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
