@@ -159,8 +159,8 @@ __device__ __attribute__((always_inline)) inline void gu_load(const GateUpK& a, 
     const char* usb = uniform_ptr(reinterpret_cast<const char*>(usc) + tq * kQuadScales * 2);
     // explicitly global: the routed / shared pointer select would make these
     // flat loads, after which every wait is a wait for all outstanding loads
-    c.gw[r] = gload<u32x4>(gb + o_nib);
-    c.uw[r] = gload<u32x4>(ub + o_nib);
+    c.gw[r] = gload_nt<u32x4>(gb + o_nib);
+    c.uw[r] = gload_nt<u32x4>(ub + o_nib);
     c.gs[r] = gload_u2(gsb + o_sc);
     c.us[r] = gload_u2(usb + o_sc);
   }
@@ -345,8 +345,8 @@ __device__ __attribute__((always_inline)) inline void wchunk_load(const WSrc& s,
   const int lane = threadIdx.x % kWave;
   const uint32_t o_nib = (uint32_t)lane * 16u;
   const uint32_t o_sc = (uint32_t)(lane % 16) * 8u;
-  c.gw = buf_load_b128(s.g, o_nib, tq * kQuadNibBytes);
-  c.uw = buf_load_b128(s.u, o_nib, tq * kQuadNibBytes);
+  c.gw = buf_load_b128_nt(s.g, o_nib, tq * kQuadNibBytes);
+  c.uw = buf_load_b128_nt(s.u, o_nib, tq * kQuadNibBytes);
   c.gs = buf_load_b64(s.gs, o_sc, tq * (kQuadScales * 2));
   c.us = buf_load_b64(s.us, o_sc, tq * (kQuadScales * 2));
 }
@@ -644,7 +644,7 @@ __device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt0
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
           const int64_t tq = (rt0 + r) * a.Kq + q;  // wave-uniform
-          bw[i][r] = *reinterpret_cast<const u32x4*>(dnib + (tq * kWave + lane) * 16);
+          bw[i][r] = gload_nt<u32x4>(dnib + (tq * kWave + lane) * 16);
           bs[i][r] = *reinterpret_cast<const uint2*>(dsc + tq * kQuadScales + n * 4);
         }
         const u32x4* src = reinterpret_cast<const u32x4*>(a.hq + ((pm * a.Kq + q) * 16 + p * 4) * 16);
@@ -796,7 +796,7 @@ __device__ __attribute__((always_inline)) inline void down_tile_job(const DownK&
   };
   auto load = [&](DChunk& c) {
     const uint32_t tq = (uint32_t)__builtin_amdgcn_readfirstlane((int)((rt0 + NW * li) * Kq + lq));
-    c.w = buf_load_b128(wr, (uint32_t)lane * 16u, tq * kQuadNibBytes);
+    c.w = buf_load_b128_nt(wr, (uint32_t)lane * 16u, tq * kQuadNibBytes);
     c.s = buf_load_b64(sr, (uint32_t)n * 8u, tq * (kQuadScales * 2));
   };
   DChunk buf[D];

@@ -180,6 +180,20 @@ __device__ inline uint2 buf_load_b64(BufRsrc r, uint32_t voff, uint32_t soff) {
   return make_uint2(v[0], v[1]);
 }
 
+// Weight loads with the nontemporal hint (cache policy nt): a decode step
+// streams each active expert's weights once, and without the hint that
+// stream displaces the lines its hand-offs and activations reuse (C2 59.4 ->
+// 57.4 us, Mixtral T = 1 77.4 -> 73.8, DSV3 T = 1 91.5 -> 86.1).
+constexpr int kLoadNt = 2;
+__device__ inline u32x4 buf_load_b128_nt(BufRsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kLoadNt);
+}
+template <typename T>
+__device__ inline T gload_nt(const void* ptr) {
+  typedef const __attribute__((address_space(1))) T* global_ptr;
+  return __builtin_nontemporal_load((global_ptr)ptr);
+}
+
 __device__ inline float buf_load_f32(BufRsrc r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
 }
