@@ -765,7 +765,9 @@ __global__ __launch_bounds__(256) void route_logits_big_kernel(RouteK a) {
 // products x * bf16(w) are exact in fp32, and H fp32 additions in any order
 // add at most H 2^-24 of sum |x bf16(w)| (taken as H 2^-22, 4x margin, for
 // whatever order and internal precision the MFMA uses); Cauchy-Schwarz bounds
-// sum |x||w| by |x| |w|.  Tokens with a non-finite approximate logit or norm
+// sum |x||w| by |x| |w|, with |x| and |w| taken as their computed fp32 norms
+// plus sqrt(H + 8) 2^-63, which covers what squares and sums below 2^-126 can
+// lose (so rows of tiny entries get a bound, not 0).  Tokens with a non-finite approximate logit or norm
 // take every expert as a candidate (the full exact row), so NaN and inf
 // follow the contract exactly as on the one-pass path.
 constexpr int kApproxTok = 64;     // tokens per approx workgroup (4 waves x 16)
@@ -899,8 +901,15 @@ __global__ __launch_bounds__(256) void route_candidates_kernel(RouteK a, const f
   // C(H) of the bound, with 2^-8 relative room for the rounding of the norms
   const float cH = (1.0f / 512.0f + (float)a.H * (1.0f / 4194304.0f) * 1.002f) * (1.0f + 1.0f / 256.0f);
   const float sqrtH = sqrtf((float)a.H) * 1.01f;
+  // The norms are fp32 sums of H + 8 squares.  Squares and partial sums below
+  // 2^-126 may be flushed or lose bits, at most 2^-126 each, so the true
+  // |v|^2 <= computed + (H + 8) 2^-126 and |v| <= computed + sqrt(H + 8) 2^-63:
+  // that slack is added to both norms.  Without it a token (or an expert row)
+  // of entries below about 2^-75 would get a norm of 0 and a bound far below
+  // the bf16 rounding error of its approximate logits.
+  const float slack = sqrtf((float)a.H + 8.0f) * 1.0842022e-19f * 1.01f;
   for (int64_t t = (int64_t)blockIdx.x * 4 + w; t < a.T; t += (int64_t)gridDim.x * 4) {
-    const float nxt = nx[t];
+    const float nxt = nx[t] + slack;
     float lo[NV], hi[NV];
     bool all = !isfinite(nxt);
 #pragma unroll
@@ -913,8 +922,9 @@ __global__ __launch_bounds__(256) void route_candidates_kernel(RouteK a, const f
       // + fp32 rounding of m and of the interval ends, + inputs the matrix
       // cores may flush as denormals (each |x| or |w| < 2^-126, so their
       // products sum to at most 2^-126 sqrt(H) (|x| + |w|))
-      const float bnd = cH * nxt * nw[ec] + (fabsf(l) + fabsf(b)) * (1.0f / 4194304.0f) +
-                        sqrtH * 2.4e-38f * (nxt + nw[ec]) + 1e-30f;
+      const float nwe = nw[ec] + slack;
+      const float bnd = cH * nxt * nwe + (fabsf(l) + fabsf(b)) * (1.0f / 4194304.0f) +
+                        sqrtH * 2.4e-38f * (nxt + nwe) + 1e-30f;
       all = all || (e < a.E && !(isfinite(m) && isfinite(bnd)));
       lo[v] = m - bnd;
       hi[v] = m + bnd;

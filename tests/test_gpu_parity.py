@@ -141,10 +141,10 @@ def test_route_full_size_configs(dev, name):
     b = synth.zipf_bias(cfg.E, cfg.zipf) if cfg.zipf else None
     w, idx = phantom_moe.route(to_bf16_tensor(xb, dev), torch.from_numpy(W).to(dev), cfg.k, cfg.score,
                                None if b is None else torch.from_numpy(b).to(dev))
-    sub = np.arange(cfg.T) if cfg.T <= 256 else np.random.default_rng(0).choice(cfg.T, 256, replace=False)
-    ridx, rw = oracle.route(xb[sub], W, cfg.k, cfg.score_mode, b)
-    np.testing.assert_array_equal(idx.cpu().numpy()[sub], ridx)
-    np.testing.assert_allclose(w.cpu().numpy()[sub], rw, rtol=1e-6, atol=1e-7)
+    # every token of the batch (the prefill batches run the two-pass router)
+    ridx, rw = oracle.route(xb, W, cfg.k, cfg.score_mode, b)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-6, atol=1e-7)
     np.testing.assert_allclose(w.sum(-1).cpu().numpy(), 1.0, atol=1e-5)
 
 
@@ -264,8 +264,39 @@ FULL = ["qwen3_decode_t1", "qwen3_decode_t32_zipf", "mixtral_decode_t1", "mixtra
         "qwen3_prefill_t4096", "dsv3_decode_t1", "dsv3_decode_t8", "dsv3_decode_t64", "dsv3_prefill_t2048"]
 
 
+def covering_tokens(idx: np.ndarray, E: int, block: int = 64) -> np.ndarray:
+    """Tokens whose outputs together touch every work item of the expert
+    GEMMs: every (expert, block-position block) of the stable per-expert
+    segments (the gate/up items are 128-position blocks or their 64-position
+    halves, the down items 64-position blocks, each over all rows), chosen
+    greedily (each token covers its k slots' blocks).  Segment position of
+    slot s = t*k + j: its rank among the slots of expert idx[t, j] in slot
+    order."""
+    T, k = idx.shape
+    flat = idx.reshape(-1).astype(np.int64)
+    order = np.argsort(flat, kind="stable")
+    counts = np.bincount(flat, minlength=E)
+    starts = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    pos = np.empty_like(order)
+    pos[order] = np.arange(flat.size) - starts[flat[order]]
+    nblk = -(-counts // block)
+    base = np.concatenate([[0], np.cumsum(nblk)[:-1]])
+    item = (base[flat] + pos // block).reshape(T, k)
+    covered = np.zeros(int(nblk.sum()), dtype=bool)
+    chosen = []
+    while not covered.all():
+        gain = (~covered[item]).sum(axis=1)
+        t = int(np.argmax(gain))
+        chosen.append(t)
+        covered[item[t]] = True
+    return np.sort(np.asarray(chosen, dtype=np.int64))
+
+
 @pytest.mark.parametrize("name", FULL)
 def test_moe_forward_full_size_vs_oracle(dev, name):
+    """Full-size layers: routing of every token equal to the oracle's; outputs
+    of every token for decode batches, and for prefill batches of a token set
+    that covers every GEMM work item (covering_tokens)."""
     cfg = synth.CONFIGS[name]
     print(f"[case] {name}", flush=True)
     dl = synth.device_layer(cfg, dev)
@@ -274,7 +305,16 @@ def test_moe_forward_full_size_vs_oracle(dev, name):
     y, w, idx = phantom_moe.moe_forward(to_bf16_tensor(xb, dev), dl.router_w, ex, cfg.k, cfg.score,
                                         dl.router_bias, return_routing=True)
     torch.cuda.synchronize()
-    sub = np.arange(cfg.T) if cfg.T <= 64 else np.sort(np.random.default_rng(1).choice(cfg.T, 48, replace=False))
+    if cfg.T <= 64:
+        sub = np.arange(cfg.T)
+    else:
+        b = None if dl.router_bias is None else dl.router_bias.cpu().numpy()
+        all_idx, all_w = oracle.route(xb, dl.router_w.cpu().numpy(), cfg.k, cfg.score_mode, b)
+        np.testing.assert_array_equal(idx.cpu().numpy(), all_idx)
+        np.testing.assert_allclose(w.cpu().numpy(), all_w, rtol=1e-6, atol=1e-7)
+        sub = covering_tokens(all_idx, cfg.E)
+        print(f"[case] {name}: routing of all {cfg.T} tokens equal; outputs of {sub.size} covering tokens",
+              flush=True)
     ry, ridx, rw = oracle_for_device_layer(dl, xb, sub)
     np.testing.assert_array_equal(idx.cpu().numpy()[sub], ridx)
     np.testing.assert_allclose(w.cpu().numpy()[sub], rw, rtol=1e-6, atol=1e-7)

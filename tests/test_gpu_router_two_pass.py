@@ -110,3 +110,24 @@ def test_wide_logit_range(dev):
     W *= (10.0 ** rng.uniform(-6, 3, size=(E, 1))).astype(np.float32)
     xf = synth.bf16_bits_to_f32(xb) * (10.0 ** rng.uniform(-4, 4, size=(T, 1))).astype(np.float32)
     check(dev, synth.f32_to_bf16_bits(xf.astype(np.float32)), W.astype(np.float32), k)
+
+
+@pytest.mark.parametrize("H,E,k", [(512, 128, 8), (2048, 128, 8), (7168, 256, 8)])
+def test_tiny_rows_underflow(dev, H, E, k):
+    """Tokens and expert rows scaled by 2^-80 (every square underflows fp32)
+    and by 2^-66..2^-72 (squares in or near the subnormal range): their fp32
+    norms lose everything or most bits, and the bound still has to cover the
+    bf16 rounding of the approximate logits, so routing stays the oracle's."""
+    T = 256
+    rng, xb, W = base_inputs(T, H, E, seed=H + E + 3)
+    xf = synth.bf16_bits_to_f32(xb).astype(np.float64)
+    scale_t = np.ones((T, 1))
+    scale_t[::4] = 2.0 ** -80
+    scale_t[1::8] = 2.0 ** -70
+    scale_t[3::16] = 2.0 ** -66
+    xf = (xf * scale_t).astype(np.float32)
+    scale_e = np.ones((E, 1))
+    scale_e[::3] = 2.0 ** -80
+    scale_e[1::10] = 2.0 ** -72
+    W = (W.astype(np.float64) * scale_e).astype(np.float32)
+    check(dev, synth.f32_to_bf16_bits(xf), W, k)
