@@ -136,6 +136,19 @@ PHANTOM_MOE_API size_t phantom_moe_workspace_bytes(int64_t T, int64_t H, int64_t
 PHANTOM_MOE_API int phantom_moe_workspace_status(void* workspace, size_t workspace_bytes, uint32_t* status,
                                                  hipStream_t stream);
 
+/* A process-wide pinned host word (hipHostMalloc, mapped, coherent; 256
+ * bytes, allocated on the first call and kept until the process ends) into
+ * which every later launch of the single-launch decode path stores a
+ * non-zero status bit when one of its waits gives up, as it also sets the
+ * workspace's bits.  The host reads it with a plain load, without
+ * synchronising, and writes 0 to clear it: a failure of any earlier call
+ * (graph replays included) becomes visible at the next check, where
+ * phantom_moe_workspace_status would have to wait for the stream.  Launches
+ * made before the first call do not write it.  Returns null (and sets
+ * phantom_moe_last_error) if the allocation fails.  No counterpart in the
+ * reference, whose errors exit the process (kernels/common/cuda_utils.h:31-52). */
+PHANTOM_MOE_API uint32_t* phantom_moe_status_word(void);
+
 /* Library options (process-wide; initialised from the environment on first
  * use: PHANTOM_MOE_DECODE=staged, PHANTOM_MOE_DECODE_KSPLIT=1,
  * PHANTOM_MOE_DECODE_X8=0).  A/B and
@@ -145,7 +158,10 @@ PHANTOM_MOE_API int phantom_moe_workspace_status(void* workspace, size_t workspa
 #define PHANTOM_MOE_OPT_FUSED_WAIT_POLLS 3 /* bound of each wait of the single-launch path (default 2^18 polls) */
 /* Failure injection for tests of the error path: bit 0 makes the logit wait,
  * bit 1 the gate/up wait, expect a tag nobody writes, so it gives up after
- * FUSED_WAIT_POLLS polls (every wave still exits; outputs NaN, status set). */
+ * FUSED_WAIT_POLLS polls (every wave still exits; outputs NaN, status set);
+ * bit 2 makes the last workgroup read the generation counter one ahead, as a
+ * workgroup that starts after workgroup 0 gave up waiting for it would (it
+ * must still take its own launch's tag: outputs unchanged, no status). */
 #define PHANTOM_MOE_OPT_FUSED_FAULT 4
 /* 1: a batch-1, top-8 decode without a shared expert (compiled for H 2048,
  * I 768, E 128) runs with expert slot j on XCD j of an 8-XCD, 256-CU part
@@ -188,7 +204,15 @@ PHANTOM_MOE_API int phantom_moe_permute(const int32_t* topk_idx, int64_t T, int 
  * host, replacing the launch-per-stage structure of sparse_matmul.cu:256-363;
  * other shapes run router, gate/up, down and combine as separate launches.
  * Both give the same routing (bit for bit) and outputs within the layer
- * tolerance.  Alignment: nibble buffers 16 bytes, scale buffers 8, x 8,
+ * tolerance.  The single launch is a persistent grid of one workgroup per
+ * CU whose workgroups wait on each other, so it needs every workgroup
+ * resident at once: the GPU must not be shared with other work (other
+ * streams or processes holding CUs, CU masks) while it runs.  It is launched
+ * as an ordinary kernel (so it can be captured into a graph); if workgroups
+ * are not co-resident, the bounded waits give up, the outputs they own are
+ * NaN, and the status bits are set in the workspace and in the word of
+ * phantom_moe_status_word.  PHANTOM_MOE_DECODE=staged (or the option
+ * PHANTOM_MOE_OPT_DECODE_FUSED) turns the single launch off.  Alignment: nibble buffers 16 bytes, scale buffers 8, x 8,
  * router_w 16, workspace 256. */
 PHANTOM_MOE_API int phantom_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int E, int top_k,
                         int score_mode, const float* router_w, const float* router_bias,
@@ -209,9 +233,10 @@ PHANTOM_MOE_API int phantom_moe_forward(const void* x, int x_dtype, int64_t T, i
  * PHANTOM_MOE_EWORKSPACE -- with H 2048, I 768, E 128, top-8 that is
  * T <= 128 tokens.  Every call on one GPU shares that GPU's array, so calls
  * that may overlap on one GPU (different streams without ordering between
- * them) race and must not be issued.  The status word of the single-launch
- * path is not readable here: a wait that gives up shows as NaN outputs (and
- * topk_idx -1 when the routing was lost). */
+ * them) race and must not be issued.  The workspace status of the
+ * single-launch path is not readable here: a wait that gives up shows as NaN
+ * outputs (and topk_idx -1 when the routing was lost), and in the word of
+ * phantom_moe_status_word once that has been called. */
 PHANTOM_MOE_API int phantom_moe_forward_static(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int E,
                                                int top_k, int score_mode, const float* router_w,
                                                const float* router_bias, const uint8_t* gate_nib,

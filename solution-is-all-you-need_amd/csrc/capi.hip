@@ -165,6 +165,14 @@ const Tuning& tuning() {
   return g_tuning;
 }
 
+namespace {
+std::atomic<uint32_t*> g_host_status_dev{nullptr};
+uint32_t* g_host_status_host = nullptr;
+std::mutex g_host_status_mu;
+}  // namespace
+
+uint32_t* host_status_word() { return g_host_status_dev.load(std::memory_order_acquire); }
+
 int set_error(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -537,7 +545,7 @@ int phantom_moe_set_option(int option, int value) {
       c.fused_wait_polls = (uint32_t)value;
       break;
     case PHANTOM_MOE_OPT_FUSED_FAULT:
-      if (value < 0 || value > 3) return fail(PHANTOM_MOE_EINVAL, "FUSED_FAULT takes 0..3, got %d", value);
+      if (value < 0 || value > 7) return fail(PHANTOM_MOE_EINVAL, "FUSED_FAULT takes 0..7, got %d", value);
       c.fused_fault = (uint32_t)value;
       break;
     case PHANTOM_MOE_OPT_DECODE_X8:
@@ -563,6 +571,32 @@ int phantom_moe_get_option(int option, int* value) {
     default: return fail(PHANTOM_MOE_EINVAL, "unknown option %d", option);
   }
   return ok();
+}
+
+uint32_t* phantom_moe_status_word(void) {
+  std::lock_guard<std::mutex> lk(pmoe::g_host_status_mu);
+  if (pmoe::g_host_status_host) {
+    ok();
+    return pmoe::g_host_status_host;
+  }
+  void* h = nullptr;
+  hipError_t e = hipHostMalloc(&h, 256, hipHostMallocMapped | hipHostMallocPortable | hipHostMallocCoherent);
+  if (e != hipSuccess) {
+    launch_status(e, "status_word: hipHostMalloc");
+    return nullptr;
+  }
+  memset(h, 0, 256);
+  void* d = nullptr;
+  e = hipHostGetDevicePointer(&d, h, 0);
+  if (e != hipSuccess) {
+    (void)hipHostFree(h);
+    launch_status(e, "status_word: hipHostGetDevicePointer");
+    return nullptr;
+  }
+  pmoe::g_host_status_host = static_cast<uint32_t*>(h);
+  pmoe::g_host_status_dev.store(static_cast<uint32_t*>(d), std::memory_order_release);
+  ok();
+  return pmoe::g_host_status_host;
 }
 
 int phantom_moe_workspace_status(void* workspace, size_t workspace_bytes, uint32_t* status, hipStream_t stream) {

@@ -116,9 +116,11 @@ struct FusedK {
   uint32_t* slots;     // [T * E][4] tagged logits
   uint32_t* hv;        // [T*k + T][I / 2][4] tagged h units
   FusedLds lds;        // dynamic LDS layout
+  uint32_t* host_status;  // pinned host word set on a failure, or null
   uint32_t wait_polls;  // bound of every wait
   uint32_t skew_route;  // added to the tag the logit wait expects (non-zero only to test the failure path)
   uint32_t skew_h;      // the same for the h wait
+  uint32_t skew_gen;    // added to the counter the last workgroup reads (non-zero only to test a late start)
 };
 
 // 4 qs bytes (little endian word) -> 8 fp16 values n - 8, exactly, in the
@@ -175,8 +177,34 @@ __device__ inline void wait_vmcnt_le(int n) {
 #undef PMOE_W
 }
 
-__device__ inline void set_status(uint32_t* ctl, uint32_t bit) {
+// A wait gave up: the bit goes into the workspace's status word, and, where
+// the process registered one (phantom_moe_status_word), into a pinned host
+// word that the host reads without synchronising (a plain system-scope
+// store: any non-zero value tells the host to look).  Only failure paths
+// call this.
+__device__ inline void set_status(uint32_t* ctl, uint32_t* host, uint32_t bit) {
   __hip_atomic_fetch_or(&ctl[1], bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (host) __hip_atomic_store(host, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// This launch's hand-off tag.  Normally the generation counter + 1.  The
+// counter only advances at the end of a launch, once workgroup 0 has seen
+// every workgroup's presence word carry the launch's tag, or once that wait
+// gave up: a workgroup that starts after it gave up (it was not resident)
+// reads the advanced counter, one ahead of its launch.  Its own presence
+// word then still holds the previous launch's tag, which is counter - 1 from
+// where it stands, and it takes the counter's value: its launch's tag, not
+// the next launch's (so it never publishes stale data under a tag a later
+// launch will accept).  A fresh (zero) or foreign presence word fails the
+// {t, ~t} check and gives the normal tag.  skew is added to the counter
+// read (non-zero only where a test forces the late-start case).
+__device__ inline uint32_t launch_tag(const uint32_t* ctl, const uint64_t* own_presence, uint32_t skew) {
+  const uint32_t g =
+      (uint32_t)uni((int)__hip_atomic_load(&ctl[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) + skew;
+  const uint64_t pr = __hip_atomic_load(own_presence, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t plo = (uint32_t)uni((int)(uint32_t)pr), phi = (uint32_t)uni((int)(uint32_t)(pr >> 32));
+  const bool late = phi == ~plo && plo + 1u == g;
+  return late ? g : g + 1u;
 }
 
 // The router's fixed-order fp64 dot of x[t] (bf16) and W[e] (router.hip):
@@ -359,7 +387,8 @@ __device__ inline void ballot_segments(int T, int k, int E, int has_shared, cons
 // sets *s_fail and the status bit.
 template <int I_>
 __device__ inline void poll_h_units(int pos0, int nun, int tid, int stride, BufRsrc hv_r, uint32_t want,
-                                    uint32_t wait_polls, uint32_t* ctl, int* s_fail, char* s_hb, uint32_t hrow,
+                                    uint32_t wait_polls, uint32_t* ctl, uint32_t* host_status, int* s_fail,
+                                    char* s_hb, uint32_t hrow,
                                     int hunits, int upos, int KgI, uint64_t md_upos) {
   const int lane = threadIdx.x % kWave;
   for (int i0 = 0; i0 < nun; i0 += stride * kHUnits) {
@@ -384,7 +413,7 @@ __device__ inline void poll_h_units(int pos0, int nun, int tid, int stride, BufR
       if (it >= wait_polls) {
         if (lane == 0) {
           *s_fail = 1;
-          set_status(ctl, kStatusExpertWait);
+          set_status(ctl, host_status, kStatusExpertWait);
         }
         break;
       }
@@ -467,8 +496,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
   float* s_xs = reinterpret_cast<float*>(lds + a.lds.x + align_lds((uint32_t)(T + 1) * Kq * 256u));
 
   // ---- 0. generation; logits published as computed; x operand -------------
-  const uint32_t tag =
-      (uint32_t)uni((int)__hip_atomic_load(&a.ctl[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) + 1u;
+  const uint32_t tag = launch_tag(a.ctl, &a.presence[b], b == G - 1 ? a.skew_gen : 0u);
   const BufRsrc slot_r = buf_rsrc(a.slots, (uint32_t)(T * E * 16));
   // at most one (token, expert) logit per wave: the grid has >= T*E waves
   const int task = w * G + b;
@@ -520,7 +548,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
       if (__all(all)) break;
       if (it >= a.wait_polls) {
         poll_failed = true;
-        if (lane == 0) set_status(a.ctl, kStatusRouteWait);
+        if (lane == 0) set_status(a.ctl, a.host_status, kStatusRouteWait);
         break;
       }
     }
@@ -580,7 +608,8 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
   }
   if (threadIdx.x == 0) s_fail = 0;
   if (tpoll < T && lane == 0) s_pfail[tpoll] = poll_failed ? 1 : 0;
-  lds_barrier();  // every wave of the workgroup has read the generation
+  asm volatile("" ::"s"(tag));  // this wave's counter and presence loads have returned
+  lds_barrier();                // every wave of the workgroup has read the generation
   if (threadIdx.x == 0) __hip_atomic_store(&a.presence[b], tag64(tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   int pf = 0;
@@ -1028,12 +1057,12 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
     if (seg_wave) {
       if (w < S)
         poll_h_units<I_>(seg_beg(w), seg_cnt(w) * upos, lane, kWave, hv_r, tag + a.skew_h, a.wait_polls,
-                         a.ctl, &s_fail, s_hb, hrow, hunits, upos, KgI, a.md_upos);
+                         a.ctl, a.host_status, &s_fail, s_hb, hrow, hunits, upos, KgI, a.md_upos);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
     } else {
-      poll_h_units<I_>(0, npos * upos, (int)threadIdx.x, kFThreads, hv_r, tag + a.skew_h, a.wait_polls, a.ctl, &s_fail,
-                       s_hb, hrow, hunits, upos, KgI, a.md_upos);
+      poll_h_units<I_>(0, npos * upos, (int)threadIdx.x, kFThreads, hv_r, tag + a.skew_h, a.wait_polls, a.ctl,
+                       a.host_status, &s_fail, s_hb, hrow, hunits, upos, KgI, a.md_upos);
       lds_barrier();
     }
     // The h operand of position m of a segment sits in MFMA rows 2m (fp16 hi)
@@ -1140,7 +1169,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
         if (!done) done = __hip_atomic_load(&a.presence[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tag64(tag);
         if (__all(done)) break;
         if (it >= a.wait_polls) {
-          if (lane == 0) set_status(a.ctl, kStatusPresenceWait);
+          if (lane == 0) set_status(a.ctl, a.host_status, kStatusPresenceWait);
           break;
         }
         __builtin_amdgcn_s_sleep(2);
@@ -1224,9 +1253,11 @@ struct X8K {
   uint32_t* xslots;  // [E] device-scope tagged logits, kX8SlotStride bytes apart
   uint32_t* xh;      // [8][I / 2][4] tagged h units
   uint32_t* xpart;   // [8][H / 2][4] tagged down partials (device scope)
+  uint32_t* host_status;
   uint32_t wait_polls;
   uint32_t skew_route;
   uint32_t skew_h;
+  uint32_t skew_gen;
 };
 
 // The nibble expansions of dequant_unit_bf16 and dequant_unit_f16s as plain
@@ -1327,8 +1358,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 
   // ---- 0. generation; logits; x operand ---------------------------------------
-  const uint32_t tag =
-      (uint32_t)uni((int)__hip_atomic_load(&a.ctl[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) + 1u;
+  const uint32_t tag = launch_tag(a.ctl, &a.presence[b], b == kX8Grid - 1 ? a.skew_gen : 0u);
   if (threadIdx.x == 0) s_hfail = 0;
   // Logit e is computed once, by wave 0 of workgroup e (the router's
   // fixed-order contract), and published device-scope in slot e; every
@@ -1399,14 +1429,15 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
       if (__all(all)) break;
       if (it >= a.wait_polls) {
         failed = true;
-        if (lane == 0) set_status(a.ctl, kStatusRouteWait);
+        if (lane == 0) set_status(a.ctl, a.host_status, kStatusRouteWait);
         break;
       }
     }
     for (int e = lane; e < E; e += kWave) s_rank[e] = 0;
     if (lane == 0) s_pfail = failed ? 1 : 0;
   }
-  lds_barrier();  // every wave has read the generation; logits and x operand in LDS
+  asm volatile("" ::"s"(tag));  // this wave's counter and presence loads have returned
+  lds_barrier();                // every wave has read the generation; logits and x operand in LDS
   if (threadIdx.x == 0) __hip_atomic_store(&a.presence[b], tag64(tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const bool route_failed = uni(s_pfail) != 0;
 
@@ -1671,7 +1702,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
       if (it >= a.wait_polls) {
         if (lane == 0) {
           s_hfail = 1;
-          set_status(a.ctl, kStatusExpertWait);
+          set_status(a.ctl, a.host_status, kStatusExpertWait);
         }
         break;
       }
@@ -1750,7 +1781,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
     for (uint32_t it = 0;; ++it) {
       if (__all(ok)) break;
       if (it >= a.wait_polls) {
-        if (lane == 0) set_status(a.ctl, kStatusExpertWait);
+        if (lane == 0) set_status(a.ctl, a.host_status, kStatusExpertWait);
         break;
       }
       poll_clobber();
@@ -1780,7 +1811,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_x8_kernel(X8K a) {
         if (!done) done = __hip_atomic_load(&a.presence[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tag64(tag);
         if (__all(done)) break;
         if (it >= a.wait_polls) {
-          if (lane == 0) set_status(a.ctl, kStatusPresenceWait);
+          if (lane == 0) set_status(a.ctl, a.host_status, kStatusPresenceWait);
           break;
         }
         __builtin_amdgcn_s_sleep(2);
@@ -1902,6 +1933,8 @@ static hipError_t launch_x8(const FusedPlan& pl, const RouteArgs& r, const Exper
   a.wait_polls = cfg.fused_wait_polls;
   a.skew_route = (cfg.fused_fault & 1u) ? 1u : 0u;
   a.skew_h = (cfg.fused_fault & 2u) ? 1u : 0u;
+  a.skew_gen = (cfg.fused_fault & 4u) ? 1u : 0u;
+  a.host_status = host_status_word();
   static bool attr_set = false;
   auto kernel = moe_decode_x8_kernel<2048, 768, 128>;
   if (!attr_set) {
@@ -1965,6 +1998,8 @@ hipError_t launch_decode_fused(const FusedPlan& pl, const RouteArgs& r, const Ex
   a.wait_polls = cfg.fused_wait_polls;
   a.skew_route = (cfg.fused_fault & 1u) ? 1u : 0u;
   a.skew_h = (cfg.fused_fault & 2u) ? 1u : 0u;
+  a.skew_gen = (cfg.fused_fault & 4u) ? 1u : 0u;
+  a.host_status = host_status_word();
   return launch_fused(a, pl, stream);
 }
 

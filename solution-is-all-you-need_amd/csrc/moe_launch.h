@@ -92,7 +92,8 @@ struct LibConfig {
   bool decode_x8;  // batch-1 top-8 decode per XCD where the shape and the device allow
   bool force_ksplit;
   uint32_t fused_wait_polls;  // bound of each wait of the single-launch path
-  uint32_t fused_fault;       // failure injection for tests: bit 0 the logit wait, bit 1 the gate/up wait
+  uint32_t fused_fault;       // failure injection for tests: bit 0 the logit wait, bit 1 the gate/up wait,
+                              // bit 2 the last workgroup reads the generation one ahead (a late start)
 };
 // Tuning overrides for sweeps, read from the environment once, on first use
 // (0 = the shape-chosen value):
@@ -110,6 +111,10 @@ const Tuning& tuning();
 constexpr uint32_t kFusedWaitPollsDefault = 1u << 18;
 LibConfig lib_config();
 void set_lib_config(const LibConfig& c);
+// Device address of the pinned host word the single-launch kernels store a
+// status bit into when a wait gives up (null until phantom_moe_status_word
+// has allocated it).
+uint32_t* host_status_word();
 
 // Workspace carve-up.  Every region is 256-byte aligned.
 struct Workspace {

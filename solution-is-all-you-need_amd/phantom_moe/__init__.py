@@ -5,6 +5,8 @@ Python surface over libphantom_moe.so (C ABI in include/phantom_moe.h):
   PhantomTopKRouter   drop-in for the reference router module
                       (tests/test_moe_routing.py:43-72)
   moe_forward         router -> permute -> Q4_0 SwiGLU experts -> combine
+  check_status        raise if a single-launch decode call (eager or a
+                      graph replay) gave up a wait (FusedWaitError)
   route, permute      the first two stages on their own
   MoEWeights          repacked Q4_0 expert weights resident in HBM
   q4_0                GGUF Q4_0 pack / unpack / device repack
@@ -16,7 +18,7 @@ Python surface over libphantom_moe.so (C ABI in include/phantom_moe.h):
                       (imported on demand: ``from phantom_moe import hf``)
 """
 from . import gguf, legacy, q4_0, synth
-from ._lib import PhantomMoEError
+from ._lib import FusedWaitError, PhantomMoEError, check_status, set_sync_check
 from .ops import MoEWeights, PreparedForward, moe_forward, permute, route
 from .router import PhantomTopKRouter
 
@@ -32,4 +34,7 @@ __all__ = [
     "gguf",
     "synth",
     "PhantomMoEError",
+    "FusedWaitError",
+    "check_status",
+    "set_sync_check",
 ]

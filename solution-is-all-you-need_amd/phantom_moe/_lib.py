@@ -42,6 +42,7 @@ SIGNATURES = {
     "phantom_q4_0_dequant_f32": (_int, [_vp, _i64, _i64, _vp, _vp]),
     "phantom_moe_workspace_bytes": (_sz, [_i64, _i64, _i64, _int, _int, _int]),
     "phantom_moe_workspace_status": (_int, [_vp, _sz, _vp, _vp]),
+    "phantom_moe_status_word": (ctypes.POINTER(ctypes.c_uint32), []),
     "phantom_moe_set_option": (_int, [_int, _int]),
     "phantom_moe_get_option": (_int, [_int, _vp]),
     "phantom_moe_route": (_int, [_vp, _int, _vp, _vp, _i64, _i64, _int, _int, _int, _vp, _vp, _vp, _sz, _vp]),
@@ -66,6 +67,8 @@ SIGNATURES = {
 
 _lock = threading.Lock()
 _lib = None
+_status_word = None  # ctypes view of the pinned host word (phantom_moe_status_word)
+_sync_check = os.environ.get("PHANTOM_MOE_SYNC_CHECK", "0") == "1"
 
 
 OPT_DECODE_FUSED = 1  # PHANTOM_MOE_OPT_DECODE_FUSED
@@ -110,6 +113,13 @@ def load(path: str = LIB_PATH):
         runtimes = _hip_runtimes_mapped()
         if len(runtimes) > 1:
             raise PhantomMoEError(f"two HIP runtimes are mapped in this process: {sorted(runtimes)}")
+        global _status_word
+        if torch.cuda.is_available():
+            ptr = lib.phantom_moe_status_word()
+            if not ptr:
+                raise PhantomMoEError("phantom_moe_status_word failed: "
+                                      + lib.phantom_moe_last_error().decode(errors="replace"))
+            _status_word = ptr.contents
         _lib = lib
         return lib
 
@@ -132,6 +142,53 @@ def set_option(option: int, value: int) -> int:
     check(lib.phantom_moe_get_option(option, ctypes.byref(old)), "phantom_moe_get_option")
     check(lib.phantom_moe_set_option(option, value), "phantom_moe_set_option")
     return old.value
+
+
+_STATUS_BITS = ((1, "the router logits"), (2, "the gate/up results or the down partials"),
+                (4, "every workgroup to start"))
+
+
+class FusedWaitError(PhantomMoEError):
+    """A single-launch decode call gave up one of its bounded waits: the
+    outputs it could not compute are NaN.  Its workgroups were not all
+    resident at once (another stream or process held CUs)."""
+
+
+def check_status() -> None:
+    """Raise FusedWaitError if a single-launch decode call of this process
+    (eager or a graph replay) gave up a wait since the last check.  Reads the
+    pinned host word the kernels set on failure: no synchronisation, so a
+    failure shows once its call has finished on the GPU."""
+    w = _status_word
+    if w is None:
+        return
+    v = w.value
+    if v == 0:
+        return
+    w.value = 0
+    what = ", ".join(name for bit, name in _STATUS_BITS if v & bit) or f"status {v:#x}"
+    raise FusedWaitError(
+        f"single-launch decode: a bounded wait gave up (waiting for {what}); the outputs that call could not "
+        "compute are NaN.  Its workgroups must all be resident at once: do not share the GPU with other work "
+        "while it runs, or set PHANTOM_MOE_DECODE=staged for the staged launches.")
+
+
+def set_sync_check(on: bool) -> bool:
+    """With sync check on, every layer call waits for its stream and checks
+    the status word before it returns (for debugging; off by default, or
+    PHANTOM_MOE_SYNC_CHECK=1).  Returns the previous setting."""
+    global _sync_check
+    old = _sync_check
+    _sync_check = bool(on)
+    return old
+
+
+def after_call(device) -> None:
+    """Status check after a layer call: immediate under sync check, else
+    whatever earlier calls have left."""
+    if _sync_check:
+        torch.cuda.current_stream(device).synchronize()
+    check_status()
 
 
 def workspace_status(ws: torch.Tensor) -> int:

@@ -194,6 +194,7 @@ def moe_forward(x: torch.Tensor, router_weight: torch.Tensor, experts: MoEWeight
     idx = torch.empty((T, top_k), dtype=torch.int32, device=x.device)
     w = torch.empty((T, top_k), dtype=torch.float32, device=x.device)
     lib = _lib.load()
+    _lib.check_status()  # a failure an earlier call left
     has_sh = experts.shared is not None
     nbytes = lib.phantom_moe_workspace_bytes(T, H, experts.I, E, top_k, int(has_sh))
     ws = workspace(x.device, nbytes)
@@ -206,6 +207,7 @@ def moe_forward(x: torch.Tensor, router_weight: torch.Tensor, experts: MoEWeight
         *sh, y.data_ptr(), idx.data_ptr(), w.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device),
     )
     _lib.check(rc, "phantom_moe_forward")
+    _lib.after_call(x.device)
     y = y.reshape(*lead, H)
     if return_routing:
         return y, w.reshape(*lead, top_k), idx.reshape(*lead, top_k)
@@ -258,8 +260,10 @@ class PreparedForward:
         self._ctypes = ctypes
 
     def __call__(self, stream: int | None = None) -> torch.Tensor:
+        _lib.check_status()
         s = _lib.stream_handle(self.device) if stream is None else stream
         rc = self._fn(*self._args, s)
         if rc:
             _lib.check(rc, "phantom_moe_forward")
+        _lib.after_call(self.device)
         return self.y

@@ -61,6 +61,22 @@ def run(prep, stream=None):
     return prep.y.clone(), prep.topk_w.clone(), prep.topk_idx.clone()
 
 
+def faulty_call(prep):
+    """One call whose wait is forced to give up: the pinned status word makes
+    it raise FusedWaitError, from the call itself or from the check after
+    the stream has finished; the outputs are read afterwards."""
+    with pytest.raises(phantom_moe.FusedWaitError):
+        prep()
+        torch.cuda.synchronize()
+        phantom_moe.check_status()
+    torch.cuda.synchronize()
+    try:  # workgroups that gave up after the check above stored the bit again
+        phantom_moe.check_status()
+    except phantom_moe.FusedWaitError:
+        pass
+    return prep.y.clone(), prep.topk_w.clone(), prep.topk_idx.clone()
+
+
 CASES = [
     synth.MoEConfig("f_t1", 512, 256, 32, 8, 1),
     synth.MoEConfig("f_t1_e16_k4", 256, 128, 16, 4, 1),
@@ -190,8 +206,7 @@ def test_x8_wait_failure_is_reported(dev, option, fault):
     y_ok, w_ok, i_ok = run(prep)
     option(_lib.OPT_FUSED_WAIT_POLLS, 64)
     option(_lib.OPT_FUSED_FAULT, fault)
-    y, w, idx = run(prep)
-    torch.cuda.synchronize()
+    y, w, idx = faulty_call(prep)
     st = _lib.workspace_status(prep.workspace)
     assert st & fault, f"status {st:#x} lacks bit {fault:#x}"
     assert torch.isnan(y).all()
@@ -292,8 +307,7 @@ def test_fused_wait_failure_is_reported(dev, option, fault):
     y_ok, w_ok, i_ok = run(prep)
     option(_lib.OPT_FUSED_WAIT_POLLS, 64)
     option(_lib.OPT_FUSED_FAULT, fault)
-    y, w, idx = run(prep)
-    torch.cuda.synchronize()
+    y, w, idx = faulty_call(prep)
     st = _lib.workspace_status(prep.workspace)
     assert st & fault, f"status {st:#x} lacks bit {fault:#x}"
     assert torch.isnan(y).all()
@@ -335,3 +349,80 @@ def test_fused_nonfinite_activations(dev):
     finally:
         _lib.set_option(_lib.OPT_DECODE_FUSED, old)
     assert torch.equal(iss, idx)
+
+
+def small_fused_layer(dev, seed=9):
+    cfg = synth.MoEConfig("fail_t1", 256, 128, 16, 4, 1)
+    L = synth.host_layer(cfg)
+    ex = dev_weights(L, dev)
+    W = torch.from_numpy(L.router_w).to(dev)
+    x = to_bf16_tensor(synth.activations(1, cfg.H, seed=seed), dev)
+    assert kernels(cfg) == FUSED
+    return cfg, ex, W, x
+
+
+@pytest.mark.parametrize("sync_check", [False, True], ids=["next_call", "sync_check"])
+def test_wait_failure_raises_from_moe_forward(dev, option, sync_check):
+    """A forced wait failure reaches the caller of moe_forward as
+    FusedWaitError, not as silent NaN: under sync check from the failing
+    call itself, otherwise from the next call (the kernel stores the bit
+    into the pinned host word; no synchronisation on the normal path).  The
+    call after that is correct again."""
+    cfg, ex, W, x = small_fused_layer(dev)
+    y_ok = phantom_moe.moe_forward(x, W, ex, cfg.k).clone()
+    torch.cuda.synchronize()
+    phantom_moe.check_status()
+    option(_lib.OPT_FUSED_WAIT_POLLS, 64)
+    option(_lib.OPT_FUSED_FAULT, 2)
+    old = phantom_moe.set_sync_check(sync_check)
+    try:
+        if sync_check:
+            with pytest.raises(phantom_moe.FusedWaitError, match="gate/up"):
+                phantom_moe.moe_forward(x, W, ex, cfg.k)
+        else:
+            y_bad = phantom_moe.moe_forward(x, W, ex, cfg.k)
+            torch.cuda.synchronize()
+            assert torch.isnan(y_bad).all()
+            _lib.set_option(_lib.OPT_FUSED_FAULT, 0)
+            with pytest.raises(phantom_moe.FusedWaitError, match="gate/up"):
+                phantom_moe.moe_forward(x, W, ex, cfg.k)
+    finally:
+        phantom_moe.set_sync_check(old)
+    _lib.set_option(_lib.OPT_FUSED_FAULT, 0)
+    torch.cuda.synchronize()
+    phantom_moe.check_status()  # the raise cleared the word
+    y2 = phantom_moe.moe_forward(x, W, ex, cfg.k)
+    torch.cuda.synchronize()
+    phantom_moe.check_status()
+    assert torch.equal(y2, y_ok)
+
+
+@pytest.mark.parametrize("x8", [1, 0], ids=["per_xcd", "generic"])
+def test_late_start_takes_its_launch_tag(dev, option, x8):
+    """A workgroup that starts after workgroup 0 gave up waiting for it reads
+    the generation counter one ahead of its launch.  Forced from the host
+    (the last workgroup adds one to the counter it reads), it must still take
+    its own launch's tag from its presence word: outputs equal to a normal
+    call's, bit for bit, on two calls in a row, with no status set.  Taking
+    the counter + 1 instead would publish its h units under a tag nobody in
+    its launch waits for (NaN outputs and status bits)."""
+    if x8:
+        cfg, dl, prep, xb = x8_prep(dev, seed=31)
+    else:
+        option(_lib.OPT_DECODE_X8, 0)
+        cfg, ex, W, x = small_fused_layer(dev, seed=31)
+        prep = phantom_moe.PreparedForward(ex, W, 1, cfg.k, x=x)
+    y_ok, w_ok, i_ok = run(prep)  # every presence word now holds this call's tag
+    option(_lib.OPT_FUSED_WAIT_POLLS, 4096)
+    option(_lib.OPT_FUSED_FAULT, 4)
+    for call in range(2):
+        y, w, idx = run(prep)
+        torch.cuda.synchronize()
+        phantom_moe.check_status()
+        assert _lib.workspace_status(prep.workspace) == 0, f"call {call}"
+        assert torch.equal(y, y_ok) and torch.equal(w, w_ok) and torch.equal(idx, i_ok), f"call {call}"
+    _lib.set_option(_lib.OPT_FUSED_FAULT, 0)
+    y, _, _ = run(prep)
+    torch.cuda.synchronize()
+    assert _lib.workspace_status(prep.workspace) == 0
+    assert torch.equal(y, y_ok)
