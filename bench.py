@@ -46,7 +46,14 @@ PREFILL_T = 1024  # from this batch on, a workload is priced against the MFMA ro
 # The metric of the benchmark this line reports.
 METRIC = "MoE-layer decode tok/s + % of HBM peak; prefill grouped-GEMM % of MFMA peak"
 HEADLINE = "qwen3_decode_t1"
-SUB_WORKLOADS = ("qwen3_prefill_t4096", "qwen3_decode_t32_zipf")
+# Every other workload of the benchmark, each its own sub-record.
+SUB_WORKLOADS = ("qwen3_prefill_t4096", "qwen3_decode_t32_zipf", "mixtral_decode_t1", "mixtral_decode_t16",
+                 "dsv3_decode_t1", "dsv3_decode_t8", "dsv3_decode_t64", "dsv3_prefill_t2048")
+# Spin cycles queued ahead of each timed graph replay (torch.cuda._sleep), so
+# the start event fires once the host has queued the whole replay: the
+# interval between the events is the GPU's time for the K steps, without the
+# host's cost of submitting the graph.
+PRE_REPLAY_SPIN_CYCLES = 400_000
 # The reference's router benchmark: PhantomTopKRouter at hidden 4096, 16
 # experts, top-2, one fp32 token (tests/test_moe_routing.py:199-203); its
 # published latency is 54.51 us on an RTX 4050 laptop GPU
@@ -72,7 +79,11 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--layers", type=int, default=16, help="distinct layer instances to rotate over")
+    p.add_argument("--layers", type=int, default=None,
+                   help="distinct layer instances to rotate over (default: 16 Qwen3-shaped, else enough for "
+                        "4.5 GB of weights, at least 3)")
+    p.add_argument("--replays", type=int, default=5,
+                   help="timed HIP graph replays of K steps each (the median is reported)")
     p.add_argument("--workload", default=None,
                    help="one workload alone (default: the batch-1 Qwen3 headline plus the sub-records)")
     p.add_argument("--no-subs", action="store_true", help="the headline alone, without the sub-records")
@@ -116,6 +127,16 @@ class HipEvents:
     def destroy(self, evs):
         for e in evs:
             self.hip.hipEventDestroy(ctypes.c_void_p(e))
+
+
+def default_layers(cfg) -> int:
+    """Layer instances to rotate over: enough that the weights the steps
+    touch between two visits of one instance (L - 1 steps of active experts)
+    exceed the 256 MB last-level cache; 16 for the Qwen3-shaped layers."""
+    if cfg.H == 2048:
+        return 16
+    per_layer = (cfg.E + (1 if cfg.shared else 0)) * 3 * cfg.H * cfg.I * 18 // 32
+    return max(3, -(-int(4.5e9) // per_layer))
 
 
 def gate_up_bytes(cfg, U: int) -> int:
@@ -225,16 +246,28 @@ def cpu_baseline(cfg, host_layer, budget_s: float):
     n_pre, el_pre = timed(pre, threads, share)
     del pre
     model, simd = cpu_info()
+    r_all, r_one = cfg.T * n_all / el_all, cfg.T * n_one / el_one
+    # value is the faster thread setting of the reference path (weights kept
+    # packed).  At decode sizes one thread tends to win: the numpy dequant of
+    # the active experts runs on one thread either way, and the small torch
+    # ops (one router row, a few-row matmuls) pay a fork/join per op on many.
+    best_one = r_one > r_all
+    n_b, el_b, th_b = (n_one, el_one, 1) if best_one else (n_all, el_all, threads)
     return {
-        "value": round(cfg.T * n_all / el_all, 3),
+        "value": round(max(r_all, r_one), 3),
         "unit": "tokens/s",
-        "cores": threads,
+        "cores": th_b,
         "kind": "port",
-        "sample": f"{n_all} forwards of one {cfg.T}-token layer instance ({cfg.T * n_all} tokens, {el_all:.1f} s) on "
-                  f"{threads} threads: torch fp32 router, numpy Q4_0 dequant of every active expert on every call, "
-                  f"torch bf16 SwiGLU, index_add_ combine (oracle/ref_cpu_path.py)",
-        "one_thread": {"value": round(cfg.T * n_one / el_one, 3), "unit": "tokens/s", "cores": 1,
+        "sample": f"{n_b} forwards of one {cfg.T}-token layer instance ({cfg.T * n_b} tokens, {el_b:.1f} s) on "
+                  f"{th_b} thread(s), the faster of 1 and {threads}: torch fp32 router, numpy Q4_0 dequant of every "
+                  f"active expert on every call, torch bf16 SwiGLU, index_add_ combine (oracle/ref_cpu_path.py)",
+        "all_threads": {"value": round(r_all, 3), "unit": "tokens/s", "cores": threads,
+                        "sample": f"{n_all} forwards ({el_all:.1f} s)"},
+        "one_thread": {"value": round(r_one, 3), "unit": "tokens/s", "cores": 1,
                        "sample": f"{n_one} forwards ({el_one:.1f} s)"},
+        "thread_note": "the numpy dequant of the active experts is single-threaded in both settings; at small "
+                       "batches the torch ops are a router row and few-row matmuls, where many threads add a "
+                       "fork/join per op, so one thread can be the faster setting",
         "predequantized": {"value": round(cfg.T * n_pre / el_pre, 3), "unit": "tokens/s", "cores": threads,
                            "sample": f"{n_pre} forwards ({el_pre:.1f} s) on bf16 weights dequantised once up front"},
         "cpu": model,
@@ -263,7 +296,7 @@ def bench_legacy(args):
     B, D, Dffn, pct = w["B"], w["D"], w["D_ffn"], w["sparsity"]
     dev = torch.device("cuda:0")
     per_layer = 3 * Dffn * D * 2
-    L = max(1, min(args.layers, (4 << 30) // per_layer + 1))
+    L = max(1, min(args.layers or 16, (4 << 30) // per_layer + 1))
     gen = torch.Generator(device=dev)
     layers = []
     for l in range(L):
@@ -349,7 +382,8 @@ def bench_moe(args, cfg, with_cpu: bool) -> dict:
     from phantom_moe import _lib, synth
 
     dev = torch.device("cuda:0")
-    L = max(1, args.layers)
+    L = max(1, args.layers if args.layers else default_layers(cfg))
+    K = args.steps
 
     # ---- resident inputs: L distinct layer instances --------------------
     layers = []
@@ -370,8 +404,14 @@ def bench_moe(args, cfg, with_cpu: bool) -> dict:
 
     lib = _lib.load()
     stream = _lib.stream_handle(dev)
+    # Steps run in one continuous rotation over the instances (warm-up, the
+    # eager pass, the untimed replay, the timed replays): an instance is
+    # touched again only after the L - 1 others, so its weights come from
+    # HBM, never from the last-level cache.
+    pos = 0
     for i in range(args.warmup):
-        layers[i % L](stream)
+        layers[pos % L](stream)
+        pos += 1
     torch.cuda.synchronize()
 
     use_events = not args.no_stage_events
@@ -380,36 +420,59 @@ def bench_moe(args, cfg, with_cpu: bool) -> dict:
     events = ev.create(n_ev * args.steps) if use_events else []
     arrays = [(ctypes.c_void_p * n_ev)(*events[i * n_ev:(i + 1) * n_ev]) for i in range(args.steps)] if use_events else []
 
-    # ---- timed region: exactly K steps between two synchronisations ------
+    # ---- eager pass: exactly K steps between two synchronisations, stage
+    # events around every stage (stage times, the dominant kernel's roofline)
+    eager_layer = []
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
+    for i in range(K):
         if use_events:
             lib.phantom_moe_set_profile_events(arrays[i], n_ev)
-        layers[i % L](stream)
+        eager_layer.append(pos % L)
+        layers[pos % L](stream)
+        pos += 1
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     if use_events:
         lib.phantom_moe_set_profile_events(None, 0)
     elapsed = t1 - t0
 
-    # ---- the same K steps captured in one HIP graph and replayed --------
-    # (value and ms_per_step come from the replay unless --no-graph; the
-    # stage events above stay eager, one event pair per stage)
-    graph_elapsed = None
+    # ---- timed replays: the K steps captured in a HIP graph (one graph per
+    # replay, each continuing the rotation), an untimed replay first; each
+    # timed replay is bracketed by synchronisations, and by two events on its
+    # stream queued behind a short spin so the interval is the GPU's time for
+    # the K steps.  value and ms_per_step come from the median replay.
+    replay_ms = []
+    wall_s = []
+    replay_layers = []
     if not args.no_graph:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            gstream = _lib.stream_handle(dev)
-            for i in range(args.steps):
-                layers[i % L](gstream)
-        graph.replay()  # untimed warm-up replay
+        graphs = []
+        for r in range(args.replays + 1):
+            graph = torch.cuda.CUDAGraph()
+            seq = [(pos + r * K + i) % L for i in range(K)]
+            with torch.cuda.graph(graph):
+                gstream = _lib.stream_handle(dev)
+                for l in seq:
+                    layers[l](gstream)
+            graphs.append(graph)
+            replay_layers.append(seq)
+        replay_layers = replay_layers[1:]
+        pos += (args.replays + 1) * K
+        graphs[0].replay()  # untimed
         torch.cuda.synchronize()
-        g0 = time.perf_counter()
-        graph.replay()
-        torch.cuda.synchronize()
-        graph_elapsed = time.perf_counter() - g0
-        del graph
+        for graph in graphs[1:]:
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            w0 = time.perf_counter()
+            torch.cuda._sleep(PRE_REPLAY_SPIN_CYCLES)
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            wall_s.append(time.perf_counter() - w0)
+            replay_ms.append(e0.elapsed_time(e1))
+        del graphs
 
     if args.copy_bytes > 0:
         src = torch.ones(args.copy_bytes, dtype=torch.uint8, device=dev)
@@ -429,21 +492,24 @@ def bench_moe(args, cfg, with_cpu: bool) -> dict:
     stages = {name: [] for name in STAGES}
     layer_ms = []
     if use_events:
-        for i in range(args.steps):
+        for i in range(K):
             e = events[i * n_ev:(i + 1) * n_ev]
             layer_ms.append(ev.elapsed_ms(e[0], e[-1]))
             for j, name in enumerate(STAGES):
                 stages[name].append(ev.elapsed_ms(e[j], e[j + 1]))
         ev.destroy(events)
-    steps_U = [U[i % L] for i in range(args.steps)]
+    steps_U = [U[l] for l in eager_layer]
     resident_gb = round(sum(x.experts.nbytes() for x in layers) / 1e9, 3)
     del layers
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
 
     eager_elapsed = elapsed
-    if graph_elapsed is not None:
-        elapsed = graph_elapsed
+    clock_U = steps_U
+    if replay_ms:
+        med = int(np.argsort(replay_ms)[len(replay_ms) // 2])
+        elapsed = replay_ms[med] * 1e-3
+        clock_U = [U[l] for l in replay_layers[med]]
     value = cfg.T * args.steps / elapsed
     out = {
         "metric": metric_name(cfg),
@@ -464,24 +530,32 @@ def bench_moe(args, cfg, with_cpu: bool) -> dict:
             "score": cfg.score, "zipf_bias_s": cfg.zipf, "shared_expert": cfg.shared,
             "layer_instances": L, "weights_resident_gb": resident_gb,
             "active_experts_per_step_mean": round(float(np.mean(steps_U)), 2),
-            "timing": "one HIP graph replay of the K steps" if graph_elapsed is not None else "eager launches",
+            "timing": (f"median of {len(replay_ms)} HIP graph replays of the K steps, HIP events on the replay "
+                       f"stream; one rotation over the instances across warm-up, eager pass and replays"
+                       if replay_ms else "eager launches, wall clock"),
         },
         "workspace_status": status,
     }
-    if graph_elapsed is not None:
+    if replay_ms:
+        out["replays"] = {
+            "ms_per_step": [round(m / args.steps, 5) for m in replay_ms],
+            "wall_ms_per_step": [round(w * 1e3 / args.steps, 5) for w in wall_s],
+            "wall_note": "host clock around each replay (synchronisation to synchronisation): adds the "
+                         "pre-replay spin and the host's graph submission",
+        }
         out["eager"] = {"tokens_per_s": round(cfg.T * args.steps / eager_elapsed, 2),
                         "ms_per_step": round(eager_elapsed * 1e3 / args.steps, 5)}
     # whole-layer HBM rate on the graph clock, on both bases: all algorithmic
     # bytes, and the active experts' weights alone
-    lay_bytes = float(sum(layer_bytes(cfg, u) for u in steps_U))
-    exp_bytes = float(sum(expert_bytes(cfg, u) for u in steps_U))
+    lay_bytes = float(sum(layer_bytes(cfg, u) for u in clock_U))
+    exp_bytes = float(sum(expert_bytes(cfg, u) for u in clock_U))
     out["layer_hbm"] = {
         "full_bytes_gbs": round(lay_bytes / elapsed / 1e9, 1),
         "full_bytes_frac": round(lay_bytes / elapsed / 1e9 / HBM_PEAK_GBS, 4),
         "expert_bytes_gbs": round(exp_bytes / elapsed / 1e9, 1),
         "expert_bytes_frac": round(exp_bytes / elapsed / 1e9 / HBM_PEAK_GBS, 4),
         "bytes_per_step": round(lay_bytes / args.steps),
-        "clock": "graph replay, launch gaps included",
+        "clock": "graph replay (median), launch gaps between kernels included",
     }
     if use_events:
         # the kernel the gate/up stage launches at this shape; one kernel for
@@ -527,6 +601,7 @@ def bench_moe(args, cfg, with_cpu: bool) -> dict:
             "avg_launch_us": round(gu_ms * 1e3 / args.steps, 3),
         })
         lay_ms = float(np.sum(layer_ms))
+        eager_bytes = float(sum(layer_bytes(cfg, u) for u in steps_U))
         stage_us = {k: round(float(np.mean(v)) * 1e3, 3) for k, v in stages.items()}
         if fused:
             # one kernel: the events around it are the layer; the others
@@ -536,8 +611,8 @@ def bench_moe(args, cfg, with_cpu: bool) -> dict:
         out["layer"] = {
             "gpu_us_per_step": round(lay_ms * 1e3 / args.steps, 3),
             "stage_us": stage_us,
-            "hbm_achieved_gbs": round(lay_bytes / (lay_ms * 1e-3) / 1e9, 1),
-            "hbm_frac": round(lay_bytes / (lay_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "hbm_achieved_gbs": round(eager_bytes / (lay_ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(eager_bytes / (lay_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "tflops": round(layer_flops(cfg) * args.steps / (lay_ms * 1e-3) / 1e12, 3),
             "mfma_frac": round(layer_flops(cfg) * args.steps / (lay_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
             "clock": "eager, events around each step",
@@ -553,7 +628,8 @@ def bench_moe(args, cfg, with_cpu: bool) -> dict:
 def bench_router_ref(args) -> dict:
     """phantom_moe_route alone at the reference's router benchmark shape
     (hidden 4096, 16 experts, top-2, one fp32 token): K calls timed eagerly
-    with events around each, then as one HIP graph replay."""
+    with events around each, then HIP graph replays of the K calls (events on
+    the replay stream, median replay)."""
     import numpy as np
     import torch
 
@@ -599,10 +675,17 @@ def bench_router_ref(args) -> dict:
             call(i, gs)
     graph.replay()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    graph.replay()
-    torch.cuda.synchronize()
-    g_us = (time.perf_counter() - t0) * 1e6 / args.steps
+    reps = []
+    for _ in range(max(1, args.replays)):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(PRE_REPLAY_SPIN_CYCLES)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        reps.append(e0.elapsed_time(e1) * 1e3 / args.steps)
+    g_us = float(np.median(reps))
     del graph
     return {
         "metric": "router latency (PhantomTopKRouter.forward: logits, top-k, softmax)",
@@ -618,7 +701,7 @@ def bench_router_ref(args) -> dict:
 
 
 def sub_record(rec: dict) -> dict:
-    keep = ("metric", "value", "unit", "ms_per_step", "config", "eager", "layer_hbm", "roofline", "layer",
+    keep = ("metric", "value", "unit", "ms_per_step", "config", "replays", "eager", "layer_hbm", "roofline", "layer",
             "workspace_status")
     return {k: rec[k] for k in keep if k in rec}
 
