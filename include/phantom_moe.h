@@ -151,7 +151,7 @@ PHANTOM_MOE_API uint32_t* phantom_moe_status_word(void);
 
 /* Library options (process-wide; initialised from the environment on first
  * use: PHANTOM_MOE_DECODE=staged, PHANTOM_MOE_DECODE_KSPLIT=1,
- * PHANTOM_MOE_DECODE_X8=0).  A/B and
+ * PHANTOM_MOE_DECODE_X8=0, PHANTOM_MOE_DECODE_STREAM=0|2).  A/B and
  * test switches with no counterpart in the reference. */
 #define PHANTOM_MOE_OPT_DECODE_FUSED 1 /* 1: decode batches that fit take the single-launch path (default) */
 #define PHANTOM_MOE_OPT_DECODE_KSPLIT 2 /* 1: staged decode expert stages always as the K-split kernels (default 0) */
@@ -167,6 +167,11 @@ PHANTOM_MOE_API uint32_t* phantom_moe_status_word(void);
  * I 768, E 128) runs with expert slot j on XCD j of an 8-XCD, 256-CU part
  * (default); 0: in the generic single-launch kernel. */
 #define PHANTOM_MOE_OPT_DECODE_X8 5
+/* The one-token layer as one launch that streams the weights (experts too
+ * large for the single launch above, e.g. Mixtral-8x7B- or
+ * DeepSeek-V3-shaped): 1 where no other single launch fits (default), 2 for
+ * every one-token shape (in place of the kernels above), 0 never. */
+#define PHANTOM_MOE_OPT_DECODE_STREAM 6
 PHANTOM_MOE_API int phantom_moe_set_option(int option, int value);
 PHANTOM_MOE_API int phantom_moe_get_option(int option, int* value);
 

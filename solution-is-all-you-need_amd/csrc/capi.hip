@@ -84,6 +84,8 @@ LibConfig config_from_env() {
   c.force_ksplit = k && strcmp(k, "1") == 0;
   const char* x8 = getenv("PHANTOM_MOE_DECODE_X8");
   c.decode_x8 = !(x8 && strcmp(x8, "0") == 0);
+  const char* st = getenv("PHANTOM_MOE_DECODE_STREAM");
+  c.decode_stream = (st && strcmp(st, "0") == 0) ? 0 : (st && strcmp(st, "2") == 0) ? 2 : 1;
   c.fused_wait_polls = kFusedWaitPollsDefault;
   c.fused_fault = 0;
   return c;
@@ -121,6 +123,7 @@ Tuning tuning_from_env() {
 std::atomic<int> g_opt_fused{1};
 std::atomic<int> g_opt_ksplit{0};
 std::atomic<int> g_opt_x8{1};
+std::atomic<int> g_opt_stream{1};
 std::atomic<uint32_t> g_opt_polls{kFusedWaitPollsDefault};
 std::atomic<uint32_t> g_opt_fault{0};
 std::once_flag g_opt_once;
@@ -132,6 +135,7 @@ void init_options() {
     g_opt_fused.store(c.decode_fused ? 1 : 0);
     g_opt_ksplit.store(c.force_ksplit ? 1 : 0);
     g_opt_x8.store(c.decode_x8 ? 1 : 0);
+    g_opt_stream.store(c.decode_stream);
     g_opt_polls.store(c.fused_wait_polls);
     g_opt_fault.store(c.fused_fault);
     g_tuning = tuning_from_env();
@@ -146,6 +150,7 @@ LibConfig lib_config() {
   c.decode_fused = g_opt_fused.load(std::memory_order_relaxed) != 0;
   c.force_ksplit = g_opt_ksplit.load(std::memory_order_relaxed) != 0;
   c.decode_x8 = g_opt_x8.load(std::memory_order_relaxed) != 0;
+  c.decode_stream = g_opt_stream.load(std::memory_order_relaxed);
   c.fused_wait_polls = g_opt_polls.load(std::memory_order_relaxed);
   c.fused_fault = g_opt_fault.load(std::memory_order_relaxed);
   return c;
@@ -156,6 +161,7 @@ void set_lib_config(const LibConfig& c) {
   g_opt_fused.store(c.decode_fused ? 1 : 0);
   g_opt_ksplit.store(c.force_ksplit ? 1 : 0);
   g_opt_x8.store(c.decode_x8 ? 1 : 0);
+  g_opt_stream.store(c.decode_stream);
   g_opt_polls.store(c.fused_wait_polls);
   g_opt_fault.store(c.fused_fault);
 }
@@ -198,12 +204,17 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
   // single-launch path writes; its own regions follow when the shape takes it.
   const size_t o_ctl = take(kCtlBytes);
   const bool fused = I > 0 && fused_shape_ok(T, H, I, E, k, has_shared);
-  size_t o_pres = 0, o_slots = 0, o_hv = 0, o_xsl = 0, o_xh = 0, o_xpt = 0;
+  const bool strm = I > 0 && stream_shape_ok(T, H, I, E, k, has_shared);
+  size_t o_pres = 0, o_slots = 0, o_hv = 0, o_xsl = 0, o_xh = 0, o_xpt = 0, o_ssl = 0, o_sdv = 0;
   const bool x8 = fused && x8_shape(T, H, I, E, k, has_shared);
-  if (fused) {
+  if (fused || strm) {
     o_pres = take(sizeof(uint64_t) * (size_t)kFusedMaxGrid);
     o_slots = take((size_t)16 * (size_t)(T * E));
     o_hv = take((size_t)16 * (size_t)((T * k + T) * (I / 2)));
+  }
+  if (strm) {
+    o_ssl = take((size_t)kStreamSlotStride * (size_t)E);
+    o_sdv = take((size_t)16 * (size_t)(k + 1) * (size_t)(H / 2));
   }
   if (x8) {
     o_xsl = take((size_t)256 * (size_t)E);  // device-scope logit slots, 256 bytes apart
@@ -238,11 +249,15 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
     char* b = static_cast<char*>(base);
     ws->ctl = reinterpret_cast<uint32_t*>(b + o_ctl);
     ws->fused = FusedWs();
-    if (fused) {
+    if (fused || strm) {
       ws->fused.ctl = ws->ctl;
       ws->fused.presence = reinterpret_cast<uint64_t*>(b + o_pres);
       ws->fused.slots = reinterpret_cast<uint32_t*>(b + o_slots);
       ws->fused.hv = reinterpret_cast<uint32_t*>(b + o_hv);
+    }
+    if (strm) {
+      ws->fused.sslots = reinterpret_cast<uint32_t*>(b + o_ssl);
+      ws->fused.sdv = reinterpret_cast<uint32_t*>(b + o_sdv);
     }
     if (x8) {
       ws->fused.xslots = reinterpret_cast<uint32_t*>(b + o_xsl);
@@ -421,6 +436,17 @@ int run_forward(const ForwardCall& c, void* workspace, hipStream_t stream) {
         if (int rc = launch_status(record_stage(i, stream), "profile event")) return rc;
       return ok();
     }
+    // one token with experts too large to stage whole: the streaming single launch
+    const pmoe::StreamPlan sp = ws.fused.sslots ? pmoe::stream_plan(T, H, I, E, top_k, has_shared)
+                                                : pmoe::StreamPlan{};
+    if (sp.ok) {
+      if (int rc = launch_status(record_stage(0, stream), "profile event")) return rc;
+      if (int rc = launch_status(record_stage(1, stream), "profile event")) return rc;
+      if (int rc = launch_status(pmoe::launch_decode_stream(sp, r, a, ws.fused, stream), "decode_stream")) return rc;
+      for (int i = 2; i < PHANTOM_MOE_PROFILE_EVENTS; ++i)
+        if (int rc = launch_status(record_stage(i, stream), "profile event")) return rc;
+      return ok();
+    }
   }
 
   const bool gemm = pmoe::gemm_regime(T, top_k, E);
@@ -461,6 +487,8 @@ const char* phantom_moe_expert_kernels(int64_t T, int64_t H, int64_t I, int E, i
   if (fp.ok) {
     // the whole layer is one launch
     gu = dn = fp.spec == pmoe::kFusedSpecX8 ? "moe_decode_x8_kernel" : "moe_decode_fused_kernel";
+  } else if (pmoe::stream_plan(T, H, I, E, top_k, has_shared ? 1 : 0).ok) {
+    gu = dn = "moe_decode_stream_kernel";
   } else if (pmoe::gemm_regime(T, top_k, E)) {
     gu = "gemm_gate_up_kernel";
     dn = "gemm_down_kernel";
@@ -552,6 +580,10 @@ int phantom_moe_set_option(int option, int value) {
       if (value != 0 && value != 1) return fail(PHANTOM_MOE_EINVAL, "DECODE_X8 takes 0 or 1, got %d", value);
       c.decode_x8 = value != 0;
       break;
+    case PHANTOM_MOE_OPT_DECODE_STREAM:
+      if (value < 0 || value > 2) return fail(PHANTOM_MOE_EINVAL, "DECODE_STREAM takes 0, 1 or 2, got %d", value);
+      c.decode_stream = value;
+      break;
     default:
       return fail(PHANTOM_MOE_EINVAL, "unknown option %d", option);
   }
@@ -568,6 +600,7 @@ int phantom_moe_get_option(int option, int* value) {
     case PHANTOM_MOE_OPT_FUSED_WAIT_POLLS: *value = (int)c.fused_wait_polls; break;
     case PHANTOM_MOE_OPT_FUSED_FAULT: *value = (int)c.fused_fault; break;
     case PHANTOM_MOE_OPT_DECODE_X8: *value = c.decode_x8 ? 1 : 0; break;
+    case PHANTOM_MOE_OPT_DECODE_STREAM: *value = c.decode_stream; break;
     default: return fail(PHANTOM_MOE_EINVAL, "unknown option %d", option);
   }
   return ok();

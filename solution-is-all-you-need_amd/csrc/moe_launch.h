@@ -71,6 +71,9 @@ struct FusedWs {
   uint32_t* xslots = nullptr;  // [E] tagged logits, 256 bytes apart
   uint32_t* xh = nullptr;      // [8][I / 2][4] tagged h units
   uint32_t* xpart = nullptr;   // [8][H / 2][4] tagged down partials
+  // the streaming one-token kernel's (null unless stream_shape_ok)
+  uint32_t* sslots = nullptr;  // [E] tagged logits, kStreamSlotStride bytes apart
+  uint32_t* sdv = nullptr;     // [k + shared][H / 2][4] tagged expert outputs (hv holds its h)
 };
 // Device-independent shape limits (the workspace plan reserves the fused
 // regions for these shapes).
@@ -79,6 +82,26 @@ bool fused_shape_ok(int64_t T, int64_t H, int64_t I, int E, int k, int has_share
 FusedPlan fused_plan(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
 // The dynamic LDS layout for ng gate/up and nd down items per workgroup.
 FusedLds fused_lds_layout(int T, int k, int E, int has_shared, int H, int I, int ng, int nd, int S_max);
+
+// ---- the single-launch layer for one token with experts too large to stage
+// whole (decode_stream.hip): every wave streams its weights through its own
+// ring of direct-to-LDS copies.
+constexpr uint32_t kStreamSlotStride = 128;  // bytes between its device-scope logit slots
+struct StreamLds {
+  uint32_t x, xs, lv, topk, h, red, ring;  // byte offsets: x operand, its sums, logits, top-k scratch, h, reduction, rings
+  uint32_t ring_wave, bytes;              // ring bytes per wave, total
+  int ns_gu, ns_dn;                       // ring stages (quads in flight) of gate/up and of down
+  int yrows;                              // rows of y each workgroup combines
+};
+struct StreamPlan {
+  bool ok;
+  int G;  // workgroups (one per CU)
+  StreamLds lds;
+};
+// Device-independent shape limits (the workspace reserves its regions for them).
+bool stream_shape_ok(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
+// The launch plan on the current device; .ok false means another path.
+StreamPlan stream_plan(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
 
 // Library options: initialised once from the environment on first use,
 // changed afterwards only by phantom_moe_set_option:
@@ -92,6 +115,7 @@ struct LibConfig {
   bool decode_x8;  // batch-1 top-8 decode per XCD where the shape and the device allow
   bool force_ksplit;
   uint32_t fused_wait_polls;  // bound of each wait of the single-launch path
+  int decode_stream;  // one-token streaming single launch: 0 off, 1 where no other single launch fits, 2 for every one-token shape
   uint32_t fused_fault;       // failure injection for tests: bit 0 the logit wait, bit 1 the gate/up wait,
                               // bit 2 the last workgroup reads the generation one ahead (a late start)
 };
@@ -234,6 +258,8 @@ bool gate_up_tile_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_
 bool down_tile_regime(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
 
 // The whole layer in one launch (decode_fused.hip); plan from fused_plan.
+hipError_t launch_decode_stream(const StreamPlan& pl, const RouteArgs& r, const ExpertArgs& x, const FusedWs& ws,
+                                hipStream_t stream);
 hipError_t launch_decode_fused(const FusedPlan& pl, const RouteArgs& r, const ExpertArgs& x, const FusedWs& ws,
                                hipStream_t stream);
 

@@ -15,7 +15,7 @@ ROOT = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(ROOT, "csrc")
 INCLUDE = os.path.join(os.path.dirname(ROOT), "include")
 SOURCES = ["q4_repack.hip", "router.hip", "expert_ffn.hip", "expert_gemm.hip", "decode_fused.hip",
-           "legacy_ffn.hip", "gate_calibrate.hip", "capi.hip"]
+           "decode_stream.hip", "legacy_ffn.hip", "gate_calibrate.hip", "capi.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

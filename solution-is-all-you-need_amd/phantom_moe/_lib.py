@@ -76,6 +76,7 @@ OPT_DECODE_KSPLIT = 2  # PHANTOM_MOE_OPT_DECODE_KSPLIT
 OPT_FUSED_WAIT_POLLS = 3  # PHANTOM_MOE_OPT_FUSED_WAIT_POLLS
 OPT_FUSED_FAULT = 4  # PHANTOM_MOE_OPT_FUSED_FAULT
 OPT_DECODE_X8 = 5  # PHANTOM_MOE_OPT_DECODE_X8
+OPT_DECODE_STREAM = 6  # PHANTOM_MOE_OPT_DECODE_STREAM
 
 
 class PhantomMoEError(RuntimeError):

@@ -82,6 +82,30 @@ def test_version_and_sizes():
     c = lib.phantom_moe_workspace_bytes(32, 2048, 768, 128, 8, 1)
     assert 0 < a < b and a < c
     assert lib.phantom_moe_workspace_bytes(0, 2048, 768, 128, 8, 0) == 0
+    # one-token layers reserve the streaming single launch's hand-off regions
+    # (logit slots 128 B apart, h units, expert-output units) on top of the
+    # staged plan's; a two-token layer does not
+    one = lib.phantom_moe_workspace_bytes(1, 4096, 14336, 8, 2, 0)
+    two = lib.phantom_moe_workspace_bytes(2, 4096, 14336, 8, 2, 0)
+    assert one > 16 * 3 * (14336 // 2) + 16 * 3 * (4096 // 2) + 128 * 8
+    assert two > 0
+
+
+def test_decode_stream_option():
+    """PHANTOM_MOE_OPT_DECODE_STREAM takes 0 (off), 1 (default: where no
+    staging single launch fits) or 2 (every one-token shape); anything else
+    is rejected and leaves the value unchanged."""
+    lib = _lib.load()
+    old = _lib.set_option(_lib.OPT_DECODE_STREAM, 2)
+    try:
+        v = ctypes.c_int()
+        assert lib.phantom_moe_get_option(_lib.OPT_DECODE_STREAM, ctypes.byref(v)) == 0 and v.value == 2
+        assert lib.phantom_moe_set_option(_lib.OPT_DECODE_STREAM, 3) == EINVAL
+        assert "DECODE_STREAM" in lib.phantom_moe_last_error().decode()
+        assert lib.phantom_moe_set_option(_lib.OPT_DECODE_STREAM, -1) == EINVAL
+        assert lib.phantom_moe_get_option(_lib.OPT_DECODE_STREAM, ctypes.byref(v)) == 0 and v.value == 2
+    finally:
+        _lib.set_option(_lib.OPT_DECODE_STREAM, old)
 
 
 def _route(**kw):
