@@ -214,7 +214,7 @@ size_t plan_workspace(int64_t T, int64_t H, int64_t I, int E, int k, int has_sha
   }
   if (strm) {
     o_ssl = take((size_t)kStreamSlotStride * (size_t)E);
-    o_sdv = take((size_t)16 * (size_t)(k + 1) * (size_t)(H / 2));
+    o_sdv = take((size_t)16 * (size_t)(k + 1) * (size_t)stream_kx_max(ceil_div(I, kQuad)) * (size_t)(H / 2));
   }
   if (x8) {
     o_xsl = take((size_t)256 * (size_t)E);  // device-scope logit slots, 256 bytes apart

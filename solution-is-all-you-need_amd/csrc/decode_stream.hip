@@ -57,6 +57,7 @@ struct StreamK {
   const float* bias;  // [E] or null
   int H, I, E, k, score_mode, has_shared;
   int Kq, KqI, S;  // quads of H and of I; slots with work (k + shared)
+  int kx;          // slices of I the down work of a slot is cut into
   const uint8_t* gate_nib;
   const uint16_t* gate_sc;
   const uint8_t* up_nib;
@@ -85,21 +86,24 @@ struct StreamK {
   uint32_t skew_gen;
 };
 
-// Down row tiles of the workgroups serving one slot: the G workgroups are
-// cut into S contiguous ranges, workgroup b serving slot j(b) =
-// floor(b S / G); the NT tiles of H of a slot are cut evenly over its
-// range.
+// Down work of workgroup b: the G workgroups are cut into S contiguous
+// ranges, workgroup b serving slot j(b) = floor(b S / G).  A slot's
+// workgroups are dealt round robin over kx slices of I (slice kk = li % kx
+// for the li-th workgroup of the range); those of one slice cut the NT row
+// tiles of H evenly.  A workgroup then needs h only for its slice of I.
 struct DnWork {
-  int slot, t0, nt;  // slot, first tile, tiles
+  int slot, kk, t0, nt;  // slot, slice of I, first tile, tiles
 };
-__device__ inline DnWork dn_work(int b, int G, int S, int NT) {
+__device__ inline DnWork dn_work(int b, int G, int S, int NT, int kx) {
   DnWork d;
   d.slot = (int)(((int64_t)b * S) / G);
   const int g0 = (int)(((int64_t)d.slot * G + S - 1) / S);  // first workgroup of the slot
   const int g1 = (int)(((int64_t)(d.slot + 1) * G + S - 1) / S);
   const int nw = g1 - g0, li = b - g0;
-  d.t0 = (int)(((int64_t)li * NT) / nw);
-  d.nt = (int)(((int64_t)(li + 1) * NT) / nw) - d.t0;
+  d.kk = li % kx;
+  const int ng = (nw - d.kk + kx - 1) / kx, tg = li / kx;  // workgroups of the slice; this one's rank
+  d.t0 = (int)(((int64_t)tg * NT) / ng);
+  d.nt = (int)(((int64_t)(tg + 1) * NT) / ng) - d.t0;
   return d;
 }
 
@@ -233,44 +237,94 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_stream_kernel(StreamK a)
     a.topk_w[threadIdx.x] = route_failed ? __builtin_nanf("") : s_sel_w[threadIdx.x];
   }
 
-  // ---- 2. gate/up items of this wave --------------------------------------------
+  // ---- 2. gate/up: this workgroup's items, split evenly over its waves ------------
+  // Workgroup b owns items u = b + m G (m = 0 .. nI - 1); item u is the 16-row
+  // tile r = u % NTI of I of slot j = u / NTI.  Their nI Kq quads, in item
+  // order, are cut into kFW contiguous ranges, one per wave, and each wave
+  // streams its range through its ring without a break at item boundaries.
+  // An item inside one wave's range is finished by that wave; an item cut
+  // between waves is summed from their partials (LDS, in wave order) after
+  // a barrier.  Every row of the MFMAs' A operand holds the token's x, so
+  // every row of a result holds the token's sums: element 0 of every lane is
+  // row 16 r + n of I, and only that element is scaled and summed (per
+  // group: scale times the sum over x (1 + n/16), and scale times the sum of
+  // x).
   const BufRsrc hv_r = buf_rsrc(a.hv, (uint32_t)(S * (I / 2) * 16));
   const int ns_gu = a.lds.ns_gu;
   const uint32_t bmask = vgpr_const(0x00780078u);
-  for (int u = w * G + b; u < S * NTI; u += kFW * G) {
-    const int j = u / NTI, r = u - j * NTI;
-    const int e = route_failed ? 0 : uni(s_sel_idx[j]);
-    const bool sh = e < 0;
-    // Every row of the MFMAs' A operand holds the token's x, so every row of
-    // a result holds the token's sums: element 0 of every lane is row 16 r + n
-    // of I, and only that element is scaled and summed (per group: scale
-    // times the sum over x (1 + n/16), and scale times the sum of x).
-    float ag = 0.0f, au = 0.0f, cg = 0.0f, cu = 0.0f;
+  float* s_gpart = s_red;  // [kFW waves][first | last segment][16 rows][ag, au, cg, cu]
+  const int nI = b < S * NTI ? (S * NTI - b + G - 1) / G : 0;
+  const int Tq = nI * Kq;
+  auto range_lo = [&](int ww) { return (int)(((int64_t)ww * Tq) / kFW); };
+  // h of item m from every lane's sums for row 16 r + n
+  auto publish = [&](int m, float ag, float au, float cg, float cu) {
+    const int u = b + m * G, j = u / NTI, r = u - j * NTI;
+    float h = __builtin_nanf("");
     if (!route_failed) {
-      const uint32_t nib_b = (uint32_t)I * (uint32_t)Kq * 64u, sc_b = (uint32_t)I * (uint32_t)Kq * 8u;
+      const float g = kUnitScale * ag - kUnitBias * cg;
+      const float uu = kUnitScale * au - kUnitBias * cu;
+      h = g * (1.0f / (1.0f + expf(-g))) * uu;
+    }
+    const uint32_t hb = float_to_half_bits(h);
+    const uint32_t lb = float_to_half_bits(h - half_bits_to_float32(hb));
+    const uint32_t hb2 = __shfl_down(hb, 1, kWave), lb2 = __shfl_down(lb, 1, kWave);
+    if (p == 0 && (n & 1) == 0) {
+      u32x4 v;
+      v.x = hb | (hb2 << 16);
+      v.y = tag;
+      v.z = lb | (lb2 << 16);
+      v.w = ~tag;
+      __builtin_amdgcn_raw_buffer_store_b128(v, hv_r, (j * (I / 2) + (kRowTile * r + n) / 2) * 16, 0, kDeviceScope);
+    }
+  };
+  {
+    const int g0 = range_lo(w), n_w = range_lo(w + 1) - g0;
+    // copy cursor: item im, quad iq, and the item's buffers
+    int im = g0 / Kq, iq = g0 - (g0 / Kq) * Kq;
+    i32x4 gnr = {0, 0, 0, 0}, unr = gnr, gsr = gnr, usr = gnr;
+    uint32_t itq0 = 0;
+    const uint32_t nib_b = (uint32_t)I * (uint32_t)Kq * 64u, sc_b = (uint32_t)I * (uint32_t)Kq * 8u;
+    auto item_buffers = [&]() {
+      const int u = b + im * G, j = u / NTI, r = u - j * NTI;
+      const int e = uni(s_sel_idx[j]);
+      const bool sh = e < 0;
       const uint8_t* gn = sh ? a.sh_gate_nib : a.gate_nib + (size_t)e * nib_b;
       const uint8_t* un = sh ? a.sh_up_nib : a.up_nib + (size_t)e * nib_b;
       const char* gs = reinterpret_cast<const char*>(sh ? a.sh_gate_sc : a.gate_sc) + (sh ? 0 : (size_t)e * sc_b);
       const char* us = reinterpret_cast<const char*>(sh ? a.sh_up_sc : a.up_sc) + (sh ? 0 : (size_t)e * sc_b);
-      const i32x4 gnr = buf_rsrc_words(gn, nib_b), unr = buf_rsrc_words(un, nib_b);
-      const i32x4 gsr = buf_rsrc_words(gs, sc_b), usr = buf_rsrc_words(us, sc_b);
-      const uint32_t tq0 = (uint32_t)r * (uint32_t)Kq;
-      auto issue = [&](int q, int stage) {
-        const uint32_t st = ring + (uint32_t)stage * kSGuStage;
-        const uint32_t tq = (uint32_t)uni((int)(tq0 + (uint32_t)q));
-        dma_b128_stream(gnr, st, (uint32_t)lane * 16u, tq * kQuadNibBytes);
-        dma_b128_stream(unr, st + 1024u, (uint32_t)lane * 16u, tq * kQuadNibBytes);
-        if (lane < 8) {
-          dma_b128_stream(gsr, st + 2048u, (uint32_t)lane * 16u, tq * 128u);
-          dma_b128_stream(usr, st + 2176u, (uint32_t)lane * 16u, tq * 128u);
-        }
-      };
-      const int pro = ns_gu < Kq ? ns_gu : Kq;
-      for (int q = 0; q < pro; ++q) issue(q, q);
-      int stage = 0;  // ring stage of quad q
-      for (int q = 0; q < Kq; ++q) {
-        // quad q's copies in; the younger ones (up to ns - 1 quads) may fly
-        const int younger = (q + ns_gu < Kq ? ns_gu : Kq - q) - 1;
+      gnr = buf_rsrc_words(gn, nib_b);
+      unr = buf_rsrc_words(un, nib_b);
+      gsr = buf_rsrc_words(gs, sc_b);
+      usr = buf_rsrc_words(us, sc_b);
+      itq0 = (uint32_t)r * (uint32_t)Kq;
+    };
+    auto issue_next = [&](int stage) {
+      const uint32_t st = ring + (uint32_t)stage * kSGuStage;
+      const uint32_t tq = (uint32_t)uni((int)(itq0 + (uint32_t)iq));
+      dma_b128_stream(gnr, st, (uint32_t)lane * 16u, tq * kQuadNibBytes);
+      dma_b128_stream(unr, st + 1024u, (uint32_t)lane * 16u, tq * kQuadNibBytes);
+      if (lane < 8) {
+        dma_b128_stream(gsr, st + 2048u, (uint32_t)lane * 16u, tq * 128u);
+        dma_b128_stream(usr, st + 2176u, (uint32_t)lane * 16u, tq * 128u);
+      }
+      if (++iq == Kq) {
+        iq = 0;
+        if (++im < nI) item_buffers();
+      }
+    };
+    if (!route_failed && n_w > 0) {
+      item_buffers();
+      const int pro = ns_gu < n_w ? ns_gu : n_w;
+      for (int i = 0; i < pro; ++i) issue_next(i);
+    }
+    int cm = g0 / Kq, cq = g0 - (g0 / Kq) * Kq;  // quad being summed
+    int seg_q0 = cq, seg_slot = 0;             // start quad of the segment; partial slot
+    float ag = 0.0f, au = 0.0f, cg = 0.0f, cu = 0.0f;
+    int stage = 0;  // ring stage of the quad being summed
+    for (int i = 0; i < n_w; ++i) {
+      if (!route_failed) {
+        // this quad's copies in; the younger ones (up to ns - 1 quads) may fly
+        const int younger = (i + ns_gu < n_w ? ns_gu : n_w - i) - 1;
         wait_vmcnt_le(kSGuCopies * younger);
         poll_clobber();
         const char* st = ring_p + stage * (int)kSGuStage;
@@ -278,9 +332,9 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_stream_kernel(StreamK a)
         const u32x4 uw = *reinterpret_cast<const u32x4*>(st + 1024 + lane * 16);
         const uint2 gsv = *reinterpret_cast<const uint2*>(st + 2048 + n * 8);
         const uint2 usv = *reinterpret_cast<const uint2*>(st + 2176 + n * 8);
-        const u32x4* xo = s_xop + (q * 4 + p) * 4;
+        const u32x4* xo = s_xop + (cq * 4 + p) * 4;
         const u32x4 xa[4] = {xo[0], xo[1], xo[2], xo[3]};
-        const f32x4 xs = *reinterpret_cast<const f32x4*>(s_xs + q * 4);
+        const f32x4 xs = *reinterpret_cast<const f32x4*>(s_xs + cq * 4);
         float dg[4], du[4];
         unpack_scales(gsv, dg);
         unpack_scales(usv, du);
@@ -300,32 +354,52 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_stream_kernel(StreamK a)
           cu += du[gi] * xs[gi];
         }
         // the stage is read (the MFMAs consumed it) before it is refilled
-        if (q + ns_gu < Kq) issue(q + ns_gu, stage);
+        if (i + ns_gu < n_w) issue_next(stage);
         stage = stage + 1 == ns_gu ? 0 : stage + 1;
       }
+      if (++cq == Kq || i == n_w - 1) {  // end of a segment
+        if (seg_q0 == 0 && cq == Kq) {
+          publish(cm, ag, au, cg, cu);
+        } else if (p == 0) {
+          const f32x4 v = {ag, au, cg, cu};
+          *reinterpret_cast<f32x4*>(s_gpart + ((w * 2 + seg_slot) * 16 + n) * 4) = v;
+        }
+        ag = au = cg = cu = 0.0f;
+        seg_q0 = 0;
+        seg_slot = 1;
+        if (cq == Kq) {
+          cq = 0;
+          ++cm;
+        }
+      }
     }
-    // row 16 r + n of I
-    float h = __builtin_nanf("");
-    if (!route_failed) {
-      const float g = kUnitScale * ag - kUnitBias * cg;
-      const float uu = kUnitScale * au - kUnitBias * cu;
-      h = g * (1.0f / (1.0f + expf(-g))) * uu;
+  }
+  lds_barrier();
+  // items cut between waves: wave m % kFW sums item m's partials in wave order
+  for (int m = w; m < nI; m += kFW) {
+    const int lo = m * Kq, hi = lo + Kq;
+    bool whole = false;
+    for (int ww = 0; ww < kFW; ++ww) whole = whole || (range_lo(ww) <= lo && range_lo(ww + 1) >= hi);
+    if (whole) continue;
+    float sg = 0.0f, su = 0.0f, sgc = 0.0f, suc = 0.0f;
+    for (int ww = 0; ww < kFW; ++ww) {
+      const int a0 = range_lo(ww), a1 = range_lo(ww + 1);
+      if (a1 <= lo || a0 >= hi || a1 <= a0) continue;
+      // item m is the first segment of wave ww when the wave starts inside it
+      const f32x4 v = *reinterpret_cast<const f32x4*>(s_gpart + ((ww * 2 + (a0 >= lo ? 0 : 1)) * 16 + n) * 4);
+      sg += v[0];
+      su += v[1];
+      sgc += v[2];
+      suc += v[3];
     }
-    const uint32_t hb = float_to_half_bits(h);
-    const uint32_t lb = float_to_half_bits(h - half_bits_to_float32(hb));
-    const uint32_t hb2 = __shfl_down(hb, 1, kWave), lb2 = __shfl_down(lb, 1, kWave);
-    if (p == 0 && (n & 1) == 0) {
-      u32x4 v;
-      v.x = hb | (hb2 << 16);
-      v.y = tag;
-      v.z = lb | (lb2 << 16);
-      v.w = ~tag;
-      __builtin_amdgcn_raw_buffer_store_b128(v, hv_r, (j * (I / 2) + (kRowTile * r + n) / 2) * 16, 0, kDeviceScope);
-    }
+    publish(m, sg, su, sgc, suc);
   }
 
   // ---- 3. down: this workgroup's slot and tiles -----------------------------------
-  const DnWork dw = dn_work(b, G, S, NTH);
+  const int kx = a.kx;
+  const DnWork dw = dn_work(b, G, S, NTH, kx);
+  // this workgroup's quads of I
+  const int qa = (int)(((int64_t)dw.kk * KqI) / kx), qb = (int)(((int64_t)(dw.kk + 1) * KqI) / kx);
   // waves per tile (a power of two) when the tiles are fewer than the waves:
   // they split the quads of I in contiguous slices
   int ks = 1;
@@ -339,36 +413,44 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_stream_kernel(StreamK a)
   const i32x4 dsr = buf_rsrc_words(reinterpret_cast<const char*>(sh_dn ? a.sh_down_sc : a.down_sc) +
                                        (sh_dn ? 0 : (size_t)e_dn * dsc_b), dsc_b);
   const int slice = w % ks;                    // this wave's slice of I
-  const int q0 = (int)(((int64_t)slice * KqI) / ks), q1 = (int)(((int64_t)(slice + 1) * KqI) / ks);
+  const int q0 = qa + (int)(((int64_t)slice * (qb - qa)) / ks), q1 = qa + (int)(((int64_t)(slice + 1) * (qb - qa)) / ks);
   const int nq = q1 - q0;
   // this wave's tiles: t0 + w / ks, then + kFW / ks
   const int tstep = kFW / ks;
-  auto dn_issue = [&](int tl, int q, int stage) {  // local tile tl, quad q0 + q
+  const int tl_first = w / ks;
+  // this wave's stream: its tiles (rounds rr < nr_w) times the quads of its
+  // slice, copied without a break between tiles
+  const int nr_w = (!route_failed && nq > 0 && tl_first < dw.nt) ? (dw.nt - tl_first + tstep - 1) / tstep : 0;
+  const int n_dn = nr_w * nq;
+  int d_ir = 0, d_iq = 0;  // copy cursor: round, quad
+  auto dn_issue_next = [&](int stage) {
     const uint32_t st = ring + (uint32_t)stage * kSDnStage;
-    const uint32_t tq = (uint32_t)uni((dw.t0 + tl) * KqI + q0 + q);
+    const uint32_t tq = (uint32_t)uni((dw.t0 + tl_first + d_ir * tstep) * KqI + q0 + d_iq);
     dma_b128_stream(dnr, st, (uint32_t)lane * 16u, tq * kQuadNibBytes);
     if (lane < 8) dma_b128_stream(dsr, st + 1024u, (uint32_t)lane * 16u, tq * 128u);
+    if (++d_iq == nq) {
+      d_iq = 0;
+      ++d_ir;
+    }
   };
-  const int tl_first = w / ks;
-  const bool dn_any = !route_failed && tl_first < dw.nt && nq > 0;
-  const int dn_pro = ns_dn < nq ? ns_dn : nq;
-  // the first tile's ring stages, before h is polled (they need no h)
-  if (dn_any)
-    for (int q = 0; q < dn_pro; ++q) dn_issue(tl_first, q, q);
-  // h of the slot into LDS (all threads), from the gate/up items' units: unit
-  // v holds rows i0 = 2v and i0 + 1, at K positions kmap(pp, s), kmap(pp, s + 4)
-  // of part pp = (i0 % 16) / 4 of group i0 / 32
+  // the first ring stages, before h is polled (they need no h)
+  for (int i = 0; i < (ns_dn < n_dn ? ns_dn : n_dn); ++i) dn_issue_next(i);
+  // h of the slot's rows in this workgroup's quads [qa, qb) of I into LDS
+  // (all threads), from the gate/up items' units: unit v holds rows i0 = 2v
+  // and i0 + 1, at K positions kmap(pp, s), kmap(pp, s + 4) of part
+  // pp = (i0 % 16) / 4 of group i0 / 32
   __shared__ int s_hfail;
   if (threadIdx.x == 0) s_hfail = 0;
   // zero first: groups past I (a ragged last quad) meet q = 0 there, and
   // whatever the LDS held could be NaN
-  for (int i = threadIdx.x; i < KqI * 128; i += kFThreads) reinterpret_cast<uint32_t*>(s_h)[i] = 0u;
+  for (int i = qa * 128 + (int)threadIdx.x; i < qb * 128; i += kFThreads) reinterpret_cast<uint32_t*>(s_h)[i] = 0u;
   lds_barrier();
+  const int va = qa * (kQuad / 2), vb = qb * (kQuad / 2) < I / 2 ? qb * (kQuad / 2) : I / 2;  // units
   if (!route_failed) {
     const uint32_t want = tag + a.skew_h;
-    for (int v0 = 0; v0 < I / 2; v0 += kFThreads) {
+    for (int v0 = va; v0 < vb; v0 += kFThreads) {
       const int v = v0 + (int)threadIdx.x;
-      const bool mine = v < I / 2;
+      const bool mine = v < vb;
       u32x4 hvv = {0u, 0u, 0u, 0u};
       bool ok = !mine;
       if (mine) {
@@ -408,23 +490,21 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_stream_kernel(StreamK a)
   }
   lds_barrier();
   const bool h_failed = uni(s_hfail) != 0;
-  const BufRsrc dv_r = buf_rsrc(a.dv, (uint32_t)(S * (H / 2) * 16));
+  const BufRsrc dv_r = buf_rsrc(a.dv, (uint32_t)(S * kx * (H / 2) * 16));
   // every wave runs the same number of tile rounds, so the K-split barrier
   // below is reached by all
   const int rounds = (dw.nt + tstep - 1) / tstep;
+  int stage = 0;  // ring stage of the quad being summed
   for (int rr = 0; rr < rounds; ++rr) {
     const int tl = tl_first + rr * tstep;
-    const bool have = dn_any && tl < dw.nt;
     // A operand rows alternate h hi (even rows) and h lo (odd rows), so
     // elements 0 and 1 of every lane are the hi and lo sums of output row
     // 16 tile + n; only those are scaled and summed
     float acc_hi = 0.0f, acc_lo = 0.0f;
-    if (have) {
-      if (rr > 0)
-        for (int q = 0; q < dn_pro; ++q) dn_issue(tl, q, q);
-      int stage = 0;  // ring stage of quad q
+    if (rr < nr_w) {
       for (int q = 0; q < nq; ++q) {
-        const int younger = (q + ns_dn < nq ? ns_dn : nq - q) - 1;
+        const int i = rr * nq + q;
+        const int younger = (i + ns_dn < n_dn ? ns_dn : n_dn - i) - 1;
         wait_vmcnt_le(kSDnCopies * younger);
         poll_clobber();
         const char* st = ring_p + stage * (int)kSDnStage;
@@ -443,7 +523,7 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_stream_kernel(StreamK a)
           acc_hi += dv[gi] * pv[gi][0];
           acc_lo += dv[gi] * pv[gi][1];
         }
-        if (q + ns_dn < nq) dn_issue(tl, q + ns_dn, stage);
+        if (i + ns_dn < n_dn) dn_issue_next(stage);
         stage = stage + 1 == ns_dn ? 0 : stage + 1;
       }
     }
@@ -466,7 +546,8 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_stream_kernel(StreamK a)
         v.z = __builtin_bit_cast(uint32_t, d2);
         v.w = ~tag;
         const int row = (dw.t0 + tl) * kRowTile + n;
-        __builtin_amdgcn_raw_buffer_store_b128(v, dv_r, (dw.slot * (H / 2) + row / 2) * 16, 0, kDeviceScope);
+        __builtin_amdgcn_raw_buffer_store_b128(v, dv_r, ((dw.slot * kx + dw.kk) * (H / 2) + row / 2) * 16, 0,
+                                               kDeviceScope);
       }
     }
     if (ks > 1) lds_barrier();  // s_red is free for the next round
@@ -477,15 +558,16 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_stream_kernel(StreamK a)
     const int R = a.lds.yrows;
     const int r0 = b * R;
     const int nr = r0 + R <= H ? R : (H > r0 ? H - r0 : 0);
-    // lane l: rows r0 + 2 (l % (R / 2)) .. + 1 of slot l / (R / 2), then more
-    // slots in later rounds; the slots' values go through LDS (s_red)
-    const int upr = R / 2;  // units per slot
-    float* s_d = s_red;     // [S][R] expert outputs of the rows (reused)
+    // lane l: rows r0 + 2 (l % (R / 2)) .. + 1 of part jk = l / (R / 2) (slot
+    // jk / kx, slice of I jk % kx), then more parts in later rounds; the
+    // values go through LDS (s_red)
+    const int upr = R / 2;  // units per part
+    float* s_d = s_red;     // [S][kx][R] expert outputs of the rows, by slice of I (reused)
     const uint32_t want = tag + a.skew_h;
-    for (int c0 = 0; c0 < S * upr; c0 += kWave) {
+    for (int c0 = 0; c0 < S * kx * upr; c0 += kWave) {
       const int c = c0 + lane;
       const int j = c / upr, uu = c - j * upr;
-      const bool mine = c < S * upr && 2 * uu < nr;
+      const bool mine = c < S * kx * upr && 2 * uu < nr;
       u32x4 v = {0u, 0u, 0u, 0u};
       bool ok = !mine || route_failed;
       const int off = (j * (H / 2) + r0 / 2 + uu) * 16;
@@ -513,10 +595,17 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_stream_kernel(StreamK a)
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
+    // d_j = its slices' parts summed in slice order; y = sum_j w_j d_j in
+    // slot order, plus the shared expert's d
+    auto d_of = [&](int j, int rr) {
+      float d = s_d[(j * kx) * R + rr];
+      for (int kk = 1; kk < kx; ++kk) d += s_d[(j * kx + kk) * R + rr];
+      return d;
+    };
     for (int rr = lane; rr < nr; rr += kWave) {
       float yv = 0.0f;
-      for (int j = 0; j < k; ++j) yv += s_sel_w[j] * s_d[j * R + rr];
-      if (a.has_shared) yv += s_d[k * R + rr];
+      for (int j = 0; j < k; ++j) yv += s_sel_w[j] * d_of(j, rr);
+      if (a.has_shared) yv += d_of(k, rr);
       a.y[r0 + rr] = route_failed ? __builtin_nanf("") : yv;
     }
   }
@@ -542,6 +631,19 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_stream_kernel(StreamK a)
 
 }  // namespace
 
+int stream_kx_max(int64_t KqI) {
+  // at most 16 quads of h (16 KiB of tagged units) per workgroup, up to 8 slices
+  int kx = 1;
+  while (kx < 8 && KqI > 16 * (int64_t)kx) kx *= 2;
+  return kx;
+}
+
+int stream_kx(int64_t KqI, int G, int S) {
+  int kx = stream_kx_max(KqI);
+  while (kx > 1 && kx > G / S) kx /= 2;  // every slice of every slot gets a workgroup
+  return kx;
+}
+
 bool stream_shape_ok(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared) {
   if (T != 1 || E < 1 || E > kMaxExperts || k < 1 || k > kMaxTopK || k > E) return false;
   if (H < kGroup || H % kGroup || I < kGroup || I % kGroup) return false;
@@ -549,7 +651,7 @@ bool stream_shape_ok(int64_t T, int64_t H, int64_t I, int E, int k, int has_shar
   // 32-bit buffer sizes of one expert's matrices and of the hand-off regions
   if ((uint64_t)I * Kq * 64 >= kMaxRsrcBytes || (uint64_t)H * KqI * 64 >= kMaxRsrcBytes) return false;
   const int64_t S = k + (has_shared ? 1 : 0);
-  if (S * (I / 2) * 16 >= ((int64_t)1 << 31) || S * (H / 2) * 16 >= ((int64_t)1 << 31)) return false;
+  if (S * (I / 2) * 16 >= ((int64_t)1 << 31) || S * stream_kx_max(KqI) * (H / 2) * 16 >= ((int64_t)1 << 31)) return false;
   return true;
 }
 
@@ -560,8 +662,8 @@ StreamPlan stream_plan(int64_t T, int64_t H, int64_t I, int E, int k, int has_sh
   if (!cfg.decode_fused || !cfg.decode_stream || !stream_shape_ok(T, H, I, E, k, has_shared)) return pl;
   int G = device_cus();
   if (G > kFusedMaxGrid) G = kFusedMaxGrid;
-  if (G < 2 || (int64_t)G * kFW < E) return pl;
   const int S = k + (has_shared ? 1 : 0);
+  if (G < 2 || G < S || (int64_t)G * kFW < E) return pl;
   StreamLds l = {};
   const uint32_t Kq = (uint32_t)((H + kQuad - 1) / kQuad), KqI = (uint32_t)((I + kQuad - 1) / kQuad);
   l.yrows = (int)((H + G - 1) / G);
@@ -572,7 +674,12 @@ StreamPlan stream_plan(int64_t T, int64_t H, int64_t I, int E, int k, int has_sh
   l.topk = align_lds(l.lv + (uint32_t)E * 8u);
   l.h = align_lds(l.topk + (uint32_t)k * 40u);
   l.red = align_lds(l.h + KqI * 512u);
-  const uint32_t red_bytes = (uint32_t)(kFW * 16 > S * l.yrows ? kFW * 16 : S * l.yrows) * 4u;
+  // the down phase's K-split partials, the combine's expert outputs, and
+  // before them the gate/up partials of items cut between waves
+  const int kx = stream_kx(KqI, G, S);
+  uint32_t red_floats = (uint32_t)(S * kx * l.yrows > kFW * 16 ? S * kx * l.yrows : kFW * 16);
+  if (red_floats < (uint32_t)kFW * 2 * 16 * 4) red_floats = (uint32_t)kFW * 2 * 16 * 4;
+  const uint32_t red_bytes = red_floats * 4u;
   l.ring = align_lds(l.red + red_bytes);
   if (l.ring >= kFusedDynLdsMax) return pl;
   l.ring_wave = ((uint32_t)kFusedDynLdsMax - l.ring) / kFW / 256u * 256u;
@@ -583,6 +690,7 @@ StreamPlan stream_plan(int64_t T, int64_t H, int64_t I, int E, int k, int has_sh
   if (l.ns_gu < 2 || l.ns_dn < 2) return pl;
   l.bytes = l.ring + kFW * l.ring_wave;
   pl.G = G;
+  pl.kx = kx;
   pl.lds = l;
   pl.ok = true;
   return pl;
@@ -604,6 +712,7 @@ hipError_t launch_decode_stream(const StreamPlan& pl, const RouteArgs& r, const 
   a.Kq = (int)ceil_div(r.H, kQuad);
   a.KqI = (int)ceil_div(x.I, kQuad);
   a.S = r.k + (x.has_shared ? 1 : 0);
+  a.kx = pl.kx;
   a.gate_nib = x.gate_nib;
   a.gate_sc = x.gate_scale;
   a.up_nib = x.up_nib;

@@ -73,7 +73,7 @@ struct FusedWs {
   uint32_t* xpart = nullptr;   // [8][H / 2][4] tagged down partials
   // the streaming one-token kernel's (null unless stream_shape_ok)
   uint32_t* sslots = nullptr;  // [E] tagged logits, kStreamSlotStride bytes apart
-  uint32_t* sdv = nullptr;     // [k + shared][H / 2][4] tagged expert outputs (hv holds its h)
+  uint32_t* sdv = nullptr;     // [k + shared][slices of I][H / 2][4] tagged expert output parts (hv holds h)
 };
 // Device-independent shape limits (the workspace plan reserves the fused
 // regions for these shapes).
@@ -95,11 +95,16 @@ struct StreamLds {
 };
 struct StreamPlan {
   bool ok;
-  int G;  // workgroups (one per CU)
+  int G;   // workgroups (one per CU)
+  int kx;  // slices of I a slot's down work is cut into (stream_kx)
   StreamLds lds;
 };
 // Device-independent shape limits (the workspace reserves its regions for them).
 bool stream_shape_ok(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
+// Slices of I (quads KqI) a slot's down work is cut into: the workspace bound
+// (device-independent), and the count on a device of G workgroups for S slots.
+int stream_kx_max(int64_t KqI);
+int stream_kx(int64_t KqI, int G, int S);
 // The launch plan on the current device; .ok false means another path.
 StreamPlan stream_plan(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
 

@@ -68,6 +68,10 @@ CASES = [
     synth.MoEConfig("s_k1", 256, 128, 8, 1, 1),
     synth.MoEConfig("s_e512_k32", 256, 64, 512, 32, 1),
     synth.MoEConfig("s_wide_i", 256, 4096, 8, 2, 1),
+    # I of 65 (66) quads: a slot's down work is cut into 8 slices of I, whose
+    # parts the combine sums; the second also ends I in a ragged quad
+    synth.MoEConfig("s_kx8", 256, 8320, 4, 2, 1),
+    synth.MoEConfig("s_kx8_ragged_shared", 288, 8352, 4, 2, 1, score="sigmoid", shared=True),
 ]
 
 
