@@ -31,12 +31,14 @@ __device__ inline uint64_t logit_key(double v) {
 // Top-k of one token (called by all 64 lanes of one wave); `row` holds the
 // token's E logits (global or LDS), lane l takes experts l, l + 64, ...
 //  1. Radix descent over the key bits towards the largest x with
-//     #{key >= x} >= k, the k-th largest key (one ballot + popcount per bit
-//     and per register), stopping early at any x with exactly k keys >= x.
+//     #{key >= x} >= k, the k-th largest key (two bits a step, one ballot +
+//     popcount per threshold and register), stopping early at any x with
+//     exactly k keys >= x.
 //  2. Winners: every key > x, then keys == x in increasing expert index until
 //     k are taken -- the (value desc, index asc) order's first k.
 //  3. The k winners are compacted to LDS in index order and lane i < k ranks
-//     winner i among them; rank r goes to slot r.
+//     winner i among them (the other winners read from their lanes); rank r
+//     goes to slot r.
 //  4. Weights, fp64: softmax exp(l_j - l_0) / sum_i exp(l_i - l_0), or
 //     sigmoid(l_j) / sum_i sigmoid(l_i), the sum taken in slot order; stored
 //     as fp32.
@@ -62,17 +64,31 @@ __device__ __attribute__((always_inline)) inline void wave_topk_row(const double
   }
   // Invariant: #{key >= kth} >= k.  Once it is exactly k the winners are
   // known (every other key is below kth), so the descent stops there --
-  // usually at the first bit that separates the k-th and (k+1)-th keys.
+  // usually at the first bits that separate the k-th and (k+1)-th keys.  Two
+  // bits a step: the three thresholds' counts are independent, so a step
+  // costs about one count's latency (each step waits on ballots and
+  // popcounts; one bit a step ran about 150 cycles a bit).
   uint64_t kth = 0;
   int at_kth = kWave * NV;
-  for (int bit = 63; bit >= 0 && at_kth != k; --bit) {
-    const uint64_t cand = kth | (1ull << bit);
-    int cnt = 0;
+  for (int bit = 63; bit >= 1 && at_kth != k; bit -= 2) {
+    const uint64_t hb = 1ull << bit, lb = 1ull << (bit - 1);
+    const uint64_t c1 = kth | lb, c2 = kth | hb, c3 = kth | hb | lb;
+    int n1 = 0, n2 = 0, n3 = 0;
 #pragma unroll
-    for (int v = 0; v < NV; ++v) cnt += __popcll(__ballot(key[v] >= cand));
-    if (cnt >= k) {
-      kth = cand;
-      at_kth = cnt;
+    for (int v = 0; v < NV; ++v) {
+      n1 += __popcll(__ballot(key[v] >= c1));
+      n2 += __popcll(__ballot(key[v] >= c2));
+      n3 += __popcll(__ballot(key[v] >= c3));
+    }
+    if (n3 >= k) {
+      kth = c3;
+      at_kth = n3;
+    } else if (n2 >= k) {
+      kth = c2;
+      at_kth = n2;
+    } else if (n1 >= k) {
+      kth = c1;
+      at_kth = n1;
     }
   }
   int n_gt = 0;
@@ -97,36 +113,50 @@ __device__ __attribute__((always_inline)) inline void wave_topk_row(const double
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  // lane i < k holds winner i (index order) and ranks it among the k, the
+  // others' keys and indices broadcast from their lanes
+  uint64_t mk = 0ull;
+  int me = 0;
+  double mv = 0.0;
   if (lane < k) {
-    const uint64_t mk = s_ck[lane];
-    const int me = s_ci[lane];
-    int r = 0;
-    for (int j = 0; j < k; ++j) {
-      const uint64_t kj = s_ck[j];
-      r += (kj > mk || (kj == mk && s_ci[j] < me)) ? 1 : 0;
-    }
+    mk = s_ck[lane];
+    me = s_ci[lane];
+    mv = s_cv[lane];
+  }
+  int r = 0;
+  for (int j = 0; j < k; ++j) {
+    const uint64_t kj = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(mk >> 32), j) << 32) |
+                        (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)mk, j);
+    const int cj = __builtin_amdgcn_readlane(me, j);
+    r += (kj > mk || (kj == mk && cj < me)) ? 1 : 0;
+  }
+  if (lane < k) {
     s_idx[r] = me;
-    s_val[r] = s_cv[lane];
+    s_val[r] = mv;
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  // Weights: lane i (< k) owns slot i; every lane sums the k terms in slot
-  // order, so the normaliser is the same sequential fp64 sum as the oracle's.
+  // Weights: lane i (< k) owns slot i; the k terms are summed in slot order,
+  // so the normaliser is the same sequential fp64 sum as the oracle's.
   double ej = 0.0;
+  int oi = 0;
   if (lane < k) {
     const double v = s_val[lane];
     ej = (score_mode == 0) ? exp(v - s_val[0]) : 1.0 / (1.0 + exp(-v));
-    s_e[lane] = ej;
+    oi = s_idx[lane];
   }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  double sum = 0.0;
+  for (int i = 0; i < k; ++i) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, ej);
+    sum += __builtin_bit_cast(double, ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(b >> 32), i) << 32) |
+                                          (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, i));
+  }
   if (lane < k) {
-    double sum = 0.0;
-    for (int i = 0; i < k; ++i) sum += s_e[i];
-    out_idx[lane] = s_idx[lane];
-    if (out_idx2) out_idx2[lane] = s_idx[lane];
+    out_idx[lane] = oi;
+    if (out_idx2) out_idx2[lane] = oi;
     out_w[lane] = (float)(ej / sum);
   }
+  (void)s_e;
   __builtin_amdgcn_wave_barrier();
 }
 
