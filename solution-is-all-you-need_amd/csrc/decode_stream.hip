@@ -182,7 +182,178 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_stream_kernel(StreamK a)
     s_xs[q * 4 + gi] = (sp[0] + sp[1]) + (sp[2] + sp[3]);
   }
 
-  // ---- 1. the last wave polls the logits and selects the experts ----------------
+  // ---- 1. selection (last wave) while the other waves start the shared expert --
+  // Gate/up items: item u is the 16-row tile r = u % NTI of I of slot
+  // j = u / NTI (slot k is the shared expert); workgroup b owns items
+  // u = b + m G, m = 0 .. nI - 1, of which the first nR are routed.  The
+  // shared expert's items need no routing, so waves 0 .. 6 stream them while
+  // the last wave selects the experts; the routed items follow on all eight
+  // waves.  Within each of the two groups the items' quads, in item order,
+  // are cut into equal contiguous ranges, one per wave, streamed through the
+  // wave's ring without a break at item boundaries; an item inside one
+  // wave's range is finished by that wave, an item cut between waves is
+  // summed from their partials (LDS, in wave order) after a barrier.  Every
+  // row of the MFMAs' A operand holds the token's x, so every row of a
+  // result holds the token's sums: element 0 of every lane is row 16 r + n
+  // of I, and only that element is scaled and summed (per group: scale
+  // times the sum over x (1 + n/16), and scale times the sum of x).
+  lds_barrier();  // the x operand is in LDS
+  const BufRsrc hv_r = buf_rsrc(a.hv, (uint32_t)(S * (I / 2) * 16));
+  const int ns_gu = a.lds.ns_gu;
+  const uint32_t bmask = vgpr_const(0x00780078u);
+  const int nI = b < S * NTI ? (S * NTI - b + G - 1) / G : 0;
+  const int nR = b < k * NTI ? (k * NTI - b + G - 1) / G : 0;
+  // partials of items cut between waves: [kFW waves][first | last segment][16 rows][ag, au, cg, cu],
+  // one array for the shared items and one for the routed ones
+  float* s_gpart_sh = s_red;
+  float* s_gpart_rt = s_red + kFW * 2 * 16 * 4;
+  bool route_failed = false;  // known after the selection's barrier
+  // h of item m from every lane's sums for row 16 r + n (NaN when !ok)
+  auto publish = [&](int m, float ag, float au, float cg, float cu, bool ok) {
+    const int u = b + m * G, j = u / NTI, r = u - j * NTI;
+    float h = __builtin_nanf("");
+    if (ok) {
+      const float g = kUnitScale * ag - kUnitBias * cg;
+      const float uu = kUnitScale * au - kUnitBias * cu;
+      h = g * (1.0f / (1.0f + expf(-g))) * uu;
+    }
+    const uint32_t hb = float_to_half_bits(h);
+    const uint32_t lb = float_to_half_bits(h - half_bits_to_float32(hb));
+    const uint32_t hb2 = __shfl_down(hb, 1, kWave), lb2 = __shfl_down(lb, 1, kWave);
+    if (p == 0 && (n & 1) == 0) {
+      u32x4 v;
+      v.x = hb | (hb2 << 16);
+      v.y = tag;
+      v.z = lb | (lb2 << 16);
+      v.w = ~tag;
+      __builtin_amdgcn_raw_buffer_store_b128(v, hv_r, (j * (I / 2) + (kRowTile * r + n) / 2) * 16, 0, kDeviceScope);
+    }
+  };
+  const uint32_t nib_b = (uint32_t)I * (uint32_t)Kq * 64u, sc_b = (uint32_t)I * (uint32_t)Kq * 8u;
+  // items m in [mb, mb + nit) over waves 0 .. nwv - 1; run: stream and sum
+  // (else every item this wave finishes is published as NaN)
+  auto run_items = [&](int mb, int nit, int nwv, float* gpart, bool run, bool ok) {
+    const int Tq = nit * Kq;
+    const int g0 = w < nwv ? (int)(((int64_t)w * Tq) / nwv) : Tq;
+    const int n_w = w < nwv ? (int)(((int64_t)(w + 1) * Tq) / nwv) - g0 : 0;
+    // copy cursor: item im, quad iq, and the item's buffers
+    int im = g0 / Kq, iq = g0 - (g0 / Kq) * Kq;
+    i32x4 gnr = {0, 0, 0, 0}, unr = gnr, gsr = gnr, usr = gnr;
+    uint32_t itq0 = 0;
+    auto item_buffers = [&]() {
+      const int u = b + (mb + im) * G, j = u / NTI, r = u - j * NTI;
+      const int e = j < k ? uni(s_sel_idx[j]) : -1;
+      const bool sh = e < 0;
+      const uint8_t* gn = sh ? a.sh_gate_nib : a.gate_nib + (size_t)e * nib_b;
+      const uint8_t* un = sh ? a.sh_up_nib : a.up_nib + (size_t)e * nib_b;
+      const char* gs = reinterpret_cast<const char*>(sh ? a.sh_gate_sc : a.gate_sc) + (sh ? 0 : (size_t)e * sc_b);
+      const char* us = reinterpret_cast<const char*>(sh ? a.sh_up_sc : a.up_sc) + (sh ? 0 : (size_t)e * sc_b);
+      gnr = buf_rsrc_words(gn, nib_b);
+      unr = buf_rsrc_words(un, nib_b);
+      gsr = buf_rsrc_words(gs, sc_b);
+      usr = buf_rsrc_words(us, sc_b);
+      itq0 = (uint32_t)r * (uint32_t)Kq;
+    };
+    auto issue_next = [&](int stage) {
+      const uint32_t st = ring + (uint32_t)stage * kSGuStage;
+      const uint32_t tq = (uint32_t)uni((int)(itq0 + (uint32_t)iq));
+      dma_b128_stream(gnr, st, (uint32_t)lane * 16u, tq * kQuadNibBytes);
+      dma_b128_stream(unr, st + 1024u, (uint32_t)lane * 16u, tq * kQuadNibBytes);
+      if (lane < 8) {
+        dma_b128_stream(gsr, st + 2048u, (uint32_t)lane * 16u, tq * 128u);
+        dma_b128_stream(usr, st + 2176u, (uint32_t)lane * 16u, tq * 128u);
+      }
+      if (++iq == Kq) {
+        iq = 0;
+        if (++im < nit) item_buffers();
+      }
+    };
+    if (run && n_w > 0) {
+      item_buffers();
+      const int pro = ns_gu < n_w ? ns_gu : n_w;
+      for (int i = 0; i < pro; ++i) issue_next(i);
+    }
+    int cm = g0 / Kq, cq = g0 - (g0 / Kq) * Kq;  // quad being summed
+    int seg_q0 = cq, seg_slot = 0;             // start quad of the segment; partial slot
+    float ag = 0.0f, au = 0.0f, cg = 0.0f, cu = 0.0f;
+    int stage = 0;  // ring stage of the quad being summed
+    for (int i = 0; i < n_w; ++i) {
+      if (run) {
+        // this quad's copies in; the younger ones (up to ns - 1 quads) may fly
+        const int younger = (i + ns_gu < n_w ? ns_gu : n_w - i) - 1;
+        wait_vmcnt_le(kSGuCopies * younger);
+        poll_clobber();
+        const char* st = ring_p + stage * (int)kSGuStage;
+        const u32x4 gw = *reinterpret_cast<const u32x4*>(st + lane * 16);
+        const u32x4 uw = *reinterpret_cast<const u32x4*>(st + 1024 + lane * 16);
+        const uint2 gsv = *reinterpret_cast<const uint2*>(st + 2048 + n * 8);
+        const uint2 usv = *reinterpret_cast<const uint2*>(st + 2176 + n * 8);
+        const u32x4* xo = s_xop + (cq * 4 + p) * 4;
+        const u32x4 xa[4] = {xo[0], xo[1], xo[2], xo[3]};
+        const f32x4 xs = *reinterpret_cast<const f32x4*>(s_xs + cq * 4);
+        float dg[4], du[4];
+        unpack_scales(gsv, dg);
+        unpack_scales(usv, du);
+        const uint32_t gwv[4] = {gw.x, gw.y, gw.z, gw.w};
+        const uint32_t uwv[4] = {uw.x, uw.y, uw.z, uw.w};
+        f32x4 pg[4], pu[4];
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          pg[gi] = mfma_bf16_16x16x32(xa[gi], dequant_unit_bf16(gwv[gi], bmask), z);
+          pu[gi] = mfma_bf16_16x16x32(xa[gi], dequant_unit_bf16(uwv[gi], bmask), z);
+        }
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          ag += dg[gi] * pg[gi][0];
+          au += du[gi] * pu[gi][0];
+          cg += dg[gi] * xs[gi];
+          cu += du[gi] * xs[gi];
+        }
+        // the stage is read (the MFMAs consumed it) before it is refilled
+        if (i + ns_gu < n_w) issue_next(stage);
+        stage = stage + 1 == ns_gu ? 0 : stage + 1;
+      }
+      if (++cq == Kq || i == n_w - 1) {  // end of a segment
+        if (seg_q0 == 0 && cq == Kq) {
+          publish(mb + cm, ag, au, cg, cu, ok);
+        } else if (p == 0) {
+          const f32x4 v = {ag, au, cg, cu};
+          *reinterpret_cast<f32x4*>(gpart + ((w * 2 + seg_slot) * 16 + n) * 4) = v;
+        }
+        ag = au = cg = cu = 0.0f;
+        seg_q0 = 0;
+        seg_slot = 1;
+        if (cq == Kq) {
+          cq = 0;
+          ++cm;
+        }
+      }
+    }
+  };
+  // after a barrier: items cut between waves, wave m % kFW summing item m's
+  // partials in wave order
+  auto finish_cut_items = [&](int mb, int nit, int nwv, const float* gpart, bool ok) {
+    const int Tq = nit * Kq;
+    auto range_lo = [&](int ww) { return ww < nwv ? (int)(((int64_t)ww * Tq) / nwv) : Tq; };
+    for (int m = w; m < nit; m += kFW) {
+      const int lo = m * Kq, hi = lo + Kq;
+      bool whole = false;
+      for (int ww = 0; ww < nwv; ++ww) whole = whole || (range_lo(ww) <= lo && range_lo(ww + 1) >= hi);
+      if (whole) continue;
+      float sg = 0.0f, su = 0.0f, sgc = 0.0f, suc = 0.0f;
+      for (int ww = 0; ww < nwv; ++ww) {
+        const int a0 = range_lo(ww), a1 = range_lo(ww + 1);
+        if (a1 <= lo || a0 >= hi || a1 <= a0) continue;
+        // item m is the first segment of wave ww when the wave starts inside it
+        const f32x4 v = *reinterpret_cast<const f32x4*>(gpart + ((ww * 2 + (a0 >= lo ? 0 : 1)) * 16 + n) * 4);
+        sg += v[0];
+        su += v[1];
+        sgc += v[2];
+        suc += v[3];
+      }
+      publish(mb + m, sg, su, sgc, suc, ok);
+    }
+  };
   if (w == kFW - 1) {
     const uint32_t want = tag + a.skew_route;
     constexpr int kNV = kMaxExperts / kWave;
@@ -234,172 +405,22 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_stream_kernel(StreamK a)
       s_sel_w[k] = 1.0f;
     }
   }
+  // the shared expert's items, on waves 0 .. kFW - 2 (the last wave selects)
+  run_items(nR, nI - nR, kFW - 1, s_gpart_sh, true, true);
   asm volatile("" ::"s"(tag));  // this wave's counter and presence loads have returned
   lds_barrier();
   if (threadIdx.x == 0) __hip_atomic_store(&a.presence[b], tag64(tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const bool route_failed = uni(s_pfail) != 0;
+  route_failed = uni(s_pfail) != 0;
   if (b == 0 && (int)threadIdx.x < k) {
     a.topk_idx[threadIdx.x] = route_failed ? -1 : s_sel_idx[threadIdx.x];
     a.topk_w[threadIdx.x] = route_failed ? __builtin_nanf("") : s_sel_w[threadIdx.x];
   }
 
-  // ---- 2. gate/up: this workgroup's items, split evenly over its waves ------------
-  // Workgroup b owns items u = b + m G (m = 0 .. nI - 1); item u is the 16-row
-  // tile r = u % NTI of I of slot j = u / NTI.  Their nI Kq quads, in item
-  // order, are cut into kFW contiguous ranges, one per wave, and each wave
-  // streams its range through its ring without a break at item boundaries.
-  // An item inside one wave's range is finished by that wave; an item cut
-  // between waves is summed from their partials (LDS, in wave order) after
-  // a barrier.  Every row of the MFMAs' A operand holds the token's x, so
-  // every row of a result holds the token's sums: element 0 of every lane is
-  // row 16 r + n of I, and only that element is scaled and summed (per
-  // group: scale times the sum over x (1 + n/16), and scale times the sum of
-  // x).
-  const BufRsrc hv_r = buf_rsrc(a.hv, (uint32_t)(S * (I / 2) * 16));
-  const int ns_gu = a.lds.ns_gu;
-  const uint32_t bmask = vgpr_const(0x00780078u);
-  float* s_gpart = s_red;  // [kFW waves][first | last segment][16 rows][ag, au, cg, cu]
-  const int nI = b < S * NTI ? (S * NTI - b + G - 1) / G : 0;
-  const int Tq = nI * Kq;
-  auto range_lo = [&](int ww) { return (int)(((int64_t)ww * Tq) / kFW); };
-  // h of item m from every lane's sums for row 16 r + n
-  auto publish = [&](int m, float ag, float au, float cg, float cu) {
-    const int u = b + m * G, j = u / NTI, r = u - j * NTI;
-    float h = __builtin_nanf("");
-    if (!route_failed) {
-      const float g = kUnitScale * ag - kUnitBias * cg;
-      const float uu = kUnitScale * au - kUnitBias * cu;
-      h = g * (1.0f / (1.0f + expf(-g))) * uu;
-    }
-    const uint32_t hb = float_to_half_bits(h);
-    const uint32_t lb = float_to_half_bits(h - half_bits_to_float32(hb));
-    const uint32_t hb2 = __shfl_down(hb, 1, kWave), lb2 = __shfl_down(lb, 1, kWave);
-    if (p == 0 && (n & 1) == 0) {
-      u32x4 v;
-      v.x = hb | (hb2 << 16);
-      v.y = tag;
-      v.z = lb | (lb2 << 16);
-      v.w = ~tag;
-      __builtin_amdgcn_raw_buffer_store_b128(v, hv_r, (j * (I / 2) + (kRowTile * r + n) / 2) * 16, 0, kDeviceScope);
-    }
-  };
-  {
-    const int g0 = range_lo(w), n_w = range_lo(w + 1) - g0;
-    // copy cursor: item im, quad iq, and the item's buffers
-    int im = g0 / Kq, iq = g0 - (g0 / Kq) * Kq;
-    i32x4 gnr = {0, 0, 0, 0}, unr = gnr, gsr = gnr, usr = gnr;
-    uint32_t itq0 = 0;
-    const uint32_t nib_b = (uint32_t)I * (uint32_t)Kq * 64u, sc_b = (uint32_t)I * (uint32_t)Kq * 8u;
-    auto item_buffers = [&]() {
-      const int u = b + im * G, j = u / NTI, r = u - j * NTI;
-      const int e = uni(s_sel_idx[j]);
-      const bool sh = e < 0;
-      const uint8_t* gn = sh ? a.sh_gate_nib : a.gate_nib + (size_t)e * nib_b;
-      const uint8_t* un = sh ? a.sh_up_nib : a.up_nib + (size_t)e * nib_b;
-      const char* gs = reinterpret_cast<const char*>(sh ? a.sh_gate_sc : a.gate_sc) + (sh ? 0 : (size_t)e * sc_b);
-      const char* us = reinterpret_cast<const char*>(sh ? a.sh_up_sc : a.up_sc) + (sh ? 0 : (size_t)e * sc_b);
-      gnr = buf_rsrc_words(gn, nib_b);
-      unr = buf_rsrc_words(un, nib_b);
-      gsr = buf_rsrc_words(gs, sc_b);
-      usr = buf_rsrc_words(us, sc_b);
-      itq0 = (uint32_t)r * (uint32_t)Kq;
-    };
-    auto issue_next = [&](int stage) {
-      const uint32_t st = ring + (uint32_t)stage * kSGuStage;
-      const uint32_t tq = (uint32_t)uni((int)(itq0 + (uint32_t)iq));
-      dma_b128_stream(gnr, st, (uint32_t)lane * 16u, tq * kQuadNibBytes);
-      dma_b128_stream(unr, st + 1024u, (uint32_t)lane * 16u, tq * kQuadNibBytes);
-      if (lane < 8) {
-        dma_b128_stream(gsr, st + 2048u, (uint32_t)lane * 16u, tq * 128u);
-        dma_b128_stream(usr, st + 2176u, (uint32_t)lane * 16u, tq * 128u);
-      }
-      if (++iq == Kq) {
-        iq = 0;
-        if (++im < nI) item_buffers();
-      }
-    };
-    if (!route_failed && n_w > 0) {
-      item_buffers();
-      const int pro = ns_gu < n_w ? ns_gu : n_w;
-      for (int i = 0; i < pro; ++i) issue_next(i);
-    }
-    int cm = g0 / Kq, cq = g0 - (g0 / Kq) * Kq;  // quad being summed
-    int seg_q0 = cq, seg_slot = 0;             // start quad of the segment; partial slot
-    float ag = 0.0f, au = 0.0f, cg = 0.0f, cu = 0.0f;
-    int stage = 0;  // ring stage of the quad being summed
-    for (int i = 0; i < n_w; ++i) {
-      if (!route_failed) {
-        // this quad's copies in; the younger ones (up to ns - 1 quads) may fly
-        const int younger = (i + ns_gu < n_w ? ns_gu : n_w - i) - 1;
-        wait_vmcnt_le(kSGuCopies * younger);
-        poll_clobber();
-        const char* st = ring_p + stage * (int)kSGuStage;
-        const u32x4 gw = *reinterpret_cast<const u32x4*>(st + lane * 16);
-        const u32x4 uw = *reinterpret_cast<const u32x4*>(st + 1024 + lane * 16);
-        const uint2 gsv = *reinterpret_cast<const uint2*>(st + 2048 + n * 8);
-        const uint2 usv = *reinterpret_cast<const uint2*>(st + 2176 + n * 8);
-        const u32x4* xo = s_xop + (cq * 4 + p) * 4;
-        const u32x4 xa[4] = {xo[0], xo[1], xo[2], xo[3]};
-        const f32x4 xs = *reinterpret_cast<const f32x4*>(s_xs + cq * 4);
-        float dg[4], du[4];
-        unpack_scales(gsv, dg);
-        unpack_scales(usv, du);
-        const uint32_t gwv[4] = {gw.x, gw.y, gw.z, gw.w};
-        const uint32_t uwv[4] = {uw.x, uw.y, uw.z, uw.w};
-        f32x4 pg[4], pu[4];
-#pragma unroll
-        for (int gi = 0; gi < 4; ++gi) {
-          pg[gi] = mfma_bf16_16x16x32(xa[gi], dequant_unit_bf16(gwv[gi], bmask), z);
-          pu[gi] = mfma_bf16_16x16x32(xa[gi], dequant_unit_bf16(uwv[gi], bmask), z);
-        }
-#pragma unroll
-        for (int gi = 0; gi < 4; ++gi) {
-          ag += dg[gi] * pg[gi][0];
-          au += du[gi] * pu[gi][0];
-          cg += dg[gi] * xs[gi];
-          cu += du[gi] * xs[gi];
-        }
-        // the stage is read (the MFMAs consumed it) before it is refilled
-        if (i + ns_gu < n_w) issue_next(stage);
-        stage = stage + 1 == ns_gu ? 0 : stage + 1;
-      }
-      if (++cq == Kq || i == n_w - 1) {  // end of a segment
-        if (seg_q0 == 0 && cq == Kq) {
-          publish(cm, ag, au, cg, cu);
-        } else if (p == 0) {
-          const f32x4 v = {ag, au, cg, cu};
-          *reinterpret_cast<f32x4*>(s_gpart + ((w * 2 + seg_slot) * 16 + n) * 4) = v;
-        }
-        ag = au = cg = cu = 0.0f;
-        seg_q0 = 0;
-        seg_slot = 1;
-        if (cq == Kq) {
-          cq = 0;
-          ++cm;
-        }
-      }
-    }
-  }
+  // ---- 2. gate/up: the routed items, on all waves ---------------------------------
+  finish_cut_items(nR, nI - nR, kFW - 1, s_gpart_sh, true);
+  run_items(0, nR, kFW, s_gpart_rt, !route_failed, !route_failed);
   lds_barrier();
-  // items cut between waves: wave m % kFW sums item m's partials in wave order
-  for (int m = w; m < nI; m += kFW) {
-    const int lo = m * Kq, hi = lo + Kq;
-    bool whole = false;
-    for (int ww = 0; ww < kFW; ++ww) whole = whole || (range_lo(ww) <= lo && range_lo(ww + 1) >= hi);
-    if (whole) continue;
-    float sg = 0.0f, su = 0.0f, sgc = 0.0f, suc = 0.0f;
-    for (int ww = 0; ww < kFW; ++ww) {
-      const int a0 = range_lo(ww), a1 = range_lo(ww + 1);
-      if (a1 <= lo || a0 >= hi || a1 <= a0) continue;
-      // item m is the first segment of wave ww when the wave starts inside it
-      const f32x4 v = *reinterpret_cast<const f32x4*>(s_gpart + ((ww * 2 + (a0 >= lo ? 0 : 1)) * 16 + n) * 4);
-      sg += v[0];
-      su += v[1];
-      sgc += v[2];
-      suc += v[3];
-    }
-    publish(m, sg, su, sgc, suc);
-  }
+  finish_cut_items(0, nR, kFW, s_gpart_rt, !route_failed);
 
   // ---- 3. down: this workgroup's slot and tiles -----------------------------------
   const int kx = a.kx;
@@ -685,7 +706,7 @@ StreamPlan stream_plan(int64_t T, int64_t H, int64_t I, int E, int k, int has_sh
   // the down phase's K-split partials, the combine's expert outputs, and
   // before them the gate/up partials of items cut between waves
   uint32_t red_floats = (uint32_t)(S * kx * l.yrows > kFW * 16 ? S * kx * l.yrows : kFW * 16);
-  if (red_floats < (uint32_t)kFW * 2 * 16 * 4) red_floats = (uint32_t)kFW * 2 * 16 * 4;
+  if (red_floats < (uint32_t)kFW * 2 * 16 * 4 * 2) red_floats = (uint32_t)kFW * 2 * 16 * 4 * 2;
   const uint32_t red_bytes = red_floats * 4u;
   l.ring = align_lds(l.red + red_bytes);
   if (l.ring >= kFusedDynLdsMax) return pl;
