@@ -1310,8 +1310,13 @@ static hipError_t launch_permute_multi(const int32_t* idx, int64_t T, int k, int
   return hipGetLastError();
 }
 
+// Tokens per logits workgroup.  One token a workgroup up to 16 tokens: the
+// grid then has T times as many workgroups to stream W with, which took the
+// DeepSeek-V3 eight-token route from 30.9 to 23.7 us and the Mixtral
+// sixteen-token one from 22.5 to 16.7 us; at 32 and 64 tokens the re-reads
+// of W that a one-token tile costs outweigh that (20.0 -> 23.1 us, 49 -> 76 us).
 int router_token_tile(int64_t T) {
-  if (T <= 1) return 1;
+  if (T <= 16) return 1;
   if (T <= 64) return 4;
   return kBigTT;
 }
