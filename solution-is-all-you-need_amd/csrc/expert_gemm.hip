@@ -258,65 +258,25 @@ __device__ inline int count_active(const SegSrc& seg, int* s_nact) {
   return *s_nact;
 }
 
-// VT: the leading 16-position tiles of the block that are multiplied (the
-// caller rounds the tiles holding a segment position up to 2, 4 or 8); the
-// rest lie past the segment end, so their MFMAs, A reads and scaling are
-// skipped, and their accumulators stay zero and are never stored.  A
-// compile-time count keeps the loop branch-free: a run-time test per tile
-// broke the software pipelining and cost 30%.
-template <int BM, int AW, int VT>
-__device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* lds, const i32x4& ar,
-                                  const i32x4 (&nr)[kG2NB], const i32x4 (&sr)[kG2NB], const int64_t (&rt)[kG2NB],
-                                  f32x4 acc[kG2NB][BM / 16]) {
+// The multiply-accumulate of one K quad from LDS stage st into acc (shared
+// by both kernels).  VT: the leading 16-position tiles of the block that are
+// multiplied (the caller rounds the tiles holding a segment position up to
+// 2, 4 or 8); the rest lie past the segment end, so their MFMAs, A reads and
+// scaling are skipped, and their accumulators stay zero and are never
+// stored.  A compile-time count keeps the loop branch-free: a run-time test
+// per tile broke the software pipelining and cost 30%.  RAGGED: groups at or
+// past Kg (uniform) are skipped.  a_unit[gi]: this lane's LDS unit of A group
+// gi (see gemm_tile3).
+template <int BM, int AW, int VT, bool RAGGED>
+__device__ __attribute__((always_inline)) inline void quad_math(const u32x4* st, uint32_t q, uint32_t Kg,
+                                                                const uint32_t (&a_unit)[4], uint32_t mask,
+                                                                f32x4 acc[kG2NB][BM / 16]) {
   static_assert(VT >= 1 && VT <= BM / 16, "tiles to multiply");
   constexpr int NB = kG2NB;
-  constexpr int UPR = 16 * AW;                // 16-byte units per A row
-  constexpr int RPD = kWave / UPR;            // A rows per direct-to-LDS load
-  constexpr int ND = kG2AUnits / kWave / kG2Waves;  // A loads per wave per quad
-  static_assert(BM * UPR == kG2AUnits && ND >= 1, "one stage holds the tile");
+  constexpr int UPR = 16 * AW;  // 16-byte units per A row
   const int lane = threadIdx.x % kWave;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int n = lane % 16;
-  const int p = lane / 16;
-  const uint32_t mask = vgpr_const(0x000F000Fu);
-  const uint32_t row_bytes = (uint32_t)(a.Kq * 256 * AW);
-  const uint32_t Kq = (uint32_t)a.Kq;
-  // this wave's A loads j = w + kG2Waves * i: lane l fills slot l % UPR of row
-  // j * RPD + l / UPR with logical unit (slot ^ a_swizzle(row & 15))
-  uint32_t voff[ND];
-#pragma unroll
-  for (int i = 0; i < ND; ++i) {
-    const int j = w + kG2Waves * i;
-    const int row = j * RPD + lane / UPR;
-    const int unit = (lane % UPR) ^ (int)a_swizzle((uint32_t)row & 15u);
-    voff[i] = (uint32_t)s_row[row] * row_bytes + (uint32_t)unit * 16u;
-  }
-  // the LDS offsets (16-byte units) of this lane's A operands of group gi,
-  // tile tt: hi at a_row + tt * 16 * UPR + ((p * 4 + gi) * AW ^ a_swizzle(n)),
-  // lo at that unit ^ 1 (AW * (p * 4 + gi) is even, so the pair stays adjacent)
-  const uint32_t a_row = (uint32_t)n * UPR;
-  uint32_t a_unit[4];
-#pragma unroll
-  for (int gi = 0; gi < 4; ++gi) a_unit[gi] = a_row + (((uint32_t)(p * 4 + gi) * AW) ^ a_swizzle((uint32_t)n));
-  const uint32_t lds0 = lds_addr(lds);
-  auto uni = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
-  auto copy = [&](uint32_t q, uint32_t stage) {
-    const uint32_t st = lds0 + stage * (kG2StageUnits * 16);
-    const uint32_t aoff = uni(q * 256u * AW);
-#pragma unroll
-    for (int i = 0; i < ND; ++i)
-      dma_b128_unseen(ar, uni(st + (uint32_t)(w + kG2Waves * i) * kWave * 16), voff[i], aoff);
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const uint32_t tq = uni((uint32_t)rt[b] * Kq + q);
-      dma_b128_unseen(nr[b], uni(st + (uint32_t)(kG2AUnits + (w * NB + b) * kWave) * 16), (uint32_t)lane * 16u,
-                      tq * kQuadNibBytes);
-      // the 128 scale bytes: eight lanes
-      if (lane < 8)
-        dma_b128_unseen(sr[b], uni(st + (uint32_t)(kG2AUnits + kG2BUnits + (w * NB + b) * 8) * 16),
-                        (uint32_t)lane * 16u, tq * (kQuadScales * 2));
-    }
-  };
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
   // One group: MFMAs of every tile (hi then lo), the scaling of tile tt - 1
   // after the MFMAs of tile tt.
@@ -338,7 +298,7 @@ __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* l
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b][VT - 1] += d[b] * pv[(VT - 1) & 1][b];
   };
-  auto read_a = [&](const u32x4* st, int gi, u32x4 (&ah)[VT], u32x4 (&al)[VT]) {
+  auto read_a = [&](int gi, u32x4 (&ah)[VT], u32x4 (&al)[VT]) {
 #pragma unroll
     for (int tt = 0; tt < VT; ++tt) {
       ah[tt] = st[a_unit[gi] + tt * 16 * UPR];
@@ -358,42 +318,99 @@ __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* l
       bq[b] = dequant_int_f16(bw[b][gi], mask);
     }
   };
-  // One quad from LDS stage st: B operands, then the four groups, the A reads
-  // of group gi + 1 issued before the MFMAs of group gi.  RAGGED: groups at
-  // or past Kg (uniform) are skipped.
-  auto quad = [&](const u32x4* st, uint32_t q, auto ragged) {
-    u32x4 bw[NB];
-    uint2 bs[NB];
+  // B operands, then the four groups, the A reads of group gi + 1 issued
+  // before the MFMAs of group gi
+  u32x4 bw[NB];
+  uint2 bs[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    bw[b] = st[kG2AUnits + (w * NB + b) * kWave + lane];
+    bs[b] = reinterpret_cast<const uint2*>(st + kG2AUnits + kG2BUnits + (w * NB + b) * 8)[n];
+  }
+  if constexpr (!RAGGED) {
+    u32x4 ah[2][VT], al[2][VT];
+    read_a(0, ah[0], al[0]);
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+      if (gi < 3) read_a(gi + 1, ah[(gi + 1) & 1], al[(gi + 1) & 1]);
+      u32x4 bq[NB];
+      float d[NB];
+      operands(bs, bw, gi, bq, d);
+      group_math(ah[gi & 1], al[gi & 1], bq, d);
+    }
+  } else {
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+      if (4 * q + gi >= Kg) break;
+      u32x4 ah[VT], al[VT];
+      read_a(gi, ah, al);
+      u32x4 bq[NB];
+      float d[NB];
+      operands(bs, bw, gi, bq, d);
+      group_math(ah, al, bq, d);
+    }
+  }
+}
+
+// The LDS offsets (16-byte units) of lane (n, p)'s A operands of group gi,
+// tile 0: hi at n * UPR + ((p * 4 + gi) * AW ^ a_swizzle(n)), lo at that unit
+// ^ 1 (AW * (p * 4 + gi) is even, so the pair stays adjacent); tile tt adds
+// tt * 16 * UPR.
+template <int AW>
+__device__ inline void a_units(uint32_t (&a_unit)[4]) {
+  const int lane = threadIdx.x % kWave;
+  const uint32_t n = (uint32_t)(lane % 16), p = (uint32_t)(lane / 16);
+#pragma unroll
+  for (int gi = 0; gi < 4; ++gi) a_unit[gi] = n * 16 * AW + (((p * 4 + gi) * AW) ^ a_swizzle(n));
+}
+
+// One item's K loop through the LDS ring (gate/up): both operands staged
+// two quads ahead, one barrier per quad.
+template <int BM, int AW, int VT>
+__device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* lds, const i32x4& ar,
+                                  const i32x4 (&nr)[kG2NB], const i32x4 (&sr)[kG2NB], const int64_t (&rt)[kG2NB],
+                                  f32x4 acc[kG2NB][BM / 16]) {
+  constexpr int NB = kG2NB;
+  constexpr int UPR = 16 * AW;                // 16-byte units per A row
+  constexpr int RPD = kWave / UPR;            // A rows per direct-to-LDS load
+  constexpr int ND = kG2AUnits / kWave / kG2Waves;  // A loads per wave per quad
+  static_assert(BM * UPR == kG2AUnits && ND >= 1, "one stage holds the tile");
+  const int lane = threadIdx.x % kWave;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t mask = vgpr_const(0x000F000Fu);
+  const uint32_t row_bytes = (uint32_t)(a.Kq * 256 * AW);
+  const uint32_t Kq = (uint32_t)a.Kq;
+  // this wave's A loads j = w + kG2Waves * i: lane l fills slot l % UPR of row
+  // j * RPD + l / UPR with logical unit (slot ^ a_swizzle(row & 15))
+  uint32_t voff[ND];
+#pragma unroll
+  for (int i = 0; i < ND; ++i) {
+    const int j = w + kG2Waves * i;
+    const int row = j * RPD + lane / UPR;
+    const int unit = (lane % UPR) ^ (int)a_swizzle((uint32_t)row & 15u);
+    voff[i] = (uint32_t)s_row[row] * row_bytes + (uint32_t)unit * 16u;
+  }
+  uint32_t a_unit[4];
+  a_units<AW>(a_unit);
+  const uint32_t lds0 = lds_addr(lds);
+  auto uni = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
+  auto copy = [&](uint32_t q, uint32_t stage) {
+    const uint32_t st = lds0 + stage * (kG2StageUnits * 16);
+    const uint32_t aoff = uni(q * 256u * AW);
+#pragma unroll
+    for (int i = 0; i < ND; ++i)
+      dma_b128_unseen(ar, uni(st + (uint32_t)(w + kG2Waves * i) * kWave * 16), voff[i], aoff);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      bw[b] = st[kG2AUnits + (w * NB + b) * kWave + lane];
-      bs[b] = reinterpret_cast<const uint2*>(st + kG2AUnits + kG2BUnits + (w * NB + b) * 8)[n];
-    }
-    if constexpr (!decltype(ragged)::value) {
-      u32x4 ah[2][VT], al[2][VT];
-      read_a(st, 0, ah[0], al[0]);
-#pragma unroll
-      for (int gi = 0; gi < 4; ++gi) {
-        if (gi < 3) read_a(st, gi + 1, ah[(gi + 1) & 1], al[(gi + 1) & 1]);
-        u32x4 bq[NB];
-        float d[NB];
-        operands(bs, bw, gi, bq, d);
-        group_math(ah[gi & 1], al[gi & 1], bq, d);
-      }
-    } else {
-#pragma unroll
-      for (int gi = 0; gi < 4; ++gi) {
-        if (4 * q + gi >= (uint32_t)a.Kg) break;
-        u32x4 ah[VT], al[VT];
-        read_a(st, gi, ah, al);
-        u32x4 bq[NB];
-        float d[NB];
-        operands(bs, bw, gi, bq, d);
-        group_math(ah, al, bq, d);
-      }
+      const uint32_t tq = uni((uint32_t)rt[b] * Kq + q);
+      dma_b128_unseen(nr[b], uni(st + (uint32_t)(kG2AUnits + (w * NB + b) * kWave) * 16), (uint32_t)lane * 16u,
+                      tq * kQuadNibBytes);
+      // the 128 scale bytes: eight lanes
+      if (lane < 8)
+        dma_b128_unseen(sr[b], uni(st + (uint32_t)(kG2AUnits + kG2BUnits + (w * NB + b) * 8) * 16),
+                        (uint32_t)lane * 16u, tq * (kQuadScales * 2));
     }
   };
-
   copy(0, 0);
   if (Kq > 1) copy(1, 1);
   // quads whose four groups are all real; a ragged last quad (H or I not a
@@ -412,8 +429,8 @@ __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* l
     stage = stage == kG2Stages - 1 ? 0u : stage + 1u;
     return st;
   };
-  for (uint32_t q = 0; q < Kq_full; ++q) quad(top(q), q, std::false_type{});
-  if (Kq_full < Kq) quad(top(Kq_full), Kq_full, std::true_type{});
+  for (uint32_t q = 0; q < Kq_full; ++q) quad_math<BM, AW, VT, false>(top(q), q, (uint32_t)a.Kg, a_unit, mask, acc);
+  if (Kq_full < Kq) quad_math<BM, AW, VT, true>(top(Kq_full), Kq_full, (uint32_t)a.Kg, a_unit, mask, acc);
   lds_barrier();  // every wave has left the ring before it is reused
 }
 

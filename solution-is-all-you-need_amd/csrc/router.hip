@@ -358,7 +358,8 @@ __device__ void wave_topk(const RouteK& a, int64_t t, uint64_t* s_ck, double* s_
 }
 
 // MFMA-ordered copy of x (bf16) and fp32 group sums for tokens [t0, t0+TT),
-// spread over the gridDim.x workgroups that share this token tile.
+// spread over the nparts workgroups that share this token tile (this one is
+// number part).
 // Layout [t][q][p][gi][8]: one 16-byte chunk per (token, quad, part, group);
 // chunk (p, gi) of quad q holds elements kmap(p, 0..7) of group 4q + gi, read
 // as two 8-byte runs (4p..4p+3 and 4p+16..4p+19).  A group's sum adds its
@@ -368,14 +369,14 @@ __device__ void wave_topk(const RouteK& a, int64_t t, uint64_t* s_ck, double* s_
 // copy (it cannot prove they do not alias), so a chunk at a time paid one
 // memory round trip per chunk (16 of them per thread for 4096 tokens).
 constexpr int kPrepBatch = 8;
-__device__ void prep_x_tile(const RouteK& a, int64_t t0, int TT) {
+__device__ void prep_x_tile(const RouteK& a, int64_t t0, int TT, int part, int nparts) {
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
   const int Kg = (int)(a.H / kGroup);
   const int per_tok = (int)a.Kq * 16;
   const int n = TT * per_tok;
   const int lane = threadIdx.x % kWave;
-  const int stride = (int)(gridDim.x * blockDim.x);
-  const int wave0 = (int)(blockIdx.x * blockDim.x) + (int)(threadIdx.x / kWave) * kWave;
+  const int stride = nparts * (int)blockDim.x;
+  const int wave0 = part * (int)blockDim.x + (int)(threadIdx.x / kWave) * kWave;
   for (int c00 = wave0; c00 < n; c00 += kPrepBatch * stride) {  // wave-uniform
     uint2 lo[kPrepBatch], hi[kPrepBatch];
 #pragma unroll
@@ -527,7 +528,7 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteK a) {
       }
     }
     // the MFMA-ordered copy of x, its loads in flight with the first batch's
-    if (c0 == 0 && a.prep_x) prep_x_tile(a, t0, TT);
+    if (c0 == 0 && a.prep_x) prep_x_tile(a, t0, TT, (int)blockIdx.x, (int)gridDim.x);
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
 #pragma unroll
@@ -690,7 +691,7 @@ __global__ __launch_bounds__(256) void route_logits_big_kernel(RouteK a) {
   const int64_t t0 = (int64_t)blockIdx.y * TT;
   const int e0 = blockIdx.x * (4 * EW) + w * EW;
   const XT* x = static_cast<const XT*>(a.x);
-  if (a.prep_x) prep_x_tile(a, t0, TT);
+  if (a.prep_x) prep_x_tile(a, t0, TT, (int)blockIdx.x, (int)gridDim.x);
   if (a.counter && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *a.counter = 0;
   float bias_e = 0.0f;
   if (a.bias) {
@@ -750,8 +751,9 @@ __global__ __launch_bounds__(256) void route_logits_big_kernel(RouteK a) {
 // For prefill batches the fixed-order fp64 logits of every (token, expert)
 // pair cost 100 us at 4096 tokens of H 2048, E 128 -- while only the top k
 // of each token, and the experts near the k-th, decide anything.  So:
-//   route_approx_kernel: L~ = x . bf16(w) on the matrix cores (fp32
-//     accumulation) for every pair, plus the norms |x_t| and |w_e|;
+//   route_approx_kernel: L~ = x . (w_hi + w_lo) on the matrix cores for every
+//     pair, with w_hi = bf16(w) and w_lo = bf16(w - w_hi) (both rounded to
+//     nearest), plus the norms |x_t| and |w_e|;
 //   route_candidates_kernel (one wave per token): the error bound
 //     |L~ - L| <= C(H) |x_t| |w_e| gives every expert an interval; experts
 //     whose upper end reaches the k-th largest lower end are the candidates
@@ -761,13 +763,19 @@ __global__ __launch_bounds__(256) void route_logits_big_kernel(RouteK a) {
 //     fp64 logits (contract above) of the candidate pairs, 16 tokens per wave
 //     so each lane's slice of the weight row is loaded once per 16 pairs;
 //   route_select_kernel: the exact selection and weights, unchanged.
-// The bound: bf16 rounding of w is at most 2^-9 |w| (round to nearest), the
-// products x * bf16(w) are exact in fp32, and H fp32 additions in any order
-// add at most H 2^-24 of sum |x bf16(w)| (taken as H 2^-22, 4x margin, for
-// whatever order and internal precision the MFMA uses); Cauchy-Schwarz bounds
-// sum |x||w| by |x| |w|, with |x| and |w| taken as their computed fp32 norms
-// plus sqrt(H + 8) 2^-63, which covers what squares and sums below 2^-126 can
-// lose (so rows of tiny entries get a bound, not 0).  Tokens with a non-finite approximate logit or norm
+// The bound.  Rounding: w - w_hi is exact in fp32, so |w - w_hi - w_lo| <=
+// 2^-8 |w - w_hi| <= 2^-16 |w| (an 8-bit significand rounds to within 2^-8
+// of the value), and |w_hi| + |w_lo| <= (1 + 2^-7) |w|.  Arithmetic: the
+// products of two bf16 values are exact in fp32; each 32-wide K step s is
+// summed by two chained MFMAs from zero (64 products, at most 63 roundings
+// of 2^-24, taken 4x for whatever order and internal precision the matrix
+// cores use: 252 u), and the S = ceil(H / 32) step sums are added in fp32
+// on the vector ALU (S u more).  With Cauchy-Schwarz, sum |x| |w| <= |x| |w|,
+// so C(H) = 2^-16 + (252 + S) 2^-24 (1 + 2^-7), with margin; |x| and |w| are
+// taken as their computed fp32 norms plus sqrt(H + 8) 2^-63, which covers
+// what squares and sums below 2^-126 can lose (so rows of tiny entries get a
+// bound, not 0), and denormal inputs or products the matrix cores may flush
+// add an absolute term.  Tokens with a non-finite approximate logit or norm
 // take every expert as a candidate (the full exact row), so NaN and inf
 // follow the contract exactly as on the one-pass path.
 constexpr int kApproxTok = 64;     // tokens per approx workgroup (4 waves x 16)
@@ -777,17 +785,37 @@ constexpr int kApproxUnits = kApproxExp * kApproxChunk / 8 / 256;  // 8-wide W u
 constexpr int kExactTok = 1024;    // tokens scanned per exact workgroup (a multiple of 256)
 constexpr int kExactP = 16;        // token pairs per wave pass
 
+// Workgroup b of a one-dimensional grid of n_eb x n_tt runs on XCD b % 8.
+// When the token tiles divide evenly over the XCDs, XCD x takes token tiles
+// x, x + 8, ... with every expert block of each, so a tile's x is fetched
+// into that XCD's L2 once and read there by all n_eb workgroups (the plain
+// order put a tile's expert blocks on n_eb different XCDs, each fetching it).
+__device__ inline void xcd_tile_map(int64_t b, int64_t n_eb, int64_t n_tt, int64_t* eb, int64_t* tt) {
+  if (n_tt % 8 == 0) {
+    const int64_t j = b / 8;
+    *tt = b % 8 + 8 * (j / n_eb);
+    *eb = j % n_eb;
+  } else {
+    *tt = b / n_eb;
+    *eb = b % n_eb;
+  }
+}
+
 __global__ __launch_bounds__(256) void route_approx_kernel(RouteK a, float* approx, float* nx, float* nw) {
-  // W chunk as bf16 B operands: [expert tile][K step][lane] 16-byte units
+  // W chunk as bf16 B operands w_hi and w_lo: [expert tile][K step][lane] 16-byte units
   __shared__ u32x4 s_w[(kApproxExp / 16) * (kApproxChunk / 32) * kWave];
+  __shared__ u32x4 s_wl[(kApproxExp / 16) * (kApproxChunk / 32) * kWave];
   __shared__ float s_nw[kApproxExp];
   const int lane = threadIdx.x % kWave;
   const int w = threadIdx.x / kWave;
-  const int64_t t0 = (int64_t)blockIdx.y * kApproxTok;
-  const int e0 = blockIdx.x * kApproxExp;
+  const int64_t n_eb = ceil_div(a.E, kApproxExp);
+  int64_t eb, tt;
+  xcd_tile_map(blockIdx.x, n_eb, ceil_div(a.T, kApproxTok), &eb, &tt);
+  const int64_t t0 = tt * kApproxTok;
+  const int e0 = (int)eb * kApproxExp;
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
-  if (a.prep_x) prep_x_tile(a, t0, kApproxTok);
-  if (a.counter && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *a.counter = 0;
+  if (a.prep_x) prep_x_tile(a, t0, kApproxTok, (int)eb, (int)n_eb);
+  if (a.counter && blockIdx.x == 0 && threadIdx.x == 0) *a.counter = 0;
   // A rows: token t0 + 16 w + lane % 16 (clamped), K 8 (lane / 16) .. + 8 of each step
   const int64_t tr = t0 + 16 * w + lane % 16;
   const uint16_t* xrow = x + (tr < a.T ? tr : a.T - 1) * a.H + 8 * (lane / 16);
@@ -824,16 +852,23 @@ __global__ __launch_bounds__(256) void route_approx_kernel(RouteK a, float* appr
     for (int i = 0; i < kApproxUnits; ++i) {
       const int u = threadIdx.x + 256 * i;
       const int e = u / 32, kb = u % 32;
-      u32x4 v = {0u, 0u, 0u, 0u};
+      u32x4 v = {0u, 0u, 0u, 0u}, vl = {0u, 0u, 0u, 0u};
       if (8 * kb < kc) {
         const float f[8] = {wr[i][0].x, wr[i][0].y, wr[i][0].z, wr[i][0].w,
                             wr[i][1].x, wr[i][1].y, wr[i][1].z, wr[i][1].w};
 #pragma unroll
         for (int j = 0; j < 8; ++j) sw[i] = __builtin_fmaf(f[j], f[j], sw[i]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = float_to_bf16_bits(f[2 * j]) | (float_to_bf16_bits(f[2 * j + 1]) << 16);
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t h0 = float_to_bf16_bits(f[2 * j]), h1 = float_to_bf16_bits(f[2 * j + 1]);
+          v[j] = h0 | (h1 << 16);
+          vl[j] = float_to_bf16_bits(f[2 * j] - bf16_bits_to_float(h0)) |
+                  (float_to_bf16_bits(f[2 * j + 1] - bf16_bits_to_float(h1)) << 16);
+        }
       }
-      s_w[((e / 16) * (kApproxChunk / 32) + kb / 4) * kWave + (e % 16) + 16 * (kb % 4)] = v;
+      const int slot = ((e / 16) * (kApproxChunk / 32) + kb / 4) * kWave + (e % 16) + 16 * (kb % 4);
+      s_w[slot] = v;
+      s_wl[slot] = vl;
     }
     u32x4 av[kApproxChunk / 32];
 #pragma unroll
@@ -849,9 +884,15 @@ __global__ __launch_bounds__(256) void route_approx_kernel(RouteK a, float* appr
         sx = __builtin_fmaf(lo, lo, sx);
         sx = __builtin_fmaf(hi, hi, sx);
       }
+      // each step's sum from zero, added on the vector ALU (the bound's
+      // S u term; chained MFMAs would add H roundings)
 #pragma unroll
-      for (int et = 0; et < kApproxExp / 16; ++et)
-        acc[et] = mfma_bf16_16x16x32(av[s], s_w[(et * (kApproxChunk / 32) + s) * kWave + lane], acc[et]);
+      for (int et = 0; et < kApproxExp / 16; ++et) {
+        const int slot = (et * (kApproxChunk / 32) + s) * kWave + lane;
+        f32x4 ps = mfma_bf16_16x16x32(av[s], s_w[slot], f32x4{0.f, 0.f, 0.f, 0.f});
+        ps = mfma_bf16_16x16x32(av[s], s_wl[slot], ps);
+        acc[et] += ps;
+      }
     }
     __syncthreads();  // every wave has read the B operands before the next chunk overwrites them
   }
@@ -880,8 +921,8 @@ __global__ __launch_bounds__(256) void route_approx_kernel(RouteK a, float* appr
       if (t < a.T && e < a.E) approx[t * a.E + e] = acc[et][j];
     }
   }
-  if (blockIdx.x == 0 && lane < 16 && tr < a.T) nx[tr] = sqrtf(sx);
-  if (blockIdx.y == 0 && threadIdx.x < kApproxExp && e0 + (int)threadIdx.x < a.E)
+  if (eb == 0 && lane < 16 && tr < a.T) nx[tr] = sqrtf(sx);
+  if (tt == 0 && threadIdx.x < kApproxExp && e0 + (int)threadIdx.x < a.E)
     nw[e0 + threadIdx.x] = sqrtf(s_nw[threadIdx.x]);
 }
 
@@ -899,7 +940,8 @@ __global__ __launch_bounds__(256) void route_candidates_kernel(RouteK a, const f
   const int lane = threadIdx.x % kWave;
   const int w = threadIdx.x / kWave;
   // C(H) of the bound, with 2^-8 relative room for the rounding of the norms
-  const float cH = (1.0f / 512.0f + (float)a.H * (1.0f / 4194304.0f) * 1.002f) * (1.0f + 1.0f / 256.0f);
+  const float S = (float)((a.H + 31) / 32);
+  const float cH = (1.0f / 65536.0f + (252.0f + S) * (1.0f / 16777216.0f) * 1.02f) * (1.0f + 1.0f / 256.0f);
   const float sqrtH = sqrtf((float)a.H) * 1.01f;
   // The norms are fp32 sums of H + 8 squares.  Squares and partial sums below
   // 2^-126 may be flushed or lose bits, at most 2^-126 each, so the true
@@ -1342,7 +1384,7 @@ static hipError_t launch_route_two_pass(const RouteK& k, const Workspace& ws, hi
   float* approx = ws.approx;
   float* nx = approx + k.T * k.E;
   float* nw = nx + k.T;
-  hipLaunchKernelGGL(route_approx_kernel, dim3((unsigned)ceil_div(k.E, kApproxExp), (unsigned)ceil_div(k.T, kApproxTok)),
+  hipLaunchKernelGGL(route_approx_kernel, dim3((unsigned)(ceil_div(k.E, kApproxExp) * ceil_div(k.T, kApproxTok))),
                      dim3(256), 0, stream, k, approx, nx, nw);
   const dim3 grid((unsigned)ceil_div(k.T, 4)), block(256);
   if (k.E <= 64) hipLaunchKernelGGL(route_candidates_kernel<1>, grid, block, 0, stream, k, approx, nx, nw, ws.cand);

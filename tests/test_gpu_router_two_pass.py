@@ -131,3 +131,40 @@ def test_tiny_rows_underflow(dev, H, E, k):
     scale_e[1::10] = 2.0 ** -72
     W = (W.astype(np.float64) * scale_e).astype(np.float32)
     check(dev, synth.f32_to_bf16_bits(xf), W, k)
+
+
+def _bf16_rne(v):
+    """float64 array -> the nearest bf16 values (ties to even), as float64."""
+    b = v.astype(np.float32).view(np.uint32).astype(np.uint64)
+    b = (b + 0x7FFF + ((b >> 16) & 1)) >> 16 << 16
+    return b.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def test_systematic_bf16_ties(dev):
+    """Router weights placed on bf16 rounding ties, with the signs of x
+    lined up so that every rounding pushes the approximate logit of expert 3
+    (the exact top 1) down and that of expert 5 (0.06 below it) up, by
+    2^-8 |w| an element: one bf16 copy of w is then off by about 1 in each
+    logit, more than 2^-9 |x| |w| covers, and expert 3 would fall out of the
+    candidates.  The hi + lo split of w leaves about 2^-12, so routing stays
+    the oracle's (checked here on the CPU for the one-copy case too)."""
+    T, H, E = 128, 288, 16
+    rng = np.random.default_rng(11)
+    x = np.ones(H)
+    x[128:256] = -1.0
+    W = rng.standard_normal((E, H)) * 0.02
+    tie, above = 1.0 + 2.0 ** -8, 1.0 + 2.0 ** -8 + 2.0 ** -20
+    W[3, :128], W[3, 128:256], W[3, 256:] = tie, above, 0.5
+    W[5, :128], W[5, 128:256], W[5, 256:] = above, tie, 0.5 - 2.0 ** -9
+    W = W.astype(np.float32)
+    w64 = W.astype(np.float64)
+    exact = w64 @ x
+    one_copy = _bf16_rne(w64) @ x
+    assert exact[3] > exact[5] and one_copy[5] - one_copy[3] > 1.9
+    b = (2.0 ** -9 + H * 2.0 ** -22) * np.linalg.norm(x) * np.linalg.norm(w64, axis=1)
+    assert one_copy[5] - b[5] > one_copy[3] + b[3], "the construction defeats a 2^-9 bound"
+    scales = 2.0 ** rng.integers(-3, 4, size=(T, 1))
+    xb = synth.f32_to_bf16_bits((x[None, :] * scales).astype(np.float32))
+    for k in (1, 2):
+        ridx = check(dev, xb, W, k)
+        assert (ridx[:, 0] == 3).all()
