@@ -220,7 +220,6 @@ constexpr int kG2NB = 2;         // B operands per wave in both kernels
 constexpr int kG2BUnits = kG2Waves * kG2NB * kWave;  // nibbles: one 1 KiB unit row per operand
 constexpr int kG2SUnits = kG2Waves * kG2NB * 8;      // scales: 128 B per operand
 constexpr int kG2StageUnits = kG2AUnits + kG2BUnits + kG2SUnits;
-constexpr int kG2LoadsPerQuad = kG2AUnits / kWave / kG2Waves + 2 * kG2NB;  // per wave
 
 // Column swizzle of the A rows in LDS.  gfx950 serves a wave's ds_read_b128
 // in four cycles of 16 lanes, lane l in cycle group (b0 ^ b1 ^ b2, b3) of its
@@ -260,8 +259,8 @@ __device__ inline int count_active(const SegSrc& seg, int* s_nact) {
 
 // The multiply-accumulate of one K quad from LDS stage st into acc (shared
 // by both kernels).  VT: the leading 16-position tiles of the block that are
-// multiplied (the caller rounds the tiles holding a segment position up to
-// 2, 4 or 8); the rest lie past the segment end, so their MFMAs, A reads and
+// multiplied (the caller passes the number of tiles that hold a segment
+// position); the rest lie past the segment end, so their MFMAs, A reads and
 // scaling are skipped, and their accumulators stay zero and are never
 // stored.  A compile-time count keeps the loop branch-free: a run-time test
 // per tile broke the software pipelining and cost 30%.  RAGGED: groups at or
@@ -375,6 +374,13 @@ __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* l
   constexpr int RPD = kWave / UPR;            // A rows per direct-to-LDS load
   constexpr int ND = kG2AUnits / kWave / kG2Waves;  // A loads per wave per quad
   static_assert(BM * UPR == kG2AUnits && ND >= 1, "one stage holds the tile");
+  // A load i of the waves fills rows [8 RPD i, 8 RPD (i + 1)); only the loads
+  // that reach a multiplied tile (rows below 16 VT) are issued: the rest would
+  // copy rows that no MFMA reads (at 64 positions to a 128-position block,
+  // half of the A bytes)
+  constexpr int NDV = (16 * VT + kG2Waves * RPD - 1) / (kG2Waves * RPD);
+  static_assert(NDV >= 1 && NDV <= ND, "A loads issued");
+  constexpr int kLoads = NDV + 2 * NB;  // copies per wave per quad
   const int lane = threadIdx.x % kWave;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t mask = vgpr_const(0x000F000Fu);
@@ -398,7 +404,7 @@ __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* l
     const uint32_t st = lds0 + stage * (kG2StageUnits * 16);
     const uint32_t aoff = uni(q * 256u * AW);
 #pragma unroll
-    for (int i = 0; i < ND; ++i)
+    for (int i = 0; i < NDV; ++i)
       dma_b128_unseen(ar, uni(st + (uint32_t)(w + kG2Waves * i) * kWave * 16), voff[i], aoff);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -420,7 +426,7 @@ __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* l
   uint32_t stage = 0;
   auto top = [&](uint32_t q) {
     asm volatile("" ::: "memory");
-    if (q + 1 < Kq) wait_vm_lgkm0<kG2LoadsPerQuad>();  // quad q's copies done, q + 1's may fly
+    if (q + 1 < Kq) wait_vm_lgkm0<kLoads>();  // quad q's copies done, q + 1's may fly
     else wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();  // every wave's copies are in; stage (q - 1) % 3 is free
     asm volatile("" ::: "memory");
@@ -488,9 +494,19 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_gate_up_kernel(GemmK a)
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) acc[b][tt] = z;
     const int vt = __builtin_amdgcn_readfirstlane((int)ceil_div(c.end - c.m0, (int64_t)16));
-    if (vt > 4) gemm_tile3<BM, 1, 8>(a, s_row, lds_a, ar, nr, sr, rt, acc);
-    else if (vt > 2) gemm_tile3<BM, 1, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc);
-    else gemm_tile3<BM, 1, 2>(a, s_row, lds_a, ar, nr, sr, rt, acc);
+    // exactly the tiles that hold a position (a block of 65 positions takes 5
+    // tiles, not 8: at about 64 positions an expert, DeepSeek-V3's prefill
+    // multiplied half again its positions with rounding to 2, 4 or 8)
+    switch (vt) {
+      case 1: gemm_tile3<BM, 1, 1>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 2: gemm_tile3<BM, 1, 2>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 3: gemm_tile3<BM, 1, 3>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 4: gemm_tile3<BM, 1, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 5: gemm_tile3<BM, 1, 5>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 6: gemm_tile3<BM, 1, 6>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 7: gemm_tile3<BM, 1, 7>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      default: gemm_tile3<BM, 1, 8>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+    }
 
     // SwiGLU, then h as the fp16 pair hi + lo into LDS in down-operand chunk
     // order [group of the workgroup][position][part p'][hi 8, lo 8]: element
@@ -576,8 +592,12 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_down_kernel(GemmK a) {
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) acc[b][tt] = z;
     const int vt = __builtin_amdgcn_readfirstlane((int)ceil_div(c.end - c.m0, (int64_t)16));
-    if (vt > 2) gemm_tile3<BM, 2, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc);
-    else gemm_tile3<BM, 2, 2>(a, s_row, lds_a, ar, nr, sr, rt, acc);
+    switch (vt) {
+      case 1: gemm_tile3<BM, 2, 1>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 2: gemm_tile3<BM, 2, 2>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 3: gemm_tile3<BM, 2, 3>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      default: gemm_tile3<BM, 2, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+    }
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const int64_t t = (c.nb * kG2Waves + w) * NB + b;
