@@ -1352,14 +1352,14 @@ static hipError_t launch_permute_multi(const int32_t* idx, int64_t T, int k, int
   return hipGetLastError();
 }
 
-// Tokens per logits workgroup.  One token a workgroup up to 16 tokens: the
-// grid then has T times as many workgroups to stream W with, which took the
-// DeepSeek-V3 eight-token route from 30.9 to 23.7 us and the Mixtral
-// sixteen-token one from 22.5 to 16.7 us; at 32 and 64 tokens the re-reads
-// of W that a one-token tile costs outweigh that (20.0 -> 23.1 us, 49 -> 76 us).
+// Tokens per logits workgroup.  Small tiles give the grid more workgroups to
+// stream W with, large ones re-read W less.  Measured routes (us), tiles of
+// 1 / 2 / 4 tokens: DeepSeek-V3 8 tokens 22.5 / 24.8 / 29.7, Mixtral 16
+// tokens 15.6 / 18.7 / 22.2, Qwen3 32 tokens 21.8 / 17.7 / 19.7, DeepSeek-V3
+// 64 tokens 72.1 / 46.8 / 47.8.
 int router_token_tile(int64_t T) {
   if (T <= 16) return 1;
-  if (T <= 64) return 4;
+  if (T <= 64) return 2;
   return kBigTT;
 }
 
@@ -1368,9 +1368,9 @@ static hipError_t launch_logits_t(const RouteK& k, int TT, int n_ttiles, hipStre
   if (TT == 1) {
     dim3 grid((unsigned)ceil_div(k.E, 4 * 1), (unsigned)n_ttiles);
     hipLaunchKernelGGL((route_logits_kernel<XT, 1, 1, 8>), grid, dim3(256), 0, stream, k);
-  } else if (TT == 4) {
+  } else if (TT == 2) {
     dim3 grid((unsigned)ceil_div(k.E, 4 * 2), (unsigned)n_ttiles);
-    hipLaunchKernelGGL((route_logits_kernel<XT, 4, 2, 8>), grid, dim3(256), 0, stream, k);
+    hipLaunchKernelGGL((route_logits_kernel<XT, 2, 2, 8>), grid, dim3(256), 0, stream, k);
   } else {
     dim3 grid((unsigned)ceil_div(k.E, 4 * kBigEW), (unsigned)n_ttiles);
     hipLaunchKernelGGL((route_logits_big_kernel<XT, kBigTT, kBigEW>), grid, dim3(256), 0, stream, k);
