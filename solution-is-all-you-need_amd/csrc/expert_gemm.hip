@@ -184,18 +184,34 @@ struct TileCoord {
 };
 
 // half >= 0: only positions [BM / 2 half, BM / 2 (half + 1)) of the block.
+// The active slots' descriptors in LDS, copied once per launch: read there,
+// an item's set-up issues no global load, after which the compiler would
+// wait for every outstanding store of the wave (the gate/up kernel's storing
+// waves keep theirs in flight into the next item).
+struct SegLds {
+  int e[kMaxExperts + 1], beg[kMaxExperts + 1], end[kMaxExperts + 1];
+};
+
+__device__ inline void seg_to_lds(const SegSrc& seg, int n_act, SegLds* sl) {
+  for (int u = threadIdx.x; u < n_act; u += blockDim.x) {
+    const int4 d = seg.desc[u];
+    sl->e[u] = d.x;
+    sl->beg[u] = d.y;
+    sl->end[u] = d.z;
+  }
+}
+
 template <int BM>
-__device__ inline TileCoord tile_coord(const GemmK& a, const int4* s_desc, const int* s_mb, int n_act,
+__device__ inline TileCoord tile_coord(const GemmK& a, const SegLds* sl, const int* s_mb, int n_act,
                                        const XcdPlan& xp, int64_t item, int64_t n_nb, int64_t* s_row,
                                        int half = -1) {
   TileCoord c;
   const int64_t mb = xp.b0 + item / n_nb;
   c.nb = item % n_nb;
   const int u = segment_of_block(s_mb, n_act, mb);
-  const int4 d = s_desc[u];
-  c.e = __builtin_amdgcn_readfirstlane(d.x);
-  c.m0 = (int64_t)d.y + (mb - s_mb[u]) * BM;
-  c.end = d.z;
+  c.e = __builtin_amdgcn_readfirstlane(sl->e[u]);
+  c.m0 = (int64_t)sl->beg[u] + (mb - s_mb[u]) * BM;
+  c.end = sl->end[u];
   if (half >= 0) {
     c.m0 += (int64_t)half * (BM / 2);
     c.end = c.end < c.m0 + BM / 2 ? c.end : c.m0 + BM / 2;
@@ -363,35 +379,42 @@ __device__ inline void a_units(uint32_t (&a_unit)[4]) {
   for (int gi = 0; gi < 4; ++gi) a_unit[gi] = n * 16 * AW + (((p * 4 + gi) * AW) ^ a_swizzle(n));
 }
 
-// One item's K loop through the LDS ring (gate/up): both operands staged
-// two quads ahead, one barrier per quad.
-template <int BM, int AW, int VT>
+// One item's K loop through the LDS ring: both operands staged two quads
+// ahead, one barrier per quad.  CW waves issue the copies: with CW = 8 each
+// wave copies its own B operands and a share of A; with CW = 4 waves 0-3 copy
+// everything (wave w the B operands of waves w and w + 4, rt[o] those of wave
+// w + 4 o) and only they wait on vmcnt, so waves 4-7 may keep global stores
+// in flight through the loop (gfx9 counts loads and stores in one vmcnt, and
+// a wait for a copy would also wait for them).
+template <int BM, int AW, int VT, int CW = kG2Waves>
 __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* lds, const i32x4& ar,
-                                  const i32x4 (&nr)[kG2NB], const i32x4 (&sr)[kG2NB], const int64_t (&rt)[kG2NB],
-                                  f32x4 acc[kG2NB][BM / 16]) {
+                                  const i32x4 (&nr)[kG2NB], const i32x4 (&sr)[kG2NB],
+                                  const int64_t (&rt)[kG2Waves / CW][kG2NB], f32x4 acc[kG2NB][BM / 16]) {
   constexpr int NB = kG2NB;
+  constexpr int OWN = kG2Waves / CW;          // waves whose B operands a copying wave loads
   constexpr int UPR = 16 * AW;                // 16-byte units per A row
   constexpr int RPD = kWave / UPR;            // A rows per direct-to-LDS load
-  constexpr int ND = kG2AUnits / kWave / kG2Waves;  // A loads per wave per quad
-  static_assert(BM * UPR == kG2AUnits && ND >= 1, "one stage holds the tile");
-  // A load i of the waves fills rows [8 RPD i, 8 RPD (i + 1)); only the loads
-  // that reach a multiplied tile (rows below 16 VT) are issued: the rest would
-  // copy rows that no MFMA reads (at 64 positions to a 128-position block,
-  // half of the A bytes)
-  constexpr int NDV = (16 * VT + kG2Waves * RPD - 1) / (kG2Waves * RPD);
+  constexpr int ND = kG2AUnits / kWave / CW;  // A loads per copying wave per quad
+  static_assert(BM * UPR == kG2AUnits && ND >= 1 && CW * OWN == kG2Waves, "one stage holds the tile");
+  // A load i of the copying waves fills rows [CW RPD i, CW RPD (i + 1)); only
+  // the loads that reach a multiplied tile (rows below 16 VT) are issued: the
+  // rest would copy rows that no MFMA reads (at 64 positions to a
+  // 128-position block, half of the A bytes)
+  constexpr int NDV = (16 * VT + CW * RPD - 1) / (CW * RPD);
   static_assert(NDV >= 1 && NDV <= ND, "A loads issued");
-  constexpr int kLoads = NDV + 2 * NB;  // copies per wave per quad
+  constexpr int kLoads = NDV + 2 * OWN * NB;  // copies per copying wave per quad
   const int lane = threadIdx.x % kWave;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const bool copier = w < CW;
   const uint32_t mask = vgpr_const(0x000F000Fu);
   const uint32_t row_bytes = (uint32_t)(a.Kq * 256 * AW);
   const uint32_t Kq = (uint32_t)a.Kq;
-  // this wave's A loads j = w + kG2Waves * i: lane l fills slot l % UPR of row
+  // this wave's A loads j = w + CW * i: lane l fills slot l % UPR of row
   // j * RPD + l / UPR with logical unit (slot ^ a_swizzle(row & 15))
   uint32_t voff[ND];
 #pragma unroll
   for (int i = 0; i < ND; ++i) {
-    const int j = w + kG2Waves * i;
+    const int j = (copier ? w : 0) + CW * i;
     const int row = j * RPD + lane / UPR;
     const int unit = (lane % UPR) ^ (int)a_swizzle((uint32_t)row & 15u);
     voff[i] = (uint32_t)s_row[row] * row_bytes + (uint32_t)unit * 16u;
@@ -401,20 +424,25 @@ __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* l
   const uint32_t lds0 = lds_addr(lds);
   auto uni = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
   auto copy = [&](uint32_t q, uint32_t stage) {
+    if (!copier) return;
     const uint32_t st = lds0 + stage * (kG2StageUnits * 16);
     const uint32_t aoff = uni(q * 256u * AW);
 #pragma unroll
     for (int i = 0; i < NDV; ++i)
-      dma_b128_unseen(ar, uni(st + (uint32_t)(w + kG2Waves * i) * kWave * 16), voff[i], aoff);
+      dma_b128_unseen(ar, uni(st + (uint32_t)(w + CW * i) * kWave * 16), voff[i], aoff);
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const uint32_t tq = uni((uint32_t)rt[b] * Kq + q);
-      dma_b128_unseen(nr[b], uni(st + (uint32_t)(kG2AUnits + (w * NB + b) * kWave) * 16), (uint32_t)lane * 16u,
-                      tq * kQuadNibBytes);
-      // the 128 scale bytes: eight lanes
-      if (lane < 8)
-        dma_b128_unseen(sr[b], uni(st + (uint32_t)(kG2AUnits + kG2BUnits + (w * NB + b) * 8) * 16),
-                        (uint32_t)lane * 16u, tq * (kQuadScales * 2));
+    for (int o = 0; o < OWN; ++o) {
+      const int ow = w + CW * o;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const uint32_t tq = uni((uint32_t)rt[o][b] * Kq + q);
+        dma_b128_unseen(nr[b], uni(st + (uint32_t)(kG2AUnits + (ow * NB + b) * kWave) * 16), (uint32_t)lane * 16u,
+                        tq * kQuadNibBytes);
+        // the 128 scale bytes: eight lanes
+        if (lane < 8)
+          dma_b128_unseen(sr[b], uni(st + (uint32_t)(kG2AUnits + kG2BUnits + (ow * NB + b) * 8) * 16),
+                          (uint32_t)lane * 16u, tq * (kQuadScales * 2));
+      }
     }
   };
   copy(0, 0);
@@ -426,9 +454,13 @@ __device__ inline void gemm_tile3(const GemmK& a, const int64_t* s_row, u32x4* l
   uint32_t stage = 0;
   auto top = [&](uint32_t q) {
     asm volatile("" ::: "memory");
-    if (q + 1 < Kq) wait_vm_lgkm0<kLoads>();  // quad q's copies done, q + 1's may fly
-    else wait_vm_lgkm0<0>();
-    __builtin_amdgcn_s_barrier();  // every wave's copies are in; stage (q - 1) % 3 is free
+    if (copier) {
+      if (q + 1 < Kq) wait_vm_lgkm0<kLoads>();  // quad q's copies done, q + 1's may fly
+      else wait_vm_lgkm0<0>();
+    } else {
+      wait_vm_lgkm0<63>();  // LDS only: this wave's stores stay in flight
+    }
+    __builtin_amdgcn_s_barrier();  // every copy of quad q is in; stage (q - 1) % 3 is free
     asm volatile("" ::: "memory");
     if (q + 2 < Kq) copy(q + 2, stage == 0 ? 2u : stage - 1u);
     const u32x4* st = lds + stage * kG2StageUnits;
@@ -447,6 +479,7 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_gate_up_kernel(GemmK a)
   __shared__ u32x4 lds_a[kG2Stages * kG2StageUnits];
   __shared__ int s_mb[kMaxExperts + 2];
   __shared__ int64_t s_row[BM];
+  __shared__ SegLds s_seg;
   __shared__ int s_nact;
   const int lane = threadIdx.x % kWave;
   const int w = threadIdx.x / kWave;
@@ -458,7 +491,8 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_gate_up_kernel(GemmK a)
   }
   const i32x4 ar = buf_rsrc_words(a.a_src, (uint32_t)((a.a_zero_row + 1) * a.Kq * 256));
   const int n_act = count_active(a.seg, &s_nact);
-  const int64_t n_mb = plan_items<BM>(a.seg.desc, n_act, s_mb);
+  seg_to_lds(a.seg, n_act, &s_seg);
+  const int64_t n_mb = plan_items<BM>(a.seg.desc, n_act, s_mb);  // its barrier publishes s_seg too
   const int64_t n_nb = ceil_div(a.N, kRows);
   const XcdPlan xp = xcd_plan(n_mb, n_nb);
   const uint32_t nib_bytes = (uint32_t)(a.N * a.Kq * 64), sc_bytes = (uint32_t)(a.N * a.Kq * 8);
@@ -473,11 +507,13 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_gate_up_kernel(GemmK a)
   for (int64_t ent = xp.l; ent < xp.n_items + n_split; ent += xp.nl) {
     const int64_t item = ent < n_whole ? ent : n_whole + (ent - n_whole) / 2;
     const int part = ent < n_whole ? -1 : (int)((ent - n_whole) % 2);
-    const TileCoord c = tile_coord<BM>(a, a.seg.desc, s_mb, n_act, xp, item, n_nb, s_row, part);
+    const TileCoord c = tile_coord<BM>(a, &s_seg, s_mb, n_act, xp, item, n_nb, s_row, part);
     if (c.m0 >= c.end) continue;  // the empty second half of a block of <= BM / 2 positions
     const int64_t n_tiles = a.N / kRowTile;
     const int64_t t = c.nb * kG2Waves + w;
     const int64_t tc = t < n_tiles ? t : n_tiles - 1;  // a tile past I computes, unstored
+    const int64_t t4 = t + 4;                           // wave w + 4's tile, copied by wave w < 4
+    const int64_t tc4 = t4 < n_tiles ? t4 : n_tiles - 1;
     const bool routed = c.e < a.seg.E;
     const i32x4 nr[2] = {buf_rsrc_words(routed ? a.nib1 + (int64_t)c.e * nib_bytes : a.sh_nib1, nib_bytes),
                          buf_rsrc_words(routed ? a.nib2 + (int64_t)c.e * nib_bytes : a.sh_nib2, nib_bytes)};
@@ -486,7 +522,7 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_gate_up_kernel(GemmK a)
                               : reinterpret_cast<const uint8_t*>(a.sh_sc1), sc_bytes),
         buf_rsrc_words(routed ? reinterpret_cast<const uint8_t*>(a.sc2) + (int64_t)c.e * sc_bytes
                               : reinterpret_cast<const uint8_t*>(a.sh_sc2), sc_bytes)};
-    const int64_t rt[2] = {tc, tc};
+    const int64_t rt[2][2] = {{tc, tc}, {tc4, tc4}};
     f32x4 acc[2][TT];
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -498,14 +534,14 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_gate_up_kernel(GemmK a)
     // tiles, not 8: at about 64 positions an expert, DeepSeek-V3's prefill
     // multiplied half again its positions with rounding to 2, 4 or 8)
     switch (vt) {
-      case 1: gemm_tile3<BM, 1, 1>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
-      case 2: gemm_tile3<BM, 1, 2>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
-      case 3: gemm_tile3<BM, 1, 3>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
-      case 4: gemm_tile3<BM, 1, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
-      case 5: gemm_tile3<BM, 1, 5>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
-      case 6: gemm_tile3<BM, 1, 6>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
-      case 7: gemm_tile3<BM, 1, 7>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
-      default: gemm_tile3<BM, 1, 8>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 1: gemm_tile3<BM, 1, 1, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 2: gemm_tile3<BM, 1, 2, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 3: gemm_tile3<BM, 1, 3, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 4: gemm_tile3<BM, 1, 4, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 5: gemm_tile3<BM, 1, 5, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 6: gemm_tile3<BM, 1, 6, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 7: gemm_tile3<BM, 1, 7, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      default: gemm_tile3<BM, 1, 8, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
     }
 
     // SwiGLU, then h as the fp16 pair hi + lo into LDS in down-operand chunk
@@ -533,8 +569,11 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_gate_up_kernel(GemmK a)
       }
     }
     lds_barrier();
+    // the stores from waves 4-7, which issue no copies (see gemm_tile3): they
+    // drain while the next item's copies and MFMAs run
     constexpr int kGroups = kG2Waves / 2;
-    for (int cidx = threadIdx.x; cidx < kGroups * BM * 4; cidx += blockDim.x) {
+    constexpr int kStoreThreads = kG2Waves / 2 * kWave;
+    for (int cidx = (int)threadIdx.x - kStoreThreads; cidx >= 0 && cidx < kGroups * BM * 4; cidx += kStoreThreads) {
       const int g2 = cidx / (BM * 4);
       const int m = (cidx / 4) % BM;
       const int p2 = cidx % 4;
@@ -559,6 +598,7 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_down_kernel(GemmK a) {
   __shared__ u32x4 lds_a[kG2Stages * kG2StageUnits];
   __shared__ int s_mb[kMaxExperts + 2];
   __shared__ int64_t s_row[BM];
+  __shared__ SegLds s_seg;
   __shared__ int s_nact;
   const int lane = threadIdx.x % kWave;
   const int w = threadIdx.x / kWave;
@@ -566,24 +606,25 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_down_kernel(GemmK a) {
   const int p = lane / 16;
   const i32x4 ar = buf_rsrc_words(a.a_src, (uint32_t)((a.a_zero_row + 1) * a.Kq * 512));
   const int n_act = count_active(a.seg, &s_nact);
-  const int64_t n_mb = plan_items<BM>(a.seg.desc, n_act, s_mb);
+  seg_to_lds(a.seg, n_act, &s_seg);
+  const int64_t n_mb = plan_items<BM>(a.seg.desc, n_act, s_mb);  // its barrier publishes s_seg too
   const int64_t n_nb = ceil_div(a.N, kRows);
   const int64_t n_tiles = a.N / kRowTile;
   const XcdPlan xp = xcd_plan(n_mb, n_nb);
   const uint32_t nib_bytes = (uint32_t)(a.N * a.Kq * 64), sc_bytes = (uint32_t)(a.N * a.Kq * 8);
   for (int64_t item = xp.l; item < xp.n_items; item += xp.nl) {
-    const TileCoord c = tile_coord<BM>(a, a.seg.desc, s_mb, n_act, xp, item, n_nb, s_row);
+    const TileCoord c = tile_coord<BM>(a, &s_seg, s_mb, n_act, xp, item, n_nb, s_row);
     const bool routed = c.e < a.seg.E;
     const i32x4 nw = buf_rsrc_words(routed ? a.nib1 + (int64_t)c.e * nib_bytes : a.sh_nib1, nib_bytes);
     const i32x4 sw = buf_rsrc_words(routed ? reinterpret_cast<const uint8_t*>(a.sc1) + (int64_t)c.e * sc_bytes
                                            : reinterpret_cast<const uint8_t*>(a.sh_sc1), sc_bytes);
     const i32x4 nr[NB] = {nw, nw};
     const i32x4 sr[NB] = {sw, sw};
-    int64_t rt[NB];
+    int64_t rt[1][NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const int64_t t = (c.nb * kG2Waves + w) * NB + b;
-      rt[b] = t < n_tiles ? t : n_tiles - 1;  // a tile past H computes, unstored
+      rt[0][b] = t < n_tiles ? t : n_tiles - 1;  // a tile past H computes, unstored
     }
     f32x4 acc[NB][TT];
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
