@@ -620,12 +620,15 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_down_kernel(GemmK a) {
                                            : reinterpret_cast<const uint8_t*>(a.sh_sc1), sc_bytes);
     const i32x4 nr[NB] = {nw, nw};
     const i32x4 sr[NB] = {sw, sw};
-    int64_t rt[1][NB];
+    // waves 0-3 copy their own operands and wave w + 4's (rt[1])
+    int64_t rt[2][NB];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const int64_t t = (c.nb * kG2Waves + w) * NB + b;
-      rt[0][b] = t < n_tiles ? t : n_tiles - 1;  // a tile past H computes, unstored
-    }
+    for (int o = 0; o < 2; ++o)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int64_t t = (c.nb * kG2Waves + w + 4 * o) * NB + b;
+        rt[o][b] = t < n_tiles ? t : n_tiles - 1;  // a tile past H computes, unstored
+      }
     f32x4 acc[NB][TT];
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -634,10 +637,10 @@ __global__ __launch_bounds__(kG2Waves * kWave) void gemm_down_kernel(GemmK a) {
       for (int tt = 0; tt < TT; ++tt) acc[b][tt] = z;
     const int vt = __builtin_amdgcn_readfirstlane((int)ceil_div(c.end - c.m0, (int64_t)16));
     switch (vt) {
-      case 1: gemm_tile3<BM, 2, 1>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
-      case 2: gemm_tile3<BM, 2, 2>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
-      case 3: gemm_tile3<BM, 2, 3>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
-      default: gemm_tile3<BM, 2, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 1: gemm_tile3<BM, 2, 1, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 2: gemm_tile3<BM, 2, 2, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      case 3: gemm_tile3<BM, 2, 3, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
+      default: gemm_tile3<BM, 2, 4, 4>(a, s_row, lds_a, ar, nr, sr, rt, acc); break;
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
