@@ -22,13 +22,14 @@
 // tolerance is 1e-2.)
 //
 // Tile pipeline.  Both operands are staged by direct-to-LDS loads into a ring
-// of kG2Stages LDS stages two K quads ahead of the MFMAs: per quad and wave,
-// the wave's share of the A rows and its own B operands (nibbles and scales).
+// of kG2Stages LDS stages two K quads ahead of the MFMAs: per quad, waves 0-3
+// copy the A rows and the B operands (nibbles and scales) of all eight waves,
+// so waves 4-7 never wait on vmcnt and their global stores stay in flight.
 // The loads are issued from inline assembly (dma_b128_unseen), so the
 // compiler adds no waits of its own; per quad there is one workgroup barrier,
-// preceded by a wait for the wave's copies of the quad about to be read (the
-// newer quad's copies stay in flight), which also guarantees every wave has
-// left the stage about to be refilled.  A rows are stored with unit s of row
+// preceded by each copying wave's wait for its copies of the quad about to
+// be read (the newer quad's copies stay in flight), which also guarantees
+// every wave has left the stage about to be refilled.  A rows are stored with unit s of row
 // r at s ^ a_swizzle(r & 15), so that no ds_read_b128 of the A operands
 // has a bank conflict (see a_swizzle).  Padded groups of K (a ragged last quad of H or I) are
 // skipped.
@@ -36,11 +37,13 @@
 // Tiling.  A workgroup of kG2Waves waves owns BM consecutive positions of
 // one expert segment and a block of weight rows; every wave multiplies all BM
 // positions with NB = 2 weight row tiles of its own, so each B operand feeds
-// BM / 16 (times AW) MFMAs.
+// up to BM / 16 (times AW) MFMAs, one per 16-position tile that holds a
+// segment position.
 //   gate/up (BM 128, AW 1): wave w takes the gate and the up operand of one
 //            16-row tile of I, so its SwiGLU epilogue has both factors of
 //            every output; the workgroup's 8 tiles are 4 whole 32-groups of
-//            I, written as down-operand chunks (hi + lo) via LDS.
+//            I, written as down-operand chunks (hi + lo) via LDS, stored by
+//            waves 4-7.
 //   down (BM 64, AW 2):  wave w takes two 16-row tiles of H.
 //
 // Schedule.  Per group the wave needs VT (times AW) A operands from LDS; the
