@@ -359,7 +359,7 @@ __device__ void wave_topk(const RouteK& a, int64_t t, uint64_t* s_ck, double* s_
 
 // MFMA-ordered copy of x (bf16) and fp32 group sums for tokens [t0, t0+TT),
 // spread over the nparts workgroups that share this token tile (this one is
-// number part).
+// number part), by nthreads threads of each (this one is number tid).
 // Layout [t][q][p][gi][8]: one 16-byte chunk per (token, quad, part, group);
 // chunk (p, gi) of quad q holds elements kmap(p, 0..7) of group 4q + gi, read
 // as two 8-byte runs (4p..4p+3 and 4p+16..4p+19).  A group's sum adds its
@@ -369,14 +369,14 @@ __device__ void wave_topk(const RouteK& a, int64_t t, uint64_t* s_ck, double* s_
 // copy (it cannot prove they do not alias), so a chunk at a time paid one
 // memory round trip per chunk (16 of them per thread for 4096 tokens).
 constexpr int kPrepBatch = 8;
-__device__ void prep_x_tile(const RouteK& a, int64_t t0, int TT, int part, int nparts) {
+__device__ void prep_x_tile(const RouteK& a, int64_t t0, int TT, int part, int nparts, int tid, int nthreads) {
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
   const int Kg = (int)(a.H / kGroup);
   const int per_tok = (int)a.Kq * 16;
   const int n = TT * per_tok;
-  const int lane = threadIdx.x % kWave;
-  const int stride = nparts * (int)blockDim.x;
-  const int wave0 = part * (int)blockDim.x + (int)(threadIdx.x / kWave) * kWave;
+  const int lane = tid % kWave;
+  const int stride = nparts * nthreads;
+  const int wave0 = part * nthreads + (tid / kWave) * kWave;
   for (int c00 = wave0; c00 < n; c00 += kPrepBatch * stride) {  // wave-uniform
     uint2 lo[kPrepBatch], hi[kPrepBatch];
 #pragma unroll
@@ -528,7 +528,8 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteK a) {
       }
     }
     // the MFMA-ordered copy of x, its loads in flight with the first batch's
-    if (c0 == 0 && a.prep_x) prep_x_tile(a, t0, TT, (int)blockIdx.x, (int)gridDim.x);
+    if (c0 == 0 && a.prep_x)
+      prep_x_tile(a, t0, TT, (int)blockIdx.x, (int)gridDim.x, (int)threadIdx.x, (int)blockDim.x);
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
 #pragma unroll
@@ -691,7 +692,7 @@ __global__ __launch_bounds__(256) void route_logits_big_kernel(RouteK a) {
   const int64_t t0 = (int64_t)blockIdx.y * TT;
   const int e0 = blockIdx.x * (4 * EW) + w * EW;
   const XT* x = static_cast<const XT*>(a.x);
-  if (a.prep_x) prep_x_tile(a, t0, TT, (int)blockIdx.x, (int)gridDim.x);
+  if (a.prep_x) prep_x_tile(a, t0, TT, (int)blockIdx.x, (int)gridDim.x, (int)threadIdx.x, (int)blockDim.x);
   if (a.counter && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *a.counter = 0;
   float bias_e = 0.0f;
   if (a.bias) {
@@ -754,7 +755,8 @@ __global__ __launch_bounds__(256) void route_logits_big_kernel(RouteK a) {
 //   route_approx_kernel: L~ = x . (w_hi + w_lo) on the matrix cores for every
 //     pair, with w_hi = bf16(w) and w_lo = bf16(w - w_hi) (both rounded to
 //     nearest), plus the norms |x_t| and |w_e|;
-//   route_candidates_kernel (one wave per token): the error bound
+//   route_candidates_kernel (one wave per token; four more waves per
+//     workgroup write the GEMM's copy of x meanwhile): the error bound
 //     |L~ - L| <= C(H) |x_t| |w_e| gives every expert an interval; experts
 //     whose upper end reaches the k-th largest lower end are the candidates
 //     (a superset of the exact top k: any expert below that has k others
@@ -814,7 +816,6 @@ __global__ __launch_bounds__(256) void route_approx_kernel(RouteK a, float* appr
   const int64_t t0 = tt * kApproxTok;
   const int e0 = (int)eb * kApproxExp;
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
-  if (a.prep_x) prep_x_tile(a, t0, kApproxTok, (int)eb, (int)n_eb);
   if (a.counter && blockIdx.x == 0 && threadIdx.x == 0) *a.counter = 0;
   // A rows: token t0 + 16 w + lane % 16 (clamped), K 8 (lane / 16) .. + 8 of each step
   const int64_t tr = t0 + 16 * w + lane % 16;
@@ -935,7 +936,7 @@ __device__ inline uint32_t f32_key(float v) {
 // Candidates of each token (one wave per token): cand[e * T + t] = 1 for a
 // candidate, else 0 and logits[t][e] = -inf.
 template <int NV>
-__global__ __launch_bounds__(256) void route_candidates_kernel(RouteK a, const float* approx, const float* nx,
+__global__ __launch_bounds__(512) void route_candidates_kernel(RouteK a, const float* approx, const float* nx,
                                                                const float* nw, uint8_t* cand) {
   const int lane = threadIdx.x % kWave;
   const int w = threadIdx.x / kWave;
@@ -950,6 +951,16 @@ __global__ __launch_bounds__(256) void route_candidates_kernel(RouteK a, const f
   // of entries below about 2^-75 would get a norm of 0 and a bound far below
   // the bf16 rounding error of its approximate logits.
   const float slack = sqrtf((float)a.H + 8.0f) * 1.0842022e-19f * 1.01f;
+  if (w >= 4) {
+    // Waves 4-7 write the workgroup's tokens' MFMA-ordered x copy and group
+    // sums meanwhile: the candidate waves are latency-bound and leave memory
+    // idle (in the approximate-logit launch the copy cost 7 us at 4096 tokens
+    // of H 2048 and 17.5 us at 2048 of H 7168)
+    if (a.prep_x)
+      for (int64_t t0 = (int64_t)blockIdx.x * 4; t0 < a.T; t0 += (int64_t)gridDim.x * 4)
+        prep_x_tile(a, t0, 4, 0, 1, (int)threadIdx.x - 4 * kWave, 4 * kWave);
+    return;
+  }
   for (int64_t t = (int64_t)blockIdx.x * 4 + w; t < a.T; t += (int64_t)gridDim.x * 4) {
     const float nxt = nx[t] + slack;
     float lo[NV], hi[NV];
@@ -1386,7 +1397,7 @@ static hipError_t launch_route_two_pass(const RouteK& k, const Workspace& ws, hi
   float* nw = nx + k.T;
   hipLaunchKernelGGL(route_approx_kernel, dim3((unsigned)(ceil_div(k.E, kApproxExp) * ceil_div(k.T, kApproxTok))),
                      dim3(256), 0, stream, k, approx, nx, nw);
-  const dim3 grid((unsigned)ceil_div(k.T, 4)), block(256);
+  const dim3 grid((unsigned)ceil_div(k.T, 4)), block(512);  // 4 candidate waves + 4 copying x
   if (k.E <= 64) hipLaunchKernelGGL(route_candidates_kernel<1>, grid, block, 0, stream, k, approx, nx, nw, ws.cand);
   else if (k.E <= 128) hipLaunchKernelGGL(route_candidates_kernel<2>, grid, block, 0, stream, k, approx, nx, nw, ws.cand);
   else if (k.E <= 256) hipLaunchKernelGGL(route_candidates_kernel<4>, grid, block, 0, stream, k, approx, nx, nw, ws.cand);
