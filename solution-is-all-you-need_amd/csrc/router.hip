@@ -70,6 +70,12 @@ struct RouteK {
   int32_t* n_tiles;
   int32_t* counter;  // select workgroups finished (fused permute); zeroed by the logits launch
   int fuse_permute;
+  // many-slot permute: the select launch counts each slot into
+  // perm_cnt[e * perm_nb + slot / perm_chunk] (zeroed by the first route
+  // launch), which the count launch would otherwise do; null when it does not
+  int32_t* perm_cnt;
+  int64_t perm_chunk;
+  int perm_nb;
 };
 
 template <typename XT>
@@ -591,8 +597,16 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteK a) {
   const int w = threadIdx.x / kWave;
   const int nw = blockDim.x / kWave;
   const bool single = gridDim.x == 1 && a.T <= kSelectWaves;
-  for (int64_t t = (int64_t)blockIdx.x * nw + w; t < a.T; t += (int64_t)gridDim.x * nw)
+  const int lane = threadIdx.x % kWave;
+  for (int64_t t = (int64_t)blockIdx.x * nw + w; t < a.T; t += (int64_t)gridDim.x * nw) {
     wave_topk<NV>(a, t, s_ck[w], s_cv[w], s_ci[w], s_val[w], s_idx[w], s_e[w], single ? s_sel : nullptr);
+    // slot t k + j (j = lane) counted for the many-slot permute; the
+    // selection of slot j is in s_idx[j] (this wave's own LDS stores)
+    if (a.perm_cnt && lane < a.k) {
+      const int e = s_idx[w][lane];
+      if (e >= 0 && e < a.E) atomicAdd(a.perm_cnt + (int64_t)e * a.perm_nb + (t * a.k + lane) / a.perm_chunk, 1);
+    }
+  }
   if (!a.do_permute) return;
   if (single) {
     // the selection reaches the permute through LDS, not a global round trip
@@ -817,6 +831,10 @@ __global__ __launch_bounds__(256) void route_approx_kernel(RouteK a, float* appr
   const int e0 = (int)eb * kApproxExp;
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
   if (a.counter && blockIdx.x == 0 && threadIdx.x == 0) *a.counter = 0;
+  if (a.perm_cnt)
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (int64_t)a.E * a.perm_nb;
+         i += (int64_t)gridDim.x * blockDim.x)
+      a.perm_cnt[i] = 0;
   // A rows: token t0 + 16 w + lane % 16 (clamped), K 8 (lane / 16) .. + 8 of each step
   const int64_t tr = t0 + 16 * w + lane % 16;
   const uint16_t* xrow = x + (tr < a.T ? tr : a.T - 1) * a.H + 8 * (lane / 16);
@@ -1345,17 +1363,167 @@ __global__ __launch_bounds__(kPermWaves * kWave) void permute_place_kernel(const
   perm_wave_rounds<true>(idx, wlo, whi, k, E, nbits, s_cnt[w], sorted_slots, slot_pos, seg_tok, tiles, s_beg, s_tb);
 }
 
-// The three launches; cnt needs E * perm_blocks(T * k) ints, tb E ints.
+// Placement with the scan folded in, when the per-block counts are few
+// (E * nb <= kFusedScanInts): every workgroup copies the whole count table
+// into LDS, forms the segment offsets, active experts and token-tile bases
+// (the exclusive scan of block_permute) and its own per-expert bases (the
+// counts of the blocks before it), then places its chunk as
+// permute_place_kernel does.  Workgroup 0 also writes what the scan launch
+// writes: offsets, active experts, descriptors, tile headers and count; the
+// shared segment's tokens are spread over all workgroups.  This saves the
+// single-workgroup scan launch and its wait between count and place.
+constexpr int kFusedScanInts = 8192;
+
+__global__ __launch_bounds__(kPermWaves * kWave) void permute_scan_place_kernel(
+    const int32_t* idx, int64_t n, int64_t T, int k, int E, int has_shared, int64_t chunk, const int32_t* cnt,
+    int32_t* offsets, int32_t* offsets_user, int32_t* active, int32_t* n_active, int4* desc, int32_t* sorted_slots,
+    int32_t* slot_pos, int32_t* seg_tok, int32_t* tiles, int32_t* n_tiles) {
+  __shared__ int s_all[kFusedScanInts];  // cnt[e * nb + b]
+  __shared__ int s_cnt[kPermWaves][kMaxExperts];
+  __shared__ int s_beg[kMaxExperts];
+  __shared__ int s_tb[kMaxExperts];
+  __shared__ int s_tmp[3 * kPermWaves];
+  const int tid = threadIdx.x;
+  const int w = tid / kWave;
+  const int nb = gridDim.x;
+  const int blk = blockIdx.x;
+  const int nbits = perm_nbits(E);
+  for (int i = tid; i < kPermWaves * kMaxExperts; i += blockDim.x) s_cnt[i / kMaxExperts][i % kMaxExperts] = 0;
+  // the count table's loads are all issued first (clamped indices) and land
+  // while the chunk's expert ids are loaded and counted
+  const int ncnt = E * nb;
+  constexpr int kRun = kFusedScanInts / (kPermWaves * kWave);
+  int v[kRun];
+#pragma unroll
+  for (int j = 0; j < kRun; ++j) {
+    const int i = j * kPermWaves * kWave + tid;
+    v[j] = cnt[i < ncnt ? i : ncnt - 1];
+  }
+  lds_barrier();
+  const int64_t lo = (int64_t)blk * chunk;
+  const int64_t hi = lo + chunk < n ? lo + chunk : n;
+  const int64_t wc = round_up(ceil_div(hi > lo ? hi - lo : 0, kPermWaves), kWave);
+  const int64_t wlo = lo + w * wc;
+  const int64_t whi = wlo + wc < hi ? wlo + wc : hi;
+  perm_wave_rounds<false>(idx, wlo, whi, 0, E, nbits, s_cnt[w], nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
+#pragma unroll
+  for (int j = 0; j < kRun; ++j) {
+    const int i = j * kPermWaves * kWave + tid;
+    if (i < ncnt) s_all[i] = v[j];
+  }
+  lds_barrier();
+  // Scan over experts: thread t owns experts t kPer .. t kPer + kPer - 1.
+  constexpr int kPer = kMaxExperts / (kPermWaves * kWave);
+  int tot[kPer], pre[kPer];
+  int my_tot = 0, my_act = 0, my_tc = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int e = tid * kPer + i;
+    int t = 0, p = 0;
+    if (e < E) {
+      // eight independent LDS reads at a time, not one dependent read per block
+      const int* ce = s_all + e * nb;
+      for (int b0 = 0; b0 < nb; b0 += 8) {
+        int c[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c[j] = b0 + j < nb ? ce[b0 + j] : 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          t += c[j];
+          p += b0 + j < blk ? c[j] : 0;
+        }
+      }
+    }
+    tot[i] = t;
+    pre[i] = p;
+    my_tot += t;
+    my_act += t > 0 ? 1 : 0;
+    my_tc += (t + 15) / 16;
+  }
+  int3 tot3;
+  const int3 ex3 = block_exclusive_scan3(make_int3(my_tot, my_act, my_tc), s_tmp, &tot3);  // has barriers
+  const int total = tot3.x, total_act = tot3.y, total_tiles = tot3.z;
+  int run = ex3.x, arun = ex3.y, trun = ex3.z;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int e = tid * kPer + i;
+    if (e < E) {
+      s_beg[e] = run;
+      s_tb[e] = trun;
+      if (blk == 0) {
+        offsets[e] = run;
+        if (offsets_user) offsets_user[e] = run;
+        if (tot[i] > 0) {
+          active[arun] = e;
+          if (desc) desc[arun] = make_int4(e, run, run + tot[i], 0);
+        }
+        if (tiles)
+          for (int j = 0; j < (tot[i] + 15) / 16; ++j)
+            *reinterpret_cast<int4*>(tiles + (int64_t)(trun + j) * kTileWords) =
+                make_int4(e, run + 16 * j, run + tot[i], 0);
+      }
+      // this block's waves place expert e from here on, in wave order
+      int b = run + pre[i];
+      for (int ww = 0; ww < kPermWaves; ++ww) {
+        const int c = s_cnt[ww][e];
+        s_cnt[ww][e] = b;
+        b += c;
+      }
+    }
+    run += tot[i];
+    arun += tot[i] > 0 ? 1 : 0;
+    trun += (tot[i] + 15) / 16;
+  }
+  if (blk == 0) {
+    if (tid == 0) {
+      offsets[E] = total;
+      if (offsets_user) offsets_user[E] = total;
+      offsets[E + 1] = total + (has_shared ? (int)T : 0);
+      if (has_shared) {
+        active[total_act] = E;
+        if (desc) desc[total_act] = make_int4(E, total, total + (int)T, 0);
+      }
+      *n_active = total_act + (has_shared ? 1 : 0);
+      if (tiles) n_tiles[0] = total_tiles + (has_shared ? (int)((T + 15) / 16) : 0);
+    }
+    if (desc) {
+      const int n_act = total_act + (has_shared ? 1 : 0);
+      const int max_active = (int)((n < E) ? n : E) + (has_shared ? 1 : 0);
+      for (int u = n_act + tid; u < max_active; u += blockDim.x) desc[u] = make_int4(-1, 0, 0, 0);
+    }
+  }
+  if (has_shared && seg_tok)
+    for (int64_t t = (int64_t)blk * blockDim.x + tid; t < T; t += (int64_t)nb * blockDim.x) seg_tok[n + t] = (int32_t)t;
+  if (has_shared && tiles) {
+    for (int64_t j = (int64_t)blk * blockDim.x + tid; j < (T + 15) / 16; j += (int64_t)nb * blockDim.x) {
+      int32_t* tw = tiles + (total_tiles + j) * kTileWords;
+      *reinterpret_cast<int4*>(tw) = make_int4(E, total + (int)(16 * j), total + (int)T, 0);
+      for (int jj = 0; jj < 16 && 16 * j + jj < T; ++jj) tw[4 + jj] = (int32_t)(16 * j + jj);
+    }
+  }
+  lds_barrier();
+  perm_wave_rounds<true>(idx, wlo, whi, k, E, nbits, s_cnt[w], sorted_slots, slot_pos, seg_tok, tiles, s_beg, s_tb);
+}
+
+// Count, then the fused scan and placement (few blocks) or the scan and
+// placement launches; cnt needs E * perm_blocks(T * k) ints, tb E ints.
 static hipError_t launch_permute_multi(const int32_t* idx, int64_t T, int k, int E, int has_shared,
                                        int32_t* offsets, int32_t* offsets_user, int32_t* active, int32_t* n_active,
                                        int32_t* sorted_slots, int32_t* slot_pos, int4* desc, int32_t* seg_tok,
                                        int32_t* tiles, int32_t* n_tiles, int32_t* cnt,
-                                       int32_t* tb, hipStream_t stream) {
+                                       int32_t* tb, hipStream_t stream, bool counted = false) {
   const int64_t n = T * k;
   const int64_t nb = perm_blocks(n);
   const int64_t chunk = ceil_div(n, nb);
-  hipLaunchKernelGGL(permute_count_kernel, dim3((unsigned)nb), dim3(kPermWaves * kWave), 0, stream, idx, n, E, chunk,
-                     cnt);
+  if (!counted)
+    hipLaunchKernelGGL(permute_count_kernel, dim3((unsigned)nb), dim3(kPermWaves * kWave), 0, stream, idx, n, E,
+                       chunk, cnt);
+  if ((int64_t)E * nb <= kFusedScanInts) {
+    hipLaunchKernelGGL(permute_scan_place_kernel, dim3((unsigned)nb), dim3(kPermWaves * kWave), 0, stream, idx, n, T,
+                       k, E, has_shared, chunk, cnt, offsets, offsets_user, active, n_active, desc, sorted_slots,
+                       slot_pos, seg_tok, tiles, n_tiles);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(1024), 0, stream, n, T, E, (int)nb, has_shared, cnt, tb,
                      offsets, offsets_user, active, n_active, desc, seg_tok, tiles, n_tiles);
   hipLaunchKernelGGL(permute_place_kernel, dim3((unsigned)nb), dim3(kPermWaves * kWave), 0, stream, idx, n, k, E,
@@ -1444,7 +1612,16 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
   const unsigned sel_blocks = (unsigned)ceil_div(r.T, kSelectWaves);
   k.fuse_permute = (r.do_permute && sel_blocks > 1 && sel_blocks <= kFusedSelectBlocks) ? 1 : 0;
   k.counter = k.fuse_permute ? ws.counter : nullptr;
-  hipError_t err = two_pass_route(r.T, r.E, r.x_dtype) && ws.approx && ws.cand && !k.fuse_permute
+  const bool two_pass = two_pass_route(r.T, r.E, r.x_dtype) && ws.approx && ws.cand && !k.fuse_permute;
+  // With two passes and a fused scan the select launch does the permute's
+  // counting (the approximate-logit launch zeroes the counts first).
+  const int64_t n_slots = r.T * r.k;
+  const bool sel_count = two_pass && r.do_permute && sel_blocks > 1 && n_slots >= kPermMultiSlots &&
+                         (int64_t)r.E * perm_blocks(n_slots) <= kFusedScanInts;
+  k.perm_cnt = sel_count ? ws.perm_cnt : nullptr;
+  k.perm_nb = (int)perm_blocks(n_slots);
+  k.perm_chunk = ceil_div(n_slots, perm_blocks(n_slots));
+  hipError_t err = two_pass
                        ? launch_route_two_pass(k, ws, stream)
                        : ((r.x_dtype == 0) ? launch_logits_t<uint16_t>(k, TT, n_ttiles, stream)
                                            : launch_logits_t<float>(k, TT, n_ttiles, stream));
@@ -1462,7 +1639,7 @@ hipError_t launch_route(const RouteArgs& r, const Workspace& ws, hipStream_t str
   if (r.T * r.k >= kPermMultiSlots)
     return launch_permute_multi(k.topk_idx, r.T, r.k, r.E, r.has_shared, ws.offsets, r.offsets_out, ws.active,
                                 ws.n_active, k.sorted_slots, k.slot_pos, k.desc, k.seg_tok, k.tiles, k.n_tiles,
-                                ws.perm_cnt, ws.perm_tb, stream);
+                                ws.perm_cnt, ws.perm_tb, stream, sel_count);
   hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, stream, k.topk_idx, r.T, r.k,
               r.E, r.has_shared, ws.offsets, r.offsets_out, ws.active, ws.n_active, k.sorted_slots, k.slot_pos,
               k.desc, k.seg_tok, k.tiles, k.n_tiles);

@@ -205,7 +205,9 @@ def test_permute_golden(dev, name):
 
 @pytest.mark.parametrize("T,k,E,mode", [(1, 8, 128, "rand"), (32, 8, 128, "rand"), (4096, 8, 128, "rand"),
                                         (2048, 8, 256, "rand"), (100, 4, 16, "one"), (77, 3, 512, "rand"),
-                                        (1, 1, 1, "one"), (9000, 2, 8, "rand")])
+                                        (1, 1, 1, "one"), (9000, 2, 8, "rand"),
+                                        # E x blocks above the fused scan's table: separate scan launch
+                                        (4096, 8, 512, "rand")])
 def test_permute_vs_numpy(dev, T, k, E, mode):
     rng = np.random.default_rng(T + k + E)
     if mode == "one":
@@ -234,6 +236,9 @@ SMALL_CASES = [
     # 8800 slots: the many-workgroup permute, feeding the token-tile table and
     # the shared expert (decode regime: 17 positions per expert on average)
     synth.MoEConfig("many_slots_tiles", 256, 256, 512, 8, 1100, shared=True),
+    # 16800 slots over 512 experts: 17 count blocks x 512 experts exceed the
+    # fused scan's table, so the scan runs as its own launch
+    synth.MoEConfig("many_slots_unfused", 256, 256, 512, 8, 2100, shared=True),
     # GEMM regime (T*k >= 64 * min(E, T*k)): fp16 operands, 128-position tiles
     synth.MoEConfig("gemm_e4", 256, 128, 4, 2, 200),
     synth.MoEConfig("gemm_multi_block", 256, 256, 2, 2, 300),
