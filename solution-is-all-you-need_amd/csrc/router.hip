@@ -1109,16 +1109,19 @@ __global__ __launch_bounds__(256) void route_exact_kernel(RouteK a, const uint8_
 //
 // For large batches the one-workgroup permute is bound by one CU's issue
 // rate (65 us for 32768 slots).  The same stable counting sort then runs as
-// three launches:
+// up to three launches:
 //   permute_count_kernel: workgroup b counts, per expert, the slots of its
-//     contiguous chunk into cnt[e][b];
+//     contiguous chunk into cnt[e][b] (after a two-pass route with a small
+//     count table the select launch has counted them instead);
 //   permute_scan_kernel (one workgroup): expert totals, the offsets, active
 //     list, descriptors, token-tile headers and shared segment exactly as the
 //     one-workgroup permute writes them, and cnt[e][b] replaced by the
 //     position where chunk b's first slot of expert e goes;
 //   permute_place_kernel: workgroup b re-counts its chunk per wave and places
 //     every slot at its chunk base + the counts of earlier waves + its rank
-//     within the round.
+//     within the round;
+//   permute_scan_place_kernel replaces the last two when the count table is
+//     small (E * chunks <= kFusedScanInts): each placing workgroup scans it.
 // Chunks, waves, rounds and lanes follow slot order, so every expert's slots
 // land in increasing slot order: the same permutation as block_permute.
 // (from kPermMultiSlots slots on; chunks of about 1024 slots, perm_blocks)
