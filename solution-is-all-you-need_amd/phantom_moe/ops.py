@@ -42,13 +42,15 @@ def _need_cuda(t: torch.Tensor, what: str) -> None:
         raise RuntimeError(f"{what} must live on the GPU (got {t.device}); this operator has no CPU path")
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+def workspace(device: torch.device, nbytes: int, stream: int | None = None) -> torch.Tensor:
     """Workspace of at least nbytes for (device, current stream).
 
     Cached per (device, stream) so calls on one stream reuse it in order;
     grows when a larger one is asked for.  Zero-filled when allocated (the
-    library keeps the call counter of its single-launch path in it)."""
-    stream = _lib.stream_handle(device)
+    library keeps the call counter of its single-launch path in it).
+    ``stream``: the current stream's handle when the caller has it."""
+    if stream is None:
+        stream = _lib.stream_handle(device)
     key = (device.index, stream)
     with _ws_lock:
         ws = _workspaces.get(key)
@@ -163,6 +165,10 @@ def permute(topk_idx: torch.Tensor, num_experts: int):
     return off, ss, sp
 
 
+# phantom_moe_workspace_bytes per forward shape (T, H, I, E, k, shared)
+_ws_bytes: dict = {}
+
+
 def moe_forward(x: torch.Tensor, router_weight: torch.Tensor, experts: MoEWeights, top_k: int,
                 score="softmax", router_bias=None, return_routing: bool = False, out: torch.Tensor | None = None):
     """The MoE layer: y[t] = sum_j w[t,j] FFN_{e[t,j]}(x[t]) (+ shared expert).
@@ -196,15 +202,19 @@ def moe_forward(x: torch.Tensor, router_weight: torch.Tensor, experts: MoEWeight
     lib = _lib.load()
     _lib.check_status()  # a failure an earlier call left
     has_sh = experts.shared is not None
-    nbytes = lib.phantom_moe_workspace_bytes(T, H, experts.I, E, top_k, int(has_sh))
-    ws = workspace(x.device, nbytes)
+    shape = (T, H, experts.I, E, top_k, int(has_sh))
+    nbytes = _ws_bytes.get(shape)
+    if nbytes is None:
+        nbytes = _ws_bytes[shape] = lib.phantom_moe_workspace_bytes(*shape)
+    stream = _lib.stream_handle(x.device)
+    ws = workspace(x.device, nbytes, stream)
     sh = [t.data_ptr() for t in experts.shared] if has_sh else [None] * 6
     rc = lib.phantom_moe_forward(
         x2.data_ptr(), 0, T, H, experts.I, E, top_k, _score_mode(score), W.data_ptr(),
         None if b is None else b.data_ptr(),
         experts.gate_nib.data_ptr(), experts.gate_scale.data_ptr(), experts.up_nib.data_ptr(),
         experts.up_scale.data_ptr(), experts.down_nib.data_ptr(), experts.down_scale.data_ptr(),
-        *sh, y.data_ptr(), idx.data_ptr(), w.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device),
+        *sh, y.data_ptr(), idx.data_ptr(), w.data_ptr(), ws.data_ptr(), ws.numel(), stream,
     )
     _lib.check(rc, "phantom_moe_forward")
     _lib.after_call(x.device)
