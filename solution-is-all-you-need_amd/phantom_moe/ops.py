@@ -133,6 +133,8 @@ def route(x: torch.Tensor, router_weight: torch.Tensor, top_k: int, score="softm
     T = x2.shape[0]
     idx = torch.empty((T, top_k), dtype=torch.int32, device=x.device)
     w = torch.empty((T, top_k), dtype=torch.float32, device=x.device)
+    if T == 0:  # an empty batch routes to empty outputs
+        return w.reshape(*lead, top_k), idx.reshape(*lead, top_k)
     lib = _lib.load()
     nbytes = lib.phantom_moe_workspace_bytes(T, H, 0, E, top_k, 0)
     ws = workspace(x.device, nbytes)
@@ -156,6 +158,8 @@ def permute(topk_idx: torch.Tensor, num_experts: int):
     off = torch.empty(num_experts + 1, dtype=torch.int32, device=idx.device)
     ss = torch.empty(T * k, dtype=torch.int32, device=idx.device)
     sp = torch.empty(T * k, dtype=torch.int32, device=idx.device)
+    if T == 0:  # no slots: every segment is empty
+        return off.zero_(), ss, sp
     lib = _lib.load()
     nbytes = lib.phantom_moe_workspace_bytes(T, 32, 0, num_experts, k, 0)
     ws = workspace(idx.device, nbytes)
@@ -199,6 +203,9 @@ def moe_forward(x: torch.Tensor, router_weight: torch.Tensor, experts: MoEWeight
         raise ValueError("out must be a contiguous fp32 tensor with T*H elements")
     idx = torch.empty((T, top_k), dtype=torch.int32, device=x.device)
     w = torch.empty((T, top_k), dtype=torch.float32, device=x.device)
+    if T == 0:  # an empty batch: empty outputs, as torch's own operators give
+        y = y.reshape(*lead, H)
+        return (y, w.reshape(*lead, top_k), idx.reshape(*lead, top_k)) if return_routing else y
     lib = _lib.load()
     _lib.check_status()  # a failure an earlier call left
     has_sh = experts.shared is not None

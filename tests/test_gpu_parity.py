@@ -222,6 +222,23 @@ def test_permute_vs_numpy(dev, T, k, E, mode):
     np.testing.assert_array_equal(rss, np.argsort(idx.reshape(-1), kind="stable"))
 
 
+def test_empty_batch(dev):
+    """No tokens: empty outputs of the right shapes (leading dims kept), as
+    torch's own operators give, and an all-zero offset table."""
+    cfg = synth.MoEConfig("empty", 256, 128, 16, 4, 1)
+    L = synth.host_layer(cfg)
+    ex = dev_weights(L, dev)
+    W = torch.from_numpy(L.router_w).to(dev)
+    x = torch.empty((2, 0, cfg.H), dtype=torch.bfloat16, device=dev)
+    y, w, idx = phantom_moe.moe_forward(x, W, ex, cfg.k, return_routing=True)
+    assert y.shape == (2, 0, cfg.H) and y.dtype == torch.float32
+    assert w.shape == (2, 0, cfg.k) and idx.shape == (2, 0, cfg.k)
+    rw, ridx = phantom_moe.route(x, W, cfg.k)
+    assert rw.shape == (2, 0, cfg.k) and ridx.shape == (2, 0, cfg.k)
+    off, ss, sp = phantom_moe.permute(torch.empty((0, cfg.k), dtype=torch.int32, device=dev), cfg.E)
+    assert off.shape == (cfg.E + 1,) and not off.any() and ss.numel() == 0 and sp.numel() == 0
+
+
 # ------------------------------------------------------------------ layer
 
 
