@@ -356,7 +356,6 @@ __global__ __launch_bounds__(kFThreads) void moe_decode_fused_kernel(FusedK a) {
   auto div_Kq4 = [&](int v) { return H_ ? v / (4 * ((H_ + kQuad - 1) / kQuad)) : fdiv(v, a.md_Kq4); };
   auto div_nrtI = [&](int v) { return I_ ? v / (I_ / kRowTile) : fdiv(v, a.md_nrtI); };
   auto div_KqI = [&](int v) { return I_ ? v / ((I_ + kQuad - 1) / kQuad) : fdiv(v, a.md_KqI); };
-  auto div_upos = [&](int v) { return I_ ? v / (64 * ((I_ + kQuad - 1) / kQuad)) : fdiv(v, a.md_upos); };
   const int Kg = H / kGroup, KgI = I / kGroup;
   const int npos = T * k + (has_sh ? T : 0);
   char* lds = reinterpret_cast<char*>(s_dyn);
