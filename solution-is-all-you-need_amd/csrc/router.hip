@@ -499,43 +499,53 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteK a) {
 
   // Chunks are loaded CB at a time (all loads of a batch issued before its
   // FMAs), then accumulated in increasing h as the contract requires.  Loads
-  // are unconditional, from clamped addresses, and out-of-range values are
-  // zeroed afterwards: a load under a branch gets its own vmcnt(0) wait,
-  // which would serialise the batch.
+  // are unconditional, from clamped addresses: a load under a branch gets its
+  // own vmcnt(0) wait, which would serialise the batch.  Pairs of a clamped
+  // expert or token are never stored, so only h needs a range: a batch of
+  // whole in-range chunks adds its values as loaded, and only the batch that
+  // reaches past H zeroes both operands of the lanes beyond it (so a
+  // non-finite value read from the clamped address adds nothing).
   const int64_t nchunks = ceil_div(a.H, 256);
+  const int64_t nfull = a.H / 256;  // chunks in range for every lane
   for (int64_t c0 = 0; c0 < nchunks; c0 += CB) {
     float wv[CB][EW][4];
     float xv[CB][TT][4];
+    bool hok[CB];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
       const int64_t h0 = (c0 + cb) * 256 + 4 * lane;
-      const bool hok = (c0 + cb) < nchunks && h0 < a.H;
-      const int64_t hc = hok ? h0 : 0;
+      hok[cb] = (c0 + cb) < nchunks && h0 < a.H;
+      const int64_t hc = hok[cb] ? h0 : 0;
 #pragma unroll
       for (int ei = 0; ei < EW; ++ei) {
-        const int e = e0 + ei;
-        const bool ok = hok && e < a.E;
-        const int64_t ec = e < a.E ? e : a.E - 1;
+        const int64_t ec = e0 + ei < a.E ? e0 + ei : a.E - 1;
         const float4 r = *reinterpret_cast<const float4*>(a.W + ec * a.H + hc);
-        wv[cb][ei][0] = ok ? r.x : 0.0f;
-        wv[cb][ei][1] = ok ? r.y : 0.0f;
-        wv[cb][ei][2] = ok ? r.z : 0.0f;
-        wv[cb][ei][3] = ok ? r.w : 0.0f;
+        wv[cb][ei][0] = r.x;
+        wv[cb][ei][1] = r.y;
+        wv[cb][ei][2] = r.z;
+        wv[cb][ei][3] = r.w;
       }
 #pragma unroll
       for (int ti = 0; ti < TT; ++ti) {
-        const int64_t t = t0 + ti;
-        const bool ok = hok && t < a.T;
-        const int64_t tc = t < a.T ? t : a.T - 1;
-        float v4[4];
-        load_x4<XT>(x, tc * a.H + hc, v4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) xv[cb][ti][i] = ok ? v4[i] : 0.0f;
+        const int64_t tc = t0 + ti < a.T ? t0 + ti : a.T - 1;
+        load_x4<XT>(x, tc * a.H + hc, xv[cb][ti]);
       }
     }
     // the MFMA-ordered copy of x, its loads in flight with the first batch's
     if (c0 == 0 && a.prep_x)
       prep_x_tile(a, t0, TT, (int)blockIdx.x, (int)gridDim.x, (int)threadIdx.x, (int)blockDim.x);
+    if (c0 + CB > nfull) {
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int ei = 0; ei < EW; ++ei) wv[cb][ei][i] = hok[cb] ? wv[cb][ei][i] : 0.0f;
+#pragma unroll
+          for (int ti = 0; ti < TT; ++ti) xv[cb][ti][i] = hok[cb] ? xv[cb][ti][i] : 0.0f;
+        }
+      }
+    }
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
 #pragma unroll
