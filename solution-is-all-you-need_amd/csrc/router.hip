@@ -1544,14 +1544,17 @@ static hipError_t launch_permute_multi(const int32_t* idx, int64_t T, int k, int
   return hipGetLastError();
 }
 
-// Tokens per logits workgroup.  Small tiles give the grid more workgroups to
+// Tokens per logits wave.  Small tiles give the grid more workgroups to
 // stream W with, large ones re-read W less.  Measured routes (us), tiles of
 // 1 / 2 / 4 tokens: DeepSeek-V3 8 tokens 22.5 / 24.8 / 29.7, Mixtral 16
-// tokens 15.6 / 18.7 / 22.2, Qwen3 32 tokens 21.8 / 17.7 / 19.7, DeepSeek-V3
-// 64 tokens 72.1 / 46.8 / 47.8.
+// tokens 15.6 / 18.7 / 22.2, Qwen3 32 tokens 21.8 / 17.7 / 19.7 (with
+// batches of eight chunks).  At 64 tokens of DeepSeek-V3 (H 7168, E 256)
+// four tokens with batches of four chunks take 32.7 against 40.8 us for two
+// tokens; eight tokens a wave took 35.0.
 int router_token_tile(int64_t T) {
   if (T <= 16) return 1;
-  if (T <= 64) return 2;
+  if (T <= 32) return 2;
+  if (T <= 64) return 4;
   return kBigTT;
 }
 
@@ -1563,6 +1566,11 @@ static hipError_t launch_logits_t(const RouteK& k, int TT, int n_ttiles, hipStre
   } else if (TT == 2) {
     dim3 grid((unsigned)ceil_div(k.E, 4 * 2), (unsigned)n_ttiles);
     hipLaunchKernelGGL((route_logits_kernel<XT, 2, 2, 8>), grid, dim3(256), 0, stream, k);
+  } else if (TT == 4) {
+    // batches of four chunks: with eight the bf16 kernel needs 256 registers
+    // (one wave a SIMD) and the 64-token route took 43.4 us, with four 203
+    dim3 grid((unsigned)ceil_div(k.E, 4 * 2), (unsigned)n_ttiles);
+    hipLaunchKernelGGL((route_logits_kernel<XT, 4, 2, 4>), grid, dim3(256), 0, stream, k);
   } else {
     dim3 grid((unsigned)ceil_div(k.E, 4 * kBigEW), (unsigned)n_ttiles);
     hipLaunchKernelGGL((route_logits_big_kernel<XT, kBigTT, kBigEW>), grid, dim3(256), 0, stream, k);

@@ -96,6 +96,8 @@ def test_route_golden(dev, name):
     (1, 2048, 128, 8, 0, "bf16"), (3, 96, 8, 2, 0, "bf16"), (5, 4096, 8, 2, 0, "f32"),
     (17, 512, 64, 6, 1, "bf16"), (64, 7168, 256, 8, 1, "bf16"), (65, 2048, 128, 8, 0, "bf16"),
     (300, 1024, 512, 32, 0, "f32"), (40, 256, 1, 1, 0, "bf16"), (33, 320, 3, 3, 1, "f32"),
+    # four-token logits waves (33-64 tokens): ragged H, E not a multiple of 8
+    (48, 416, 20, 4, 1, "bf16"), (64, 1056, 40, 8, 0, "f32"),
 ])
 def test_route_random_vs_oracle(dev, T, H, E, k, score, xdt):
     rng = np.random.default_rng(T * 131 + H + E)
@@ -109,12 +111,13 @@ def test_route_random_vs_oracle(dev, T, H, E, k, score, xdt):
     np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-6, atol=1e-7)
 
 
-@pytest.mark.parametrize("E,k", [(7, 7), (32, 32), (64, 4), (128, 8), (200, 32), (256, 16)])
-def test_route_special_values(dev, E, k):
+@pytest.mark.parametrize("E,k,T", [(7, 7, 9), (32, 32, 9), (64, 4, 9), (128, 8, 9), (200, 32, 9), (256, 16, 9),
+                                   (128, 8, 40), (256, 16, 64)])
+def test_route_special_values(dev, E, k, T):
     """NaN, +-inf, +-0 and exactly tied logits: NaN ranks below every number,
     -0 ties +0, ties go to the lower expert index (the oracle's ranks_before)."""
     rng = np.random.default_rng(1000 + E)
-    T, H = 9, 64
+    H = 64
     xb = synth.f32_to_bf16_bits(rng.standard_normal((T, H), dtype=np.float32))
     W = (rng.standard_normal((E, H), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
     W[1::5] = 0.0  # logit exactly +0 (plus bias)
