@@ -164,6 +164,10 @@ __device__ __attribute__((always_inline)) inline void gu_load(const GateUpK& a, 
     c.gs[r] = gload_u2(gsb + o_sc);
     c.us[r] = gload_u2(usb + o_sc);
   }
+  // Positions past the segment read the all-zero row T.  (Buffer loads with
+  // an out-of-range offset for them, which return zeros without a memory
+  // access, were slower here: DeepSeek-V3 8 tokens gate/up 183 -> 214 us,
+  // 64 tokens 724 -> 809 us.)
   const uint32_t xrow = ps.xoff + (uint32_t)q;  // (token, quad) row of xq / xs
   const char* xb = reinterpret_cast<const char*>(a.xq);
   const uint32_t o_x = (xrow * 16u + (uint32_t)p * 4u) * 16u;
@@ -623,9 +627,15 @@ __device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt0
   const u32x4 zero = {0u, 0u, 0u, 0u};
   const uint32_t mask = vgpr_const(0x03C003C0u);
 
+  // the operand through buffer resources; positions past the segment read
+  // zeros from beyond the buffer instead of the all-zero row, with no memory
+  // access (DeepSeek-V3 8 tokens 133.4 -> 131.9 us, 64 tokens 529.5 -> 524.7)
+  const BufRsrc hqr = buf_rsrc(a.hq, (uint32_t)(a.zero_row * a.Kq * 512));
+  const BufRsrc hsr = buf_rsrc(a.hs, (uint32_t)(a.zero_row * a.Kq * 32));
   for (int64_t m0 = beg; m0 < end; m0 += 16) {
     const int64_t pm0 = m0 + n;
-    const int64_t pm = pm0 < end ? pm0 : a.zero_row;
+    const bool preal = pm0 < end;
+    const uint32_t pm = (uint32_t)(preal ? pm0 : 0);
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     f32x4 acc[RT], corr[RT];
 #pragma unroll
@@ -647,17 +657,18 @@ __device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt0
           bw[i][r] = gload_nt<u32x4>(dnib + (tq * kWave + lane) * 16);
           bs[i][r] = *reinterpret_cast<const uint2*>(dsc + tq * kQuadScales + n * 4);
         }
-        const u32x4* src = reinterpret_cast<const u32x4*>(a.hq + ((pm * a.Kq + q) * 16 + p * 4) * 16);
+        const uint32_t o_h = preal ? ((pm * (uint32_t)a.Kq + (uint32_t)q) * 16u + (uint32_t)p * 4u) * 32u : kOutOfRange;
+        const uint32_t o_s = preal ? ((pm * (uint32_t)a.Kq * 4u + 4u * (uint32_t)q + (uint32_t)p) * 2u) * 4u : kOutOfRange;
 #pragma unroll
         for (int gi = 0; gi < 4; ++gi) {
           const bool real = 4 * q + gi < Kg;  // padded groups hold no h
-          const u32x4 h = src[2 * gi];
-          const u32x4 l = src[2 * gi + 1];
+          const u32x4 h = buf_load_b128(hqr, o_h + (uint32_t)(2 * gi) * 16u, 0);
+          const u32x4 l = buf_load_b128(hqr, o_h + (uint32_t)(2 * gi + 1) * 16u, 0);
           ah[i][gi] = real ? h : zero;
           al[i][gi] = real ? l : zero;
         }
-        const float* hsrc = a.hs + (pm * a.Kq * 4 + 4 * q + p) * 2;
-        const float s0 = hsrc[0], s1 = hsrc[1];
+        const uint2 hs2 = buf_load_b64(hsr, o_s, 0);
+        const float s0 = __builtin_bit_cast(float, hs2.x), s1 = __builtin_bit_cast(float, hs2.y);
         sp[i] = (4 * q + p < Kg) ? s0 + s1 : 0.0f;
       }
       // per-chunk partials, added to the totals once (short fp32 chains)

@@ -171,6 +171,11 @@ __device__ inline BufRsrc buf_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
 
+// A lane offset past every resource the library builds (each under 2 GiB):
+// the load returns zeros and accesses no memory.  The range check covers the
+// lane offset only, not the scalar one.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
 __device__ inline u32x4 buf_load_b128(BufRsrc r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
 }
