@@ -31,6 +31,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "expert_common.h"
 #include "moe_common.h"
 #include "moe_launch.h"
@@ -606,7 +608,7 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
 // Same decomposition as gate_up_kernel with RT 16-row tiles of H per item:
 // the activation operand of a quad (16 positions x 128 of I as fp16 hi/lo)
 // is loaded once and used for all RT tiles.  Positions past the segment
-// read the all-zero operand row of hq / hs.
+// read zeros.
 constexpr int kDownWaves = 4;
 
 template <int NQ, int RT>
@@ -632,10 +634,17 @@ __device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt0
   // access (DeepSeek-V3 8 tokens 133.4 -> 131.9 us, 64 tokens 529.5 -> 524.7)
   const BufRsrc hqr = buf_rsrc(a.hq, (uint32_t)(a.zero_row * a.Kq * 512));
   const BufRsrc hsr = buf_rsrc(a.hs, (uint32_t)(a.zero_row * a.Kq * 32));
-  for (int64_t m0 = beg; m0 < end; m0 += 16) {
-    const int64_t pm0 = m0 + n;
+  // One 16-position tile [m0, min(m0 + 16, end)).  With PK (at most 8
+  // positions) MFMA row 2i holds the fp16 hi of position m0 + i and row
+  // 2i + 1 its lo, so a group takes one operand load and one MFMA instead of
+  // two of each; the group-sum correction sits in the hi rows, and each
+  // position's output adds its two rows.
+  auto tile = [&](int64_t m0, auto pk) {
+    constexpr bool PK = decltype(pk)::value;
+    const int64_t pm0 = PK ? m0 + n / 2 : m0 + n;
     const bool preal = pm0 < end;
     const uint32_t pm = (uint32_t)(preal ? pm0 : 0);
+    const uint32_t hsel = PK ? (uint32_t)(n & 1) : 0u;  // PK: this row's half (0 hi, 1 lo)
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     f32x4 acc[RT], corr[RT];
 #pragma unroll
@@ -643,7 +652,7 @@ __device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt0
     for (int64_t q0 = ks; q0 < a.Kq; q0 += (int64_t)NQ * ksplit) {
       u32x4 bw[NQ][RT];
       uint2 bs[NQ][RT];
-      u32x4 ah[NQ][4], al[NQ][4];
+      u32x4 ah[NQ][4], al[NQ][PK ? 1 : 4];
       float sp[NQ];
       bool qok[NQ];
 #pragma unroll
@@ -658,14 +667,21 @@ __device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt0
           bs[i][r] = *reinterpret_cast<const uint2*>(dsc + tq * kQuadScales + n * 4);
         }
         const uint32_t o_h = preal ? ((pm * (uint32_t)a.Kq + (uint32_t)q) * 16u + (uint32_t)p * 4u) * 32u : kOutOfRange;
-        const uint32_t o_s = preal ? ((pm * (uint32_t)a.Kq * 4u + 4u * (uint32_t)q + (uint32_t)p) * 2u) * 4u : kOutOfRange;
+        const uint32_t o_s = preal && hsel == 0u
+                                 ? ((pm * (uint32_t)a.Kq * 4u + 4u * (uint32_t)q + (uint32_t)p) * 2u) * 4u
+                                 : kOutOfRange;
 #pragma unroll
         for (int gi = 0; gi < 4; ++gi) {
           const bool real = 4 * q + gi < Kg;  // padded groups hold no h
-          const u32x4 h = buf_load_b128(hqr, o_h + (uint32_t)(2 * gi) * 16u, 0);
-          const u32x4 l = buf_load_b128(hqr, o_h + (uint32_t)(2 * gi + 1) * 16u, 0);
-          ah[i][gi] = real ? h : zero;
-          al[i][gi] = real ? l : zero;
+          if constexpr (PK) {
+            const u32x4 v = buf_load_b128(hqr, o_h + ((uint32_t)(2 * gi) + hsel) * 16u, 0);
+            ah[i][gi] = real ? v : zero;
+          } else {
+            const u32x4 h = buf_load_b128(hqr, o_h + (uint32_t)(2 * gi) * 16u, 0);
+            const u32x4 l = buf_load_b128(hqr, o_h + (uint32_t)(2 * gi + 1) * 16u, 0);
+            ah[i][gi] = real ? h : zero;
+            al[i][gi] = real ? l : zero;
+          }
         }
         const uint2 hs2 = buf_load_b64(hsr, o_s, 0);
         const float s0 = __builtin_bit_cast(float, hs2.x), s1 = __builtin_bit_cast(float, hs2.y);
@@ -687,7 +703,7 @@ __device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt0
           for (int gi = 0; gi < 4; ++gi) {
             const u32x4 bb = dequant_unit_f16(bwv[gi], mask);
             f32x4 pp = mfma_f16_16x16x32(ah[i][gi], bb, z);
-            pp = mfma_f16_16x16x32(al[i][gi], bb, pp);
+            if constexpr (!PK) pp = mfma_f16_16x16x32(al[i][gi], bb, pp);
             part[r] += dv[gi] * pp;
           }
           corr[r] = mfma_f32_16x16x4(sp[i], dv[p], corr[r]);
@@ -699,8 +715,15 @@ __device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt0
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
       const f32x4 res = kUnitScale * acc[r] - kUnitBias * corr[r];
+      if constexpr (PK) {
+        // rows 4p, 4p + 1 are position 2p's hi and lo, rows 4p + 2, 4p + 3
+        // position 2p + 1's
+        red[ks][r][2 * p][n] = res[0] + res[1];
+        red[ks][r][2 * p + 1][n] = res[2] + res[3];
+      } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) red[ks][r][4 * p + j][n] = res[j];
+        for (int j = 0; j < 4; ++j) red[ks][r][4 * p + j][n] = res[j];
+      }
     }
     __syncthreads();
     for (int o = threadIdx.x; o < RT * 256; o += blockDim.x) {
@@ -712,6 +735,10 @@ __device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt0
       if (m0 + mm < end) a.outbuf[(m0 + mm) * a.H + (rt0 + r) * 16 + nn] = y;
     }
     __syncthreads();
+  };
+  for (int64_t m0 = beg; m0 < end; m0 += 16) {
+    if (end - m0 <= 8) tile(m0, std::true_type{});
+    else tile(m0, std::false_type{});
   }
 }
 
