@@ -39,12 +39,17 @@ __device__ inline uint64_t logit_key(double v) {
 //  3. The k winners are compacted to LDS in index order and lane i < k ranks
 //     winner i among them (the other winners read from their lanes); rank r
 //     goes to slot r.
+//  With at most kRankCountMaxE experts, steps 1-3 are one count per lane
+//  instead: the keys ranked above its own (larger, or equal at a lower index).
 //  4. Weights, fp64: softmax exp(l_j - l_0) / sum_i exp(l_i - l_0), or
 //     sigmoid(l_j) / sum_i sigmoid(l_i), the sum taken in slot order; stored
 //     as fp32.
 // Outputs (slot j = lane < k): out_idx[j], out_w[j], and out_idx2[j] when
 // out_idx2 is non-null.  The s_* arrays are this wave's LDS scratch of k
 // entries each.
+// Expert counts up to which one wave ranks by counting instead of the descent.
+constexpr int kRankCountMaxE = 32;
+
 template <int NV>
 __device__ __attribute__((always_inline)) inline void wave_topk_row(const double* row, int E, int k, int score_mode,
                                                                     uint64_t* s_ck, double* s_cv, int* s_ci,
@@ -62,6 +67,22 @@ __device__ __attribute__((always_inline)) inline void wave_topk_row(const double
     val[v] = e < E ? lv : 0.0;
     key[v] = e < E ? logit_key(lv) : 0ull;
   }
+  if (NV == 1 && E <= kRankCountMaxE) {
+    // Few experts (one key per lane): each lane counts the keys ranked above
+    // its own -- larger, or equal at a lower index -- from lane broadcasts;
+    // rank r < k goes to slot r.  The same order as the descent below, in
+    // about 7 instructions a key instead of one ballot chain per two bits.
+    int r = 0;
+    for (int j = 0; j < E; ++j) {
+      const uint64_t kj = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(key[0] >> 32), j) << 32) |
+                          (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key[0], j);
+      r += (kj > key[0] || (kj == key[0] && j < lane)) ? 1 : 0;
+    }
+    if (lane < E && r < k) {
+      s_idx[r] = lane;
+      s_val[r] = val[0];
+    }
+  } else {
   // Invariant: #{key >= kth} >= k.  Once it is exactly k the winners are
   // known (every other key is below kth), so the descent stops there --
   // usually at the first bits that separate the k-th and (k+1)-th keys.  Two
@@ -133,6 +154,7 @@ __device__ __attribute__((always_inline)) inline void wave_topk_row(const double
   if (lane < k) {
     s_idx[r] = me;
     s_val[r] = mv;
+  }
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
