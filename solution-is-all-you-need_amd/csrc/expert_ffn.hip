@@ -24,8 +24,9 @@
 // The gate/up activations x are exact bf16.  The down activations h are fp32;
 // the gate/up epilogue stores each h as an fp16 pair hi + lo (|h - hi - lo| <=
 // 2^-22 |h|) already in MFMA operand order, plus half-group sums, so the down
-// kernel only loads operands (two fp16 MFMAs per group).  fp16 bounds |h| to
-// below 65504.
+// kernel only loads operands (two fp16 MFMAs per group; one in the K-split
+// kernel for tiles of at most 8 positions, whose hi and lo share an MFMA as
+// adjacent rows).  fp16 bounds |h| to below 65504.
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
