@@ -1016,9 +1016,12 @@ static bool tile_fits(const ExpertArgs& x, const GateUpK& g) {
   return g.tiles != nullptr && gate_up_tile_regime(x.T, x.H, x.I, x.E, x.k, x.has_shared);
 }
 
-// Ring depth 3 (a tuning override may set 2..4).
+// Ring depth 3, or 2 from rows of 32 quads of H on (a tuning override may set
+// 2..4): Qwen3 at 32 tokens (16 quads) 54.2 us a layer with 3 against 54.8
+// with 2 or 4; Mixtral at 16 tokens (32 quads) 162.5 with 2 against 164.2
+// (165.3 against 166.2 on another box).
 static hipError_t launch_gate_up_tile(const ExpertArgs& x, const GateUpK& g, hipStream_t stream) {
-  const int depth = tuning().gu_depth ? tuning().gu_depth : 3;
+  const int depth = tuning().gu_depth ? tuning().gu_depth : (g.Kq >= 32 ? 2 : 3);
   // Eight waves per workgroup, one workgroup per CU (two waves per SIMD, as
   // with two 4-wave workgroups): each CU copies a tile's operand to LDS once
   // rather than twice (Qwen3 shapes, 32 tokens: 24.5 -> 23.7 us).
