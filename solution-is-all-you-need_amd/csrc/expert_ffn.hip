@@ -630,11 +630,13 @@ __device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt0
   const u32x4 zero = {0u, 0u, 0u, 0u};
   const uint32_t mask = vgpr_const(0x03C003C0u);
 
-  // the operand through buffer resources; positions past the segment read
-  // zeros from beyond the buffer instead of the all-zero row, with no memory
-  // access (DeepSeek-V3 8 tokens 133.4 -> 131.9 us, 64 tokens 529.5 -> 524.7)
-  const BufRsrc hqr = buf_rsrc(a.hq, (uint32_t)(a.zero_row * a.Kq * 512));
-  const BufRsrc hsr = buf_rsrc(a.hs, (uint32_t)(a.zero_row * a.Kq * 32));
+  // the operand through buffer resources over this segment's positions only
+  // (its size is then far below 4 GiB whatever the layer's; the launch
+  // checks it), positions past the segment reading zeros from beyond the
+  // buffer instead of the all-zero row, with no memory access (DeepSeek-V3
+  // 8 tokens 133.4 -> 131.9 us, 64 tokens 529.5 -> 524.7)
+  const BufRsrc hqr = buf_rsrc(a.hq + beg * a.Kq * 256, (uint32_t)((end - beg) * a.Kq * 512));
+  const BufRsrc hsr = buf_rsrc(a.hs + beg * a.Kq * 8, (uint32_t)((end - beg) * a.Kq * 32));
   // One 16-position tile [m0, min(m0 + 16, end)).  With PK (at most 8
   // positions) MFMA row 2i holds the fp16 hi of position m0 + i and row
   // 2i + 1 its lo, so a group takes one operand load and one MFMA instead of
@@ -644,7 +646,7 @@ __device__ inline void down_item(const DownK& a, const int4 d, const int64_t rt0
     constexpr bool PK = decltype(pk)::value;
     const int64_t pm0 = PK ? m0 + n / 2 : m0 + n;
     const bool preal = pm0 < end;
-    const uint32_t pm = (uint32_t)(preal ? pm0 : 0);
+    const uint32_t pm = (uint32_t)(preal ? pm0 - beg : 0);  // position within the segment
     const uint32_t hsel = PK ? (uint32_t)(n & 1) : 0u;  // PK: this row's half (0 hi, 1 lo)
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     f32x4 acc[RT], corr[RT];
@@ -1184,6 +1186,9 @@ static hipError_t launch_down_tile(const ExpertArgs& x, const DownK& d, hipStrea
 hipError_t launch_down(const ExpertArgs& x, const Workspace& ws, hipStream_t stream) {
   const DownK d = make_down_k(x, ws);
   if (d.tiles && down_tile_regime(x.T, x.H, x.I, x.E, x.k, x.has_shared)) return launch_down_tile(x, d, stream);
+  // the K-split kernel reads a segment's operand (at most T positions)
+  // through one buffer resource, which must stay under 2 GiB
+  if (x.T * d.Kq * 512 >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
   Split sp = choose_split(d.Kq, kDownWaves);
   int rt = 2;  // H is a multiple of 32: an even number of 16-row tiles
   // Two quads of loads in flight per wave pay off only when items are few
