@@ -218,7 +218,9 @@ PHANTOM_MOE_API int phantom_moe_permute(const int32_t* topk_idx, int64_t T, int 
  * NaN, and the status bits are set in the workspace and in the word of
  * phantom_moe_status_word.  PHANTOM_MOE_DECODE=staged (or the option
  * PHANTOM_MOE_OPT_DECODE_FUSED) turns the single launch off.  Alignment: nibble buffers 16 bytes, scale buffers 8, x 8,
- * router_w 16, workspace 256. */
+ * router_w 16, workspace 256.  Below 64 positions per expert (the decode
+ * regime), T * ceil(I / 128) * 512 must stay under 2^31 (one expert
+ * segment's down operand), else PHANTOM_MOE_EUNSUPPORTED. */
 PHANTOM_MOE_API int phantom_moe_forward(const void* x, int x_dtype, int64_t T, int64_t H, int64_t I, int E, int top_k,
                         int score_mode, const float* router_w, const float* router_bias,
                         const uint8_t* gate_nib, const uint16_t* gate_scale, const uint8_t* up_nib,

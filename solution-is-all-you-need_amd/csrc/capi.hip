@@ -379,6 +379,10 @@ int check_forward(ForwardCall& c) {
     return fail(PHANTOM_MOE_EINVAL, "repacked scale buffers must be 8-byte aligned");
   if (misaligned(c.x, 8) || misaligned(c.router_w, 16))
     return fail(PHANTOM_MOE_EINVAL, "x must be 8-byte and router_w 16-byte aligned");
+  // the decode-regime down kernel reads one expert segment's operand (at
+  // most T positions of I as fp16 hi and lo) through a 32-bit buffer resource
+  if (!pmoe::gemm_regime(c.T, c.top_k, c.E) && c.T * ((c.I + 127) / 128) * 512 >= ((int64_t)1 << 31))
+    return fail(PHANTOM_MOE_EUNSUPPORTED, "T*I too large for the decode regime (one segment's down operand above 2 GiB)");
   return 0;
 }
 

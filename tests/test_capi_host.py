@@ -163,6 +163,9 @@ def _forward(**kw):
         (dict(y=None), EINVAL),
         (dict(ws=None), EWORKSPACE),
         (dict(T=-1), EINVAL),
+        # decode regime (under 64 positions per expert) with one segment's
+        # down operand above 2 GiB
+        (dict(T=32000, I=16896, E=512, k=1), EUNSUPPORTED),
     ],
 )
 def test_forward_validation(kw, code):
