@@ -7,14 +7,17 @@
 //
 // Work decomposition.  The router's permute groups tokens per expert into
 // segments and writes one descriptor {expert, begin, end} per launch slot
-// (expert -1 for slots beyond the active count).  A workgroup owns one 16-row
-// tile of one slot's expert and splits K across up to 16 waves, each issuing
-// the loads of its one to four quads at once; there are no loops over K and
-// no dependent chains beyond descriptor -> token id -> activation, so the
-// many short waves keep HBM busy the way a plain streaming read does.  Wave
-// partials are summed in LDS in wave order, so results do not depend on
-// timing.  Every weight byte of an active expert is read from HBM once; later
-// 16-token tiles of a long segment re-read it from L2.
+// (expert -1 for slots beyond the active count), and, for the token-tile
+// kernels, a table of 16-position token tiles.  Two kernel pairs:
+//   K-split (gate_up_kernel, down_kernel): an item is RT 16-row tiles of one
+//     segment's expert; up to four waves split K, each loading one or two
+//     quads per step, and their partials are summed in LDS in wave order;
+//   token-tile (gate_up_tile_kernel, down_tile_kernel): a workgroup copies
+//     one token tile's activation operand into LDS once, and each wave
+//     streams whole row tiles through a ring of weight chunks in registers.
+// Results do not depend on timing.  Every weight byte of an active expert is
+// read from HBM once per token tile; later tiles of a long segment mostly
+// find it in L2 or the MALL.
 //
 // Arithmetic per 32-group g, token m, weight row n (see moe_common.h):
 //   P = mfma(a_m, 1 + nib_n / 16)               exact products, fp32 sums
